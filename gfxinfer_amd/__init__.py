@@ -1,0 +1,201 @@
+"""gfxinfer_amd: MI355X (gfx950) speculative-verify hot path.
+
+Python view of the C ABI declared in include/gfxinfer_amd.h.  The compute lives
+in libgfxinfer_amd.so (hand-written HIP for gfx950); this module only loads it,
+declares the signatures and offers thin wrappers that mirror the reference
+launchers (src/kernels/lowbit_gemv.hip, src/kernels/qwen_ops.hip) with the same
+argument meaning and error behaviour: a non-zero status raises GfxinferError
+carrying the reference ErrorCode value and message.
+
+There is no fallback: if the library is missing, importing the wrappers fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIBRARY = os.path.join(HERE, "libgfxinfer_amd.so")
+HEADER = os.path.join(ROOT, "include", "gfxinfer_amd.h")
+
+# include/gfxinfer/status.h:11-20
+OK, INVALID_ARGUMENT, IO_ERROR, CORRUPT_ARTIFACT, UNSUPPORTED, HIP_ERROR, OUT_OF_MEMORY, INTERNAL = range(8)
+# include/gfxinfer/artifact.h:26-33
+W2G128, W3G128, W4G128 = 1, 2, 3
+ERROR_NAMES = {0: "ok", 1: "invalid_argument", 2: "io_error", 3: "corrupt_artifact",
+               4: "unsupported", 5: "hip_error", 6: "out_of_memory", 7: "internal"}
+
+
+class GfxinferError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+def build(jobs: int = 8) -> None:
+    """Compile libgfxinfer_amd.so for gfx950 in-tree."""
+    subprocess.run(["make", "-s", "-C", HERE, f"-j{jobs}"], check=True)
+
+
+_lib: ctypes.CDLL | None = None
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+U32 = ctypes.c_uint32
+I32 = ctypes.c_int32
+F32 = ctypes.c_float
+
+# name -> (restype, argtypes).  Every function of include/gfxinfer_amd.h.
+SIGNATURES: dict[str, tuple] = {
+    "gfxinfer_last_error": (ctypes.c_char_p, []),
+    "gfxinfer_require_gfx950_device": (I32, [I32]),
+    "gfxinfer_packed_row_bytes": (SZ, [I32, SZ]),
+    "gfxinfer_tile_group128_for_gfx950": (I32, [I32, P, P, SZ, SZ, P, P]),
+    "gfxinfer_untile_group128_for_gfx950": (I32, [I32, P, P, SZ, SZ, P, P]),
+    "gfxinfer_launch_quantize_group128_gfx950": (I32, [I32, P, SZ, SZ, P, P, P, P]),
+    "gfxinfer_launch_quantize_activation_i4": (I32, [P, P, P, SZ, U32, P]),
+    "gfxinfer_launch_quantize_activation_i8": (I32, [P, P, P, SZ, U32, P]),
+    "gfxinfer_launch_gfx950_i4_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, I32, P]),
+    "gfxinfer_launch_gfx950_i4_gemm_half": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, I32, P]),
+    "gfxinfer_launch_gfx950_i4_gemm_fused": (I32, [I32, P, SZ, P, P, SZ, U32, I32, P]),
+    "gfxinfer_launch_gfx950_i8_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, P]),
+    "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
+    "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
+    "gfxinfer_launch_lowbit_row_gather_tiled_indirect": (I32, [I32, P, P, P, P, SZ, SZ, P]),
+}
+
+
+class FusedMatrix(ctypes.Structure):
+    """gfxinfer_fused_matrix (lowbit_gemv.h:128-133 Gfx12I4FusedMatrix)."""
+    _fields_ = [("tiled_weights", P), ("tiled_weight_scales", P), ("output", P), ("rows", SZ)]
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            raise RuntimeError(
+                f"{LIBRARY} is not built; run __graft_entry__.build() (hipcc for gfx950)")
+        L = ctypes.CDLL(LIBRARY)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def header_functions() -> list[str]:
+    """Names of every function declared in include/gfxinfer_amd.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gfxinfer_[a-z0-9_]+)\s*\(", text)))
+
+
+def last_error() -> str:
+    return lib().gfxinfer_last_error().decode()
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise GfxinferError(status, last_error())
+
+
+def _p(x) -> int | None:
+    """Device/host address of a torch tensor, numpy array or raw int."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    return x.ctypes.data
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+# ---- wrappers (reference launcher names, lowbit_gemv.h) ---------------------
+
+def launch_quantize_activation_i4(x, packed, scales, columns, batch, stream=None):
+    check(lib().gfxinfer_launch_quantize_activation_i4(_p(x), _p(packed), _p(scales), columns, batch, _stream(stream)))
+
+
+def launch_quantize_activation_i8(x, codes, scales, columns, batch, stream=None):
+    check(lib().gfxinfer_launch_quantize_activation_i8(_p(x), _p(codes), _p(scales), columns, batch, _stream(stream)))
+
+
+def launch_quantize_group128(fmt, weights, rows, columns, codes, scales, flag=None, stream=None):
+    check(lib().gfxinfer_launch_quantize_group128_gfx950(fmt, _p(weights), rows, columns, _p(codes), _p(scales), _p(flag), _stream(stream)))
+
+
+def launch_i4_gemm(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
+    check(lib().gfxinfer_launch_gfx950_i4_gemm(fmt, _p(w), _p(ws), _p(a), _p(as_), _p(out), rows, columns, batch, 1, _stream(stream)))
+
+
+def launch_i4_gemm_half(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
+    check(lib().gfxinfer_launch_gfx950_i4_gemm_half(fmt, _p(w), _p(ws), _p(a), _p(as_), _p(out), rows, columns, batch, 1, _stream(stream)))
+
+
+def launch_i4_gemm_fused(fmt, matrices, a, as_, columns, batch, stream=None):
+    """matrices: list of (weights, scales, output, rows)."""
+    arr = (FusedMatrix * len(matrices))(*[FusedMatrix(_p(w), _p(s), _p(o), r) for (w, s, o, r) in matrices])
+    check(lib().gfxinfer_launch_gfx950_i4_gemm_fused(fmt, ctypes.cast(arr, P), len(matrices), _p(a), _p(as_), columns, batch, 1, _stream(stream)))
+
+
+def launch_i8_gemm(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
+    check(lib().gfxinfer_launch_gfx950_i8_gemm(fmt, _p(w), _p(ws), _p(a), _p(as_), _p(out), rows, columns, batch, _stream(stream)))
+
+
+def debug_gemm_partials(fmt, w, abits, a, rows, columns, batch, partials, stream=None):
+    check(lib().gfxinfer_debug_gemm_partials(fmt, _p(w), abits, _p(a), rows, columns, batch, _p(partials), _stream(stream)))
+
+
+def launch_row_gather_tiled(fmt, w, ws, out, row, rows, columns, stream=None):
+    check(lib().gfxinfer_launch_lowbit_row_gather_tiled(fmt, _p(w), _p(ws), _p(out), row, rows, columns, _stream(stream)))
+
+
+def launch_row_gather_tiled_indirect(fmt, w, ws, out, row_ptr, rows, columns, stream=None):
+    check(lib().gfxinfer_launch_lowbit_row_gather_tiled_indirect(fmt, _p(w), _p(ws), _p(out), _p(row_ptr), rows, columns, _stream(stream)))
+
+
+# ---- host-side layout (numpy) -------------------------------------------------
+
+def packed_row_bytes(fmt: int, columns: int) -> int:
+    return int(lib().gfxinfer_packed_row_bytes(fmt, columns))
+
+
+def tile_bytes(fmt: int, rows: int, columns: int) -> int:
+    return rows * columns * (3 if fmt == W3G128 else 4) // 8
+
+
+def tile_group128(fmt, packed_codes, scales, rows, columns):
+    """Reference-packed codes + float scales -> (tiled codes, fp16 scale bits)."""
+    import numpy as np
+    packed_codes = np.ascontiguousarray(packed_codes, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    codes = np.zeros(tile_bytes(fmt, rows, columns), dtype=np.uint8)
+    tscales = np.zeros(rows * (columns // 128), dtype=np.uint16)
+    check(lib().gfxinfer_tile_group128_for_gfx950(fmt, _p(packed_codes), _p(scales), rows, columns, _p(codes), _p(tscales)))
+    return codes, tscales
+
+
+def untile_group128(fmt, codes, tscales, rows, columns):
+    """Tiled codes (+ fp16 scales) -> (int8 weights [rows, columns], fp16 scale bits [rows, G])."""
+    import numpy as np
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    w = np.empty((rows, columns), dtype=np.int8)
+    s = np.empty((rows, columns // 128), dtype=np.uint16)
+    ts = None if tscales is None else np.ascontiguousarray(tscales, dtype=np.uint16)
+    check(lib().gfxinfer_untile_group128_for_gfx950(fmt, _p(codes), _p(ts), rows, columns, _p(w), _p(s) if ts is not None else None))
+    return w, s

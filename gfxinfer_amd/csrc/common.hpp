@@ -1,0 +1,159 @@
+// Shared definitions for the gfx950 speculative-verify library: status codes,
+// error text, launch checks and the MI355X packed-weight tile layout.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "gfxinfer_amd.h"
+
+namespace gfx950 {
+
+constexpr std::size_t kGroup = 128;  // quantization group along K
+constexpr unsigned kWave = 64;       // CDNA wavefront
+
+// Records the message for gfxinfer_last_error() and returns the code.
+int32_t fail(int32_t code, const std::string& message);
+int32_t ok();
+// Maps a HIP error to GFXI_HIP_ERROR with context (reference device.cpp:24-35).
+int32_t hip_fail(hipError_t error, const char* context);
+// hipGetLastError after a launch, as every reference launcher does.
+int32_t launch_status(const char* context);
+
+inline bool valid_weight_format(int32_t format) {
+  return format == GFXI_W3G128 || format == GFXI_W4G128;
+}
+
+// ---------------------------------------------------------------------------
+// gfx950 tile layout of a group-128 packed matrix [N, K] (N % 16 == 0).
+//
+// codes : [N/16 row tiles][K/128 groups][64 lanes][L bytes]  L = 12 (W3), 16 (W4)
+// scales: [N/16 row tiles][K/128 groups][16 rows] fp16
+//
+// Lane l of a (tile, group) chunk holds row m = l % 16 of the tile and the 32
+// columns kb*32 .. kb*32+31 of the group, kb = l / 16.  Those 32 columns feed two
+// v_mfma_i32_16x16x64_i8 K-steps (h = 0, 1; 16 columns each) as the A operand.
+// Inside one K-step, operand byte j = 4*reg + byte maps to column
+//     16*h + 8*(reg >> 1) + 2*byte + (reg & 1)
+// which is the order in which packed 4-bit activations expand with two masks
+// (even columns from the low nibbles, odd columns from the high nibbles).
+//
+// W4: the 16 lane bytes are the 32 columns packed two per byte, even column in
+//     the low nibble -- the reference's own W4 byte format for 32 consecutive
+//     columns.  A nibble masked into bits 4..7 of a byte reads as 16*w in int8.
+// W3: the 12 lane bytes are three dwords S0, S1, S2 holding the eight operand
+//     registers out[o] (o = 4*h + reg) as 3-bit two's complement fields that land
+//     in bits 5..7 of each byte (int8 value 32*w) with one shift and one mask:
+//       out0 = (S0<<5)&E  out1 = (S0<<2)&E  out2 = (S1<<5)&E  out3 = (S1<<2)&E
+//       out4 = (S2<<5)&E  out5 = (S2<<2)&E                     (E = 0xE0E0E0E0)
+//       out6 = (S0&0xC0C0C0C0) | ((S1>>1)&0x20202020)
+//       out7 = (S2&0xC0C0C0C0) | ((S1>>2)&0x20202020)
+// ---------------------------------------------------------------------------
+
+__host__ __device__ constexpr unsigned lane_bytes(int32_t format) {
+  return format == GFXI_W3G128 ? 12u : 16u;
+}
+
+// Column (0..31 within the lane's 32) of operand slot (h, reg, byte).
+__host__ __device__ constexpr unsigned slot_column(unsigned h, unsigned reg, unsigned byte) {
+  return 16u * h + 8u * (reg >> 1) + 2u * byte + (reg & 1u);
+}
+
+// Inverse: (h, reg, byte) of lane column c (0..31).
+__host__ __device__ inline void column_slot(unsigned c, unsigned& h, unsigned& reg,
+                                            unsigned& byte) {
+  h = c / 16u;
+  const unsigned j = c % 16u;
+  reg = 2u * (j / 8u) + (j & 1u);
+  byte = (j % 8u) / 2u;
+}
+
+// Packs 32 signed weights (column order) of one lane chunk.
+__host__ __device__ inline void pack_lane_chunk(int32_t format, const int8_t* w32,
+                                                uint8_t* out) {
+  if (format == GFXI_W4G128) {
+    for (unsigned i = 0; i < 16; ++i) {
+      out[i] = static_cast<uint8_t>((static_cast<unsigned>(w32[2 * i]) & 0xfu) |
+                                    ((static_cast<unsigned>(w32[2 * i + 1]) & 0xfu) << 4));
+    }
+    return;
+  }
+  uint32_t s[3] = {0, 0, 0};
+  for (unsigned c = 0; c < 32; ++c) {
+    unsigned h, reg, byte;
+    column_slot(c, h, reg, byte);
+    const unsigned o = 4u * h + reg;
+    const uint32_t f = static_cast<uint32_t>(w32[c]) & 7u;
+    const unsigned base = 8u * byte;
+    switch (o) {
+      case 0: s[0] |= f << base; break;
+      case 1: s[0] |= f << (base + 3); break;
+      case 2: s[1] |= f << base; break;
+      case 3: s[1] |= f << (base + 3); break;
+      case 4: s[2] |= f << base; break;
+      case 5: s[2] |= f << (base + 3); break;
+      case 6:
+        s[0] |= (f >> 1) << (base + 6);
+        s[1] |= (f & 1u) << (base + 6);
+        break;
+      default:
+        s[2] |= (f >> 1) << (base + 6);
+        s[1] |= (f & 1u) << (base + 7);
+        break;
+    }
+  }
+  for (unsigned d = 0; d < 3; ++d) {
+    for (unsigned i = 0; i < 4; ++i) out[4 * d + i] = static_cast<uint8_t>(s[d] >> (8 * i));
+  }
+}
+
+// Signed weight at lane-chunk column c (0..31).
+__host__ __device__ inline int unpack_lane_code(int32_t format, const uint8_t* chunk,
+                                                unsigned c) {
+  if (format == GFXI_W4G128) {
+    const unsigned v = (chunk[c / 2] >> ((c & 1u) * 4u)) & 0xfu;
+    return v >= 8u ? static_cast<int>(v) - 16 : static_cast<int>(v);
+  }
+  uint32_t s[3];
+  for (unsigned d = 0; d < 3; ++d) {
+    s[d] = static_cast<uint32_t>(chunk[4 * d]) | (static_cast<uint32_t>(chunk[4 * d + 1]) << 8) |
+           (static_cast<uint32_t>(chunk[4 * d + 2]) << 16) |
+           (static_cast<uint32_t>(chunk[4 * d + 3]) << 24);
+  }
+  unsigned h, reg, byte;
+  column_slot(c, h, reg, byte);
+  const unsigned o = 4u * h + reg;
+  const unsigned base = 8u * byte;
+  uint32_t f;
+  switch (o) {
+    case 0: f = s[0] >> base; break;
+    case 1: f = s[0] >> (base + 3); break;
+    case 2: f = s[1] >> base; break;
+    case 3: f = s[1] >> (base + 3); break;
+    case 4: f = s[2] >> base; break;
+    case 5: f = s[2] >> (base + 3); break;
+    case 6: f = (((s[0] >> (base + 6)) & 3u) << 1) | ((s[1] >> (base + 6)) & 1u); break;
+    default: f = (((s[2] >> (base + 6)) & 3u) << 1) | ((s[1] >> (base + 7)) & 1u); break;
+  }
+  f &= 7u;
+  return f >= 4u ? static_cast<int>(f) - 8 : static_cast<int>(f);
+}
+
+// Byte offset of the lane chunk holding (row, column) in the tiled codes.
+__host__ __device__ inline std::size_t chunk_offset(int32_t format, std::size_t row,
+                                                    std::size_t column, std::size_t groups) {
+  const std::size_t tile = row / 16, m = row % 16;
+  const std::size_t group = column / kGroup, kb = (column % kGroup) / 32;
+  return ((tile * groups + group) * 64 + (kb * 16 + m)) * lane_bytes(format);
+}
+
+__host__ __device__ inline std::size_t scale_offset(std::size_t row, std::size_t group,
+                                                    std::size_t groups) {
+  return ((row / 16) * groups + group) * 16 + row % 16;
+}
+
+}  // namespace gfx950

@@ -1,0 +1,719 @@
+// Packed low-bit GEMV / skinny GEMM for gfx950 (MI355X), plus the activation
+// quantizers, the device weight quantizer and the tiled row gather.
+//
+// Reference semantics: src/kernels/lowbit_gemv.hip (launchers :838-1363) and
+// src/quantization.cpp.  The gfx12 WMMA iu4 path has no CDNA4 counterpart, so
+// both operands are widened to int8 and multiplied on v_mfma_i32_16x16x64_i8:
+// a W3 code lands in bits 5..7 of a byte (value 32*w), a W4 or A4 nibble in bits
+// 4..7 (16*w), an A8 code stays as is.  The MFMA sum is therefore F times the
+// exact integer dot (F = 512, 256, 32 or 16), and the fp32 epilogue folds 1/F
+// into the activation scale, which keeps fmaf(float(P), ws*as, acc) exact.
+#include <cstring>
+#include <limits>
+#include <string>
+
+#include "common.hpp"
+
+namespace gfx950 {
+namespace {
+
+using i32x4 = int __attribute__((ext_vector_type(4)));
+using u32x4 = unsigned __attribute__((ext_vector_type(4)));
+using u32x3 = unsigned __attribute__((ext_vector_type(3)));
+using u32x2 = unsigned __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Activation quantizers (lowbit_gemv.hip:373-436): one wave per (token, group);
+// lane i owns columns 2i and 2i+1.  The group maximum is exact under any
+// reduction order, and x / float(scale16) is an IEEE division, so codes and
+// scales are bit-identical to the reference.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_max(float value) {
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
+  return value;
+}
+
+template <int Bits>
+__global__ __launch_bounds__(256) void quantize_activation_kernel(
+    const __half2* __restrict__ input, uint8_t* __restrict__ output, __half* __restrict__ scales,
+    uint32_t columns, uint32_t groups, uint32_t total_groups) {
+  const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (linear >= total_groups) return;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t batch = linear / groups;
+  const uint32_t group = linear - batch * groups;
+  const __half2 pair = input[(static_cast<std::size_t>(batch) * columns + group * kGroup) / 2 + lane];
+  const float x0 = __low2float(pair);
+  const float x1 = __high2float(pair);
+  const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  constexpr float kLevels = Bits == 4 ? 7.0F : 127.0F;
+  constexpr int kClamp = Bits == 4 ? 7 : 127;
+  const __half scale16 = __float2half(maximum == 0.0F ? 1.0F : maximum / kLevels);
+  const float scale = __half2float(scale16);
+  const int low = max(-kClamp, min(kClamp, __float2int_rn(x0 / scale)));
+  const int high = max(-kClamp, min(kClamp, __float2int_rn(x1 / scale)));
+  if constexpr (Bits == 4) {
+    output[static_cast<std::size_t>(batch) * (columns / 2) + group * 64u + lane] =
+        static_cast<uint8_t>((low & 0x0f) | ((high & 0x0f) << 4));
+  } else {
+    const uint16_t both = static_cast<uint16_t>((low & 0xff) | ((high & 0xff) << 8));
+    reinterpret_cast<uint16_t*>(output)[(static_cast<std::size_t>(batch) * columns +
+                                         group * kGroup) / 2 + lane] = both;
+  }
+  if (lane == 0) scales[linear] = scale16;
+}
+
+// ---------------------------------------------------------------------------
+// Device weight quantizer: quantization.cpp:163-220 restated per (row, group)
+// thread, writing the gfx950 tile layout and fp16 scales (converter.cpp:379-387).
+// ---------------------------------------------------------------------------
+
+template <int Format>
+__device__ __forceinline__ int encode_level(float value, float scale) {
+  // quantization.cpp:29-46 followed by decode_value (:48-56): the signed level.
+  const float normalized = scale == 0.0F ? 0.0F : value / scale;
+  const float rounded = rintf(normalized);
+  int q = static_cast<int>(fminf(fmaxf(rounded, -2147483648.0F), 2147483520.0F));
+  if constexpr (Format == GFXI_W3G128) {
+    return max(-4, min(3, q));
+  } else {
+    return max(-8, min(7, q));
+  }
+}
+
+template <int Format>
+__global__ __launch_bounds__(256) void quantize_group128_kernel(
+    const float* __restrict__ weights, std::size_t rows, std::size_t columns, std::size_t groups,
+    uint8_t* __restrict__ codes, __half* __restrict__ scales, int32_t* __restrict__ non_finite) {
+  const std::size_t id = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= rows * groups) return;
+  const std::size_t row = id / groups;
+  const std::size_t group = id - row * groups;
+  const float* source = weights + row * columns + group * kGroup;
+  float maximum = 0.0F;
+  bool bad = false;
+  for (unsigned i = 0; i < kGroup; ++i) {
+    const float value = source[i];
+    if (!isfinite(value)) {
+      bad = true;
+      continue;
+    }
+    maximum = fmaxf(maximum, fabsf(value));
+  }
+  if (bad && non_finite != nullptr) *non_finite = 1;
+  // choose_scale, quantization.cpp:67-92
+  float scale = 1.0F;
+  if (maximum != 0.0F) {
+    scale = maximum / (Format == GFXI_W3G128 ? 4.0F : 8.0F);
+    for (int iteration = 0; iteration < 4; ++iteration) {
+      double numerator = 0.0;
+      double denominator = 0.0;
+      for (unsigned i = 0; i < kGroup; ++i) {
+        const float value = source[i];
+        const int level = encode_level<Format>(value, scale);
+        numerator += static_cast<double>(value) * level;
+        denominator += static_cast<double>(level) * level;
+      }
+      if (denominator == 0.0) break;
+      scale = static_cast<float>(numerator / denominator);
+    }
+    scale = fmaxf(scale, std::numeric_limits<float>::min());
+  }
+  scales[scale_offset(row, group, groups)] = __float2half(scale);
+  for (unsigned kb = 0; kb < 4; ++kb) {
+    int8_t chunk[32];
+    for (unsigned c = 0; c < 32; ++c) {
+      chunk[c] = static_cast<int8_t>(encode_level<Format>(source[kb * 32 + c], scale));
+    }
+    uint8_t packed[16];
+    pack_lane_chunk(Format, chunk, packed);
+    uint8_t* destination = codes + chunk_offset(Format, row, group * kGroup + kb * 32, groups);
+    for (unsigned i = 0; i < lane_bytes(Format); ++i) destination[i] = packed[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Operand expansion.  Every function returns int8 lanes for one 16x16x64 MFMA
+// K-step in the slot order documented in common.hpp.
+// ---------------------------------------------------------------------------
+
+// Two packed-nibble dwords (16 columns) -> four operand registers (value 16*x).
+__device__ __forceinline__ i32x4 expand_nibbles(unsigned x0, unsigned x1) {
+  i32x4 r;
+  r[0] = static_cast<int>((x0 << 4) & 0xF0F0F0F0u);
+  r[1] = static_cast<int>(x0 & 0xF0F0F0F0u);
+  r[2] = static_cast<int>((x1 << 4) & 0xF0F0F0F0u);
+  r[3] = static_cast<int>(x1 & 0xF0F0F0F0u);
+  return r;
+}
+
+// Three W3 dwords (32 columns) -> operand registers of both K-steps (value 32*w).
+__device__ __forceinline__ void expand_w3(unsigned s0, unsigned s1, unsigned s2, i32x4& h0,
+                                          i32x4& h1) {
+  constexpr unsigned E = 0xE0E0E0E0u;
+  h0[0] = static_cast<int>((s0 << 5) & E);
+  h0[1] = static_cast<int>((s0 << 2) & E);
+  h0[2] = static_cast<int>((s1 << 5) & E);
+  h0[3] = static_cast<int>((s1 << 2) & E);
+  h1[0] = static_cast<int>((s2 << 5) & E);
+  h1[1] = static_cast<int>((s2 << 2) & E);
+  h1[2] = static_cast<int>((s0 & 0xC0C0C0C0u) | ((s1 >> 1) & 0x20202020u));
+  h1[3] = static_cast<int>((s2 & 0xC0C0C0C0u) | ((s1 >> 2) & 0x20202020u));
+}
+
+// Sixteen int8 activations in column order -> operand registers in slot order.
+__device__ __forceinline__ i32x4 permute_i8(unsigned d0, unsigned d1, unsigned d2, unsigned d3) {
+  i32x4 r;
+  r[0] = static_cast<int>(__builtin_amdgcn_perm(d1, d0, 0x06040200u));
+  r[1] = static_cast<int>(__builtin_amdgcn_perm(d1, d0, 0x07050301u));
+  r[2] = static_cast<int>(__builtin_amdgcn_perm(d3, d2, 0x06040200u));
+  r[3] = static_cast<int>(__builtin_amdgcn_perm(d3, d2, 0x07050301u));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM kernel.
+//
+// One workgroup per 16-row tile (tiles of up to four fused matrices are
+// concatenated); its W waves split the K groups and combine in LDS.
+// A operand = weights (MFMA rows = matrix rows), B operand = activations
+// (MFMA columns = tokens).  For batches of at most 4 or 8 tokens the 16 MFMA
+// columns carry GP = 4 or 2 groups side by side (token slot = column % (16/GP),
+// group offset = column / (16/GP)); lane block kb of the A operand then serves
+// group kb / (4/GP) and the B operand zeroes the slots of other groups, so
+// each output column receives exactly one group's dot product.  This halves or
+// quarters the fp32 epilogue for the decode batch sizes.
+// ---------------------------------------------------------------------------
+
+struct GemmMatrix {
+  const uint8_t* weights;
+  const __half* scales;
+  void* output;
+  uint32_t tiles;
+};
+
+struct GemmArgs {
+  GemmMatrix matrix[4];
+  uint32_t tile_begin[5];
+  const uint8_t* activations;
+  const __half* activation_scales;
+  int32_t* partials;
+  uint32_t columns;
+  uint32_t groups;
+  uint32_t batch;
+};
+
+template <int Format, int ABits, int GP, int NTB, bool HalfOut, bool Partials>
+__global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
+  constexpr unsigned LB = lane_bytes(Format);
+  constexpr unsigned LPG = 4 / GP;    // A lane blocks per group
+  constexpr unsigned TPAD = 16 / GP;  // token slots per group
+  constexpr float kInvF =
+      1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
+  constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
+
+  __shared__ float reduction[8][NTB][4][64];
+
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned wave = threadIdx.x >> 6;
+  const unsigned waves = blockDim.x >> 6;
+
+  // Matrix selection for fused launches.
+  unsigned tile = blockIdx.x;
+  unsigned index = 0;
+#pragma unroll
+  for (unsigned i = 1; i < 4; ++i) {
+    if (tile >= args.tile_begin[i]) index = i;
+  }
+  const GemmMatrix matrix = args.matrix[index];
+  tile -= args.tile_begin[index];
+  const uint32_t groups = args.groups;
+  const uint32_t rows = matrix.tiles * 16u;
+  const uint8_t* weights = matrix.weights + static_cast<std::size_t>(tile) * groups * 64u * LB;
+  const __half* weight_scales = matrix.scales + static_cast<std::size_t>(tile) * groups * 16u;
+
+  const unsigned m = lane & 15u;          // A row / B,C column
+  const unsigned kb = lane >> 4;          // K lane block / C row block
+  const unsigned go_a = kb / LPG;         // group offset served by this A lane
+  const unsigned q = kb % LPG;            // rank among the lanes of that group
+  const unsigned slot = m % TPAD;         // token slot of this B/C column
+  const unsigned go_c = m / TPAD;         // group offset of this B/C column
+  const bool b_on = go_c == go_a;
+
+  const unsigned packs = (groups + GP - 1) / GP;
+  const unsigned pack_begin = packs * wave / waves;
+  const unsigned pack_end = packs * (wave + 1) / waves;
+
+  float acc[NTB][4];
+#pragma unroll
+  for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0F;
+  }
+
+  for (unsigned pack = pack_begin; pack < pack_end; ++pack) {
+    const unsigned g_a = pack * GP + go_a;
+    const bool a_valid = g_a < groups;
+    i32x4 c[NTB];
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (unsigned s = 0; s < GP; ++s) {
+      const unsigned block = q * GP + s;
+      i32x4 a0, a1;
+      if (a_valid) {
+        const uint8_t* chunk =
+            weights + (static_cast<std::size_t>(g_a) * 64u + block * 16u + m) * LB;
+        if constexpr (Format == GFXI_W3G128) {
+          const u32x3 w = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(chunk));
+          expand_w3(w[0], w[1], w[2], a0, a1);
+        } else {
+          const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(chunk));
+          a0 = expand_nibbles(w[0], w[1]);
+          a1 = expand_nibbles(w[2], w[3]);
+        }
+      } else {
+        a0 = i32x4{0, 0, 0, 0};
+        a1 = a0;
+      }
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        const unsigned token = t * 16u + slot;
+        i32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
+        if (b_on && a_valid && token < args.batch) {
+          const std::size_t column = static_cast<std::size_t>(g_a) * kGroup + block * 32u;
+          if constexpr (ABits == 4) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(
+                args.activations + static_cast<std::size_t>(token) * (args.columns / 2) + column / 2);
+            b0 = expand_nibbles(x[0], x[1]);
+            b1 = expand_nibbles(x[2], x[3]);
+          } else {
+            const u32x4* source = reinterpret_cast<const u32x4*>(
+                args.activations + static_cast<std::size_t>(token) * args.columns + column);
+            const u32x4 x = source[0];
+            const u32x4 y = source[1];
+            b0 = permute_i8(x[0], x[1], x[2], x[3]);
+            b1 = permute_i8(y[0], y[1], y[2], y[3]);
+          }
+        }
+        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c[t], 0, 0, 0);
+        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c[t], 0, 0, 0);
+      }
+    }
+    // Epilogue for this lane's C elements: rows 4*kb + r, token slot, group g_c.
+    const unsigned g_c = pack * GP + go_c;
+    if (g_c < groups) {
+      const u32x2 packed_ws = *reinterpret_cast<const u32x2*>(
+          weight_scales + static_cast<std::size_t>(g_c) * 16u + 4u * kb);
+      float ws[4];
+      ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[0] & 0xffffu)));
+      ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[0] >> 16)));
+      ws[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[1] & 0xffffu)));
+      ws[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[1] >> 16)));
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        const unsigned token = t * 16u + slot;
+        if (token < args.batch) {
+          if constexpr (Partials) {
+            const std::size_t base = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              args.partials[(base + r) * groups + g_c] = c[t][r] >> kShift;
+            }
+          } else {
+            const float as = __half2float(args.activation_scales[token * groups + g_c]) * kInvF;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[t][r] = fmaf(static_cast<float>(c[t][r]), ws[r] * as, acc[t][r]);
+            }
+          }
+        }
+      }
+    }
+  }
+  if constexpr (Partials) return;
+
+  // Combine the GP group columns of each token slot (lanes m, m+TPAD, ...).
+#pragma unroll
+  for (unsigned offset = TPAD; offset < 16u; offset <<= 1) {
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] += __shfl_xor(acc[t][r], static_cast<int>(offset));
+    }
+  }
+  if (waves > 1) {
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) reduction[wave][t][r][lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float sum = reduction[0][t][r][lane];
+        for (unsigned w = 1; w < waves; ++w) sum += reduction[w][t][r][lane];
+        acc[t][r] = sum;
+      }
+    }
+  }
+  if (go_c != 0) return;
+#pragma unroll
+  for (int t = 0; t < NTB; ++t) {
+    const unsigned token = t * 16u + slot;
+    if (token >= args.batch) continue;
+    const std::size_t base = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
+    if constexpr (HalfOut) {
+      __half* out = reinterpret_cast<__half*>(matrix.output) + base;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[r] = __float2half(acc[t][r]);
+    } else {
+      float4 value = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + base) = value;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled row gather (lowbit_gemv.hip:191-231): out[c] = fp16(w(row,c) * ws(row,g)).
+// ---------------------------------------------------------------------------
+
+template <int Format>
+__global__ __launch_bounds__(256) void row_gather_kernel(
+    const uint8_t* __restrict__ weights, const __half* __restrict__ scales,
+    __half* __restrict__ output, std::size_t row, const uint32_t* __restrict__ indirect_row,
+    std::size_t rows, std::size_t columns) {
+  const std::size_t column = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (column >= columns) return;
+  if (indirect_row != nullptr) row = *indirect_row;
+  if (row >= rows) {
+    output[column] = __float2half(0.0F);
+    return;
+  }
+  const std::size_t groups = columns / kGroup;
+  const uint8_t* chunk = weights + chunk_offset(Format, row, column, groups);
+  const int w = unpack_lane_code(Format, chunk, static_cast<unsigned>(column % 32));
+  output[column] = __float2half(static_cast<float>(w) *
+                                __half2float(scales[scale_offset(row, column / kGroup, groups)]));
+}
+
+// ---------------------------------------------------------------------------
+// Host launch helpers
+// ---------------------------------------------------------------------------
+
+bool aligned(const void* pointer, std::size_t bytes) {
+  return (reinterpret_cast<std::uintptr_t>(pointer) % bytes) == 0;
+}
+
+unsigned choose_waves(uint32_t groups, unsigned gp) {
+  const unsigned packs = (groups + gp - 1) / gp;
+  unsigned waves = (packs + 4) / 5;  // about five packs per wave
+  if (waves < 1) waves = 1;
+  if (waves > 8) waves = 8;
+  return waves;
+}
+
+template <int Format, int ABits, bool HalfOut, bool Partials>
+void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
+  const uint32_t batch = args.batch;
+  auto go = [&](auto kernel, unsigned gp) {
+    const unsigned waves = choose_waves(args.groups, gp);
+    hipLaunchKernelGGL(kernel, dim3(total_tiles), dim3(64 * waves), 0, stream, args);
+  };
+  if (batch <= 4) {
+    go(lowbit_gemm_kernel<Format, ABits, 4, 1, HalfOut, Partials>, 4);
+  } else if (batch <= 8) {
+    go(lowbit_gemm_kernel<Format, ABits, 2, 1, HalfOut, Partials>, 2);
+  } else if (batch <= 16) {
+    go(lowbit_gemm_kernel<Format, ABits, 1, 1, HalfOut, Partials>, 1);
+  } else {
+    go(lowbit_gemm_kernel<Format, ABits, 1, 2, HalfOut, Partials>, 1);
+  }
+}
+
+template <int ABits, bool HalfOut, bool Partials>
+void dispatch_gemm(int32_t format, const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
+  if (format == GFXI_W3G128) {
+    launch_gemm_kernel<GFXI_W3G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+  } else {
+    launch_gemm_kernel<GFXI_W4G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+  }
+}
+
+struct MatrixBinding {
+  const uint8_t* weights;
+  const uint16_t* scales;
+  void* output;
+  std::size_t rows;
+};
+
+// Shared validation + launch for every GEMM entry point (argument rules of
+// lowbit_gemv.hip:1123-1130, :1232-1255, :1303-1310).
+int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindings,
+                   std::size_t count, int32_t activation_bits, const void* activations,
+                   const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
+                   uint32_t batch, bool half_out, hipStream_t stream) {
+  if (!valid_weight_format(format)) {
+    return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W3G128 and W4G128");
+  }
+  if (count == 0 || count > 4 || activations == nullptr ||
+      (partials == nullptr && activation_scales == nullptr) || columns == 0 ||
+      columns % kGroup != 0 || batch == 0 || batch > 32 ||
+      columns > std::numeric_limits<uint32_t>::max() / 2) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) +
+                " requires non-null buffers, N divisible by 16, K divisible by 128, and batch "
+                "in [1,32]");
+  }
+  if (!aligned(activations, 16)) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " requires 16-byte aligned activations");
+  }
+  GemmArgs args{};
+  uint64_t tiles = 0;
+  for (std::size_t i = 0; i < count; ++i) {
+    const MatrixBinding& b = bindings[i];
+    if (b.weights == nullptr || b.scales == nullptr ||
+        (partials == nullptr && b.output == nullptr) || b.rows == 0 || b.rows % 16 != 0) {
+      return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " matrix binding is invalid");
+    }
+    if (!aligned(b.weights, 16) || !aligned(b.scales, 8) ||
+        (b.output != nullptr && !half_out && !aligned(b.output, 16))) {
+      return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " requires 16-byte aligned weights "
+                                                             "and outputs, 8-byte aligned scales");
+    }
+    args.matrix[i] = {b.weights, reinterpret_cast<const __half*>(b.scales), b.output,
+                      static_cast<uint32_t>(b.rows / 16)};
+    args.tile_begin[i] = static_cast<uint32_t>(tiles);
+    tiles += b.rows / 16;
+  }
+  if (tiles > std::numeric_limits<uint32_t>::max() / 2) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " grid is too large");
+  }
+  for (std::size_t i = count; i < 4; ++i) {
+    args.matrix[i] = args.matrix[count - 1];
+    args.tile_begin[i] = static_cast<uint32_t>(tiles);
+  }
+  args.tile_begin[4] = static_cast<uint32_t>(tiles);
+  args.activations = static_cast<const uint8_t*>(activations);
+  args.activation_scales = reinterpret_cast<const __half*>(activation_scales);
+  args.partials = partials;
+  args.columns = static_cast<uint32_t>(columns);
+  args.groups = static_cast<uint32_t>(columns / kGroup);
+  args.batch = batch;
+  const auto total = static_cast<uint32_t>(tiles);
+  if (partials != nullptr) {
+    if (activation_bits == 4) dispatch_gemm<4, false, true>(format, args, total, stream);
+    else dispatch_gemm<8, false, true>(format, args, total, stream);
+  } else if (activation_bits == 4) {
+    if (half_out) dispatch_gemm<4, true, false>(format, args, total, stream);
+    else dispatch_gemm<4, false, false>(format, args, total, stream);
+  } else {
+    dispatch_gemm<8, false, false>(format, args, total, stream);
+  }
+  return launch_status((std::string(name) + " launch failed").c_str());
+}
+
+int32_t quantize_activation_entry(int bits, const uint16_t* input, void* output, uint16_t* scales,
+                                  std::size_t columns, uint32_t batch, hipStream_t stream) {
+  if (input == nullptr || output == nullptr || scales == nullptr || columns == 0 ||
+      columns % kGroup != 0 || batch == 0 || batch > 32 ||
+      columns > std::numeric_limits<uint32_t>::max()) {
+    return fail(GFXI_INVALID_ARGUMENT,
+                std::string(bits == 4 ? "A4" : "A8") +
+                    " quantization requires non-null buffers, batch in [1,32], and K divisible by 128");
+  }
+  if (!aligned(input, 4) || (bits == 8 && !aligned(output, 2))) {
+    return fail(GFXI_INVALID_ARGUMENT, "activation quantization requires aligned buffers");
+  }
+  const auto groups = static_cast<uint32_t>(columns / kGroup);
+  const uint32_t total = groups * batch;
+  const dim3 grid((total + 3) / 4);
+  if (bits == 4) {
+    hipLaunchKernelGGL(quantize_activation_kernel<4>, grid, dim3(256), 0, stream,
+                       reinterpret_cast<const __half2*>(input), static_cast<uint8_t*>(output),
+                       reinterpret_cast<__half*>(scales), static_cast<uint32_t>(columns), groups,
+                       total);
+    return launch_status("A4 activation quantization launch failed");
+  }
+  hipLaunchKernelGGL(quantize_activation_kernel<8>, grid, dim3(256), 0, stream,
+                     reinterpret_cast<const __half2*>(input), static_cast<uint8_t*>(output),
+                     reinterpret_cast<__half*>(scales), static_cast<uint32_t>(columns), groups,
+                     total);
+  return launch_status("A8 activation quantization launch failed");
+}
+
+int32_t row_gather_entry(int32_t format, const uint8_t* weights, const uint16_t* scales,
+                         uint16_t* output, std::size_t row, const uint32_t* indirect,
+                         std::size_t rows, std::size_t columns, hipStream_t stream) {
+  if (!valid_weight_format(format)) {
+    return fail(GFXI_UNSUPPORTED, "tiled row gather supports W3G128 and W4G128");
+  }
+  if (weights == nullptr || scales == nullptr || output == nullptr || rows == 0 ||
+      rows % 16 != 0 || columns == 0 || columns % kGroup != 0 ||
+      (indirect == nullptr && row >= rows)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid tiled low-bit row gather arguments");
+  }
+  constexpr unsigned threads = 256;
+  const dim3 grid(static_cast<unsigned>((columns + threads - 1) / threads));
+  const auto* ws = reinterpret_cast<const __half*>(scales);
+  auto* out = reinterpret_cast<__half*>(output);
+  if (format == GFXI_W3G128) {
+    hipLaunchKernelGGL(row_gather_kernel<GFXI_W3G128>, grid, dim3(threads), 0, stream, weights, ws,
+                       out, row, indirect, rows, columns);
+  } else {
+    hipLaunchKernelGGL(row_gather_kernel<GFXI_W4G128>, grid, dim3(threads), 0, stream, weights, ws,
+                       out, row, indirect, rows, columns);
+  }
+  return launch_status("tiled low-bit row gather launch failed");
+}
+
+}  // namespace
+}  // namespace gfx950
+
+using namespace gfx950;
+
+extern "C" int32_t gfxinfer_launch_quantize_group128_gfx950(int32_t format, const float* weights,
+                                                            size_t rows, size_t columns,
+                                                            uint8_t* tiled_codes,
+                                                            uint16_t* tiled_scales_f16,
+                                                            int32_t* non_finite_flag,
+                                                            void* stream) {
+  if (!valid_weight_format(format)) {
+    return fail(GFXI_UNSUPPORTED, "device quantizer supports W3G128 and W4G128");
+  }
+  if (weights == nullptr || tiled_codes == nullptr || tiled_scales_f16 == nullptr || rows == 0 ||
+      rows % 16 != 0 || columns == 0 || columns % kGroup != 0) {
+    return fail(GFXI_INVALID_ARGUMENT, "group-128 quantization requires nonzero dimensions, N "
+                                       "divisible by 16, and K divisible by 128");
+  }
+  const std::size_t groups = columns / kGroup;
+  const std::size_t total = rows * groups;
+  if (total / 256 + 1 > std::numeric_limits<uint32_t>::max()) {
+    return fail(GFXI_INVALID_ARGUMENT, "device quantizer grid is too large");
+  }
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  auto s = static_cast<hipStream_t>(stream);
+  auto* scales = reinterpret_cast<__half*>(tiled_scales_f16);
+  if (format == GFXI_W3G128) {
+    hipLaunchKernelGGL(quantize_group128_kernel<GFXI_W3G128>, grid, dim3(256), 0, s, weights, rows,
+                       columns, groups, tiled_codes, scales, non_finite_flag);
+  } else {
+    hipLaunchKernelGGL(quantize_group128_kernel<GFXI_W4G128>, grid, dim3(256), 0, s, weights, rows,
+                       columns, groups, tiled_codes, scales, non_finite_flag);
+  }
+  return launch_status("device weight quantizer launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_quantize_activation_i4(const uint16_t* input,
+                                                          uint8_t* packed_output, uint16_t* scales,
+                                                          size_t columns, uint32_t batch,
+                                                          void* stream) {
+  return quantize_activation_entry(4, input, packed_output, scales, columns, batch,
+                                   static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_quantize_activation_i8(const uint16_t* input,
+                                                          int8_t* quantized_output,
+                                                          uint16_t* scales, size_t columns,
+                                                          uint32_t batch, void* stream) {
+  return quantize_activation_entry(8, input, quantized_output, scales, columns, batch,
+                                   static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm(int32_t format, const uint8_t* tiled_weights,
+                                                  const uint16_t* tiled_weight_scales,
+                                                  const uint8_t* packed_activations,
+                                                  const uint16_t* activation_scales, float* output,
+                                                  size_t rows, size_t columns, uint32_t batch,
+                                                  int32_t sequential_w3, void* stream) {
+  (void)sequential_w3;
+  const MatrixBinding binding{tiled_weights, tiled_weight_scales, output, rows};
+  return gemm_entry("gfx950 INT4 GEMM", format, &binding, 1, 4, packed_activations,
+                    activation_scales, nullptr, columns, batch, false,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_half(int32_t format, const uint8_t* tiled_weights,
+                                                       const uint16_t* tiled_weight_scales,
+                                                       const uint8_t* packed_activations,
+                                                       const uint16_t* activation_scales,
+                                                       uint16_t* output, size_t rows,
+                                                       size_t columns, uint32_t batch,
+                                                       int32_t sequential_w3, void* stream) {
+  (void)sequential_w3;
+  const MatrixBinding binding{tiled_weights, tiled_weight_scales, output, rows};
+  return gemm_entry("gfx950 INT4 GEMM FP16 epilogue", format, &binding, 1, 4, packed_activations,
+                    activation_scales, nullptr, columns, batch, true,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
+                                                        const gfxinfer_fused_matrix* matrices,
+                                                        size_t matrix_count,
+                                                        const uint8_t* packed_activations,
+                                                        const uint16_t* activation_scales,
+                                                        size_t columns, uint32_t batch,
+                                                        int32_t sequential_w3, void* stream) {
+  (void)sequential_w3;
+  if (matrices == nullptr || matrix_count < 2 || matrix_count > 4) {
+    return fail(GFXI_INVALID_ARGUMENT,
+                "gfx950 fused INT4 GEMM requires 2..4 matrices and batch in [1,32]");
+  }
+  MatrixBinding bindings[4];
+  for (std::size_t i = 0; i < matrix_count; ++i) {
+    bindings[i] = {matrices[i].tiled_weights, matrices[i].tiled_weight_scales, matrices[i].output,
+                   matrices[i].rows};
+  }
+  return gemm_entry("gfx950 fused INT4 GEMM", format, bindings, matrix_count, 4,
+                    packed_activations, activation_scales, nullptr, columns, batch, false,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i8_gemm(int32_t format, const uint8_t* tiled_weights,
+                                                  const uint16_t* tiled_weight_scales,
+                                                  const int8_t* quantized_activations,
+                                                  const uint16_t* activation_scales, float* output,
+                                                  size_t rows, size_t columns, uint32_t batch,
+                                                  void* stream) {
+  const MatrixBinding binding{tiled_weights, tiled_weight_scales, output, rows};
+  return gemm_entry("gfx950 INT8 GEMM", format, &binding, 1, 8, quantized_activations,
+                    activation_scales, nullptr, columns, batch, false,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_debug_gemm_partials(int32_t format, const uint8_t* tiled_weights,
+                                                int32_t activation_bits, const void* activations,
+                                                size_t rows, size_t columns, uint32_t batch,
+                                                int32_t* partials, void* stream) {
+  if (activation_bits != 4 && activation_bits != 8) {
+    return fail(GFXI_INVALID_ARGUMENT, "activation_bits must be 4 or 8");
+  }
+  if (partials == nullptr) return fail(GFXI_INVALID_ARGUMENT, "partials buffer is null");
+  // Scales are not read on this path; any non-null 8-byte aligned pointer will do.
+  const MatrixBinding binding{tiled_weights, reinterpret_cast<const uint16_t*>(tiled_weights),
+                              nullptr, rows};
+  return gemm_entry("gfx950 GEMM partials", format, &binding, 1, activation_bits, activations,
+                    nullptr, partials, columns, batch, false, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled(int32_t format,
+                                                           const uint8_t* tiled_weights,
+                                                           const uint16_t* tiled_scales,
+                                                           uint16_t* output, size_t row,
+                                                           size_t rows, size_t columns,
+                                                           void* stream) {
+  return row_gather_entry(format, tiled_weights, tiled_scales, output, row, nullptr, rows, columns,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled_indirect(
+    int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_scales, uint16_t* output,
+    const uint32_t* row, size_t rows, size_t columns, void* stream) {
+  if (row == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect row pointer is null");
+  return row_gather_entry(format, tiled_weights, tiled_scales, output, 0, row, rows, columns,
+                          static_cast<hipStream_t>(stream));
+}

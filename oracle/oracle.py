@@ -1,0 +1,221 @@
+"""numpy binding of the CPU oracle (liboracle.so) and of the reference quantizer
+compiled in place (_ref/libgfxref.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() and by
+bench.py's cpu_baseline leg, always as the checker; the product never loads it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+W2, W3, W4 = 1, 2, 3
+GROUP = 128
+
+_lib = None
+_ref = None
+
+
+def build(reference: bool = False) -> None:
+    """Compile liboracle.so (and _ref/ when the reference tree is present)."""
+    targets = ["all"] + (["ref"] if reference else [])
+    subprocess.run(["make", "-s", "-C", HERE] + targets, check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        _lib = ctypes.CDLL(path)
+        _declare(_lib)
+    return _lib
+
+
+def ref_lib() -> ctypes.CDLL | None:
+    """The reference's own quantizer, or None when _ref/ was not built."""
+    global _ref
+    if _ref is None:
+        path = os.path.join(HERE, "_ref", "libgfxref.so")
+        if not os.path.exists(path):
+            return None
+        _ref = ctypes.CDLL(path)
+        _ref.ref_quantize_group128.restype = ctypes.c_int
+        _ref.ref_quantize_group128.argtypes = [P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, P, P]
+        _ref.ref_dequantize_group128.restype = ctypes.c_int
+        _ref.ref_dequantize_group128.argtypes = [P, P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, P]
+        _ref.ref_packed_row_bytes.restype = ctypes.c_size_t
+        _ref.ref_packed_row_bytes.argtypes = [ctypes.c_int, ctypes.c_size_t]
+    return _ref
+
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+U = ctypes.c_uint
+F = ctypes.c_float
+I = ctypes.c_int
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    sig = {
+        "orc_f32_to_f16": (ctypes.c_uint16, [F]),
+        "orc_f16_to_f32": (F, [ctypes.c_uint16]),
+        "orc_f32_to_f16_array": (None, [P, P, SZ]),
+        "orc_packed_row_bytes": (SZ, [I, SZ]),
+        "orc_quantize_group128": (I, [P, SZ, SZ, I, P, P]),
+        "orc_unpack_weights": (None, [P, SZ, SZ, I, P]),
+        "orc_quantize_activation_i4": (I, [P, P, P, SZ, U]),
+        "orc_quantize_activation_i8": (I, [P, P, P, SZ, U]),
+        "orc_unpack_a4": (None, [P, SZ, U, P]),
+        "orc_gemm_partials": (None, [P, P, SZ, SZ, U, P]),
+        "orc_gemm_epilogue": (None, [P, P, P, SZ, SZ, U, P]),
+        "orc_dequant_dot_gemv": (None, [P, P, P, P, SZ, SZ, U, P]),
+        "orc_dequant_dot_gemv_packed": (None, [P, I, P, P, P, SZ, SZ, U, P]),
+        "orc_max_threads": (I, []),
+        "orc_rms_norm": (None, [P, P, P, SZ, U, F, I]),
+        "orc_residual_add_rms_norm": (None, [P, P, P, P, P, SZ, U, F, I]),
+        "orc_dual_rms_norm_concat": (None, [P, P, P, P, P, SZ, F, I]),
+        "orc_silu_multiply_quantize_i4": (I, [P, P, P, P, SZ, U]),
+        "orc_silu_multiply": (None, [P, P, P, SZ]),
+        "orc_gdn_conv_update": (None, [P, P, P, P, P, P, SZ, U]),
+        "orc_gdn_recurrent": (None, [P, P, P, P, P, P, P, P, P, P, P, P, P, U, U, U, U]),
+        "orc_gdn_restore_conv": (None, [P, P, SZ, U]),
+        "orc_gdn_restore_recurrent": (None, [P, P, P, P, U, U, U, U]),
+        "orc_head_norm_rope": (None, [P, SZ, P, P, SZ, SZ, SZ, ctypes.c_uint64, U, F]),
+        "orc_kv_append": (None, [P, P, P, P, SZ, SZ, U]),
+        "orc_gated_attention": (None, [P, P, P, P, P, SZ, U, U, U, U, F]),
+        "orc_argmax": (None, [P, SZ, SZ, U, P, P]),
+        "orc_accept": (SZ, [P, P, SZ]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---- fp16 / bf16 ------------------------------------------------------------
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_array(ptr(x), ptr(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+# ---- weight quantizer -------------------------------------------------------
+
+def packed_row_bytes(fmt: int, columns: int) -> int:
+    return int(lib().orc_packed_row_bytes(fmt, columns))
+
+
+def quantize_group128(w: np.ndarray, fmt: int):
+    """Returns (status, codes [N, row_bytes] uint8, scales [N, G] float32)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    codes = np.zeros((rows, max(1, packed_row_bytes(fmt, cols))), dtype=np.uint8)
+    scales = np.zeros((rows, max(1, cols // GROUP)), dtype=np.float32)
+    status = lib().orc_quantize_group128(ptr(w), rows, cols, fmt, ptr(codes), ptr(scales))
+    return int(status), codes, scales
+
+
+def ref_quantize_group128(w: np.ndarray, fmt: int):
+    R = ref_lib()
+    if R is None:
+        return None
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    codes = np.zeros((rows, max(1, int(R.ref_packed_row_bytes(fmt, cols)))), dtype=np.uint8)
+    scales = np.zeros((rows, max(1, cols // GROUP)), dtype=np.float32)
+    status = R.ref_quantize_group128(ptr(w), rows, cols, fmt, ptr(codes), ptr(scales))
+    return int(status), codes, scales
+
+
+def unpack_weights(codes: np.ndarray, rows: int, cols: int, fmt: int) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty((rows, cols), dtype=np.int8)
+    lib().orc_unpack_weights(ptr(codes), rows, cols, fmt, ptr(out))
+    return out
+
+
+# ---- activation quantizers --------------------------------------------------
+
+def quantize_activation_i4(x16: np.ndarray):
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    B, K = x16.shape
+    packed = np.zeros((B, K // 2), dtype=np.uint8)
+    scales = np.zeros((B, K // GROUP), dtype=np.uint16)
+    st = lib().orc_quantize_activation_i4(ptr(x16), ptr(packed), ptr(scales), K, B)
+    assert st == 0, st
+    return packed, scales
+
+
+def quantize_activation_i8(x16: np.ndarray):
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    B, K = x16.shape
+    codes = np.zeros((B, K), dtype=np.int8)
+    scales = np.zeros((B, K // GROUP), dtype=np.uint16)
+    st = lib().orc_quantize_activation_i8(ptr(x16), ptr(codes), ptr(scales), K, B)
+    assert st == 0, st
+    return codes, scales
+
+
+def unpack_a4(packed: np.ndarray, K: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    B = packed.shape[0]
+    out = np.empty((B, K), dtype=np.int8)
+    lib().orc_unpack_a4(ptr(packed), K, B, ptr(out))
+    return out
+
+
+# ---- GEMM -------------------------------------------------------------------
+
+def gemm_partials(w: np.ndarray, a: np.ndarray) -> np.ndarray:
+    """int32 P[B, N, G] from signed int8 w [N, K] and a [B, K]."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    N, K = w.shape
+    B = a.shape[0]
+    out = np.empty((B, N, K // GROUP), dtype=np.int32)
+    lib().orc_gemm_partials(ptr(w), ptr(a), N, K, B, ptr(out))
+    return out
+
+
+def gemm_epilogue(partials: np.ndarray, ws16: np.ndarray, as16: np.ndarray) -> np.ndarray:
+    partials = np.ascontiguousarray(partials, dtype=np.int32)
+    ws16 = np.ascontiguousarray(ws16, dtype=np.uint16)
+    as16 = np.ascontiguousarray(as16, dtype=np.uint16)
+    B, N, G = partials.shape
+    out = np.empty((B, N), dtype=np.float32)
+    lib().orc_gemm_epilogue(ptr(partials), ptr(ws16), ptr(as16), N, G * GROUP, B, ptr(out))
+    return out
+
+
+def dequant_dot_gemv_packed(codes, fmt, ws, a, as16, N, K):
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    as16 = np.ascontiguousarray(as16, dtype=np.uint16)
+    B = a.shape[0]
+    out = np.empty((B, N), dtype=np.float32)
+    lib().orc_dequant_dot_gemv_packed(ptr(codes), fmt, ptr(ws), ptr(a), ptr(as16), N, K, B, ptr(out))
+    return out
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())

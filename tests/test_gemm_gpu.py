@@ -1,0 +1,251 @@
+"""GPU parity of the packed low-bit path against the CPU oracle, through the C ABI.
+
+Bars: integer codes, scales and per-group int32 partial sums bit-exact; fp32
+GEMM outputs within 2e-5 of max|y| of the oracle's sequential epilogue (the
+reference harness accepts 0.008*max(1,|y|), src/cli/main.cpp:1499).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from gpu_util import dev, empty, host, say
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _half(x):
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_mfma_operand_layout(device):
+    """v_mfma_i32_16x16x64_i8: A and B share the K-slot order; lane l of C holds
+    rows 4*(l//16)..+3 of column l%16 (the assumption of tests/kernel_model.py)."""
+    path = os.path.join(HERE, "hip", "libmfma_probe.so")
+    L = ctypes.CDLL(path)
+    rng = np.random.default_rng(17)
+    a = rng.integers(-128, 128, size=(64, 16), dtype=np.int8)
+    b = rng.integers(-128, 128, size=(64, 16), dtype=np.int8)
+    da, db, dc = dev(a), dev(b), empty((64, 4), np.int32)
+    say("mfma probe")
+    assert L.mfma_probe(ctypes.c_void_p(da.data_ptr()), ctypes.c_void_p(db.data_ptr()),
+                        ctypes.c_void_p(dc.data_ptr())) == 0
+    c = host(dc)
+    A = a.astype(np.int64).reshape(4, 16, 16)  # [kb][row][j]
+    B = b.astype(np.int64).reshape(4, 16, 16)  # [kb][col][j]
+    C = np.einsum("krj,kcj->rc", A, B)
+    expected = np.empty((64, 4), dtype=np.int64)
+    for lane in range(64):
+        for r in range(4):
+            expected[lane, r] = C[4 * (lane // 16) + r, lane % 16]
+    assert np.array_equal(c.astype(np.int64), expected)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("batch,columns", [(1, 5120), (5, 5120), (5, 17408), (32, 5120)])
+def test_activation_quantizer_bit_exact(device, gx, orc, bits, batch, columns):
+    rng = np.random.default_rng(batch * columns + bits)
+    x = rng.standard_normal((batch, columns)).astype(np.float32)
+    x[0, :128] = 0.0                              # all-zero group -> scale 1
+    x[-1, 128:256] = np.float32(3.5)              # constant group
+    x[-1, 256:384] = rng.standard_normal(128) * 1e-4  # tiny values
+    x16 = _half(x)
+    if bits == 4:
+        want_codes, want_scales = orc.quantize_activation_i4(x16)
+        codes = empty((batch, columns // 2), np.uint8)
+    else:
+        want_codes, want_scales = orc.quantize_activation_i8(x16)
+        codes = empty((batch, columns), np.int8)
+    scales = empty((batch, columns // 128), np.uint16)
+    say("quantize_activation", bits, batch, columns)
+    fn = gx.launch_quantize_activation_i4 if bits == 4 else gx.launch_quantize_activation_i8
+    fn(dev(x16), codes, scales, columns, batch)
+    assert np.array_equal(host(codes).view(want_codes.dtype), want_codes)
+    assert np.array_equal(host(scales, np.uint16), want_scales)
+
+
+def _pad16(w):
+    rows = (w.shape[0] + 15) // 16 * 16
+    out = np.zeros((rows, w.shape[1]), dtype=np.float32)
+    out[: w.shape[0]] = w
+    return out
+
+
+@pytest.mark.parametrize("fmt,name", [(2, "w3"), (3, "w4")])
+def test_device_quantizer_matches_reference_golden(device, gx, orc, fmt, name):
+    from conftest import golden
+    g = golden(f"quant_{name}.npz")
+    for case in ["planted_3x256", "normal_32x256", "baseline_16x512", "edges_16x128"]:
+        w = g[f"{case}__input"]
+        rows0, cols = w.shape
+        wp = _pad16(w)
+        rows = wp.shape[0]
+        codes = empty((gx.tile_bytes(fmt, rows, cols),), np.uint8)
+        scales = empty((rows * cols // 128,), np.uint16)
+        flag = empty((1,), np.int32)
+        say("device quantizer golden", name, case)
+        gx.launch_quantize_group128(fmt, dev(wp), rows, cols, codes, scales, flag)
+        wq, s16 = gx.untile_group128(fmt, host(codes), host(scales, np.uint16), rows, cols)
+        want_w = orc.unpack_weights(g[f"{case}__codes"], rows0, cols, fmt)
+        assert np.array_equal(wq[:rows0], want_w), case
+        assert np.array_equal(s16[:rows0], orc.f32_to_f16_bits(g[f"{case}__scales"])), case
+        assert int(host(flag)[0]) == 0
+
+
+def test_device_quantizer_flags_non_finite(device, gx):
+    w = np.zeros((16, 128), np.float32)
+    w[3, 5] = np.inf
+    codes = empty((gx.tile_bytes(2, 16, 128),), np.uint8)
+    scales = empty((16,), np.uint16)
+    flag = empty((1,), np.int32)
+    say("device quantizer non-finite")
+    gx.launch_quantize_group128(2, dev(w), 16, 128, codes, scales, flag)
+    assert int(host(flag)[0]) == 1
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+def test_device_quantizer_full_shape(device, gx, orc, fmt):
+    rows, cols = 17408, 5120
+    rng = np.random.default_rng(0x5EED0001)
+    w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    codes = empty((gx.tile_bytes(fmt, rows, cols),), np.uint8)
+    scales = empty((rows * cols // 128,), np.uint16)
+    say("device quantizer full shape", fmt)
+    gx.launch_quantize_group128(fmt, dev(w), rows, cols, codes, scales)
+    _, ocodes, oscales = orc.quantize_group128(w, fmt)
+    tiled, tscales = gx.tile_group128(fmt, ocodes, oscales, rows, cols)
+    assert np.array_equal(host(codes), tiled)
+    assert np.array_equal(host(scales, np.uint16), tscales)
+
+
+def _problem(orc, gx, fmt, abits, rows, cols, batch, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    _, codes, scales = orc.quantize_group128(w, fmt)
+    tiled, tscales = gx.tile_group128(fmt, codes, scales, rows, cols)
+    wint = orc.unpack_weights(codes, rows, cols, fmt)
+    x16 = _half(rng.standard_normal((batch, cols)))
+    if abits == 4:
+        acts, as16 = orc.quantize_activation_i4(x16)
+        aint = orc.unpack_a4(acts, cols)
+    else:
+        acts, as16 = orc.quantize_activation_i8(x16)
+        aint = acts
+    return dict(tiled=tiled, tscales=tscales, wint=wint, ws16=orc.f32_to_f16_bits(scales),
+                acts=acts, as16=as16, aint=aint, x16=x16)
+
+
+CASES = [
+    # (fmt, abits, rows, cols, batch)
+    (2, 4, 64, 640, 1), (2, 4, 64, 640, 2), (2, 4, 64, 640, 3), (2, 4, 64, 640, 4),
+    (2, 4, 64, 640, 5), (2, 4, 64, 640, 7), (2, 4, 64, 640, 8), (2, 4, 64, 640, 9),
+    (2, 4, 64, 640, 16), (2, 4, 64, 640, 17), (2, 4, 64, 640, 31), (2, 4, 64, 640, 32),
+    (3, 4, 64, 640, 1), (3, 4, 64, 640, 5), (3, 4, 64, 640, 12), (3, 4, 64, 640, 32),
+    (2, 8, 64, 640, 1), (2, 8, 64, 640, 5), (2, 8, 64, 640, 32),
+    (3, 8, 64, 640, 3), (3, 8, 64, 640, 16),
+    (2, 4, 17408, 5120, 5), (2, 4, 5120, 17408, 5), (3, 4, 17408, 5120, 5),
+    (2, 4, 17408, 5120, 1), (2, 4, 17408, 5120, 32), (2, 8, 17408, 5120, 1),
+]
+
+
+@pytest.mark.parametrize("fmt,abits,rows,cols,batch", CASES)
+def test_gemm_partials_bit_exact_and_output(device, gx, orc, fmt, abits, rows, cols, batch):
+    p = _problem(orc, gx, fmt, abits, rows, cols, batch, seed=rows + cols + batch + fmt * 7 + abits)
+    want_P = orc.gemm_partials(p["wint"], p["aint"])
+    want_y = orc.gemm_epilogue(want_P, p["ws16"], p["as16"])
+    dw, dws = dev(p["tiled"]), dev(p["tscales"])
+    da, das = dev(p["acts"]), dev(p["as16"])
+    P = empty((batch, rows, cols // 128), np.int32)
+    say("gemm partials", fmt, abits, rows, cols, batch)
+    gx.debug_gemm_partials(fmt, dw, abits, da, rows, cols, batch, P)
+    assert np.array_equal(host(P), want_P)
+    y = empty((batch, rows), np.float32)
+    say("gemm output", fmt, abits, rows, cols, batch)
+    if abits == 4:
+        gx.launch_i4_gemm(fmt, dw, dws, da, das, y, rows, cols, batch)
+    else:
+        gx.launch_i8_gemm(fmt, dw, dws, da, das, y, rows, cols, batch)
+    got = host(y)
+    scale = max(1e-30, float(np.abs(want_y).max()))
+    assert np.abs(got - want_y).max() <= 2e-5 * scale
+
+
+def test_gemm_half_output(device, gx, orc):
+    fmt, rows, cols, batch = 2, 5120, 10240, 1  # mtp.fc shape
+    p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=21)
+    want = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+    y = empty((batch, rows), np.uint16)
+    say("gemm half", rows, cols)
+    gx.launch_i4_gemm_half(fmt, dev(p["tiled"]), dev(p["tscales"]), dev(p["acts"]), dev(p["as16"]), y, rows, cols, batch)
+    got = host(y, np.uint16).view(np.float16).astype(np.float32)
+    ref16 = want.astype(np.float16).astype(np.float32)
+    assert np.abs(got - ref16).max() <= 2e-5 * np.abs(want).max() + np.abs(ref16).max() * 2 ** -10
+
+
+def test_gemm_fused_four_matrices(device, gx, orc):
+    """GDN input projection set: qkv/z/a/b (8192, 4096, 32, 32 rows) from K=5120."""
+    fmt, cols, batch = 3, 5120, 5
+    rng = np.random.default_rng(33)
+    x16 = _half(rng.standard_normal((batch, cols)))
+    acts, as16 = orc.quantize_activation_i4(x16)
+    aint = orc.unpack_a4(acts, cols)
+    mats, wants, outs = [], [], []
+    for i, rows in enumerate((8192, 4096, 32, 32)):
+        w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+        _, codes, scales = orc.quantize_group128(w, fmt)
+        tiled, ts = gx.tile_group128(fmt, codes, scales, rows, cols)
+        wants.append(orc.gemm_epilogue(orc.gemm_partials(orc.unpack_weights(codes, rows, cols, fmt), aint),
+                                       orc.f32_to_f16_bits(scales), as16))
+        out = empty((batch, rows), np.float32)
+        outs.append(out)
+        mats.append((dev(tiled), dev(ts), out, rows))
+    say("gemm fused")
+    gx.launch_i4_gemm_fused(fmt, mats, dev(acts), dev(as16), cols, batch)
+    for out, want in zip(outs, wants):
+        assert np.abs(host(out) - want).max() <= 2e-5 * np.abs(want).max()
+
+
+def test_quantize_then_gemm_matches_float_reference(device, gx, orc):
+    """fp16 x -> A4 on GPU -> W3A4 GEMM on GPU vs the dequant-dot reference of
+    src/cli/main.cpp:1468-1495 at the BASELINE tolerance (1e-2 relative)."""
+    fmt, rows, cols, batch = 2, 17408, 5120, 5
+    p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=44)
+    codes = empty((batch, cols // 2), np.uint8)
+    scales = empty((batch, cols // 128), np.uint16)
+    y = empty((batch, rows), np.float32)
+    say("quant+gemm")
+    gx.launch_quantize_activation_i4(dev(p["x16"]), codes, scales, cols, batch)
+    gx.launch_i4_gemm(fmt, dev(p["tiled"]), dev(p["tscales"]), codes, scales, y, rows, cols, batch)
+    got = host(y)
+    ws = p["ws16"].view(np.float16).astype(np.float32)
+    ref = orc.lib()
+    out = np.empty((batch, rows), np.float32)
+    ref.orc_dequant_dot_gemv(orc.ptr(np.ascontiguousarray(p["wint"])), orc.ptr(np.ascontiguousarray(ws)),
+                             orc.ptr(p["aint"]), orc.ptr(p["as16"]), rows, cols, batch, orc.ptr(out))
+    assert np.all(np.abs(got - out) <= 1e-2 * np.maximum(1.0, np.abs(out)))
+    assert np.abs(got - out).max() <= 1e-4 * np.abs(out).max()
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+def test_row_gather(device, gx, orc, fmt):
+    rows, cols = 64, 5120
+    p = _problem(orc, gx, fmt, 4, rows, cols, 1, seed=55)
+    ws = p["ws16"].view(np.float16).astype(np.float32)
+    dw, dws = dev(p["tiled"]), dev(p["tscales"])
+    out = empty((cols,), np.uint16)
+    for row in (0, 17, 63):
+        say("row gather", fmt, row)
+        gx.launch_row_gather_tiled(fmt, dw, dws, out, row, rows, cols)
+        want = _half(p["wint"][row].astype(np.float32) * np.repeat(ws[row], 128))
+        assert np.array_equal(host(out, np.uint16), want)
+    idx = dev(np.array([41], np.uint32))
+    gx.launch_row_gather_tiled_indirect(fmt, dw, dws, out, idx, rows, cols)
+    want = _half(p["wint"][41].astype(np.float32) * np.repeat(ws[41], 128))
+    assert np.array_equal(host(out, np.uint16), want)
+    idx = dev(np.array([rows + 5], np.uint32))  # out of range -> zeros (lowbit_gemv.hip:202-205)
+    gx.launch_row_gather_tiled_indirect(fmt, dw, dws, out, idx, rows, cols)
+    assert np.all(host(out, np.uint16) == 0)
