@@ -80,6 +80,13 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIBRARY):
             raise RuntimeError(
                 f"{LIBRARY} is not built; run __graft_entry__.build() (hipcc for gfx950)")
+        # PyTorch-ROCm ships its own libamdhip64 (soname libamdhip64.so.7).  Loading it
+        # first lets this library bind to that same HIP runtime; loading
+        # /opt/rocm's copy first would put two HIP runtimes in one process.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIBRARY)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

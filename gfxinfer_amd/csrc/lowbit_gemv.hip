@@ -8,6 +8,7 @@
 // 4..7 (16*w), an A8 code stays as is.  The MFMA sum is therefore F times the
 // exact integer dot (F = 512, 256, 32 or 16), and the fp32 epilogue folds 1/F
 // into the activation scale, which keeps fmaf(float(P), ws*as, acc) exact.
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <string>
@@ -134,6 +135,17 @@ __global__ __launch_bounds__(256) void quantize_group128_kernel(
   }
 }
 
+// Buffer descriptors: one SGPR resource per stream, a lane-constant VGPR offset
+// and a wave-uniform SGPR offset per access, so a load costs no address VGPRs.
+// Reads past num_records return zeros (used for a missing last group).
+constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
+constexpr int kStreaming = 2;             // nt: weights are read exactly once
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           kBufferWord3);
+}
+
 // ---------------------------------------------------------------------------
 // Operand expansion.  Every function returns int8 lanes for one 16x16x64 MFMA
 // K-step in the slot order documented in common.hpp.
@@ -179,12 +191,13 @@ __device__ __forceinline__ i32x4 permute_i8(unsigned d0, unsigned d1, unsigned d
 // One workgroup per 16-row tile (tiles of up to four fused matrices are
 // concatenated); its W waves split the K groups and combine in LDS.
 // A operand = weights (MFMA rows = matrix rows), B operand = activations
-// (MFMA columns = tokens).  For batches of at most 4 or 8 tokens the 16 MFMA
-// columns carry GP = 4 or 2 groups side by side (token slot = column % (16/GP),
-// group offset = column / (16/GP)); lane block kb of the A operand then serves
-// group kb / (4/GP) and the B operand zeroes the slots of other groups, so
-// each output column receives exactly one group's dot product.  This halves or
-// quarters the fp32 epilogue for the decode batch sizes.
+// (MFMA columns = tokens).  Each group is one pair of 16x16x64 MFMAs whose A
+// operand is the group's 768/1024 contiguous bytes read with lane l = layout
+// lane l.  For batches of at most 4 or 8 tokens the 16 MFMA columns are split
+// into GP = 4 or 2 token windows of 16/GP slots: group j of a pack feeds only
+// window j (the other B lanes are zero), so one set of four accumulators per
+// lane collects GP groups and the fp32 epilogue runs once per pack instead of
+// once per group.
 // ---------------------------------------------------------------------------
 
 struct GemmMatrix {
@@ -205,20 +218,55 @@ struct GemmArgs {
   uint32_t batch;
 };
 
-template <int Format, int ABits, int GP, int NTB, bool HalfOut, bool Partials>
-__global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
+// Dynamic LDS: one private region per wave holding the activations of the
+// wave's current chunk of groups for every live token ([batch][pitch]), already
+// expanded to MFMA operand bytes ([group][lane block kb][K-step h][16 bytes]),
+// a 16-byte zero line read by lanes outside a group's token window, and the
+// chunk's activation scales as fp32 already multiplied by 1/F.  After the MFMA
+// loop the region holds the wave's partial sums for the cross-wave reduction.
+struct GemmLds {
+  uint32_t pitch;         // bytes per token row (chunk bytes + 16: rotates LDS banks)
+  uint32_t zero_offset;   // zero line
+  uint32_t scale_offset;  // fp32 scales [batch][chunk groups]
+  uint32_t region;        // bytes per wave
+};
+
+__host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32_t batch, int abits,
+                                                    uint32_t ntb) {
+  GemmLds l{};
+  (void)abits;
+  l.pitch = chunk_groups * 128u + 16u;  // operand-ready int8: 128 bytes per token per group
+  l.zero_offset = batch * l.pitch;
+  l.scale_offset = l.zero_offset + 16u;
+  uint32_t region = l.scale_offset + batch * chunk_groups * 4u;
+  const uint32_t reduce = ntb * 4u * 64u * 4u;
+  if (region < reduce) region = reduce;
+  l.region = (region + 15u) & ~15u;
+  return l;
+}
+
+// Workgroups of up to 16 waves (large K) for the 16-token variants; the
+// 32-token and A8 variants need more registers and stop at 8 waves.
+template <int Format, int ABits, int GP, int NTB, int CH, bool HalfOut, bool Partials>
+__global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_gemm_kernel(
+    GemmArgs args, GemmLds layout) {
   constexpr unsigned LB = lane_bytes(Format);
-  constexpr unsigned LPG = 4 / GP;    // A lane blocks per group
-  constexpr unsigned TPAD = 16 / GP;  // token slots per group
+  constexpr unsigned WD = LB / 4;        // weight dwords per lane per group
+  constexpr unsigned TPAD = 16 / GP;     // token slots per window
+  constexpr unsigned CHG = CH * GP;      // groups per chunk
+  constexpr unsigned AGB = ABits == 4 ? 64u : 128u;  // activation bytes per token per group
   constexpr float kInvF =
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
 
-  __shared__ float reduction[8][NTB][4][64];
+  extern __shared__ __align__(16) uint8_t lds_all[];
 
   const unsigned lane = threadIdx.x & 63u;
-  const unsigned wave = threadIdx.x >> 6;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep every
+  // per-wave offset in SGPRs (buffer soffset) instead of waterfall loops.
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const unsigned waves = blockDim.x >> 6;
+  uint8_t* lds = lds_all + wave * layout.region;
 
   // Matrix selection for fused launches.
   unsigned tile = blockIdx.x;
@@ -230,21 +278,39 @@ __global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
   const GemmMatrix matrix = args.matrix[index];
   tile -= args.tile_begin[index];
   const uint32_t groups = args.groups;
+  const uint32_t batch = args.batch;
   const uint32_t rows = matrix.tiles * 16u;
-  const uint8_t* weights = matrix.weights + static_cast<std::size_t>(tile) * groups * 64u * LB;
-  const __half* weight_scales = matrix.scales + static_cast<std::size_t>(tile) * groups * 16u;
+  const uint32_t row_bytes = ABits == 4 ? args.columns / 2 : args.columns;
+  const auto weights = buffer(matrix.weights + static_cast<std::size_t>(tile) * groups * 64u * LB,
+                              groups * 64u * LB);
+  const auto weight_scales =
+      buffer(matrix.scales + static_cast<std::size_t>(tile) * groups * 16u, groups * 32u);
+  const auto activations = buffer(args.activations, batch * row_bytes);
 
-  const unsigned m = lane & 15u;          // A row / B,C column
-  const unsigned kb = lane >> 4;          // K lane block / C row block
-  const unsigned go_a = kb / LPG;         // group offset served by this A lane
-  const unsigned q = kb % LPG;            // rank among the lanes of that group
-  const unsigned slot = m % TPAD;         // token slot of this B/C column
-  const unsigned go_c = m / TPAD;         // group offset of this B/C column
-  const bool b_on = go_c == go_a;
+  const unsigned n = lane & 15u;   // B/C column
+  const unsigned kb = lane >> 4;   // K lane block (A, B) / row block (C)
+  const unsigned slot = n % TPAD;  // token slot of column n
+  const unsigned window = n / TPAD;
+  const unsigned w_voffset = lane * LB;
+  const unsigned ws_voffset = (window * 16u + 4u * kb) * 2u;
 
   const unsigned packs = (groups + GP - 1) / GP;
   const unsigned pack_begin = packs * wave / waves;
   const unsigned pack_end = packs * (wave + 1) / waves;
+
+  // LDS byte offset of this lane's B operand for group j of a pack, token block t
+  // (relative to the pack's first group); lanes outside the window read zeros.
+  uint32_t b_offset[GP][NTB];
+#pragma unroll
+  for (unsigned j = 0; j < GP; ++j) {
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+      const unsigned token = t * 16u + slot;
+      b_offset[j][t] = (window == j && token < batch) ? token * layout.pitch + j * 128u + kb * 32u
+                                                       : 0xffffffffu;
+    }
+  }
+  if (lane < 4) reinterpret_cast<uint32_t*>(lds + layout.zero_offset)[lane] = 0u;
 
   float acc[NTB][4];
 #pragma unroll
@@ -253,81 +319,152 @@ __global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
     for (int r = 0; r < 4; ++r) acc[t][r] = 0.0F;
   }
 
-  for (unsigned pack = pack_begin; pack < pack_end; ++pack) {
-    const unsigned g_a = pack * GP + go_a;
-    const bool a_valid = g_a < groups;
-    i32x4 c[NTB];
+  constexpr unsigned kPieces = AGB / 16;  // 16-byte source pieces per token per group
+  constexpr unsigned kRowPieces = CHG * kPieces;
+  constexpr unsigned kMaxTokens = TPAD * NTB;  // batch capacity of this variant
+  constexpr unsigned kMaxPieces = (kMaxTokens * kRowPieces + 63u) / 64u;
+  const auto act_scales = buffer(args.activation_scales, batch * groups * 2u);
+  for (unsigned base = pack_begin; base < pack_end; base += CH) {
+    const unsigned g0 = base * GP;
+    // 1) Activation pieces of this chunk (L2-resident), loaded first.  Piece i
+    //    is token i / kRowPieces, bytes (i % kRowPieces) * 16 of the chunk.
+    const unsigned total_pieces = batch * kRowPieces;
+    u32x4 stage[kMaxPieces];
+    constexpr unsigned kScaleIters = (kMaxTokens * CHG + 63u) / 64u;
+    unsigned short stage_scale[kScaleIters];
 #pragma unroll
-    for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
+    for (unsigned p = 0; p < kMaxPieces; ++p) {
+      const unsigned i = p * 64u + lane;
+      const unsigned token = min(i / kRowPieces, batch - 1u);
+      const unsigned rem = i % kRowPieces;
+      stage[p] = __builtin_amdgcn_raw_buffer_load_b128(activations, token * row_bytes + rem * 16u,
+                                                       g0 * AGB, 0);
+    }
+    if constexpr (!Partials) {
+      // entry e < batch * CHG: scale of (token e / CHG, group g0 + e % CHG)
 #pragma unroll
-    for (unsigned s = 0; s < GP; ++s) {
-      const unsigned block = q * GP + s;
-      i32x4 a0, a1;
-      if (a_valid) {
-        const uint8_t* chunk =
-            weights + (static_cast<std::size_t>(g_a) * 64u + block * 16u + m) * LB;
-        if constexpr (Format == GFXI_W3G128) {
-          const u32x3 w = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(chunk));
-          expand_w3(w[0], w[1], w[2], a0, a1);
-        } else {
-          const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(chunk));
-          a0 = expand_nibbles(w[0], w[1]);
-          a1 = expand_nibbles(w[2], w[3]);
-        }
-      } else {
-        a0 = i32x4{0, 0, 0, 0};
-        a1 = a0;
-      }
-#pragma unroll
-      for (int t = 0; t < NTB; ++t) {
-        const unsigned token = t * 16u + slot;
-        i32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
-        if (b_on && a_valid && token < args.batch) {
-          const std::size_t column = static_cast<std::size_t>(g_a) * kGroup + block * 32u;
-          if constexpr (ABits == 4) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(
-                args.activations + static_cast<std::size_t>(token) * (args.columns / 2) + column / 2);
-            b0 = expand_nibbles(x[0], x[1]);
-            b1 = expand_nibbles(x[2], x[3]);
-          } else {
-            const u32x4* source = reinterpret_cast<const u32x4*>(
-                args.activations + static_cast<std::size_t>(token) * args.columns + column);
-            const u32x4 x = source[0];
-            const u32x4 y = source[1];
-            b0 = permute_i8(x[0], x[1], x[2], x[3]);
-            b1 = permute_i8(y[0], y[1], y[2], y[3]);
-          }
-        }
-        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c[t], 0, 0, 0);
-        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c[t], 0, 0, 0);
+      for (unsigned it = 0; it < kScaleIters; ++it) {
+        const unsigned e = it * 64u + lane;
+        const unsigned token = min(e / CHG, batch - 1u);
+        stage_scale[it] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, (token * groups + e % CHG) * 2u,
+                                                               g0 * 2u, 0);
       }
     }
-    // Epilogue for this lane's C elements: rows 4*kb + r, token slot, group g_c.
-    const unsigned g_c = pack * GP + go_c;
-    if (g_c < groups) {
-      const u32x2 packed_ws = *reinterpret_cast<const u32x2*>(
-          weight_scales + static_cast<std::size_t>(g_c) * 16u + 4u * kb);
-      float ws[4];
-      ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[0] & 0xffffu)));
-      ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[0] >> 16)));
-      ws[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[1] & 0xffffu)));
-      ws[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(packed_ws[1] >> 16)));
+    // 2) Weights and weight scales of CH packs, all in flight together.
+    unsigned wreg[CH][GP][WD];
+    u32x2 wsreg[CH];
 #pragma unroll
-      for (int t = 0; t < NTB; ++t) {
-        const unsigned token = t * 16u + slot;
-        if (token < args.batch) {
-          if constexpr (Partials) {
-            const std::size_t base = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
+    for (unsigned ci = 0; ci < CH; ++ci) {
+      const unsigned pack = min(base + ci, pack_end - 1u);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              args.partials[(base + r) * groups + g_c] = c[t][r] >> kShift;
-            }
-          } else {
-            const float as = __half2float(args.activation_scales[token * groups + g_c]) * kInvF;
+      for (unsigned j = 0; j < GP; ++j) {
+        const unsigned g_offset = (pack * GP + j) * 64u * LB;  // past the end -> zeros
+        if constexpr (Format == GFXI_W3G128) {
+          const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
+          wreg[ci][j][0] = w[0];
+          wreg[ci][j][1] = w[1];
+          wreg[ci][j][2] = w[2];
+        } else {
+          const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(weights, w_voffset, g_offset, kStreaming);
+          wreg[ci][j][0] = w[0];
+          wreg[ci][j][1] = w[1];
+          wreg[ci][j][2] = w[2];
+          wreg[ci][j][3] = w[3];
+        }
+      }
+      if constexpr (!Partials) {
+        wsreg[ci] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, ws_voffset, pack * GP * 32u, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3) Expand the activations into operand bytes and stage them (and the
+    //    scales) into this wave's LDS region.
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              acc[t][r] = fmaf(static_cast<float>(c[t][r]), ws[r] * as, acc[t][r]);
-            }
+    for (unsigned p = 0; p < kMaxPieces; ++p) {
+      const unsigned i = p * 64u + lane;
+      if (i < total_pieces) {
+        const unsigned token = i / kRowPieces;
+        const unsigned rem = i % kRowPieces;
+        const u32x4 x = stage[p];
+        if constexpr (ABits == 4) {
+          // 32 columns (group rem / 4, lane block rem % 4) -> two K-steps
+          *reinterpret_cast<i32x4*>(lds + token * layout.pitch + rem * 32u) = expand_nibbles(x[0], x[1]);
+          *reinterpret_cast<i32x4*>(lds + token * layout.pitch + rem * 32u + 16u) = expand_nibbles(x[2], x[3]);
+        } else {
+          // 16 columns = one K-step of (group rem / 8, lane block (rem / 2) % 4)
+          *reinterpret_cast<i32x4*>(lds + token * layout.pitch + rem * 16u) = permute_i8(x[0], x[1], x[2], x[3]);
+        }
+      }
+    }
+    if constexpr (!Partials) {
+#pragma unroll
+      for (unsigned it = 0; it < kScaleIters; ++it) {
+        const unsigned e = it * 64u + lane;
+        if (e < batch * CHG) {
+          reinterpret_cast<float*>(lds + layout.scale_offset)[e] =
+              __half2float(__ushort_as_half(stage_scale[it])) * kInvF;
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 4) Compute.
+#pragma unroll
+    for (unsigned ci = 0; ci < CH; ++ci) {
+      const unsigned pack = base + ci;
+      if (pack >= pack_end) break;
+      i32x4 c[NTB];
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
+#pragma unroll
+      for (unsigned j = 0; j < GP; ++j) {
+        const unsigned g = pack * GP + j;
+        if (g >= groups) break;  // wave-uniform: partial last pack
+        i32x4 a0, a1;
+        if constexpr (Format == GFXI_W3G128) {
+          expand_w3(wreg[ci][j][0], wreg[ci][j][1], wreg[ci][j][2], a0, a1);
+        } else {
+          a0 = expand_nibbles(wreg[ci][j][0], wreg[ci][j][1]);
+          a1 = expand_nibbles(wreg[ci][j][2], wreg[ci][j][3]);
+        }
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) {
+          const bool on = b_offset[j][t] != 0xffffffffu;
+          const uint32_t off = on ? b_offset[j][t] + ci * GP * 128u : layout.zero_offset;
+          const i32x4 b0 = *reinterpret_cast<const i32x4*>(lds + off);
+          const i32x4 b1 = *reinterpret_cast<const i32x4*>(lds + (on ? off + 16u : off));
+          c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c[t], 0, 0, 0);
+          c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c[t], 0, 0, 0);
+        }
+      }
+      // Epilogue: lane holds rows 4*kb + r of column n = (token slot, group g_c).
+      const unsigned g_c = pack * GP + window;
+      if constexpr (Partials) {
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) {
+          const unsigned token = t * 16u + slot;
+          if (g_c < groups && token < batch) {
+            const std::size_t row0 = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) args.partials[(row0 + r) * groups + g_c] = c[t][r] >> kShift;
+          }
+        }
+      } else {
+        // Columns of dead tokens or of a missing last group hold exact zeros.
+        const u32x2 pw = wsreg[ci];
+        float ws[4];
+        ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] & 0xffffu)));
+        ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] >> 16)));
+        ws[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] & 0xffffu)));
+        ws[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] >> 16)));
+        const float* scales = reinterpret_cast<const float*>(lds + layout.scale_offset);
+        const unsigned gl = min(g_c, groups - 1u) - g0;
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) {
+          const unsigned token = min(t * 16u + slot, batch - 1u);
+          const float as = scales[token * CHG + gl];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[t][r] = fmaf(static_cast<float>(c[t][r]), ws[r] * as, acc[t][r]);
           }
         }
       }
@@ -335,7 +472,7 @@ __global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
   }
   if constexpr (Partials) return;
 
-  // Combine the GP group columns of each token slot (lanes m, m+TPAD, ...).
+  // Combine the GP windows of each token slot (lanes n, n+TPAD, ...).
 #pragma unroll
   for (unsigned offset = TPAD; offset < 16u; offset <<= 1) {
 #pragma unroll
@@ -345,36 +482,35 @@ __global__ __launch_bounds__(512) void lowbit_gemm_kernel(GemmArgs args) {
     }
   }
   if (waves > 1) {
+    float* mine = reinterpret_cast<float*>(lds);  // this wave's region is free now
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) reduction[wave][t][r][lane] = acc[t][r];
+      for (int r = 0; r < 4; ++r) mine[(t * 4 + r) * 64 + lane] = acc[t][r];
     }
     __syncthreads();
     if (wave != 0) return;
+    for (unsigned w = 1; w < waves; ++w) {
+      const float* other = reinterpret_cast<const float*>(lds_all + w * layout.region);
 #pragma unroll
-    for (int t = 0; t < NTB; ++t) {
+      for (int t = 0; t < NTB; ++t) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float sum = reduction[0][t][r][lane];
-        for (unsigned w = 1; w < waves; ++w) sum += reduction[w][t][r][lane];
-        acc[t][r] = sum;
+        for (int r = 0; r < 4; ++r) acc[t][r] += other[(t * 4 + r) * 64 + lane];
       }
     }
   }
-  if (go_c != 0) return;
+  if (window != 0) return;
 #pragma unroll
   for (int t = 0; t < NTB; ++t) {
-    const unsigned token = t * 16u + slot;
-    if (token >= args.batch) continue;
-    const std::size_t base = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
+    if (t * 16u + slot >= batch) continue;
+    const std::size_t out = static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
     if constexpr (HalfOut) {
-      __half* out = reinterpret_cast<__half*>(matrix.output) + base;
+      __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) out[r] = __float2half(acc[t][r]);
+      for (int r = 0; r < 4; ++r) o[r] = __float2half(acc[t][r]);
     } else {
       float4 value = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + base) = value;
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
     }
   }
 }
@@ -410,29 +546,44 @@ bool aligned(const void* pointer, std::size_t bytes) {
   return (reinterpret_cast<std::uintptr_t>(pointer) % bytes) == 0;
 }
 
+// GFXI_GEMM_WAVES (1..16) overrides the waves per workgroup; a tuning knob.
+int waves_override() {
+  static const int value = [] {
+    const char* text = std::getenv("GFXI_GEMM_WAVES");
+    const int v = text != nullptr ? std::atoi(text) : 0;
+    return v >= 1 && v <= 16 ? v : 0;
+  }();
+  return value;
+}
+
 unsigned choose_waves(uint32_t groups, unsigned gp) {
-  const unsigned packs = (groups + gp - 1) / gp;
-  unsigned waves = (packs + 4) / 5;  // about five packs per wave
+  if (const int forced = waves_override(); forced != 0) return static_cast<unsigned>(forced);
+  (void)gp;
+  unsigned waves = (groups + 9) / 10;  // about ten groups (one load chunk) per wave
   if (waves < 1) waves = 1;
-  if (waves > 8) waves = 8;
+  if (waves > 16) waves = 16;
   return waves;
 }
 
 template <int Format, int ABits, bool HalfOut, bool Partials>
 void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
   const uint32_t batch = args.batch;
-  auto go = [&](auto kernel, unsigned gp) {
-    const unsigned waves = choose_waves(args.groups, gp);
-    hipLaunchKernelGGL(kernel, dim3(total_tiles), dim3(64 * waves), 0, stream, args);
+  auto go = [&](auto kernel, unsigned gp, unsigned ch, unsigned ntb) {
+    unsigned waves = choose_waves(args.groups, 1);
+    if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
+    const GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
+    hipLaunchKernelGGL(kernel, dim3(total_tiles), dim3(64 * waves), layout.region * waves, stream,
+                       args, layout);
   };
+  // CH = packs per load chunk: about ten groups of weights in flight per wave.
   if (batch <= 4) {
-    go(lowbit_gemm_kernel<Format, ABits, 4, 1, HalfOut, Partials>, 4);
+    go(lowbit_gemm_kernel<Format, ABits, 4, 1, 3, HalfOut, Partials>, 4, 3, 1);
   } else if (batch <= 8) {
-    go(lowbit_gemm_kernel<Format, ABits, 2, 1, HalfOut, Partials>, 2);
+    go(lowbit_gemm_kernel<Format, ABits, 2, 1, 5, HalfOut, Partials>, 2, 5, 1);
   } else if (batch <= 16) {
-    go(lowbit_gemm_kernel<Format, ABits, 1, 1, HalfOut, Partials>, 1);
+    go(lowbit_gemm_kernel<Format, ABits, 1, 1, 6, HalfOut, Partials>, 1, 6, 1);
   } else {
-    go(lowbit_gemm_kernel<Format, ABits, 1, 2, HalfOut, Partials>, 1);
+    go(lowbit_gemm_kernel<Format, ABits, 1, 2, 5, HalfOut, Partials>, 1, 5, 2);
   }
 }
 

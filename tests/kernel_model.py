@@ -60,7 +60,11 @@ def regs_to_bytes(regs) -> np.ndarray:
 
 def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray, rows: int,
                       columns: int, batch: int) -> np.ndarray:
-    """int32 P[batch, rows, G] as the kernel computes it (exact integer model)."""
+    """int32 P[batch, rows, G] as the kernel computes it (exact integer model).
+
+    Each group is one MFMA pair: A lane l = layout lane l of the group; B lane
+    (column n, block kb) is live only when n // TPAD is the group's window in its
+    pack and the token slot n % TPAD (+16 t) is below the batch."""
     G = columns // 128
     LB = lane_bytes(fmt)
     F = (32 if fmt == W3 else 16) * (16 if abits == 4 else 1)
@@ -72,31 +76,23 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
         GP, NTB = 1, 1
     else:
         GP, NTB = 1, 2
-    LPG, TPAD = 4 // GP, 16 // GP
+    TPAD = 16 // GP
     chunks = tiled.reshape(rows // 16, G, 64, LB)
     lanes = np.arange(64)
-    m = lanes % 16
+    n = lanes % 16
     kb = lanes // 16
-    go_a = kb // LPG
-    q = kb % LPG
-    slot = m % TPAD
-    go_c = m // TPAD
-    b_on = go_c == go_a
+    slot = n % TPAD
+    window = n // TPAD
     out = np.zeros((batch, rows, G), dtype=np.int64)
     packs = (G + GP - 1) // GP
     for tile in range(rows // 16):
         for pack in range(packs):
-            g_a = pack * GP + go_a
-            a_valid = g_a < G
             C = np.zeros((NTB, 16, 16), dtype=np.int64)  # [t][row][column]
-            for s in range(GP):
-                block = q * GP + s
-                # A operand bytes per lane for h = 0, 1
-                raw = np.zeros((64, LB), dtype=np.uint8)
-                for l in range(64):
-                    if a_valid[l]:
-                        raw[l] = chunks[tile, g_a[l], block[l] * 16 + m[l]]
-                d = raw.view(np.uint32).reshape(64, LB // 4)
+            for j in range(GP):
+                g = pack * GP + j
+                if g >= G:
+                    break
+                d = chunks[tile, g].copy().view(np.uint32).reshape(64, LB // 4)
                 if fmt == W3:
                     h0, h1 = expand_w3(d[:, 0], d[:, 1], d[:, 2])
                 else:
@@ -104,12 +100,12 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
                 A = [regs_to_bytes(h0).astype(np.int64), regs_to_bytes(h1).astype(np.int64)]
                 for t in range(NTB):
                     token = t * 16 + slot
-                    on = b_on & a_valid & (token < batch)
+                    on = (window == j) & (token < batch)
                     Bh = [np.zeros((64, 16), dtype=np.int64), np.zeros((64, 16), dtype=np.int64)]
                     for l in range(64):
                         if not on[l]:
                             continue
-                        col = g_a[l] * 128 + block[l] * 32
+                        col = g * 128 + kb[l] * 32
                         if abits == 4:
                             x = acts[token[l], col // 2: col // 2 + 16].copy().view(np.uint32)
                             regs = [expand_nibbles(x[0:1], x[1:2]), expand_nibbles(x[2:3], x[3:4])]
@@ -124,7 +120,6 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
                         Ar = A[h].reshape(4, 16, 16)   # [kb][row][j]
                         Br = Bh[h].reshape(4, 16, 16)  # [kb][col][j]
                         C[t] += np.einsum("krj,kcj->rc", Ar, Br)
-            # epilogue: lane l holds C[4*kb + r][m] for column m -> token slot, group g_c
             for t in range(NTB):
                 for col in range(16):
                     token = t * 16 + col % TPAD
@@ -133,4 +128,6 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
                         v = C[t][:, col]
                         assert np.all(v % F == 0)
                         out[token, tile * 16:(tile + 1) * 16, g_c] = v // F
+                    else:
+                        assert np.all(C[t][:, col] == 0)
     return out.astype(np.int32)
