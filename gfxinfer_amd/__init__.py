@@ -66,6 +66,29 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled_indirect": (I32, [I32, P, P, P, P, SZ, SZ, P]),
+    "gfxinfer_launch_rms_norm": (I32, [P, P, P, SZ, F32, I32, P]),
+    "gfxinfer_launch_rms_norm_batch": (I32, [P, P, P, SZ, U32, F32, I32, P]),
+    "gfxinfer_launch_residual_add_rms_norm_batch": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
+    "gfxinfer_launch_rms_norm_quantize_i4": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
+    "gfxinfer_launch_residual_add_rms_norm_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, U32, F32, I32, P]),
+    "gfxinfer_launch_dual_rms_norm_concat": (I32, [P, P, P, P, P, SZ, F32, I32, P]),
+    "gfxinfer_launch_silu_multiply": (I32, [P, P, P, SZ, P]),
+    "gfxinfer_launch_silu_multiply_quantize_i4": (I32, [P, P, P, P, SZ, U32, P]),
+    "gfxinfer_launch_float_to_half": (I32, [P, P, SZ, P]),
+    "gfxinfer_launch_gdn_conv_update_block": (I32, [P, P, P, P, P, P, SZ, U32, P]),
+    "gfxinfer_launch_gdn_recurrent_decode_block": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, P, P]),
+    "gfxinfer_launch_gdn_recurrent_window": (I32, [P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, P]),
+    "gfxinfer_launch_gdn_output_quantize_i4": (I32, [P, P, P, P, P, P, U32, U32, U32, P]),
+    "gfxinfer_launch_gdn_restore_prefix_all": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, U32, U32, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_block": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, ctypes.c_uint64, U32, F32, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_block_indirect_position": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, P, U32, F32, P]),
+    "gfxinfer_launch_kv_append_block": (I32, [P, P, P, P, SZ, SZ, U32, SZ, P]),
+    "gfxinfer_launch_kv_append_block_indirect_position": (I32, [P, P, P, P, P, SZ, U32, SZ, P]),
+    "gfxinfer_launch_argmax_batch": (I32, [P, P, SZ, SZ, U32, P]),
+    "gfxinfer_launch_argmax_mapped": (I32, [P, P, P, SZ, P]),
+    "gfxinfer_attention_workspace_bytes": (SZ, [U32, U32, SZ]),
+    "gfxinfer_launch_gated_attention_decode_block": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
 }
 
 

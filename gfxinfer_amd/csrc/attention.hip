@@ -1,0 +1,278 @@
+// Causal gated GQA decode attention over a verify block (k+1 <= 32 query tokens)
+// for gfx950: split-context flash decoding on v_mfma_f32_16x16x32_f16.
+//
+// Reference semantics: gated_attention_decode (src/kernels/qwen_ops.hip:698-766):
+// token t of the block attends to the first base + t cached positions, scores
+// are q.k / sqrt(head_size), softmax over positions, output = softmax(s).V *
+// sigmoid(gate) rounded to fp16, the gate being the second half of each head's
+// 2*head_size query-projection row.  The reference runs one 256-thread block per
+// (head, token) that walks the whole context; here one workgroup per (KV head,
+// 64-position split) stages K and V^T in LDS once and serves all
+// (q_heads/kv_heads) x tokens query rows of that KV head with MFMA, writing a
+// split-local (max, sum, unnormalized output); a combine kernel merges splits.
+#include <cmath>
+#include <limits>
+#include <string>
+
+#include "common.hpp"
+
+namespace gfx950 {
+namespace {
+
+using h8 = _Float16 __attribute__((ext_vector_type(8)));
+using f4 = float __attribute__((ext_vector_type(4)));
+using u32x4 = unsigned __attribute__((ext_vector_type(4)));
+
+constexpr unsigned kD = 128;       // head size
+constexpr unsigned kSplit = 64;    // positions per workgroup
+constexpr unsigned kTiles = kSplit / 16;  // score tiles of 16 positions
+constexpr unsigned kSteps = kSplit / 32;  // P.V K-steps of 32 positions
+constexpr unsigned kPad = 8;       // LDS row padding (halves)
+constexpr unsigned kRow = kSplit + kPad;
+
+struct AttnArgs {
+  const __half* query;        // [T][Hq][D]
+  const __half* key_cache;    // [capacity][Hkv][D]
+  const __half* value_cache;  // [capacity][Hkv][D]
+  float* partial_o;           // [T*Hq][splits][D]
+  float* partial_ml;          // [T*Hq][splits][2]  (max, sum)
+  uint64_t base_count;        // positions visible to token 0
+  const uint64_t* indirect_position;  // if set: base_count = *p + 1
+  uint32_t tokens, q_heads, kv_heads, splits, capacity;
+  float scale;
+};
+
+__device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
+  return a.indirect_position != nullptr ? *a.indirect_position + 1u : a.base_count;
+}
+
+__global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
+  __shared__ __align__(16) _Float16 ks[kSplit][kD + kPad];  // K rows of the split
+  __shared__ __align__(16) _Float16 vt[kD][kRow];           // V transposed: [d][position]
+  __shared__ __align__(16) _Float16 ps[4][16][kRow];        // per-wave P tile
+
+  const unsigned split = blockIdx.x, hk = blockIdx.y;
+  const uint64_t base = base_count_of(a);
+  const uint64_t max_count = base + a.tokens - 1;  // visible positions of the last token
+  const uint64_t p0 = static_cast<uint64_t>(split) * kSplit;
+  if (p0 >= max_count) return;  // uniform: nothing visible in this split
+  const unsigned tid = threadIdx.x, lane = tid & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const unsigned group = a.q_heads / a.kv_heads;
+  const unsigned rows = group * a.tokens;
+
+  // Stage K [pos][d] and V^T [d][pos] for the split's positions (zeros past the
+  // last visible position or the cache capacity).
+  const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
+  for (unsigned i = tid; i < kSplit * (kD / 8); i += blockDim.x) {
+    const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
+    const uint64_t pos = p0 + p;
+    u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+    if (pos < limit) {
+      const std::size_t at = (pos * a.kv_heads + hk) * kD + d8;
+      kv = *reinterpret_cast<const u32x4*>(a.key_cache + at);
+      vv = *reinterpret_cast<const u32x4*>(a.value_cache + at);
+    }
+    *reinterpret_cast<u32x4*>(&ks[p][d8]) = kv;
+    const _Float16* v = reinterpret_cast<const _Float16*>(&vv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt[d8 + e][p] = v[e];
+  }
+  __syncthreads();
+
+  const unsigned m = lane & 15u, kb = lane >> 4;
+  const unsigned row_tiles = (rows + 15) / 16;
+  for (unsigned rt = wave; rt < row_tiles; rt += 4) {
+    // Q operand rows (row = t * group + g -> head hk*group + g of token t).
+    const unsigned qrow = rt * 16 + m;
+    h8 q[4];
+    if (qrow < rows) {
+      const unsigned t = qrow / group, g = qrow - t * group;
+      const __half* src = a.query + (static_cast<std::size_t>(t) * a.q_heads + hk * group + g) * kD + 8 * kb;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) q[s] = *reinterpret_cast<const h8*>(src + 32 * s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) q[s] = h8{};
+    }
+    // S = Q K^T for the split's positions (kTiles tiles of 16).
+    f4 sc[kTiles];
+#pragma unroll
+    for (unsigned j = 0; j < kTiles; ++j) {
+      f4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const h8 kk = *reinterpret_cast<const h8*>(&ks[j * 16 + m][32 * s + 8 * kb]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(q[s], kk, acc, 0, 0, 0);
+      }
+      sc[j] = acc;
+    }
+    // Mask, scale, split-local softmax.  Lane holds rows 4*kb + r, position j*16 + m.
+    float mx[4], sum[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const unsigned row = rt * 16 + 4 * kb + r;
+      const uint64_t count = row < rows ? base + row / group : 0;  // visible positions
+      float best = -INFINITY;
+#pragma unroll
+      for (unsigned j = 0; j < kTiles; ++j) {
+        const uint64_t pos = p0 + j * 16 + m;
+        const float s = pos < count ? sc[j][r] * a.scale : -INFINITY;
+        sc[j][r] = s;
+        best = fmaxf(best, s);
+      }
+      best = fmaxf(best, __shfl_xor(best, 1));
+      best = fmaxf(best, __shfl_xor(best, 2));
+      best = fmaxf(best, __shfl_xor(best, 4));
+      best = fmaxf(best, __shfl_xor(best, 8));
+      float total = 0.0F;
+#pragma unroll
+      for (unsigned j = 0; j < kTiles; ++j) {
+        const float p = best == -INFINITY ? 0.0F : expf(sc[j][r] - best);
+        total += p;
+        ps[wave][4 * kb + r][j * 16 + m] = static_cast<_Float16>(p);
+      }
+      total += __shfl_xor(total, 1);
+      total += __shfl_xor(total, 2);
+      total += __shfl_xor(total, 4);
+      total += __shfl_xor(total, 8);
+      mx[r] = best;
+      sum[r] = total;
+    }
+    // O = P V: 8 tiles of 16 head dims, kSteps K-steps of 32 positions.
+    h8 pa[kSteps];
+#pragma unroll
+    for (unsigned s = 0; s < kSteps; ++s) pa[s] = *reinterpret_cast<const h8*>(&ps[wave][m][32 * s + 8 * kb]);
+#pragma unroll
+    for (int dj = 0; dj < 8; ++dj) {
+      f4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (unsigned s = 0; s < kSteps; ++s) {
+        const h8 vv = *reinterpret_cast<const h8*>(&vt[dj * 16 + m][32 * s + 8 * kb]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[s], vv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned row = rt * 16 + 4 * kb + r;
+        if (row < rows) {
+          const unsigned t = row / group, g = row - t * group;
+          const std::size_t idx = static_cast<std::size_t>(t) * a.q_heads + hk * group + g;
+          a.partial_o[(idx * a.splits + split) * kD + dj * 16 + m] = acc[r];
+        }
+      }
+    }
+    if (m == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned row = rt * 16 + 4 * kb + r;
+        if (row < rows) {
+          const unsigned t = row / group, g = row - t * group;
+          const std::size_t idx = static_cast<std::size_t>(t) * a.q_heads + hk * group + g;
+          a.partial_ml[(idx * a.splits + split) * 2] = mx[r];
+          a.partial_ml[(idx * a.splits + split) * 2 + 1] = sum[r];
+        }
+      }
+    }
+  }
+}
+
+// Merge the splits of each (token, q head) and apply the sigmoid gate.  One
+// wave per (token, head); lane owns head dims 2l, 2l+1.
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, const float* __restrict__ gate,
+                                                                __half* __restrict__ output) {
+  const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (linear >= a.tokens * a.q_heads) return;
+  const unsigned lane = threadIdx.x & 63u;
+  const uint32_t t = linear / a.q_heads, qh = linear - t * a.q_heads;
+  const uint64_t count = base_count_of(a) + t;
+  const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
+  const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
+  float best = -INFINITY;
+  for (unsigned s = 0; s < used; ++s) best = fmaxf(best, ml[2 * s]);
+  float o0 = 0.0F, o1 = 0.0F, total = 0.0F;
+  const float* po = a.partial_o + static_cast<std::size_t>(linear) * a.splits * kD + 2 * lane;
+  for (unsigned s = 0; s < used; ++s) {
+    const float w = expf(ml[2 * s] - best);
+    total = fmaf(ml[2 * s + 1], w, total);
+    const float2 v = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD);
+    o0 = fmaf(v.x, w, o0);
+    o1 = fmaf(v.y, w, o1);
+  }
+  const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
+  const float g0 = 1.0F / (1.0F + expf(-g[2 * lane]));
+  const float g1 = 1.0F / (1.0F + expf(-g[2 * lane + 1]));
+  __half* out = output + static_cast<std::size_t>(linear) * kD + 2 * lane;
+  out[0] = __float2half(o0 / total * g0);
+  out[1] = __float2half(o1 / total * g1);
+}
+
+int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t* key_cache,
+                        const uint16_t* value_cache, uint16_t* output, uint64_t base_count,
+                        const uint64_t* indirect, size_t capacity, uint32_t batch, uint32_t q_heads,
+                        uint32_t kv_heads, uint32_t head_size, float* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+}  // namespace
+}  // namespace gfx950
+
+using namespace gfx950;
+
+extern "C" size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_heads,
+                                                     size_t capacity) {
+  const std::size_t splits = (capacity + kSplit - 1) / kSplit;
+  return static_cast<std::size_t>(batch) * q_heads * splits * (kD + 2) * sizeof(float);
+}
+
+namespace gfx950 {
+namespace {
+int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t* key_cache,
+                        const uint16_t* value_cache, uint16_t* output, uint64_t base_count,
+                        const uint64_t* indirect, size_t capacity, uint32_t batch, uint32_t q_heads,
+                        uint32_t kv_heads, uint32_t head_size, float* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  if (query == nullptr || gate == nullptr || key_cache == nullptr || value_cache == nullptr ||
+      output == nullptr || workspace == nullptr || batch == 0 || batch > 32 || q_heads == 0 ||
+      kv_heads == 0 || q_heads % kv_heads != 0 || head_size != kD || capacity == 0 ||
+      capacity > (1u << 24) || (indirect == nullptr && (base_count == 0 || base_count + batch - 1 > capacity))) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid gated attention decode arguments (head size 128, "
+                                       "1..32 tokens, visible positions within capacity)");
+  }
+  if (workspace_bytes < gfxinfer_attention_workspace_bytes(batch, q_heads, capacity)) {
+    return fail(GFXI_INVALID_ARGUMENT, "attention workspace is too small");
+  }
+  const auto splits = static_cast<uint32_t>((capacity + kSplit - 1) / kSplit);
+  float* partial_o = workspace;
+  float* partial_ml = workspace + static_cast<std::size_t>(batch) * q_heads * splits * kD;
+  AttnArgs args{reinterpret_cast<const __half*>(query), reinterpret_cast<const __half*>(key_cache),
+                reinterpret_cast<const __half*>(value_cache), partial_o, partial_ml, base_count, indirect,
+                batch, q_heads, kv_heads, splits, static_cast<uint32_t>(capacity),
+                1.0F / std::sqrt(static_cast<float>(kD))};
+  hipLaunchKernelGGL(attention_split_kernel, dim3(splits, kv_heads), dim3(256), 0, stream, args);
+  if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
+  const uint32_t total = batch * q_heads;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3((total + 3) / 4), dim3(256), 0, stream, args, gate,
+                     reinterpret_cast<__half*>(output));
+  return launch_status("gated attention combine launch failed");
+}
+}  // namespace
+}  // namespace gfx950
+
+extern "C" int32_t gfxinfer_launch_gated_attention_decode_block(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, size_t base_token_count, size_t capacity, uint32_t batch, uint32_t q_heads,
+    uint32_t kv_heads, uint32_t head_size, float* workspace, size_t workspace_bytes, void* stream) {
+  return attention_entry(query, gate, key_cache, value_cache, output, base_token_count, nullptr, capacity,
+                         batch, q_heads, kv_heads, head_size, workspace, workspace_bytes,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_indirect_position(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, const uint64_t* base_position, size_t capacity, uint32_t batch,
+    uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (base_position == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect position is null");
+  return attention_entry(query, gate, key_cache, value_cache, output, 0, base_position, capacity, batch,
+                         q_heads, kv_heads, head_size, workspace, workspace_bytes,
+                         static_cast<hipStream_t>(stream));
+}

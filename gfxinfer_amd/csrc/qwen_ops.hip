@@ -1,0 +1,971 @@
+// Decoder-block operators of the speculative verify step for gfx950: RMSNorms
+// (plus fused RMSNorm -> A4 quantization), SwiGLU -> A4, the GDN (gated delta
+// network) causal conv, window recurrence with per-token logs and prefix
+// rollback, per-head Q/K RMSNorm + partial RoPE, KV append, greedy argmax.
+//
+// Reference semantics: src/kernels/qwen_ops.hip.  Shapes the reference bakes in
+// (48 value heads, 16 key heads, 24/4 attention heads x 256) are parameters here.
+#include <cmath>
+#include <limits>
+#include <string>
+
+#include "common.hpp"
+
+namespace gfx950 {
+namespace {
+
+using u32x4 = unsigned __attribute__((ext_vector_type(4)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_float(uint16_t value) {
+  return __uint_as_float(static_cast<uint32_t>(value) << 16U);  // qwen_ops.hip:27-29
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float value) {
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) value += __shfl_xor(value, offset);
+  return value;
+}
+
+__device__ __forceinline__ float wave_max(float value) {
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
+  return value;
+}
+
+// Sum over the 16 lanes of a row (lanes l, l^1, ..., l^8).
+__device__ __forceinline__ float row16_sum(float value) {
+  value += __shfl_xor(value, 1);
+  value += __shfl_xor(value, 2);
+  value += __shfl_xor(value, 4);
+  value += __shfl_xor(value, 8);
+  return value;
+}
+
+// Block-wide sum for blockDim.x <= 1024 (all threads receive the result).
+__device__ float block_sum(float value, float* scratch) {
+  value = wave_sum(value);
+  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch[wave] = value;
+  __syncthreads();
+  float total = 0.0F;
+  for (unsigned w = 0; w < waves; ++w) total += scratch[w];
+  return total;
+}
+
+// One wave quantizes 128 fp16 values (two per lane) to A4G128 exactly as
+// quantize_activation_i4 (lowbit_gemv.hip:373-407) does.
+__device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_t* codes,
+                                                  __half* scale_out, unsigned lane) {
+  const float x0 = __half2float(x0h), x1 = __half2float(x1h);
+  const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  const __half scale16 = __float2half(maximum == 0.0F ? 1.0F : maximum / 7.0F);
+  const float scale = __half2float(scale16);
+  const int low = max(-7, min(7, __float2int_rn(x0 / scale)));
+  const int high = max(-7, min(7, __float2int_rn(x1 / scale)));
+  codes[lane] = static_cast<uint8_t>((low & 0x0f) | ((high & 0x0f) << 4));
+  if (lane == 0) *scale_out = scale16;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm family (qwen_ops.hip:31-106, 176-217).  One workgroup per row.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float norm_scale(const uint16_t* weight, std::size_t i, bool unit) {
+  float s = bf16_to_float(weight[i]);
+  return unit ? s + 1.0F : s;
+}
+
+// Mode 0: plain RMSNorm.  Mode 1: residual add (fp16 round) then RMSNorm of the
+// rounded sum.  Quantize: also (or only) emit A4 codes + scales of the output.
+template <bool Residual, bool Quantize>
+__global__ __launch_bounds__(256) void rms_norm_kernel(
+    const __half* __restrict__ input, const float* __restrict__ update,
+    __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
+    __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
+    uint32_t elements, float epsilon, bool unit_offset) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __half* row = reinterpret_cast<__half*>(smem);           // [elements] staged values
+  float* scratch = reinterpret_cast<float*>(smem + ((elements * 2 + 15) & ~15u));
+  const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
+  float square = 0.0F;
+  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
+    __half v = input[base + i];
+    if constexpr (Residual) {
+      v = __float2half(__half2float(v) + update[base + i]);
+      residual_out[base + i] = v;
+    }
+    row[i] = v;
+    const float f = __half2float(v);
+    square = fmaf(f, f, square);
+  }
+  const float total = block_sum(square, scratch);
+  const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
+  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
+    const __half n = __float2half(__half2float(row[i]) * inverse * norm_scale(weight, i, unit_offset));
+    row[i] = n;
+    if (output != nullptr) output[base + i] = n;
+  }
+  if constexpr (Quantize) {
+    __syncthreads();
+    const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const uint32_t groups = elements / 128u;
+    for (uint32_t g = wave; g < groups; g += waves) {
+      quantize_group_a4(row[g * 128u + 2u * lane], row[g * 128u + 2u * lane + 1u],
+                        codes + static_cast<std::size_t>(blockIdx.x) * (elements / 2) + g * 64u,
+                        scales + static_cast<std::size_t>(blockIdx.x) * groups + g, lane);
+    }
+  }
+}
+
+// qwen_ops.hip:65-106: two RMSNorms written side by side.
+__global__ __launch_bounds__(256) void dual_rms_norm_kernel(
+    const __half* __restrict__ left, const uint16_t* __restrict__ left_weight,
+    const __half* __restrict__ right, const uint16_t* __restrict__ right_weight,
+    __half* __restrict__ output, uint32_t elements, float epsilon, bool unit_offset) {
+  __shared__ float scratch[16];
+  const bool second = blockIdx.x != 0;
+  const __half* input = second ? right : left;
+  const uint16_t* weight = second ? right_weight : left_weight;
+  output += second ? elements : 0;
+  float square = 0.0F;
+  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
+    const float f = __half2float(input[i]);
+    square = fmaf(f, f, square);
+  }
+  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + epsilon);
+  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
+    output[i] = __float2half(__half2float(input[i]) * inverse * norm_scale(weight, i, unit_offset));
+  }
+}
+
+// qwen_ops.hip:108-163: fp16(silu(g) * u), then the A4 quantizer.  One wave per
+// (token, group of 128).
+template <bool Quantize>
+__global__ __launch_bounds__(256) void silu_multiply_kernel(
+    const float* __restrict__ gate, const float* __restrict__ up, __half* __restrict__ output,
+    uint8_t* __restrict__ codes, __half* __restrict__ scales, uint32_t columns, uint32_t total_groups) {
+  const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (linear >= total_groups) return;
+  const unsigned lane = threadIdx.x & 63u;
+  const uint32_t groups = columns / 128u;
+  const uint32_t token = linear / groups, group = linear - token * groups;
+  const std::size_t at = static_cast<std::size_t>(token) * columns + group * 128u + 2u * lane;
+  const float2 g = *reinterpret_cast<const float2*>(gate + at);
+  const float2 u = *reinterpret_cast<const float2*>(up + at);
+  const __half p0 = __float2half(silu(g.x) * u.x);
+  const __half p1 = __float2half(silu(g.y) * u.y);
+  if (output != nullptr) {
+    output[at] = p0;
+    output[at + 1] = p1;
+  }
+  if constexpr (Quantize) {
+    quantize_group_a4(p0, p1, codes + static_cast<std::size_t>(token) * (columns / 2) + group * 64u,
+                      scales + linear, lane);
+  }
+}
+
+__global__ void float_to_half_kernel(const float* __restrict__ in, __half* __restrict__ out,
+                                     std::size_t n) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __float2half(in[i]);
+}
+
+// ---------------------------------------------------------------------------
+// GDN causal depthwise conv (qwen_ops.hip:219-261).  Thread per channel.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void gdn_conv_kernel(
+    const float* __restrict__ projected, const uint16_t* __restrict__ weight,
+    const __half* __restrict__ initial_state, __half* __restrict__ final_state,
+    __half* __restrict__ output, __half* __restrict__ appended_log, uint32_t channels,
+    uint32_t tokens) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= channels) return;
+  __half state[4];
+  float w[4];
+#pragma unroll
+  for (int tap = 0; tap < 4; ++tap) {
+    state[tap] = initial_state[static_cast<std::size_t>(c) * 4 + tap];
+    w[tap] = bf16_to_float(weight[static_cast<std::size_t>(c) * 4 + tap]);
+  }
+  for (uint32_t t = 0; t < tokens; ++t) {
+    state[0] = state[1];
+    state[1] = state[2];
+    state[2] = state[3];
+    state[3] = __float2half(projected[static_cast<std::size_t>(t) * channels + c]);
+    if (appended_log != nullptr) appended_log[static_cast<std::size_t>(t) * channels + c] = state[3];
+    float conv = 0.0F;
+#pragma unroll
+    for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(state[tap]), w[tap], conv);
+    output[static_cast<std::size_t>(t) * channels + c] = __float2half(silu(conv));
+  }
+#pragma unroll
+  for (int tap = 0; tap < 4; ++tap) final_state[static_cast<std::size_t>(c) * 4 + tap] = state[tap];
+}
+
+// ---------------------------------------------------------------------------
+// GDN window recurrence (qwen_ops.hip:263-411), gfx950 layout.
+//
+// Workgroup = (value head h, block of 16 state columns); 256 threads = 4 waves x
+// (4 columns x 16 k-slices).  Lane (ks, col) holds the 8 state rows ks*8..ks*8+7
+// of its column in registers for the whole window, so each token costs two
+// 16-lane xor reductions and no barrier.  A prologue puts the normalized q/k
+// of every token, the per-token decay and beta, and the 16 value columns into
+// LDS; the state tile is loaded and stored through LDS so global accesses are
+// row-contiguous.  The unnormalized output o[t][h][v] goes to `mixed`; a second
+// kernel applies the head RMSNorm, weight and SiLU(z) gate.
+// ---------------------------------------------------------------------------
+
+constexpr unsigned kGdnD = 128;      // head size (both key and value)
+constexpr unsigned kGdnCols = 16;    // state columns per workgroup
+constexpr unsigned kGdnMaxTokens = 32;
+
+struct GdnArgs {
+  const __half* qkv;        // conv output [T][2*Hk*D + Hv*D]
+  const float* a;           // [T][Hv]
+  const float* b;           // [T][Hv]
+  const uint16_t* a_log;    // bf16 [Hv]
+  const uint16_t* dt_bias;  // bf16 [Hv]
+  const float* initial;     // [Hv][D][D]
+  float* final_state;       // [Hv][D][D]
+  float* mixed;             // [T][Hv*D] unnormalized output
+  float* key_log;           // [T][Hk*D] or null
+  float* delta_log;         // [T][Hv*D] or null
+  float* decay_log;         // [T][Hv] or null
+  uint32_t tokens;
+  uint32_t key_heads;
+  uint32_t value_heads;
+};
+
+__global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs args) {
+  constexpr unsigned D = kGdnD;
+  __shared__ float qn[kGdnMaxTokens][D];
+  __shared__ float kn[kGdnMaxTokens][D];
+  __shared__ float vv[kGdnMaxTokens][kGdnCols];
+  __shared__ float decay_s[kGdnMaxTokens];
+  __shared__ float beta_s[kGdnMaxTokens];
+  __shared__ float tile[D][kGdnCols + 1];
+
+  const unsigned blocks_per_head = D / kGdnCols;
+  const unsigned h = blockIdx.x / blocks_per_head;
+  const unsigned cb = blockIdx.x - h * blocks_per_head;
+  const unsigned ratio = args.value_heads / args.key_heads;
+  const unsigned kh = h / ratio;
+  const unsigned T = args.tokens;
+  const std::size_t key_elements = static_cast<std::size_t>(args.key_heads) * D;
+  const std::size_t value_elements = static_cast<std::size_t>(args.value_heads) * D;
+  const std::size_t stride = 2 * key_elements + value_elements;
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const bool log_keys = args.key_log != nullptr && (h % ratio) == 0 && cb == 0;
+
+  // Prologue (a): normalized q (with the 1/sqrt(D) query scale) and k per token.
+  const float query_scale = 0.08838834764831845F;  // 1/sqrt(128), qwen_ops.hip:325
+  for (unsigned t = wave; t < T; t += 4) {
+    const __half* row = args.qkv + static_cast<std::size_t>(t) * stride;
+    const float q0 = __half2float(row[kh * D + 2 * lane]);
+    const float q1 = __half2float(row[kh * D + 2 * lane + 1]);
+    const float k0 = __half2float(row[key_elements + kh * D + 2 * lane]);
+    const float k1 = __half2float(row[key_elements + kh * D + 2 * lane + 1]);
+    const float qs = wave_sum(q0 * q0 + q1 * q1);
+    const float ks = wave_sum(k0 * k0 + k1 * k1);
+    const float iq = rsqrtf(qs + 1.0e-6F) * query_scale;
+    const float ik = rsqrtf(ks + 1.0e-6F);
+    qn[t][2 * lane] = q0 * iq;
+    qn[t][2 * lane + 1] = q1 * iq;
+    kn[t][2 * lane] = k0 * ik;
+    kn[t][2 * lane + 1] = k1 * ik;
+    if (log_keys) {
+      float* kl = args.key_log + static_cast<std::size_t>(t) * key_elements + kh * D;
+      kl[2 * lane] = k0 * ik;
+      kl[2 * lane + 1] = k1 * ik;
+    }
+  }
+  // Prologue (b): decay and beta per token (qwen_ops.hip:342-349).
+  if (tid < T) {
+    const float a_value = args.a[static_cast<std::size_t>(tid) * args.value_heads + h] +
+                          bf16_to_float(args.dt_bias[h]);
+    const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
+    const float g = -expf(bf16_to_float(args.a_log[h])) * softplus;
+    const float decay = expf(g);
+    decay_s[tid] = decay;
+    beta_s[tid] = 1.0F / (1.0F + expf(-args.b[static_cast<std::size_t>(tid) * args.value_heads + h]));
+    if (args.decay_log != nullptr && cb == 0) {
+      args.decay_log[static_cast<std::size_t>(tid) * args.value_heads + h] = decay;
+    }
+  }
+  // Prologue (c): the 16 value columns of every token.
+  for (unsigned i = tid; i < T * kGdnCols; i += blockDim.x) {
+    const unsigned t = i / kGdnCols, c = i - t * kGdnCols;
+    vv[t][c] = __half2float(args.qkv[static_cast<std::size_t>(t) * stride + 2 * key_elements +
+                                     static_cast<std::size_t>(h) * D + cb * kGdnCols + c]);
+  }
+  // Prologue (d): state tile [D rows][16 columns], row-contiguous 64-byte reads.
+  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
+    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
+    tile[r][c4 * 4 + 0] = v[0];
+    tile[r][c4 * 4 + 1] = v[1];
+    tile[r][c4 * 4 + 2] = v[2];
+    tile[r][c4 * 4 + 3] = v[3];
+  }
+  __syncthreads();
+
+  const unsigned ks = lane & 15u;              // k-slice: rows ks*8 .. ks*8+7
+  const unsigned col = wave * 4u + (lane >> 4);  // column within the block
+  float S[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
+  const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
+
+  for (unsigned t = 0; t < T; ++t) {
+    const float decay = decay_s[t], beta = beta_s[t];
+    float kv[8], qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kv[i] = kn[t][ks * 8 + i];
+      qv[i] = qn[t][ks * 8 + i];
+    }
+    float memory = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = S[i] * decay;
+      memory = fmaf(S[i], kv[i], memory);
+    }
+    memory = row16_sum(memory);
+    const float delta = (vv[t][col] - memory) * beta;
+    float o = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = fmaf(kv[i], delta, S[i]);
+      o = fmaf(S[i], qv[i], o);
+    }
+    o = row16_sum(o);
+    if (ks == 0) {
+      args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
+      if (args.delta_log != nullptr) {
+        args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
+      }
+    }
+  }
+
+  // Epilogue: state back through the LDS tile, row-contiguous stores.
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tile[ks * 8 + i][col] = S[i];
+  __syncthreads();
+  float* final_state = args.final_state + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
+    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    f32x4 v = {tile[r][c4 * 4 + 0], tile[r][c4 * 4 + 1], tile[r][c4 * 4 + 2], tile[r][c4 * 4 + 3]};
+    *reinterpret_cast<f32x4*>(final_state + static_cast<std::size_t>(r) * D + c4 * 4) = v;
+  }
+}
+
+// Head RMSNorm * weight * SiLU(z) (qwen_ops.hip:386-409) of the mixed output,
+// optionally followed by the A4 quantizer (a head is exactly one 128 group).
+// One wave per (token, value head).
+template <bool Quantize>
+__global__ __launch_bounds__(256) void gdn_output_kernel(
+    const float* __restrict__ mixed, const float* __restrict__ z, const uint16_t* __restrict__ weight,
+    __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
+    uint32_t value_heads, uint32_t total) {
+  const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (linear >= total) return;
+  const unsigned lane = threadIdx.x & 63u;
+  const uint32_t t = linear / value_heads, h = linear - t * value_heads;
+  const std::size_t row = static_cast<std::size_t>(t) * value_heads * kGdnD + h * kGdnD;
+  const float2 o = *reinterpret_cast<const float2*>(mixed + row + 2 * lane);
+  const float inverse = rsqrtf(wave_sum(o.x * o.x + o.y * o.y) / static_cast<float>(kGdnD) + 1.0e-6F);
+  const float2 g = *reinterpret_cast<const float2*>(z + row + 2 * lane);
+  const __half r0 = __float2half(o.x * inverse * bf16_to_float(weight[2 * lane]) * silu(g.x));
+  const __half r1 = __float2half(o.y * inverse * bf16_to_float(weight[2 * lane + 1]) * silu(g.y));
+  if (output != nullptr) {
+    output[row + 2 * lane] = r0;
+    output[row + 2 * lane + 1] = r1;
+  }
+  if constexpr (Quantize) {
+    quantize_group_a4(r0, r1, codes + row / 2, scales + linear, lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefix rollback over all GDN layers (qwen_ops.hip:467-539): replay the first
+// `accepted` logged tokens onto the pre-window states with the forward pass's
+// exact fp32 operations (S = S * decay, then S = fmaf(k, delta, S)).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void gdn_restore_conv_kernel(
+    __half* __restrict__ states, const __half* __restrict__ logs, uint32_t channels,
+    uint32_t layers, uint32_t max_logged, uint32_t accepted) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<std::size_t>(layers) * channels) return;
+  const std::size_t layer = i / channels, c = i - layer * channels;
+  __half* s = states + i * 4;
+  const __half* log = logs + layer * max_logged * channels;
+  __half w[4] = {s[0], s[1], s[2], s[3]};
+  for (uint32_t t = 0; t < accepted; ++t) {
+    w[0] = w[1];
+    w[1] = w[2];
+    w[2] = w[3];
+    w[3] = log[static_cast<std::size_t>(t) * channels + c];
+  }
+  s[0] = w[0];
+  s[1] = w[1];
+  s[2] = w[2];
+  s[3] = w[3];
+}
+
+// Thread per four consecutive state columns of one row.
+__global__ __launch_bounds__(256) void gdn_restore_recurrent_kernel(
+    float* __restrict__ states, const float* __restrict__ key_logs, const float* __restrict__ delta_logs,
+    const float* __restrict__ decay_logs, uint32_t layers, uint32_t max_logged, uint32_t accepted,
+    uint32_t key_heads, uint32_t value_heads) {
+  constexpr unsigned D = kGdnD;
+  const std::size_t per_layer = static_cast<std::size_t>(value_heads) * D * (D / 4);
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= per_layer * layers) return;
+  const std::size_t layer = i / per_layer;
+  const std::size_t rem = i - layer * per_layer;
+  const unsigned h = static_cast<unsigned>(rem / (D * (D / 4)));
+  const unsigned k = static_cast<unsigned>((rem / (D / 4)) % D);
+  const unsigned v4 = static_cast<unsigned>(rem % (D / 4));
+  const unsigned kh = h / (value_heads / key_heads);
+  const std::size_t key_elements = static_cast<std::size_t>(key_heads) * D;
+  const std::size_t value_elements = static_cast<std::size_t>(value_heads) * D;
+  f32x4* s = reinterpret_cast<f32x4*>(states) + i;
+  f32x4 S = *s;
+  const float* key_log = key_logs + layer * max_logged * key_elements + static_cast<std::size_t>(kh) * D + k;
+  const float* delta_log = delta_logs + layer * max_logged * value_elements + static_cast<std::size_t>(h) * D + v4 * 4;
+  const float* decay_log = decay_logs + layer * max_logged * value_heads + h;
+  for (uint32_t t = 0; t < accepted; ++t) {
+    const float decay = decay_log[static_cast<std::size_t>(t) * value_heads];
+    const float key = key_log[static_cast<std::size_t>(t) * key_elements];
+    const f32x4 delta = *reinterpret_cast<const f32x4*>(delta_log + static_cast<std::size_t>(t) * value_elements);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      S[j] = S[j] * decay;
+      S[j] = fmaf(key, delta[j], S[j]);
+    }
+  }
+  *s = S;
+}
+
+// ---------------------------------------------------------------------------
+// Per-head RMSNorm(1 + w) + partial rotate-half RoPE for Q and K heads
+// (qwen_ops.hip:599-676).  One wave per (token, head); lane owns dims l, l+64.
+// ---------------------------------------------------------------------------
+
+struct RopeArgs {
+  const float* query_input;  // [T][Hq][query_stride]
+  const uint16_t* query_weight;
+  __half* query_output;      // [T][Hq][D]
+  const float* key_input;    // [T][Hkv][key_stride]
+  const uint16_t* key_weight;
+  __half* key_output;        // [T][Hkv][D]
+  uint32_t query_heads, query_stride, key_heads, key_stride, rotary, tokens;
+  uint64_t base_position;
+  const uint64_t* indirect_position;
+  float theta;
+};
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
+  constexpr unsigned D = 128;
+  const uint32_t heads = a.query_heads + a.key_heads;
+  const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (linear >= heads * a.tokens) return;
+  const unsigned lane = threadIdx.x & 63u;
+  const uint32_t t = linear / heads, local = linear - t * heads;
+  const bool is_key = local >= a.query_heads;
+  const uint32_t head = is_key ? local - a.query_heads : local;
+  const uint32_t count = is_key ? a.key_heads : a.query_heads;
+  const uint32_t stride = is_key ? a.key_stride : a.query_stride;
+  const float* in = (is_key ? a.key_input : a.query_input) + (static_cast<std::size_t>(t) * count + head) * stride;
+  const uint16_t* w = is_key ? a.key_weight : a.query_weight;
+  __half* out = (is_key ? a.key_output : a.query_output) + (static_cast<std::size_t>(t) * count + head) * D;
+  const uint64_t base = a.indirect_position != nullptr ? *a.indirect_position : a.base_position;
+  const float position = static_cast<float>(base + t);
+  const float x0 = in[lane], x1 = in[lane + 64];
+  const float inverse = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / static_cast<float>(D) + 1.0e-6F);
+  const float n0 = x0 * (inverse * (1.0F + bf16_to_float(w[lane])));
+  const float n1 = x1 * (inverse * (1.0F + bf16_to_float(w[lane + 64])));
+  float v0 = n0;
+  const unsigned half = a.rotary / 2;
+  // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.
+  const float partner = __shfl(n0, lane < half ? lane + half : lane - half);
+  if (lane < a.rotary) {
+    const unsigned fi = lane % half;
+    const float exponent = (2.0F * static_cast<float>(fi)) / static_cast<float>(a.rotary);
+    const float inverse_frequency = powf(a.theta, -exponent);
+    const float angle = position * inverse_frequency;
+    const float rotated = lane < half ? -partner : partner;
+    v0 = fmaf(n0, cosf(angle), rotated * sinf(angle));
+  }
+  out[lane] = __float2half(v0);
+  out[lane + 64] = __float2half(n1);
+}
+
+// K (fp16) and V (fp32 -> fp16) rows into the contiguous cache at the (device)
+// position (qwen_ops.hip:678-696).
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const __half* __restrict__ key, const float* __restrict__ value, __half* __restrict__ key_cache,
+    __half* __restrict__ value_cache, uint64_t position, const uint64_t* __restrict__ indirect,
+    uint32_t elements, uint32_t tokens) {
+  if (indirect != nullptr) position = *indirect;
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<std::size_t>(tokens) * elements) return;
+  const std::size_t at = position * elements + i;
+  key_cache[at] = key[i];
+  value_cache[at] = __float2half(value[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax per row, ties -> lowest index (qwen_ops.hip:768-807), optional
+// id remap.  One 256-thread workgroup per row.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(
+    const float* __restrict__ logits, const uint32_t* __restrict__ token_ids, uint32_t* __restrict__ out,
+    uint32_t vocabulary, std::size_t stride) {
+  __shared__ float best_value[4];
+  __shared__ uint32_t best_index[4];
+  const float* row = logits + static_cast<std::size_t>(blockIdx.x) * stride;
+  float bv = -INFINITY;
+  uint32_t bi = 0;
+  for (uint32_t i = threadIdx.x; i < vocabulary; i += blockDim.x) {
+    const float v = row[i];
+    if (v > bv) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) {
+    const float ov = __shfl_xor(bv, offset);
+    const uint32_t oi = __shfl_xor(bi, offset);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    best_value[wave] = bv;
+    best_index[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (unsigned w = 1; w < blockDim.x / 64; ++w) {
+      if (better(best_value[w], best_index[w], bv, bi)) {
+        bv = best_value[w];
+        bi = best_index[w];
+      }
+    }
+    out[blockIdx.x] = token_ids != nullptr ? token_ids[bi] : bi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers
+// ---------------------------------------------------------------------------
+
+bool valid_epsilon(float epsilon) { return std::isfinite(epsilon) && epsilon > 0.0F; }
+
+int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_t* input,
+                   const float* update, uint16_t* residual_out, const uint16_t* weight,
+                   uint16_t* output, uint8_t* codes, uint16_t* scales, std::size_t elements,
+                   uint32_t batch, float epsilon, bool unit, hipStream_t stream) {
+  if (input == nullptr || weight == nullptr || elements == 0 || batch == 0 ||
+      !valid_epsilon(epsilon) || elements > (1u << 20) ||
+      (residual && (update == nullptr || residual_out == nullptr)) ||
+      (!quantize && output == nullptr) ||
+      (quantize && (codes == nullptr || scales == nullptr || elements % 128 != 0))) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string("invalid ") + name + " arguments");
+  }
+  const auto e = static_cast<uint32_t>(elements);
+  const std::size_t smem = ((e * 2 + 15) & ~15u) + 64;
+  auto* in = reinterpret_cast<const __half*>(input);
+  auto* ro = reinterpret_cast<__half*>(residual_out);
+  auto* out = reinterpret_cast<__half*>(output);
+  auto* sc = reinterpret_cast<__half*>(scales);
+  if (residual && quantize) {
+    hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(batch), dim3(256), smem, stream, in, update, ro,
+                       weight, out, codes, sc, e, epsilon, unit);
+  } else if (residual) {
+    hipLaunchKernelGGL((rms_norm_kernel<true, false>), dim3(batch), dim3(256), smem, stream, in, update, ro,
+                       weight, out, codes, sc, e, epsilon, unit);
+  } else if (quantize) {
+    hipLaunchKernelGGL((rms_norm_kernel<false, true>), dim3(batch), dim3(256), smem, stream, in, update, ro,
+                       weight, out, codes, sc, e, epsilon, unit);
+  } else {
+    hipLaunchKernelGGL((rms_norm_kernel<false, false>), dim3(batch), dim3(256), smem, stream, in, update,
+                       ro, weight, out, codes, sc, e, epsilon, unit);
+  }
+  return launch_status((std::string(name) + " launch failed").c_str());
+}
+
+}  // namespace
+}  // namespace gfx950
+
+using namespace gfx950;
+
+// ---- norms ------------------------------------------------------------------
+
+extern "C" int32_t gfxinfer_launch_rms_norm(const uint16_t* input, const uint16_t* bf16_weight,
+                                            uint16_t* output, size_t elements, float epsilon,
+                                            int32_t add_unit_offset, void* stream) {
+  return norm_entry("RMSNorm", false, false, input, nullptr, nullptr, bf16_weight, output, nullptr,
+                    nullptr, elements, 1, epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_rms_norm_batch(const uint16_t* input, const uint16_t* bf16_weight,
+                                                  uint16_t* output, size_t elements, uint32_t batch,
+                                                  float epsilon, int32_t add_unit_offset,
+                                                  void* stream) {
+  return norm_entry("batched RMSNorm", false, false, input, nullptr, nullptr, bf16_weight, output,
+                    nullptr, nullptr, elements, batch, epsilon, add_unit_offset != 0,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_residual_add_rms_norm_batch(
+    const uint16_t* residual, const float* update, uint16_t* residual_output,
+    const uint16_t* bf16_weight, uint16_t* normalized_output, size_t elements, uint32_t batch,
+    float epsilon, int32_t add_unit_offset, void* stream) {
+  return norm_entry("fused residual/RMSNorm", true, false, residual, update, residual_output,
+                    bf16_weight, normalized_output, nullptr, nullptr, elements, batch, epsilon,
+                    add_unit_offset != 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_rms_norm_quantize_i4(const uint16_t* input,
+                                                        const uint16_t* bf16_weight,
+                                                        uint16_t* normalized_output,
+                                                        uint8_t* packed_output, uint16_t* scales,
+                                                        size_t elements, uint32_t batch,
+                                                        float epsilon, int32_t add_unit_offset,
+                                                        void* stream) {
+  return norm_entry("RMSNorm/A4", false, true, input, nullptr, nullptr, bf16_weight,
+                    normalized_output, packed_output, scales, elements, batch, epsilon,
+                    add_unit_offset != 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4(
+    const uint16_t* residual, const float* update, uint16_t* residual_output,
+    const uint16_t* bf16_weight, uint16_t* normalized_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, uint32_t batch, float epsilon, int32_t add_unit_offset,
+    void* stream) {
+  return norm_entry("fused residual/RMSNorm/A4", true, true, residual, update, residual_output,
+                    bf16_weight, normalized_output, packed_output, scales, elements, batch,
+                    epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
+    const uint16_t* left, const uint16_t* left_bf16_weight, const uint16_t* right,
+    const uint16_t* right_bf16_weight, uint16_t* concatenated_output, size_t elements,
+    float epsilon, int32_t add_unit_offset, void* stream) {
+  if (left == nullptr || left_bf16_weight == nullptr || right == nullptr ||
+      right_bf16_weight == nullptr || concatenated_output == nullptr || elements == 0 ||
+      elements > (1u << 30) || !valid_epsilon(epsilon)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid dual RMSNorm/concat arguments");
+  }
+  hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const __half*>(left), left_bf16_weight,
+                     reinterpret_cast<const __half*>(right), right_bf16_weight,
+                     reinterpret_cast<__half*>(concatenated_output), static_cast<uint32_t>(elements),
+                     epsilon, add_unit_offset != 0);
+  return launch_status("dual RMSNorm/concat launch failed");
+}
+
+// ---- SwiGLU -----------------------------------------------------------------
+
+extern "C" int32_t gfxinfer_launch_silu_multiply_quantize_i4(const float* gate, const float* up,
+                                                             uint8_t* packed_output,
+                                                             uint16_t* scales,
+                                                             size_t elements_per_row,
+                                                             uint32_t batch, void* stream) {
+  if (gate == nullptr || up == nullptr || packed_output == nullptr || scales == nullptr ||
+      elements_per_row == 0 || elements_per_row % 128 != 0 || batch == 0 || batch > 32 ||
+      elements_per_row > (1u << 30)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid fused SiLU/A4 quantization arguments");
+  }
+  const auto columns = static_cast<uint32_t>(elements_per_row);
+  const uint32_t total = columns / 128 * batch;
+  hipLaunchKernelGGL(silu_multiply_kernel<true>, dim3((total + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), gate, up, nullptr, packed_output,
+                     reinterpret_cast<__half*>(scales), columns, total);
+  return launch_status("fused SiLU/A4 quantization launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_silu_multiply(const float* gate, const float* up,
+                                                 uint16_t* output, size_t elements,
+                                                 void* stream) {
+  if (gate == nullptr || up == nullptr || output == nullptr || elements == 0 ||
+      elements % 128 != 0 || elements > (1u << 30)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid SiLU multiply arguments (elements must be a "
+                                       "nonzero multiple of 128)");
+  }
+  const auto columns = static_cast<uint32_t>(elements);
+  const uint32_t total = columns / 128;
+  hipLaunchKernelGGL(silu_multiply_kernel<false>, dim3((total + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), gate, up, reinterpret_cast<__half*>(output),
+                     nullptr, nullptr, columns, total);
+  return launch_status("SiLU multiply launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_float_to_half(const float* input, uint16_t* output,
+                                                 size_t elements, void* stream) {
+  if (input == nullptr || output == nullptr || elements == 0) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid float-to-half arguments");
+  }
+  hipLaunchKernelGGL(float_to_half_kernel, dim3(static_cast<unsigned>((elements + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), input,
+                     reinterpret_cast<__half*>(output), elements);
+  return launch_status("float-to-half launch failed");
+}
+
+// ---- GDN ----------------------------------------------------------------------
+
+extern "C" int32_t gfxinfer_launch_gdn_conv_update_block(
+    const float* projected_qkv, const uint16_t* bf16_conv_weight, const uint16_t* initial_conv_state,
+    uint16_t* final_conv_state, uint16_t* convolved_qkv, uint16_t* appended_log, size_t channels,
+    uint32_t batch, void* stream) {
+  if (projected_qkv == nullptr || bf16_conv_weight == nullptr || initial_conv_state == nullptr ||
+      final_conv_state == nullptr || convolved_qkv == nullptr || channels == 0 || batch == 0 ||
+      channels > (1u << 30)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid block GDN convolution arguments");
+  }
+  const auto c = static_cast<uint32_t>(channels);
+  hipLaunchKernelGGL(gdn_conv_kernel, dim3((c + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), projected_qkv, bf16_conv_weight,
+                     reinterpret_cast<const __half*>(initial_conv_state),
+                     reinterpret_cast<__half*>(final_conv_state), reinterpret_cast<__half*>(convolved_qkv),
+                     reinterpret_cast<__half*>(appended_log), c, batch);
+  return launch_status("block GDN convolution update launch failed");
+}
+
+namespace {
+int32_t gdn_check(const char* name, uint32_t batch, uint32_t key_heads, uint32_t value_heads,
+                  uint32_t head_size) {
+  if (batch == 0 || batch > kGdnMaxTokens || key_heads == 0 || value_heads == 0 ||
+      value_heads % key_heads != 0 || head_size != kGdnD) {
+    return fail(GFXI_INVALID_ARGUMENT,
+                std::string(name) + " requires 1..32 tokens, value heads a multiple of key heads "
+                                    "and head size 128");
+  }
+  return GFXI_OK;
+}
+}  // namespace
+
+extern "C" int32_t gfxinfer_launch_gdn_recurrent_decode_block(
+    const uint16_t* convolved_qkv, const float* projected_z, const float* projected_a,
+    const float* projected_b, const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias,
+    const uint16_t* bf16_norm_weight, const float* initial_recurrent_state,
+    float* final_recurrent_state, uint16_t* output, float* key_log, float* delta_log,
+    float* decay_log, uint32_t batch, uint32_t key_heads, uint32_t value_heads,
+    uint32_t head_size, float* mixed_workspace, void* stream) {
+  if (convolved_qkv == nullptr || projected_z == nullptr || projected_a == nullptr ||
+      projected_b == nullptr || bf16_a_log == nullptr || bf16_dt_bias == nullptr ||
+      bf16_norm_weight == nullptr || initial_recurrent_state == nullptr ||
+      final_recurrent_state == nullptr || output == nullptr || mixed_workspace == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid block GDN recurrent decode arguments");
+  }
+  if (const int32_t s = gdn_check("block GDN recurrent decode", batch, key_heads, value_heads, head_size);
+      s != GFXI_OK) {
+    return s;
+  }
+  auto st = static_cast<hipStream_t>(stream);
+  GdnArgs args{reinterpret_cast<const __half*>(convolved_qkv), projected_a, projected_b, bf16_a_log,
+               bf16_dt_bias, initial_recurrent_state, final_recurrent_state, mixed_workspace,
+               key_log, delta_log, decay_log, batch, key_heads, value_heads};
+  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(256), 0, st, args);
+  if (const int32_t s = launch_status("block GDN recurrent decode launch failed"); s != GFXI_OK) return s;
+  const uint32_t total = batch * value_heads;
+  hipLaunchKernelGGL(gdn_output_kernel<false>, dim3((total + 3) / 4), dim3(256), 0, st,
+                     mixed_workspace, projected_z, bf16_norm_weight, reinterpret_cast<__half*>(output),
+                     nullptr, nullptr, value_heads, total);
+  return launch_status("block GDN output norm launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_gdn_output_quantize_i4(
+    const float* mixed, const float* projected_z, const uint16_t* bf16_norm_weight,
+    uint16_t* output, uint8_t* packed_output, uint16_t* scales, uint32_t batch,
+    uint32_t value_heads, uint32_t head_size, void* stream) {
+  if (mixed == nullptr || projected_z == nullptr || bf16_norm_weight == nullptr ||
+      packed_output == nullptr || scales == nullptr || batch == 0 || batch > kGdnMaxTokens ||
+      value_heads == 0 || head_size != kGdnD) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid GDN output/A4 arguments");
+  }
+  const uint32_t total = batch * value_heads;
+  hipLaunchKernelGGL(gdn_output_kernel<true>, dim3((total + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), mixed, projected_z, bf16_norm_weight,
+                     reinterpret_cast<__half*>(output), packed_output, reinterpret_cast<__half*>(scales),
+                     value_heads, total);
+  return launch_status("GDN output/A4 launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_gdn_recurrent_window(
+    const uint16_t* convolved_qkv, const float* projected_a, const float* projected_b,
+    const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias, const float* initial_recurrent_state,
+    float* final_recurrent_state, float* mixed, float* key_log, float* delta_log, float* decay_log,
+    uint32_t batch, uint32_t key_heads, uint32_t value_heads, uint32_t head_size, void* stream) {
+  if (convolved_qkv == nullptr || projected_a == nullptr || projected_b == nullptr ||
+      bf16_a_log == nullptr || bf16_dt_bias == nullptr || initial_recurrent_state == nullptr ||
+      final_recurrent_state == nullptr || mixed == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid GDN recurrent window arguments");
+  }
+  if (const int32_t s = gdn_check("GDN recurrent window", batch, key_heads, value_heads, head_size);
+      s != GFXI_OK) {
+    return s;
+  }
+  GdnArgs args{reinterpret_cast<const __half*>(convolved_qkv), projected_a, projected_b, bf16_a_log,
+               bf16_dt_bias, initial_recurrent_state, final_recurrent_state, mixed, key_log,
+               delta_log, decay_log, batch, key_heads, value_heads};
+  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), args);
+  return launch_status("GDN recurrent window launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_gdn_restore_prefix_all(
+    uint16_t* conv_states, float* recurrent_states, const uint16_t* appended_logs,
+    const float* key_logs, const float* delta_logs, const float* decay_logs, size_t channels,
+    uint32_t layer_count, uint32_t maximum_logged_tokens, uint32_t accepted_tokens,
+    uint32_t key_heads, uint32_t value_heads, uint32_t head_size, void* stream) {
+  if (conv_states == nullptr || recurrent_states == nullptr || appended_logs == nullptr ||
+      key_logs == nullptr || delta_logs == nullptr || decay_logs == nullptr || channels == 0 ||
+      layer_count == 0 || maximum_logged_tokens == 0 || accepted_tokens == 0 ||
+      accepted_tokens > maximum_logged_tokens || channels > (1u << 24) || key_heads == 0 ||
+      value_heads == 0 || value_heads % key_heads != 0 || head_size != kGdnD) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid all-layer GDN prefix restore arguments");
+  }
+  auto st = static_cast<hipStream_t>(stream);
+  const std::size_t conv_threads = static_cast<std::size_t>(layer_count) * channels;
+  hipLaunchKernelGGL(gdn_restore_conv_kernel, dim3(static_cast<unsigned>((conv_threads + 255) / 256)),
+                     dim3(256), 0, st, reinterpret_cast<__half*>(conv_states),
+                     reinterpret_cast<const __half*>(appended_logs), static_cast<uint32_t>(channels),
+                     layer_count, maximum_logged_tokens, accepted_tokens);
+  if (const int32_t s = launch_status("all-layer GDN convolution prefix restore launch failed"); s != GFXI_OK) {
+    return s;
+  }
+  const std::size_t threads = static_cast<std::size_t>(layer_count) * value_heads * kGdnD * (kGdnD / 4);
+  hipLaunchKernelGGL(gdn_restore_recurrent_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, st, recurrent_states, key_logs, delta_logs, decay_logs, layer_count,
+                     maximum_logged_tokens, accepted_tokens, key_heads, value_heads);
+  return launch_status("all-layer GDN recurrent prefix restore launch failed");
+}
+
+// ---- attention helpers ----------------------------------------------------------
+
+namespace {
+int32_t rope_entry(const float* query_input, const uint16_t* query_weight, uint16_t* query_output,
+                   size_t query_heads, size_t query_stride, const float* key_input,
+                   const uint16_t* key_weight, uint16_t* key_output, size_t key_heads,
+                   size_t key_stride, size_t head_size, size_t rotary, uint64_t base,
+                   const uint64_t* indirect, uint32_t batch, float theta, hipStream_t stream) {
+  if (query_input == nullptr || query_weight == nullptr || query_output == nullptr ||
+      key_input == nullptr || key_weight == nullptr || key_output == nullptr || query_heads == 0 ||
+      key_heads == 0 || head_size != 128 || rotary == 0 || rotary > 64 || rotary % 2 != 0 ||
+      query_stride < head_size || key_stride < head_size || batch == 0 || !std::isfinite(theta) ||
+      theta <= 0.0F || query_heads > 4096 || key_heads > 4096) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid Q/K RMSNorm/RoPE arguments (head size 128, even "
+                                       "rotary size <= 64)");
+  }
+  RopeArgs a{query_input, query_weight, reinterpret_cast<__half*>(query_output), key_input, key_weight,
+             reinterpret_cast<__half*>(key_output), static_cast<uint32_t>(query_heads),
+             static_cast<uint32_t>(query_stride), static_cast<uint32_t>(key_heads),
+             static_cast<uint32_t>(key_stride), static_cast<uint32_t>(rotary), batch, base, indirect,
+             theta};
+  const uint32_t waves = static_cast<uint32_t>(query_heads + key_heads) * batch;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, a);
+  return launch_status("Q/K RMSNorm/RoPE launch failed");
+}
+
+int32_t kv_entry(const uint16_t* key, const float* value, uint16_t* key_cache, uint16_t* value_cache,
+                 uint64_t position, const uint64_t* indirect, size_t capacity, uint32_t batch,
+                 size_t kv_elements, hipStream_t stream) {
+  if (key == nullptr || value == nullptr || key_cache == nullptr || value_cache == nullptr ||
+      batch == 0 || kv_elements == 0 || kv_elements > (1u << 24) ||
+      (indirect == nullptr && position + batch > capacity)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid block KV append arguments");
+  }
+  const std::size_t n = static_cast<std::size_t>(batch) * kv_elements;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<const __half*>(key), value, reinterpret_cast<__half*>(key_cache),
+                     reinterpret_cast<__half*>(value_cache), position, indirect,
+                     static_cast<uint32_t>(kv_elements), batch);
+  return launch_status("block KV append launch failed");
+}
+}  // namespace
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_block(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, uint64_t base_position,
+    uint32_t batch, float rope_theta, void* stream) {
+  return rope_entry(query_input, query_bf16_weight, query_output, query_head_count, query_input_stride,
+                    key_input, key_bf16_weight, key_output, key_head_count, key_input_stride, head_size,
+                    rotary_size, base_position, nullptr, batch, rope_theta,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size,
+    const uint64_t* base_position, uint32_t batch, float rope_theta, void* stream) {
+  if (base_position == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect position is null");
+  return rope_entry(query_input, query_bf16_weight, query_output, query_head_count, query_input_stride,
+                    key_input, key_bf16_weight, key_output, key_head_count, key_input_stride, head_size,
+                    rotary_size, 0, base_position, batch, rope_theta, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_kv_append_block(const uint16_t* key, const float* value,
+                                                   uint16_t* key_cache, uint16_t* value_cache,
+                                                   size_t position, size_t capacity,
+                                                   uint32_t batch, size_t kv_elements,
+                                                   void* stream) {
+  return kv_entry(key, value, key_cache, value_cache, position, nullptr, capacity, batch, kv_elements,
+                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_kv_append_block_indirect_position(
+    const uint16_t* key, const float* value, uint16_t* key_cache, uint16_t* value_cache,
+    const uint64_t* position, size_t capacity, uint32_t batch, size_t kv_elements, void* stream) {
+  if (position == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect position is null");
+  return kv_entry(key, value, key_cache, value_cache, 0, position, capacity, batch, kv_elements,
+                  static_cast<hipStream_t>(stream));
+}
+
+// ---- argmax -------------------------------------------------------------------------
+
+extern "C" int32_t gfxinfer_launch_argmax_batch(const float* logits, uint32_t* tokens,
+                                                size_t vocabulary_size, size_t row_stride,
+                                                uint32_t batch, void* stream) {
+  if (logits == nullptr || tokens == nullptr || vocabulary_size == 0 || row_stride < vocabulary_size ||
+      batch == 0 || vocabulary_size > 0xffffffffu) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid batched argmax arguments");
+  }
+  hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     logits, nullptr, tokens, static_cast<uint32_t>(vocabulary_size), row_stride);
+  return launch_status("batched argmax launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_argmax_mapped(const float* logits, const uint32_t* token_ids,
+                                                 uint32_t* token, size_t vocabulary_size,
+                                                 void* stream) {
+  if (logits == nullptr || token_ids == nullptr || token == nullptr || vocabulary_size == 0 ||
+      vocabulary_size > 0xffffffffu) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid mapped argmax arguments");
+  }
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), logits,
+                     token_ids, token, static_cast<uint32_t>(vocabulary_size), vocabulary_size);
+  return launch_status("mapped argmax launch failed");
+}

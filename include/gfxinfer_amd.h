@@ -166,6 +166,175 @@ int32_t gfxinfer_launch_lowbit_row_gather_tiled_indirect(int32_t format,
                                                          size_t rows, size_t columns,
                                                          void* stream);
 
+
+/* ---- decoder operators: src/kernels/qwen_ops.hip -------------------------- */
+
+/* qwen_ops.h:14-21 launch_rms_norm: fp16 row -> fp16(x * rsqrt(mean(x^2) + eps) * (w [+1])). */
+int32_t gfxinfer_launch_rms_norm(const uint16_t* input, const uint16_t* bf16_weight,
+                                 uint16_t* output, size_t elements, float epsilon,
+                                 int32_t add_unit_offset, void* stream);
+
+/* qwen_ops.h:23-31 launch_rms_norm_batch: one row per token. */
+int32_t gfxinfer_launch_rms_norm_batch(const uint16_t* input, const uint16_t* bf16_weight,
+                                       uint16_t* output, size_t elements, uint32_t batch,
+                                       float epsilon, int32_t add_unit_offset, void* stream);
+
+/* qwen_ops.h:70-81 launch_residual_add_rms_norm_batch: r = fp16(res + upd) is written to
+ * residual_output and RMS-normalized into normalized_output. */
+int32_t gfxinfer_launch_residual_add_rms_norm_batch(const uint16_t* residual, const float* update,
+                                                    uint16_t* residual_output,
+                                                    const uint16_t* bf16_weight,
+                                                    uint16_t* normalized_output, size_t elements,
+                                                    uint32_t batch, float epsilon,
+                                                    int32_t add_unit_offset, void* stream);
+
+/* RMSNorm fused with the A4G128 quantizer of its fp16 output (codes [batch, elements/2],
+ * scales [batch, elements/128]); normalized_output may be NULL.  No reference
+ * counterpart: the reference runs launch_rms_norm_batch then
+ * launch_quantize_activation_i4 (qwen_runtime.cpp:116-127); the codes are identical. */
+int32_t gfxinfer_launch_rms_norm_quantize_i4(const uint16_t* input, const uint16_t* bf16_weight,
+                                             uint16_t* normalized_output, uint8_t* packed_output,
+                                             uint16_t* scales, size_t elements, uint32_t batch,
+                                             float epsilon, int32_t add_unit_offset, void* stream);
+
+/* Residual add + RMSNorm + A4G128 quantizer in one kernel; same codes as
+ * launch_residual_add_rms_norm_batch followed by launch_quantize_activation_i4. */
+int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4(
+    const uint16_t* residual, const float* update, uint16_t* residual_output,
+    const uint16_t* bf16_weight, uint16_t* normalized_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, uint32_t batch, float epsilon, int32_t add_unit_offset,
+    void* stream);
+
+/* qwen_ops.h:33-42 launch_dual_rms_norm_concat: [norm(left) | norm(right)]. */
+int32_t gfxinfer_launch_dual_rms_norm_concat(const uint16_t* left, const uint16_t* left_bf16_weight,
+                                             const uint16_t* right,
+                                             const uint16_t* right_bf16_weight,
+                                             uint16_t* concatenated_output, size_t elements,
+                                             float epsilon, int32_t add_unit_offset, void* stream);
+
+/* qwen_ops.h:44-49 launch_silu_multiply: fp16(silu(g) * u); elements % 128 == 0. */
+int32_t gfxinfer_launch_silu_multiply(const float* gate, const float* up, uint16_t* output,
+                                      size_t elements, void* stream);
+
+/* qwen_ops.h:51-61 launch_silu_multiply_quantize_i4. */
+int32_t gfxinfer_launch_silu_multiply_quantize_i4(const float* gate, const float* up,
+                                                  uint8_t* packed_output, uint16_t* scales,
+                                                  size_t elements_per_row, uint32_t batch,
+                                                  void* stream);
+
+/* qwen_ops.h launch_float_to_half (qwen_ops.hip:809-815). */
+int32_t gfxinfer_launch_float_to_half(const float* input, uint16_t* output, size_t elements,
+                                      void* stream);
+
+/* qwen_ops.h launch_gdn_conv_update_block (qwen_ops.hip:1020-1047): 4-tap causal conv + SiLU
+ * over `batch` tokens; fp16 states [channels, 4]; appended_log [batch, channels] may be NULL. */
+int32_t gfxinfer_launch_gdn_conv_update_block(const float* projected_qkv,
+                                              const uint16_t* bf16_conv_weight,
+                                              const uint16_t* initial_conv_state,
+                                              uint16_t* final_conv_state, uint16_t* convolved_qkv,
+                                              uint16_t* appended_log, size_t channels,
+                                              uint32_t batch, void* stream);
+
+/* qwen_ops.h launch_gdn_recurrent_decode_block (qwen_ops.hip:1076-1107): gated delta rule over a
+ * window of batch <= 32 tokens.  Head counts are parameters (the reference hard-codes 48/16);
+ * head_size must be 128.  States fp32 [value_heads, 128, 128] (row k, column v).  Logs:
+ * key [batch, key_heads*128], delta [batch, value_heads*128], decay [batch, value_heads], any
+ * may be NULL.  mixed_workspace: fp32 [batch, value_heads*128] scratch for the pre-norm output
+ * (the reference has no such argument: its one-block-per-head kernel normalizes in place). */
+int32_t gfxinfer_launch_gdn_recurrent_decode_block(
+    const uint16_t* convolved_qkv, const float* projected_z, const float* projected_a,
+    const float* projected_b, const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias,
+    const uint16_t* bf16_norm_weight, const float* initial_recurrent_state,
+    float* final_recurrent_state, uint16_t* output, float* key_log, float* delta_log,
+    float* decay_log, uint32_t batch, uint32_t key_heads, uint32_t value_heads,
+    uint32_t head_size, float* mixed_workspace, void* stream);
+
+/* The two halves of gfxinfer_launch_gdn_recurrent_decode_block for callers that fuse the
+ * out-projection's A4 quantization: the window recurrence writing the pre-norm output, and the
+ * head RMSNorm * weight * SiLU(z) -> fp16 -> A4G128 step (a 128-wide head is one group). */
+int32_t gfxinfer_launch_gdn_recurrent_window(
+    const uint16_t* convolved_qkv, const float* projected_a, const float* projected_b,
+    const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias, const float* initial_recurrent_state,
+    float* final_recurrent_state, float* mixed, float* key_log, float* delta_log, float* decay_log,
+    uint32_t batch, uint32_t key_heads, uint32_t value_heads, uint32_t head_size, void* stream);
+int32_t gfxinfer_launch_gdn_output_quantize_i4(const float* mixed, const float* projected_z,
+                                               const uint16_t* bf16_norm_weight, uint16_t* output,
+                                               uint8_t* packed_output, uint16_t* scales,
+                                               uint32_t batch, uint32_t value_heads,
+                                               uint32_t head_size, void* stream);
+
+/* qwen_ops.h launch_gdn_restore_prefix_all (qwen_ops.hip:1141-1179): replay the first
+ * accepted_tokens (1..maximum_logged_tokens) logged tokens of every layer onto the pre-window
+ * conv and recurrent states, bit-identical to running only those tokens.  Logs are
+ * [layer][maximum_logged_tokens][...]. */
+int32_t gfxinfer_launch_gdn_restore_prefix_all(
+    uint16_t* conv_states, float* recurrent_states, const uint16_t* appended_logs,
+    const float* key_logs, const float* delta_logs, const float* decay_logs, size_t channels,
+    uint32_t layer_count, uint32_t maximum_logged_tokens, uint32_t accepted_tokens,
+    uint32_t key_heads, uint32_t value_heads, uint32_t head_size, void* stream);
+
+/* qwen_ops.h:179-195 launch_qk_rms_norm_rope_block: per-head RMSNorm(1+w) and partial
+ * rotate-half RoPE of the first rotary_size dims at positions base+t.  head_size 128,
+ * rotary_size even and <= 64. */
+int32_t gfxinfer_launch_qk_rms_norm_rope_block(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, uint64_t base_position,
+    uint32_t batch, float rope_theta, void* stream);
+
+/* qwen_ops.h:197-215: base position read from device memory (graph-capture variant). */
+int32_t gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size,
+    const uint64_t* base_position, uint32_t batch, float rope_theta, void* stream);
+
+/* qwen_ops.h launch_kv_append_block: K (fp16) and V (fp32 -> fp16) rows of `batch` tokens into
+ * caches [capacity][kv_elements] at position..position+batch-1. */
+int32_t gfxinfer_launch_kv_append_block(const uint16_t* key, const float* value,
+                                        uint16_t* key_cache, uint16_t* value_cache,
+                                        size_t position, size_t capacity, uint32_t batch,
+                                        size_t kv_elements, void* stream);
+int32_t gfxinfer_launch_kv_append_block_indirect_position(
+    const uint16_t* key, const float* value, uint16_t* key_cache, uint16_t* value_cache,
+    const uint64_t* position, size_t capacity, uint32_t batch, size_t kv_elements, void* stream);
+
+/* qwen_ops.h launch_argmax_batch (qwen_ops.hip:1496-1514): per-row argmax over the first
+ * vocabulary_size logits of stride row_stride; ties go to the lowest index. */
+int32_t gfxinfer_launch_argmax_batch(const float* logits, uint32_t* tokens, size_t vocabulary_size,
+                                     size_t row_stride, uint32_t batch, void* stream);
+
+/* qwen_ops.h launch_argmax_mapped: token = token_ids[argmax] (MTP shortlist). */
+int32_t gfxinfer_launch_argmax_mapped(const float* logits, const uint32_t* token_ids,
+                                      uint32_t* token, size_t vocabulary_size, void* stream);
+
+
+/* ---- verify attention: src/kernels/qwen_ops.hip:698-766 --------------------- */
+
+/* Bytes of fp32 workspace gfxinfer_launch_gated_attention_decode_block needs. */
+size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, size_t capacity);
+
+/* qwen_ops.h:256-265 launch_gated_attention_decode_block: causal GQA decode attention of a
+ * block of batch <= 32 tokens; token t sees the first base_token_count + t cached positions.
+ * query fp16 [batch, q_heads, 128]; gate fp32 [batch, q_heads, 256] (second half of each head
+ * row); caches fp16 [capacity, kv_heads, 128]; output fp16 [batch, q_heads, 128].  Head counts
+ * are parameters (the reference hard-codes 24/4 x 256).  workspace: split-local partial
+ * results, gfxinfer_attention_workspace_bytes() bytes (no reference counterpart: the
+ * reference walks the context serially inside one block). */
+int32_t gfxinfer_launch_gated_attention_decode_block(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, size_t base_token_count, size_t capacity, uint32_t batch, uint32_t q_heads,
+    uint32_t kv_heads, uint32_t head_size, float* workspace, size_t workspace_bytes, void* stream);
+
+/* qwen_ops.h:267-276: base_token_count = *base_position + 1 read from device memory. */
+int32_t gfxinfer_launch_gated_attention_decode_block_indirect_position(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, const uint64_t* base_position, size_t capacity, uint32_t batch,
+    uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

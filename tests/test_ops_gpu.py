@@ -1,0 +1,390 @@
+"""GPU parity of the decoder operators (gfxinfer_amd/csrc/qwen_ops.hip,
+attention.hip) against the CPU oracle, through the C ABI.
+
+Bars: copies and integer codes bit-exact; fp16 outputs within a few fp16 ulps;
+GDN state within fp32 1e-5 (relative to the state's magnitude); attention
+within 1e-2; rollback bit-exact against running only the accepted prefix.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import dev, empty, host, say
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def _half(x):
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def _f(h):
+    return np.asarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def _bf16(x):
+    x = np.asarray(x, dtype=np.float32)
+    return (x.view(np.uint32) >> 16).astype(np.uint16)  # truncation: exact for test values
+
+
+def _close16(got, want, rel=2.0 ** -9, atol=1e-6):
+    g, w = _f(got), _f(want)
+    return np.all(np.abs(g - w) <= rel * np.abs(w) + atol)
+
+
+# ---- norms --------------------------------------------------------------------
+
+@pytest.mark.parametrize("batch", [1, 5, 32])
+def test_rms_norm_batch_and_fused_quantize(device, gx, orc, batch):
+    n = 5120
+    rng = np.random.default_rng(batch)
+    x = _half(rng.standard_normal((batch, n)) * 2)
+    w = _bf16(np.round(rng.standard_normal(n) * 64) / 1024)
+    want = np.empty_like(x)
+    orc.lib().orc_rms_norm(orc.ptr(x), orc.ptr(w), orc.ptr(want), n, batch, EPS, 1)
+    out = empty((batch, n), np.uint16)
+    say("rms_norm_batch", batch)
+    L = gx.lib()
+    dx, dw = dev(x), dev(w)
+    gx.check(L.gfxinfer_launch_rms_norm_batch(dx.data_ptr(), dw.data_ptr(), out.data_ptr(), n, batch, EPS, 1, None))
+    got = host(out, np.uint16)
+    assert _close16(got, want)
+    # fused RMSNorm -> A4: the codes are exactly the A4 quantization of its own fp16 output
+    normed = empty((batch, n), np.uint16)
+    codes = empty((batch, n // 2), np.uint8)
+    scales = empty((batch, n // 128), np.uint16)
+    say("rms_norm_quantize_i4", batch)
+    gx.check(L.gfxinfer_launch_rms_norm_quantize_i4(dx.data_ptr(), dw.data_ptr(), normed.data_ptr(), codes.data_ptr(),
+                                                    scales.data_ptr(), n, batch, EPS, 1, None))
+    g_norm = host(normed, np.uint16)
+    assert np.array_equal(g_norm, got)
+    c, s = orc.quantize_activation_i4(g_norm)
+    assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
+
+
+@pytest.mark.parametrize("batch", [1, 5])
+def test_residual_add_rms_norm_and_fused_quantize(device, gx, orc, batch):
+    n = 5120
+    rng = np.random.default_rng(10 + batch)
+    res = _half(rng.standard_normal((batch, n)))
+    upd = rng.standard_normal((batch, n)).astype(np.float32)
+    w = _bf16(np.round(rng.standard_normal(n) * 64) / 1024)
+    want_r = np.empty_like(res)
+    want_n = np.empty_like(res)
+    orc.lib().orc_residual_add_rms_norm(orc.ptr(res), orc.ptr(upd), orc.ptr(want_r), orc.ptr(w), orc.ptr(want_n),
+                                        n, batch, EPS, 1)
+    L = gx.lib()
+    dr, du, dw = dev(res), dev(upd), dev(w)
+    ro, no = empty((batch, n), np.uint16), empty((batch, n), np.uint16)
+    say("residual_add_rms_norm", batch)
+    gx.check(L.gfxinfer_launch_residual_add_rms_norm_batch(dr.data_ptr(), du.data_ptr(), ro.data_ptr(), dw.data_ptr(),
+                                                           no.data_ptr(), n, batch, EPS, 1, None))
+    assert np.array_equal(host(ro, np.uint16), want_r)  # one add, one rounding: exact
+    assert _close16(host(no, np.uint16), want_n)
+    codes, scales = empty((batch, n // 2), np.uint8), empty((batch, n // 128), np.uint16)
+    ro2, no2 = empty((batch, n), np.uint16), empty((batch, n), np.uint16)
+    gx.check(L.gfxinfer_launch_residual_add_rms_norm_quantize_i4(dr.data_ptr(), du.data_ptr(), ro2.data_ptr(), dw.data_ptr(),
+                                                                 no2.data_ptr(), codes.data_ptr(), scales.data_ptr(),
+                                                                 n, batch, EPS, 1, None))
+    assert np.array_equal(host(ro2, np.uint16), want_r)
+    c, s = orc.quantize_activation_i4(host(no2, np.uint16))
+    assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
+
+
+def test_dual_rms_norm_concat(device, gx, orc):
+    n = 5120
+    rng = np.random.default_rng(3)
+    left, right = _half(rng.standard_normal(n)), _half(rng.standard_normal(n) * 3)
+    lw, rw = _bf16(rng.standard_normal(n) * 0.05), _bf16(rng.standard_normal(n) * 0.05)
+    want = np.empty(2 * n, np.uint16)
+    orc.lib().orc_dual_rms_norm_concat(orc.ptr(left), orc.ptr(lw), orc.ptr(right), orc.ptr(rw), orc.ptr(want), n, EPS, 1)
+    out = empty((2 * n,), np.uint16)
+    say("dual_rms_norm_concat")
+    gx.check(gx.lib().gfxinfer_launch_dual_rms_norm_concat(dev(left).data_ptr(), dev(lw).data_ptr(), dev(right).data_ptr(),
+                                                           dev(rw).data_ptr(), out.data_ptr(), n, EPS, 1, None))
+    assert _close16(host(out, np.uint16), want)
+
+
+@pytest.mark.parametrize("batch", [1, 5, 32])
+def test_silu_multiply_quantize(device, gx, orc, batch):
+    n = 17408
+    rng = np.random.default_rng(20 + batch)
+    g = (rng.standard_normal((batch, n)) * 2).astype(np.float32)
+    u = rng.standard_normal((batch, n)).astype(np.float32)
+    want = np.empty((batch, n), np.uint16)
+    orc.lib().orc_silu_multiply(orc.ptr(g), orc.ptr(u), orc.ptr(want), batch * n)
+    L = gx.lib()
+    dg, du = dev(g), dev(u)
+    prod = empty((batch, n), np.uint16)
+    say("silu_multiply", batch)
+    gx.check(L.gfxinfer_launch_silu_multiply(dg.data_ptr(), du.data_ptr(), prod.data_ptr(), batch * n, None))
+    got = host(prod, np.uint16)
+    assert _close16(got, want, rel=2.0 ** -10)
+    codes, scales = empty((batch, n // 2), np.uint8), empty((batch, n // 128), np.uint16)
+    gx.check(L.gfxinfer_launch_silu_multiply_quantize_i4(dg.data_ptr(), du.data_ptr(), codes.data_ptr(), scales.data_ptr(),
+                                                         n, batch, None))
+    c, s = orc.quantize_activation_i4(got)  # fused kernel == quantizer of the same fp16 products
+    assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
+
+
+# ---- GDN ------------------------------------------------------------------------
+
+HK, HV, D = 16, 32, 128
+C = 2 * HK * D + HV * D
+
+
+def _gdn_inputs(seed, T):
+    rng = np.random.default_rng(seed)
+    qkv = _half(rng.standard_normal((T, C)))
+    z = rng.standard_normal((T, HV * D)).astype(np.float32)
+    a = rng.standard_normal((T, HV)).astype(np.float32)
+    b = rng.standard_normal((T, HV)).astype(np.float32)
+    a_log = _bf16(np.zeros(HV))
+    dt_bias = _bf16(np.zeros(HV))
+    norm_w = _bf16(np.ones(D))
+    s0 = (rng.standard_normal((HV, D, D)) * 0.1).astype(np.float32)
+    return qkv, z, a, b, a_log, dt_bias, norm_w, s0
+
+
+def _gpu_window(gx, d, T, s0, logs=True):
+    L = gx.lib()
+    fin = empty((HV, D, D), np.float32)
+    out = empty((T, HV * D), np.uint16)
+    work = empty((T, HV * D), np.float32)
+    kl, dl, yl = (empty((T, HK * D), np.float32), empty((T, HV * D), np.float32), empty((T, HV), np.float32)) if logs else (None, None, None)
+    gx.check(L.gfxinfer_launch_gdn_recurrent_decode_block(
+        d["qkv"].data_ptr(), d["z"].data_ptr(), d["a"].data_ptr(), d["b"].data_ptr(), d["a_log"].data_ptr(),
+        d["dt"].data_ptr(), d["nw"].data_ptr(), s0.data_ptr(), fin.data_ptr(), out.data_ptr(),
+        kl.data_ptr() if logs else None, dl.data_ptr() if logs else None, yl.data_ptr() if logs else None,
+        T, HK, HV, D, work.data_ptr(), None))
+    return fin, out, kl, dl, yl
+
+
+def test_gdn_window_matches_oracle(device, gx, orc):
+    """Hv=32, Hk=16, d=128, T=32 tokens."""
+    T = 32
+    qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(41, T)
+    want_s = np.empty_like(s0)
+    want_o = np.empty((T, HV * D), np.uint16)
+    wk, wd, wy = np.empty((T, HK * D), np.float32), np.empty((T, HV * D), np.float32), np.empty((T, HV), np.float32)
+    orc.lib().orc_gdn_recurrent(orc.ptr(qkv), orc.ptr(z), orc.ptr(a), orc.ptr(b), orc.ptr(a_log), orc.ptr(dt),
+                                orc.ptr(nw), orc.ptr(s0), orc.ptr(want_s), orc.ptr(want_o), orc.ptr(wk), orc.ptr(wd),
+                                orc.ptr(wy), T, HK, HV, D)
+    d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
+    say("gdn window T=32")
+    fin, out, kl, dl, yl = _gpu_window(gx, d, T, dev(s0))
+    got_s = host(fin)
+    assert np.abs(got_s - want_s).max() <= 1e-5 * max(1.0, np.abs(want_s).max())
+    assert np.abs(host(kl) - wk).max() <= 1e-6
+    assert np.abs(host(dl) - wd).max() <= 1e-5 * max(1.0, np.abs(wd).max())
+    assert np.abs(host(yl) - wy).max() <= 1e-6
+    go, wo = _f(host(out, np.uint16)), _f(want_o)
+    assert np.abs(go - wo).max() <= 1e-2 * max(1.0, np.abs(wo).max())
+
+
+def test_gdn_closed_forms(device, gx, orc):
+    """beta = 0 (b -> -inf) with decay 1 (a -> -inf): state unchanged; zero state and
+    one token: S = k_hat (outer) beta * v."""
+    T = 1
+    qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(42, T)
+    d = dict(qkv=dev(qkv), z=dev(z), a=dev(np.full((T, HV), -1e4, np.float32)), b=dev(np.full((T, HV), -1e4, np.float32)),
+             a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
+    say("gdn closed form: identity")
+    fin, *_ = _gpu_window(gx, d, T, dev(s0))
+    assert np.array_equal(host(fin), s0)
+    zero = np.zeros_like(s0)
+    d["a"], d["b"] = dev(a), dev(b)
+    say("gdn closed form: outer product")
+    fin, *_ = _gpu_window(gx, d, T, dev(zero))
+    q = _f(qkv[0])
+    beta = 1 / (1 + np.exp(-b[0].astype(np.float64)))
+    for h in (0, 7, 31):
+        kh = h // (HV // HK)
+        k = q[HK * D + kh * D: HK * D + kh * D + D].astype(np.float64)
+        khat = k / np.sqrt((k * k).sum() + 1e-6)
+        v = q[2 * HK * D + h * D: 2 * HK * D + h * D + D].astype(np.float64)
+        want = np.outer(khat, beta[h] * v)
+        assert np.abs(host(fin)[h] - want).max() <= 1e-5
+
+
+@pytest.mark.parametrize("accepted", [1, 5, 17, 32])
+def test_gdn_rollback_equals_prefix_run(device, gx, orc, accepted):
+    """restore(A) on the pre-window state == running only the first A tokens, bit for
+    bit (same fp32 operations in the same order); also against the oracle replay."""
+    T, layers = 32, 2
+    L = gx.lib()
+    conv_states, conv_logs, states = [], [], []
+    key_logs, delta_logs, decay_logs, prefix_states, pre = [], [], [], [], []
+    for layer in range(layers):
+        qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(100 + layer, T)
+        d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
+        say("gdn rollback window", accepted, layer)
+        _, _, kl, dl, yl = _gpu_window(gx, d, T, dev(s0))
+        key_logs.append(host(kl)); delta_logs.append(host(dl)); decay_logs.append(host(yl))
+        dp = dict(qkv=dev(qkv[:accepted]), z=dev(z[:accepted]), a=dev(a[:accepted]), b=dev(b[:accepted]),
+                  a_log=d["a_log"], dt=d["dt"], nw=d["nw"])
+        fin, *_ = _gpu_window(gx, dp, accepted, dev(s0), logs=False)
+        prefix_states.append(host(fin))
+        pre.append(s0)
+        rng = np.random.default_rng(200 + layer)
+        conv_states.append(_half(rng.standard_normal((C, 4))))
+        conv_logs.append(_half(rng.standard_normal((T, C))))
+    st = dev(np.stack(pre))
+    cs = dev(np.stack(conv_states))
+    say("gdn restore all layers", accepted)
+    gx.check(L.gfxinfer_launch_gdn_restore_prefix_all(cs.data_ptr(), st.data_ptr(), dev(np.stack(conv_logs)).data_ptr(),
+                                                      dev(np.stack(key_logs)).data_ptr(), dev(np.stack(delta_logs)).data_ptr(),
+                                                      dev(np.stack(decay_logs)).data_ptr(), C, layers, T, accepted,
+                                                      HK, HV, D, None))
+    got = host(st)
+    for layer in range(layers):
+        assert np.array_equal(got[layer], prefix_states[layer])
+        want = pre[layer].copy()
+        orc.lib().orc_gdn_restore_recurrent(orc.ptr(want), orc.ptr(key_logs[layer]), orc.ptr(delta_logs[layer]),
+                                            orc.ptr(decay_logs[layer]), accepted, HK, HV, D)
+        assert np.array_equal(got[layer], want)  # same operations, same order
+        wc = conv_states[layer].copy()
+        orc.lib().orc_gdn_restore_conv(orc.ptr(wc), orc.ptr(conv_logs[layer]), C, accepted)
+        assert np.array_equal(host(cs, np.uint16)[layer], wc)
+
+
+def test_gdn_restore_rejects_bad_accept(gx):
+    fake = 1 << 20
+    L = gx.lib()
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
+
+
+def test_gdn_conv(device, gx, orc):
+    T = 32
+    rng = np.random.default_rng(5)
+    proj = rng.standard_normal((T, C)).astype(np.float32)
+    w = _bf16(rng.standard_normal((C, 4)) * 0.5)
+    s0 = _half(rng.standard_normal((C, 4)))
+    want_f, want_o, want_l = np.empty_like(s0), np.empty((T, C), np.uint16), np.empty((T, C), np.uint16)
+    orc.lib().orc_gdn_conv_update(orc.ptr(proj), orc.ptr(w), orc.ptr(s0), orc.ptr(want_f), orc.ptr(want_o),
+                                  orc.ptr(want_l), C, T)
+    fin, out, log = empty((C, 4), np.uint16), empty((T, C), np.uint16), empty((T, C), np.uint16)
+    say("gdn conv")
+    gx.check(gx.lib().gfxinfer_launch_gdn_conv_update_block(dev(proj).data_ptr(), dev(w).data_ptr(), dev(s0).data_ptr(),
+                                                            fin.data_ptr(), out.data_ptr(), log.data_ptr(), C, T, None))
+    assert np.array_equal(host(fin, np.uint16), want_f)
+    assert np.array_equal(host(log, np.uint16), want_l)
+    assert _close16(host(out, np.uint16), want_o, rel=2.0 ** -9, atol=1e-4)
+
+
+def test_gdn_output_quantize(device, gx, orc):
+    T = 5
+    rng = np.random.default_rng(6)
+    mixed = rng.standard_normal((T, HV * D)).astype(np.float32)
+    z = rng.standard_normal((T, HV * D)).astype(np.float32)
+    w = _bf16(np.ones(D))
+    out, codes, scales = empty((T, HV * D), np.uint16), empty((T, HV * D // 2), np.uint8), empty((T, HV), np.uint16)
+    say("gdn output quantize")
+    gx.check(gx.lib().gfxinfer_launch_gdn_output_quantize_i4(dev(mixed).data_ptr(), dev(z).data_ptr(), dev(w).data_ptr(),
+                                                             out.data_ptr(), codes.data_ptr(), scales.data_ptr(), T, HV, D, None))
+    o = host(out, np.uint16)
+    m = mixed.reshape(T, HV, D).astype(np.float64)
+    inv = 1 / np.sqrt((m * m).mean(axis=2, keepdims=True) + 1e-6)
+    zz = z.reshape(T, HV, D).astype(np.float64)
+    want = (m * inv * (zz / (1 + np.exp(-zz)))).reshape(T, HV * D)
+    assert np.abs(_f(o) - want).max() <= 2e-3 * np.abs(want).max()
+    c, s = orc.quantize_activation_i4(o)
+    assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
+
+
+# ---- attention ---------------------------------------------------------------------
+
+HQ, HKV, AD = 40, 8, 128
+
+
+@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 64), (32, 4065)])
+def test_attention_matches_oracle(device, gx, orc, T, base):
+    capacity = 4096 + 32
+    rng = np.random.default_rng(T * 7 + base)
+    q = _half(rng.standard_normal((T, HQ, AD)))
+    gate = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
+    kc = np.zeros((capacity, HKV, AD), np.uint16)
+    vc = np.zeros((capacity, HKV, AD), np.uint16)
+    n = base + T - 1
+    kc[:n] = _half(rng.standard_normal((n, HKV, AD)))
+    vc[:n] = _half(rng.standard_normal((n, HKV, AD)))
+    want = np.empty((T, HQ, AD), np.uint16)
+    orc.lib().orc_gated_attention(orc.ptr(q), orc.ptr(gate), orc.ptr(kc), orc.ptr(vc), orc.ptr(want), base, T, HQ, HKV, AD,
+                                  np.float32(1 / np.sqrt(AD)))
+    L = gx.lib()
+    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, capacity)
+    work = empty((wb // 4,), np.float32)
+    out = empty((T, HQ, AD), np.uint16)
+    say("attention", T, base)
+    gx.check(L.gfxinfer_launch_gated_attention_decode_block(dev(q).data_ptr(), dev(gate).data_ptr(), dev(kc).data_ptr(),
+                                                            dev(vc).data_ptr(), out.data_ptr(), base, capacity, T, HQ, HKV,
+                                                            AD, work.data_ptr(), wb, None))
+    got, w = _f(host(out, np.uint16)), _f(want)
+    assert np.abs(got - w).max() <= 1e-2 * max(1.0, np.abs(w).max())
+    pos = dev(np.array([base - 1], np.uint64))
+    out2 = empty((T, HQ, AD), np.uint16)
+    gx.check(L.gfxinfer_launch_gated_attention_decode_block_indirect_position(
+        dev(q).data_ptr(), dev(gate).data_ptr(), dev(kc).data_ptr(), dev(vc).data_ptr(), out2.data_ptr(), pos.data_ptr(),
+        capacity, T, HQ, HKV, AD, work.data_ptr(), wb, None))
+    assert np.array_equal(host(out2, np.uint16), host(out, np.uint16))
+
+
+def test_qk_norm_rope_and_kv_append(device, gx, orc):
+    T, rot, theta, base = 5, 32, np.float32(1e7), 1234
+    rng = np.random.default_rng(8)
+    qin = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
+    kin = rng.standard_normal((T, HKV, AD)).astype(np.float32)
+    qw, kw = _bf16(rng.standard_normal(AD) * 0.1), _bf16(rng.standard_normal(AD) * 0.1)
+    wq, wk = np.empty((T, HQ, AD), np.uint16), np.empty((T, HKV, AD), np.uint16)
+    orc.lib().orc_head_norm_rope(orc.ptr(qin), 2 * AD, orc.ptr(qw), orc.ptr(wq), HQ, AD, rot, base, T, theta)
+    orc.lib().orc_head_norm_rope(orc.ptr(kin), AD, orc.ptr(kw), orc.ptr(wk), HKV, AD, rot, base, T, theta)
+    L = gx.lib()
+    qo, ko = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
+    say("qk norm rope")
+    gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(dev(qin).data_ptr(), dev(qw).data_ptr(), qo.data_ptr(), HQ, 2 * AD,
+                                                      dev(kin).data_ptr(), dev(kw).data_ptr(), ko.data_ptr(), HKV, AD, AD,
+                                                      rot, base, T, theta, None))
+    assert _close16(host(qo, np.uint16), wq, rel=2.0 ** -8, atol=2e-3)
+    assert _close16(host(ko, np.uint16), wk, rel=2.0 ** -8, atol=2e-3)
+    pos = dev(np.array([base], np.uint64))
+    qo2, ko2 = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
+    gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
+        dev(qin).data_ptr(), dev(qw).data_ptr(), qo2.data_ptr(), HQ, 2 * AD, dev(kin).data_ptr(), dev(kw).data_ptr(),
+        ko2.data_ptr(), HKV, AD, AD, rot, pos.data_ptr(), T, theta, None))
+    assert np.array_equal(host(qo2, np.uint16), host(qo, np.uint16))
+    # KV append
+    cap = 2048
+    kc, vc = empty((cap, HKV * AD), np.uint16), empty((cap, HKV * AD), np.uint16)
+    val = rng.standard_normal((T, HKV * AD)).astype(np.float32)
+    gx.check(L.gfxinfer_launch_kv_append_block(ko.data_ptr(), dev(val).data_ptr(), kc.data_ptr(), vc.data_ptr(), base, cap,
+                                               T, HKV * AD, None))
+    assert np.array_equal(host(kc, np.uint16)[base:base + T], host(ko, np.uint16).reshape(T, -1))
+    assert np.array_equal(host(vc, np.uint16)[base:base + T], _half(val))
+    assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), dev(val).data_ptr(), kc.data_ptr(), vc.data_ptr(), cap - 2, cap,
+                                             T, HKV * AD, None) == gx.INVALID_ARGUMENT
+
+
+def test_argmax_ties_and_mapping(device, gx, orc):
+    V, T = 151936, 6
+    rng = np.random.default_rng(9)
+    logits = rng.standard_normal((T, V)).astype(np.float32)
+    logits[1, 500] = logits[1, 90000] = 50.0       # tie -> lowest index
+    logits[2, V - 1] = 60.0                         # last element
+    logits[3, :] = -np.inf
+    logits[4, 7] = np.nan
+    logits[4, 8] = 70.0
+    want = np.empty(T, np.uint32)
+    orc.lib().orc_argmax(orc.ptr(logits), V, V, T, None, orc.ptr(want))
+    out = empty((T,), np.uint32)
+    L = gx.lib()
+    say("argmax")
+    gx.check(L.gfxinfer_launch_argmax_batch(dev(logits).data_ptr(), out.data_ptr(), V, V, T, None))
+    got = host(out).view(np.uint32)
+    assert np.array_equal(got, want) and got[1] == 500 and got[3] == 0
+    ids = (np.arange(98304, dtype=np.uint32) * 7 + 3).astype(np.uint32)
+    one = empty((1,), np.uint32)
+    gx.check(L.gfxinfer_launch_argmax_mapped(dev(logits[2]).data_ptr(), dev(ids).data_ptr(), one.data_ptr(), 98304, None))
+    assert int(host(one).view(np.uint32)[0]) == int(ids[np.argmax(logits[2, :98304])])
