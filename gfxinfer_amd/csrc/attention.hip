@@ -202,8 +202,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   const float g0 = 1.0F / (1.0F + expf(-g[2 * lane]));
   const float g1 = 1.0F / (1.0F + expf(-g[2 * lane + 1]));
   __half* out = output + static_cast<std::size_t>(linear) * kD + 2 * lane;
-  out[0] = __float2half(o0 / total * g0);
-  out[1] = __float2half(o1 / total * g1);
+  out[0] = to_half(o0 / total * g0);
+  out[1] = to_half(o1 / total * g1);
 }
 
 int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t* key_cache,

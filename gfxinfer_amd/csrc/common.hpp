@@ -24,6 +24,15 @@ int32_t hip_fail(hipError_t error, const char* context);
 // hipGetLastError after a launch, as every reference launcher does.
 int32_t launch_status(const char* context);
 
+// fp32 -> fp16 (round to nearest even) of a value first rounded to fp32.  The
+// empty asm pins the fp32 value in a register so the compiler cannot fold a
+// preceding multiply or add into v_fma_mixlo_f16, which rounds the exact result
+// to fp16 once instead of rounding to fp32 first as the source states.
+__device__ __forceinline__ __half to_half(float x) {
+  asm volatile("" : "+v"(x));
+  return __float2half(x);
+}
+
 inline bool valid_weight_format(int32_t format) {
   return format == GFXI_W3G128 || format == GFXI_W4G128;
 }

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void quantize_activation_kernel(
   const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
   constexpr float kLevels = Bits == 4 ? 7.0F : 127.0F;
   constexpr int kClamp = Bits == 4 ? 7 : 127;
-  const __half scale16 = __float2half(maximum == 0.0F ? 1.0F : maximum / kLevels);
+  const __half scale16 = to_half(maximum == 0.0F ? 1.0F : maximum / kLevels);
   const float scale = __half2float(scale16);
   const int low = max(-kClamp, min(kClamp, __float2int_rn(x0 / scale)));
   const int high = max(-kClamp, min(kClamp, __float2int_rn(x1 / scale)));
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void quantize_group128_kernel(
     }
     scale = fmaxf(scale, std::numeric_limits<float>::min());
   }
-  scales[scale_offset(row, group, groups)] = __float2half(scale);
+  scales[scale_offset(row, group, groups)] = to_half(scale);
   for (unsigned kb = 0; kb < 4; ++kb) {
     int8_t chunk[32];
     for (unsigned c = 0; c < 32; ++c) {
@@ -507,7 +507,7 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     if constexpr (HalfOut) {
       __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = __float2half(acc[t][r]);
+      for (int r = 0; r < 4; ++r) o[r] = to_half(acc[t][r]);
     } else {
       float4 value = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
       *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256) void row_gather_kernel(
   const std::size_t groups = columns / kGroup;
   const uint8_t* chunk = weights + chunk_offset(Format, row, column, groups);
   const int w = unpack_lane_code(Format, chunk, static_cast<unsigned>(column % 32));
-  output[column] = __float2half(static_cast<float>(w) *
+  output[column] = to_half(static_cast<float>(w) *
                                 __half2float(scales[scale_offset(row, column / kGroup, groups)]));
 }
 

@@ -62,7 +62,7 @@ __device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_
                                                   __half* scale_out, unsigned lane) {
   const float x0 = __half2float(x0h), x1 = __half2float(x1h);
   const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const __half scale16 = __float2half(maximum == 0.0F ? 1.0F : maximum / 7.0F);
+  const __half scale16 = to_half(maximum == 0.0F ? 1.0F : maximum / 7.0F);
   const float scale = __half2float(scale16);
   const int low = max(-7, min(7, __float2int_rn(x0 / scale)));
   const int high = max(-7, min(7, __float2int_rn(x1 / scale)));
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
     __half v = input[base + i];
     if constexpr (Residual) {
-      v = __float2half(__half2float(v) + update[base + i]);
+      v = to_half(__half2float(v) + update[base + i]);
       residual_out[base + i] = v;
     }
     row[i] = v;
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   const float total = block_sum(square, scratch);
   const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
-    const __half n = __float2half(__half2float(row[i]) * inverse * norm_scale(weight, i, unit_offset));
+    const __half n = to_half(__half2float(row[i]) * inverse * norm_scale(weight, i, unit_offset));
     row[i] = n;
     if (output != nullptr) output[base + i] = n;
   }
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
   }
   const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + epsilon);
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
-    output[i] = __float2half(__half2float(input[i]) * inverse * norm_scale(weight, i, unit_offset));
+    output[i] = to_half(__half2float(input[i]) * inverse * norm_scale(weight, i, unit_offset));
   }
 }
 
@@ -156,8 +156,8 @@ __global__ __launch_bounds__(256) void silu_multiply_kernel(
   const std::size_t at = static_cast<std::size_t>(token) * columns + group * 128u + 2u * lane;
   const float2 g = *reinterpret_cast<const float2*>(gate + at);
   const float2 u = *reinterpret_cast<const float2*>(up + at);
-  const __half p0 = __float2half(silu(g.x) * u.x);
-  const __half p1 = __float2half(silu(g.y) * u.y);
+  const __half p0 = to_half(silu(g.x) * u.x);
+  const __half p1 = to_half(silu(g.y) * u.y);
   if (output != nullptr) {
     output[at] = p0;
     output[at + 1] = p1;
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void silu_multiply_kernel(
 __global__ void float_to_half_kernel(const float* __restrict__ in, __half* __restrict__ out,
                                      std::size_t n) {
   const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = __float2half(in[i]);
+  if (i < n) out[i] = to_half(in[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -196,12 +196,12 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(
     state[0] = state[1];
     state[1] = state[2];
     state[2] = state[3];
-    state[3] = __float2half(projected[static_cast<std::size_t>(t) * channels + c]);
+    state[3] = to_half(projected[static_cast<std::size_t>(t) * channels + c]);
     if (appended_log != nullptr) appended_log[static_cast<std::size_t>(t) * channels + c] = state[3];
     float conv = 0.0F;
 #pragma unroll
     for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(state[tap]), w[tap], conv);
-    output[static_cast<std::size_t>(t) * channels + c] = __float2half(silu(conv));
+    output[static_cast<std::size_t>(t) * channels + c] = to_half(silu(conv));
   }
 #pragma unroll
   for (int tap = 0; tap < 4; ++tap) final_state[static_cast<std::size_t>(c) * 4 + tap] = state[tap];
@@ -382,8 +382,8 @@ __global__ __launch_bounds__(256) void gdn_output_kernel(
   const float2 o = *reinterpret_cast<const float2*>(mixed + row + 2 * lane);
   const float inverse = rsqrtf(wave_sum(o.x * o.x + o.y * o.y) / static_cast<float>(kGdnD) + 1.0e-6F);
   const float2 g = *reinterpret_cast<const float2*>(z + row + 2 * lane);
-  const __half r0 = __float2half(o.x * inverse * bf16_to_float(weight[2 * lane]) * silu(g.x));
-  const __half r1 = __float2half(o.y * inverse * bf16_to_float(weight[2 * lane + 1]) * silu(g.y));
+  const __half r0 = to_half(o.x * inverse * bf16_to_float(weight[2 * lane]) * silu(g.x));
+  const __half r1 = to_half(o.y * inverse * bf16_to_float(weight[2 * lane + 1]) * silu(g.y));
   if (output != nullptr) {
     output[row + 2 * lane] = r0;
     output[row + 2 * lane + 1] = r1;
@@ -505,8 +505,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
     const float rotated = lane < half ? -partner : partner;
     v0 = fmaf(n0, cosf(angle), rotated * sinf(angle));
   }
-  out[lane] = __float2half(v0);
-  out[lane + 64] = __float2half(n1);
+  out[lane] = to_half(v0);
+  out[lane + 64] = to_half(n1);
 }
 
 // K (fp16) and V (fp32 -> fp16) rows into the contiguous cache at the (device)
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   if (i >= static_cast<std::size_t>(tokens) * elements) return;
   const std::size_t at = position * elements + i;
   key_cache[at] = key[i];
-  value_cache[at] = __float2half(value[i]);
+  value_cache[at] = to_half(value[i]);
 }
 
 // ---------------------------------------------------------------------------

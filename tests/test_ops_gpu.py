@@ -29,6 +29,23 @@ def _bf16(x):
     return (x.view(np.uint32) >> 16).astype(np.uint16)  # truncation: exact for test values
 
 
+_KEEP: list = []
+
+
+def D_(arr):
+    """Device copy whose tensor stays alive for the rest of the test (an inline
+    D_(x) would free the tensor before the kernel reads it)."""
+    t = dev(arr)
+    _KEEP.append(t)
+    return t.data_ptr()
+
+
+@pytest.fixture(autouse=True)
+def _release_kept():
+    yield
+    _KEEP.clear()
+
+
 def _close16(got, want, rel=2.0 ** -9, atol=1e-6):
     g, w = _f(got), _f(want)
     return np.all(np.abs(g - w) <= rel * np.abs(w) + atol)
@@ -102,8 +119,8 @@ def test_dual_rms_norm_concat(device, gx, orc):
     orc.lib().orc_dual_rms_norm_concat(orc.ptr(left), orc.ptr(lw), orc.ptr(right), orc.ptr(rw), orc.ptr(want), n, EPS, 1)
     out = empty((2 * n,), np.uint16)
     say("dual_rms_norm_concat")
-    gx.check(gx.lib().gfxinfer_launch_dual_rms_norm_concat(dev(left).data_ptr(), dev(lw).data_ptr(), dev(right).data_ptr(),
-                                                           dev(rw).data_ptr(), out.data_ptr(), n, EPS, 1, None))
+    gx.check(gx.lib().gfxinfer_launch_dual_rms_norm_concat(D_(left), D_(lw), D_(right),
+                                                           D_(rw), out.data_ptr(), n, EPS, 1, None))
     assert _close16(host(out, np.uint16), want)
 
 
@@ -126,7 +143,9 @@ def test_silu_multiply_quantize(device, gx, orc, batch):
     gx.check(L.gfxinfer_launch_silu_multiply_quantize_i4(dg.data_ptr(), du.data_ptr(), codes.data_ptr(), scales.data_ptr(),
                                                          n, batch, None))
     c, s = orc.quantize_activation_i4(got)  # fused kernel == quantizer of the same fp16 products
-    assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
+    gs = host(scales, np.uint16)
+    assert np.array_equal(host(codes), c)
+    assert np.array_equal(gs, s), np.argwhere(gs != s)[:8]
 
 
 # ---- GDN ------------------------------------------------------------------------
@@ -234,9 +253,9 @@ def test_gdn_rollback_equals_prefix_run(device, gx, orc, accepted):
     st = dev(np.stack(pre))
     cs = dev(np.stack(conv_states))
     say("gdn restore all layers", accepted)
-    gx.check(L.gfxinfer_launch_gdn_restore_prefix_all(cs.data_ptr(), st.data_ptr(), dev(np.stack(conv_logs)).data_ptr(),
-                                                      dev(np.stack(key_logs)).data_ptr(), dev(np.stack(delta_logs)).data_ptr(),
-                                                      dev(np.stack(decay_logs)).data_ptr(), C, layers, T, accepted,
+    gx.check(L.gfxinfer_launch_gdn_restore_prefix_all(cs.data_ptr(), st.data_ptr(), D_(np.stack(conv_logs)),
+                                                      D_(np.stack(key_logs)), D_(np.stack(delta_logs)),
+                                                      D_(np.stack(decay_logs)), C, layers, T, accepted,
                                                       HK, HV, D, None))
     got = host(st)
     for layer in range(layers):
@@ -268,7 +287,7 @@ def test_gdn_conv(device, gx, orc):
                                   orc.ptr(want_l), C, T)
     fin, out, log = empty((C, 4), np.uint16), empty((T, C), np.uint16), empty((T, C), np.uint16)
     say("gdn conv")
-    gx.check(gx.lib().gfxinfer_launch_gdn_conv_update_block(dev(proj).data_ptr(), dev(w).data_ptr(), dev(s0).data_ptr(),
+    gx.check(gx.lib().gfxinfer_launch_gdn_conv_update_block(D_(proj), D_(w), D_(s0),
                                                             fin.data_ptr(), out.data_ptr(), log.data_ptr(), C, T, None))
     assert np.array_equal(host(fin, np.uint16), want_f)
     assert np.array_equal(host(log, np.uint16), want_l)
@@ -283,7 +302,7 @@ def test_gdn_output_quantize(device, gx, orc):
     w = _bf16(np.ones(D))
     out, codes, scales = empty((T, HV * D), np.uint16), empty((T, HV * D // 2), np.uint8), empty((T, HV), np.uint16)
     say("gdn output quantize")
-    gx.check(gx.lib().gfxinfer_launch_gdn_output_quantize_i4(dev(mixed).data_ptr(), dev(z).data_ptr(), dev(w).data_ptr(),
+    gx.check(gx.lib().gfxinfer_launch_gdn_output_quantize_i4(D_(mixed), D_(z), D_(w),
                                                              out.data_ptr(), codes.data_ptr(), scales.data_ptr(), T, HV, D, None))
     o = host(out, np.uint16)
     m = mixed.reshape(T, HV, D).astype(np.float64)
@@ -319,15 +338,15 @@ def test_attention_matches_oracle(device, gx, orc, T, base):
     work = empty((wb // 4,), np.float32)
     out = empty((T, HQ, AD), np.uint16)
     say("attention", T, base)
-    gx.check(L.gfxinfer_launch_gated_attention_decode_block(dev(q).data_ptr(), dev(gate).data_ptr(), dev(kc).data_ptr(),
-                                                            dev(vc).data_ptr(), out.data_ptr(), base, capacity, T, HQ, HKV,
+    gx.check(L.gfxinfer_launch_gated_attention_decode_block(D_(q), D_(gate), D_(kc),
+                                                            D_(vc), out.data_ptr(), base, capacity, T, HQ, HKV,
                                                             AD, work.data_ptr(), wb, None))
     got, w = _f(host(out, np.uint16)), _f(want)
     assert np.abs(got - w).max() <= 1e-2 * max(1.0, np.abs(w).max())
     pos = dev(np.array([base - 1], np.uint64))
     out2 = empty((T, HQ, AD), np.uint16)
     gx.check(L.gfxinfer_launch_gated_attention_decode_block_indirect_position(
-        dev(q).data_ptr(), dev(gate).data_ptr(), dev(kc).data_ptr(), dev(vc).data_ptr(), out2.data_ptr(), pos.data_ptr(),
+        D_(q), D_(gate), D_(kc), D_(vc), out2.data_ptr(), pos.data_ptr(),
         capacity, T, HQ, HKV, AD, work.data_ptr(), wb, None))
     assert np.array_equal(host(out2, np.uint16), host(out, np.uint16))
 
@@ -344,26 +363,26 @@ def test_qk_norm_rope_and_kv_append(device, gx, orc):
     L = gx.lib()
     qo, ko = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
     say("qk norm rope")
-    gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(dev(qin).data_ptr(), dev(qw).data_ptr(), qo.data_ptr(), HQ, 2 * AD,
-                                                      dev(kin).data_ptr(), dev(kw).data_ptr(), ko.data_ptr(), HKV, AD, AD,
+    gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD,
+                                                      D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD,
                                                       rot, base, T, theta, None))
     assert _close16(host(qo, np.uint16), wq, rel=2.0 ** -8, atol=2e-3)
     assert _close16(host(ko, np.uint16), wk, rel=2.0 ** -8, atol=2e-3)
     pos = dev(np.array([base], np.uint64))
     qo2, ko2 = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
     gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
-        dev(qin).data_ptr(), dev(qw).data_ptr(), qo2.data_ptr(), HQ, 2 * AD, dev(kin).data_ptr(), dev(kw).data_ptr(),
+        D_(qin), D_(qw), qo2.data_ptr(), HQ, 2 * AD, D_(kin), D_(kw),
         ko2.data_ptr(), HKV, AD, AD, rot, pos.data_ptr(), T, theta, None))
     assert np.array_equal(host(qo2, np.uint16), host(qo, np.uint16))
     # KV append
     cap = 2048
     kc, vc = empty((cap, HKV * AD), np.uint16), empty((cap, HKV * AD), np.uint16)
     val = rng.standard_normal((T, HKV * AD)).astype(np.float32)
-    gx.check(L.gfxinfer_launch_kv_append_block(ko.data_ptr(), dev(val).data_ptr(), kc.data_ptr(), vc.data_ptr(), base, cap,
+    gx.check(L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), base, cap,
                                                T, HKV * AD, None))
     assert np.array_equal(host(kc, np.uint16)[base:base + T], host(ko, np.uint16).reshape(T, -1))
     assert np.array_equal(host(vc, np.uint16)[base:base + T], _half(val))
-    assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), dev(val).data_ptr(), kc.data_ptr(), vc.data_ptr(), cap - 2, cap,
+    assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), cap - 2, cap,
                                              T, HKV * AD, None) == gx.INVALID_ARGUMENT
 
 
@@ -381,10 +400,10 @@ def test_argmax_ties_and_mapping(device, gx, orc):
     out = empty((T,), np.uint32)
     L = gx.lib()
     say("argmax")
-    gx.check(L.gfxinfer_launch_argmax_batch(dev(logits).data_ptr(), out.data_ptr(), V, V, T, None))
+    gx.check(L.gfxinfer_launch_argmax_batch(D_(logits), out.data_ptr(), V, V, T, None))
     got = host(out).view(np.uint32)
     assert np.array_equal(got, want) and got[1] == 500 and got[3] == 0
     ids = (np.arange(98304, dtype=np.uint32) * 7 + 3).astype(np.uint32)
     one = empty((1,), np.uint32)
-    gx.check(L.gfxinfer_launch_argmax_mapped(dev(logits[2]).data_ptr(), dev(ids).data_ptr(), one.data_ptr(), 98304, None))
+    gx.check(L.gfxinfer_launch_argmax_mapped(D_(logits[2]), D_(ids), one.data_ptr(), 98304, None))
     assert int(host(one).view(np.uint32)[0]) == int(ids[np.argmax(logits[2, :98304])])
