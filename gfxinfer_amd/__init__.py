@@ -19,7 +19,8 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIBRARY = os.path.join(HERE, "libgfxinfer_amd.so")
-HEADER = os.path.join(ROOT, "include", "gfxinfer_amd.h")
+HEADERS = [os.path.join(ROOT, "include", "gfxinfer_amd.h"),
+           os.path.join(ROOT, "include", "gfxinfer_runtime.h")]
 
 # include/gfxinfer/status.h:11-20
 OK, INVALID_ARGUMENT, IO_ERROR, CORRUPT_ARTIFACT, UNSUPPORTED, HIP_ERROR, OUT_OF_MEMORY, INTERNAL = range(8)
@@ -89,6 +90,27 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_attention_workspace_bytes": (SZ, [U32, U32, SZ]),
     "gfxinfer_launch_gated_attention_decode_block": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
+    # include/gfxinfer_runtime.h
+    "gfxinfer_model_spec_qwen38_27b": (None, [P]),
+    "gfxinfer_model_create_synthetic": (I32, [P, ctypes.c_uint64, I32, P]),
+    "gfxinfer_model_destroy": (None, [P]),
+    "gfxinfer_model_stream": (P, [P]),
+    "gfxinfer_model_weight_bytes": (SZ, [P]),
+    "gfxinfer_model_find_tensor": (I32, [P, ctypes.c_char_p, P]),
+    "gfxinfer_model_copy_tensor": (I32, [P, ctypes.c_char_p, I32, P, SZ]),
+    "gfxinfer_session_create": (I32, [P, P, P]),
+    "gfxinfer_session_destroy": (None, [P]),
+    "gfxinfer_session_greedy_step": (I32, [P, U32, P]),
+    "gfxinfer_session_block_step": (I32, [P, P, SZ, P]),
+    "gfxinfer_session_mtp_draft": (I32, [P, U32, P]),
+    "gfxinfer_session_speculative_step": (I32, [P, U32, SZ, P]),
+    "gfxinfer_session_speculative_step_forced": (I32, [P, U32, SZ, U32, P]),
+    "gfxinfer_session_speculative_step_planted": (I32, [P, U32, SZ, P, P]),
+    "gfxinfer_session_position": (SZ, [P]),
+    "gfxinfer_session_mtp_position": (SZ, [P]),
+    "gfxinfer_session_get_summary": (I32, [P, P]),
+    "gfxinfer_session_copy_buffer": (I32, [P, ctypes.c_char_p, SZ, P, SZ]),
+    "gfxinfer_session_buffer_bytes": (SZ, [P, ctypes.c_char_p]),
 }
 
 
@@ -120,8 +142,8 @@ def lib() -> ctypes.CDLL:
 
 
 def header_functions() -> list[str]:
-    """Names of every function declared in include/gfxinfer_amd.h."""
-    text = open(HEADER).read()
+    """Names of every function declared in include/*.h."""
+    text = "\n".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(gfxinfer_[a-z0-9_]+)\s*\(", text)))
 

@@ -33,6 +33,20 @@ __device__ __forceinline__ __half to_half(float x) {
   return __float2half(x);
 }
 
+// Signed quantization level of value at scale (quantization.cpp:29-56: encode_value
+// then decode_value), clamped to the format's range.
+template <int Format>
+__device__ __forceinline__ int encode_level(float value, float scale) {
+  const float normalized = scale == 0.0F ? 0.0F : value / scale;
+  const float rounded = rintf(normalized);
+  int q = static_cast<int>(fminf(fmaxf(rounded, -2147483648.0F), 2147483520.0F));
+  if constexpr (Format == GFXI_W3G128) {
+    return max(-4, min(3, q));
+  } else {
+    return max(-8, min(7, q));
+  }
+}
+
 inline bool valid_weight_format(int32_t format) {
   return format == GFXI_W3G128 || format == GFXI_W4G128;
 }

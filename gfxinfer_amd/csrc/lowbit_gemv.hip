@@ -72,19 +72,6 @@ __global__ __launch_bounds__(256) void quantize_activation_kernel(
 // ---------------------------------------------------------------------------
 
 template <int Format>
-__device__ __forceinline__ int encode_level(float value, float scale) {
-  // quantization.cpp:29-46 followed by decode_value (:48-56): the signed level.
-  const float normalized = scale == 0.0F ? 0.0F : value / scale;
-  const float rounded = rintf(normalized);
-  int q = static_cast<int>(fminf(fmaxf(rounded, -2147483648.0F), 2147483520.0F));
-  if constexpr (Format == GFXI_W3G128) {
-    return max(-4, min(3, q));
-  } else {
-    return max(-8, min(7, q));
-  }
-}
-
-template <int Format>
 __global__ __launch_bounds__(256) void quantize_group128_kernel(
     const float* __restrict__ weights, std::size_t rows, std::size_t columns, std::size_t groups,
     uint8_t* __restrict__ codes, __half* __restrict__ scales, int32_t* __restrict__ non_finite) {
@@ -556,6 +543,8 @@ int waves_override() {
   return value;
 }
 
+constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per CU (and per workgroup)
+
 unsigned choose_waves(uint32_t groups, unsigned gp) {
   if (const int forced = waves_override(); forced != 0) return static_cast<unsigned>(forced);
   (void)gp;
@@ -572,6 +561,10 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
     unsigned waves = choose_waves(args.groups, 1);
     if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
     const GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
+    // A workgroup may hold at most the CU's 160 KiB of LDS (32 tokens x 136 groups
+    // would otherwise ask for 8 x 21 KiB).
+    const unsigned lds_waves = kLdsBytes / layout.region;
+    if (waves > lds_waves) waves = lds_waves;
     hipLaunchKernelGGL(kernel, dim3(total_tiles), dim3(64 * waves), layout.region * waves, stream,
                        args, layout);
   };

@@ -180,7 +180,7 @@ __global__ void float_to_half_kernel(const float* __restrict__ in, __half* __res
 
 __global__ __launch_bounds__(256) void gdn_conv_kernel(
     const float* __restrict__ projected, const uint16_t* __restrict__ weight,
-    const __half* __restrict__ initial_state, __half* __restrict__ final_state,
+    const __half* initial_state, __half* final_state,  // may alias (in-place update)
     __half* __restrict__ output, __half* __restrict__ appended_log, uint32_t channels,
     uint32_t tokens) {
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;

@@ -1,0 +1,74 @@
+// Internal definitions shared by the synthetic model ("engine") and the decode
+// session: the tensor table and the model handle behind gfxinfer_model.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "gfxinfer_runtime.h"
+
+namespace gfx950 {
+
+constexpr int32_t kBf16 = 0;  // tensor format tag of bf16 vectors / small matrices
+
+// One named tensor of the weight arena (engine.h:47-60 DeviceTensorView).
+struct Tensor {
+  std::string name;
+  int32_t format{kBf16};
+  uint64_t rows{0};
+  uint64_t columns{0};
+  std::size_t data_offset{0};
+  std::size_t data_bytes{0};
+  std::size_t auxiliary_offset{0};
+  std::size_t auxiliary_bytes{0};
+  // Synthetic value law: mean + sigma * N(0, 1).
+  float mean{0.0F};
+  float sigma{0.0F};
+};
+
+// Layer i is full attention iff (i + 1) % interval == 0 (qwen38_spec.h:45-47).
+inline bool is_attention_layer(const gfxinfer_model_spec& spec, uint32_t layer) {
+  return (layer + 1u) % spec.full_attention_interval == 0;
+}
+
+// Tensor table of a spec, in converter naming (converter.cpp:78-119,
+// qwen_runtime.cpp:1025-1080), with formats and value laws; offsets unset.
+std::vector<Tensor> model_tensors(const gfxinfer_model_spec& spec);
+// Checks the shape constraints the kernels rely on; returns GFXI_OK or the error.
+int32_t validate_spec(const gfxinfer_model_spec& spec);
+
+// FNV-1a of a tensor name: the per-tensor key of the synthetic generator.
+inline uint64_t name_hash(const std::string& name) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char c : name) {
+    h ^= c;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+}  // namespace gfx950
+
+struct gfxinfer_model {
+  gfxinfer_model_spec spec{};
+  int device{0};
+  hipStream_t stream{nullptr};
+  uint8_t* arena{nullptr};
+  std::size_t arena_bytes{0};
+  std::vector<gfx950::Tensor> tensors;
+  std::unordered_map<std::string, std::size_t> index;
+
+  const gfx950::Tensor* find(const std::string& name) const {
+    const auto it = index.find(name);
+    return it == index.end() ? nullptr : &tensors[it->second];
+  }
+  void* data(const gfx950::Tensor* t) const { return arena + t->data_offset; }
+  void* auxiliary(const gfx950::Tensor* t) const {
+    return t->auxiliary_bytes == 0 ? nullptr : arena + t->auxiliary_offset;
+  }
+};

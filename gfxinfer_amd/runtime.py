@@ -1,0 +1,217 @@
+"""Python view of the decode runtime (include/gfxinfer_runtime.h).
+
+`SyntheticModel` stands where the reference's `gfxinfer::Engine` stands
+(include/gfxinfer/engine.h), holding a seeded synthetic checkpoint in the gfx950
+tile layout; `QwenDecodeSession` mirrors `gfxinfer::QwenDecodeSession`
+(include/gfxinfer/qwen_runtime.h:47-77) method for method: greedy_step,
+block_step, mtp_draft, speculative_step, position, summary.  Errors raise
+GfxinferError with the reference ErrorCode value.  All work runs in
+libgfxinfer_amd.so; this module only marshals arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import GfxinferError, check, lib
+
+U32 = ctypes.c_uint32
+
+
+class ModelSpec(ctypes.Structure):
+    """gfxinfer_model_spec (qwen38_spec.h:15-48 as fields)."""
+    _fields_ = [(name, ctypes.c_uint32) for name in (
+        "hidden_size", "intermediate_size", "layer_count", "full_attention_interval",
+        "attention_head_count", "kv_head_count", "attention_head_size", "rotary_size",
+        "gdn_key_head_count", "gdn_value_head_count", "gdn_head_size", "vocabulary_size",
+        "tokenizer_vocabulary_size", "mtp_draft_vocabulary", "w3_mlp_layers")] + [
+        ("rms_norm_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+def qwen38_27b_spec() -> ModelSpec:
+    spec = ModelSpec()
+    lib().gfxinfer_model_spec_qwen38_27b(ctypes.byref(spec))
+    return spec
+
+
+def tiny_spec(**overrides) -> ModelSpec:
+    """A small model of the same structure for oracle parity (2 GDN + 2 attention layers)."""
+    spec = qwen38_27b_spec()
+    values = dict(hidden_size=256, intermediate_size=512, layer_count=4, attention_head_count=4,
+                  kv_head_count=2, rotary_size=64, gdn_key_head_count=2, gdn_value_head_count=16,
+                  vocabulary_size=1024, tokenizer_vocabulary_size=1000, mtp_draft_vocabulary=512,
+                  w3_mlp_layers=2)
+    values.update(overrides)
+    for k, v in values.items():
+        setattr(spec, k, v)
+    return spec
+
+
+class TensorView(ctypes.Structure):
+    """gfxinfer_tensor_view (engine.h:47-60 DeviceTensorView)."""
+    _fields_ = [("format", ctypes.c_int32), ("rows", ctypes.c_uint64), ("columns", ctypes.c_uint64),
+                ("data", ctypes.c_void_p), ("auxiliary", ctypes.c_void_p),
+                ("data_bytes", ctypes.c_size_t), ("auxiliary_bytes", ctypes.c_size_t)]
+
+
+class SessionConfig(ctypes.Structure):
+    """gfxinfer_session_config (qwen_runtime.h:23-29 DecodeSessionConfig)."""
+    _fields_ = [("maximum_context_tokens", ctypes.c_size_t), ("graph_verifier_batch", ctypes.c_uint32)]
+
+
+class SessionSummary(ctypes.Structure):
+    """gfxinfer_session_summary (qwen_runtime.h:31-37)."""
+    _fields_ = [(name, ctypes.c_size_t) for name in (
+        "arena_bytes", "maximum_context_tokens", "gdn_state_bytes", "kv_cache_bytes", "mtp_cache_bytes")]
+
+
+class SpeculativeResult(ctypes.Structure):
+    """gfxinfer_speculative_result (qwen_runtime.h:39-45 SpeculativeStepResult)."""
+    _fields_ = [("tokens", ctypes.c_uint32 * 32), ("token_count", ctypes.c_uint32),
+                ("proposed_drafts", ctypes.c_uint32), ("accepted_drafts", ctypes.c_uint32)]
+
+
+@dataclass
+class SpeculativeStepResult:
+    tokens: list[int]
+    proposed_drafts: int
+    accepted_drafts: int
+
+
+class SyntheticModel:
+    """Seeded synthetic checkpoint on one device (Engine::create equivalent)."""
+
+    def __init__(self, spec: ModelSpec, seed: int, device: int = 0):
+        self.spec = spec
+        self.seed = seed
+        handle = ctypes.c_void_p()
+        check(lib().gfxinfer_model_create_synthetic(ctypes.byref(spec), seed, device, ctypes.byref(handle)))
+        self._handle = handle
+
+    @property
+    def handle(self):
+        if self._handle is None:
+            raise GfxinferError(1, "model was closed")
+        return self._handle
+
+    def close(self):
+        if self._handle is not None:
+            lib().gfxinfer_model_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def weight_bytes(self) -> int:
+        return int(lib().gfxinfer_model_weight_bytes(self.handle))
+
+    @property
+    def stream(self) -> int:
+        return lib().gfxinfer_model_stream(self.handle)
+
+    def find_tensor(self, name: str) -> TensorView:
+        view = TensorView()
+        check(lib().gfxinfer_model_find_tensor(self.handle, name.encode(), ctypes.byref(view)))
+        return view
+
+    def tensor_bytes(self, name: str, auxiliary: bool = False) -> np.ndarray:
+        view = self.find_tensor(name)
+        n = view.auxiliary_bytes if auxiliary else view.data_bytes
+        out = np.empty(n, np.uint8)
+        check(lib().gfxinfer_model_copy_tensor(self.handle, name.encode(), int(auxiliary),
+                                               out.ctypes.data, n))
+        return out
+
+
+class QwenDecodeSession:
+    """QwenDecodeSession (qwen_runtime.h:47-77) over a SyntheticModel."""
+
+    def __init__(self, model: SyntheticModel, maximum_context_tokens: int = 4096,
+                 graph_verifier_batch: int = 0):
+        self.model = model
+        config = SessionConfig(maximum_context_tokens, graph_verifier_batch)
+        handle = ctypes.c_void_p()
+        check(lib().gfxinfer_session_create(model.handle, ctypes.byref(config), ctypes.byref(handle)))
+        self._handle = handle
+
+    def close(self):
+        if self._handle is not None:
+            lib().gfxinfer_session_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def greedy_step(self, token: int) -> int:
+        out = U32()
+        check(lib().gfxinfer_session_greedy_step(self._handle, token, ctypes.byref(out)))
+        return out.value
+
+    def block_step(self, tokens) -> list[int]:
+        arr = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros(len(arr), np.uint32)
+        check(lib().gfxinfer_session_block_step(self._handle, arr.ctypes.data, len(arr), out.ctypes.data))
+        return [int(x) for x in out]
+
+    def mtp_draft(self, token: int) -> int:
+        out = U32()
+        check(lib().gfxinfer_session_mtp_draft(self._handle, token, ctypes.byref(out)))
+        return out.value
+
+    @staticmethod
+    def _result(r: SpeculativeResult) -> SpeculativeStepResult:
+        return SpeculativeStepResult([int(r.tokens[i]) for i in range(r.token_count)],
+                                     int(r.proposed_drafts), int(r.accepted_drafts))
+
+    def speculative_step(self, seed: int, draft_count: int) -> SpeculativeStepResult:
+        r = SpeculativeResult()
+        check(lib().gfxinfer_session_speculative_step(self._handle, seed, draft_count, ctypes.byref(r)))
+        return self._result(r)
+
+    def speculative_step_forced(self, seed: int, draft_count: int, accepted: int) -> SpeculativeStepResult:
+        r = SpeculativeResult()
+        check(lib().gfxinfer_session_speculative_step_forced(self._handle, seed, draft_count, accepted,
+                                                             ctypes.byref(r)))
+        return self._result(r)
+
+    def speculative_step_planted(self, seed: int, drafts) -> SpeculativeStepResult:
+        arr = np.ascontiguousarray(drafts, dtype=np.uint32)
+        r = SpeculativeResult()
+        check(lib().gfxinfer_session_speculative_step_planted(self._handle, seed, len(arr), arr.ctypes.data,
+                                                              ctypes.byref(r)))
+        return self._result(r)
+
+    def position(self) -> int:
+        return int(lib().gfxinfer_session_position(self._handle))
+
+    def mtp_position(self) -> int:
+        return int(lib().gfxinfer_session_mtp_position(self._handle))
+
+    def summary(self) -> SessionSummary:
+        s = SessionSummary()
+        check(lib().gfxinfer_session_get_summary(self._handle, ctypes.byref(s)))
+        return s
+
+    def buffer(self, name: str, dtype=np.uint8, count: int | None = None, offset: int = 0) -> np.ndarray:
+        """Copy of a named session buffer (test accessor)."""
+        total = int(lib().gfxinfer_session_buffer_bytes(self._handle, name.encode()))
+        if total == 0:
+            raise GfxinferError(1, f"unknown session buffer {name}")
+        itemsize = np.dtype(dtype).itemsize
+        nbytes = (total - offset) if count is None else count * itemsize
+        out = np.empty(nbytes // itemsize, dtype)
+        check(lib().gfxinfer_session_copy_buffer(self._handle, name.encode(), offset, out.ctypes.data,
+                                                 out.nbytes))
+        return out

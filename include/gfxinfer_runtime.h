@@ -1,0 +1,168 @@
+/*
+ * gfxinfer_amd runtime: the MTP speculative-decoding session behind a C ABI.
+ *
+ * Replaces the reference's C++ runtime entry points (include/gfxinfer/engine.h,
+ * include/gfxinfer/qwen_runtime.h) with opaque handles and plain structs:
+ *  - gfxinfer_model    ~ gfxinfer::Engine: one device arena of weights in the gfx950
+ *                        tile layout plus the compute stream;
+ *  - gfxinfer_session  ~ gfxinfer::QwenDecodeSession: session arena, 64-layer
+ *                        verifier, MTP proposal chain, GDN rollback, hipGraphs.
+ * Status codes and gfxinfer_last_error() are those of gfxinfer_amd.h.  Every
+ * call runs on the model's compute stream; step calls synchronize it before they
+ * return, as the reference methods do.  Handles are single-owner and not
+ * thread-safe (qwen_runtime.h:47-77).
+ */
+#ifndef GFXINFER_RUNTIME_H
+#define GFXINFER_RUNTIME_H
+
+#include "gfxinfer_amd.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model shape.  The reference bakes these into include/gfxinfer/qwen38_spec.h:15-48
+ * (Qwen38Spec); here they are fields so the same code runs the 27B-shaped model and
+ * small test models. */
+typedef struct gfxinfer_model_spec {
+  uint32_t hidden_size;               /* qwen38_spec.h:18 */
+  uint32_t intermediate_size;         /* :19 */
+  uint32_t layer_count;               /* :20 */
+  uint32_t full_attention_interval;   /* :21; layer i is attention iff (i+1) % interval == 0 */
+  uint32_t attention_head_count;      /* :22 */
+  uint32_t kv_head_count;             /* :23 */
+  uint32_t attention_head_size;       /* :24; must be 128 */
+  uint32_t rotary_size;               /* :25 */
+  uint32_t gdn_key_head_count;        /* :26 */
+  uint32_t gdn_value_head_count;      /* :28 */
+  uint32_t gdn_head_size;             /* :27, :29; must be 128 */
+  uint32_t vocabulary_size;           /* :16; LM head and embedding rows */
+  uint32_t tokenizer_vocabulary_size; /* :17; argmax range of the verifier */
+  uint32_t mtp_draft_vocabulary;      /* qwen_runtime.cpp:47 kMtpDraftVocabulary */
+  uint32_t w3_mlp_layers;             /* converter.cpp:98-119: MLP of layers < this is W3, else W4 */
+  float rms_norm_epsilon;             /* qwen38_spec.h:33 */
+  float rope_theta;                   /* qwen38_spec.h:34 */
+} gfxinfer_model_spec;
+
+/* Fills the synthetic Qwen3.8-27B shape: 64 layers (48 GDN + 16 attention), hidden 5120,
+ * MLP 17408 (W3 in layers 0-55, W4 in 56-63), attention 40 Q / 8 KV heads x 128 with
+ * rotary 64, GDN 16 key / 32 value heads x 128, vocabulary 151936, MTP shortlist 98304. */
+void gfxinfer_model_spec_qwen38_27b(gfxinfer_model_spec* spec);
+
+typedef struct gfxinfer_model gfxinfer_model;
+
+/* Engine::create (engine.h:80-86) for a synthetic checkpoint: allocates one device
+ * arena, fills every tensor of the converter's naming (converter.cpp:78-119) with seeded
+ * values and quantizes the 2-D ones on the device with the group-128 quantizer
+ * (W3 for MLP layers < w3_mlp_layers, W4 for every other matrix; norms, conv1d,
+ * A_log and dt_bias stay bf16).  Values: matrices N(0, 0.02); (1+w) norms N(0, 0.02);
+ * the GDN output norm 1 + N(0, 0.02); conv1d N(0, 0.5); A_log and dt_bias N(0, 0.5).
+ * The generator is a counter-based integer hash (splitmix64, Irwin-Hall of twelve
+ * 16-bit uniforms), so a CPU restatement reproduces every value bit for bit. */
+int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* spec, uint64_t seed,
+                                        int32_t device, gfxinfer_model** out);
+void gfxinfer_model_destroy(gfxinfer_model* model);
+/* Engine::compute_stream (engine.h:89): the hipStream_t every session call runs on. */
+void* gfxinfer_model_stream(const gfxinfer_model* model);
+size_t gfxinfer_model_weight_bytes(const gfxinfer_model* model);
+
+/* DeviceTensorView (engine.h:47-60).  format: GFXI_W3G128 / GFXI_W4G128 for tiled
+ * matrices (data = tiled codes, auxiliary = tiled fp16 scales), 0 for bf16 vectors
+ * (data = bf16 values, auxiliary = NULL). */
+typedef struct gfxinfer_tensor_view {
+  int32_t format;
+  uint64_t rows;
+  uint64_t columns;
+  void* data;
+  void* auxiliary;
+  size_t data_bytes;
+  size_t auxiliary_bytes;
+} gfxinfer_tensor_view;
+
+/* Engine::find_device_tensor (engine.h:87-88). */
+int32_t gfxinfer_model_find_tensor(const gfxinfer_model* model, const char* name,
+                                   gfxinfer_tensor_view* out);
+/* Copies a tensor's data (or auxiliary, when `auxiliary` is non-zero) into host memory
+ * of `bytes` bytes.  No reference counterpart: a test accessor. */
+int32_t gfxinfer_model_copy_tensor(const gfxinfer_model* model, const char* name,
+                                   int32_t auxiliary, void* host, size_t bytes);
+
+/* DecodeSessionConfig (qwen_runtime.h:23-29).  Activations are always A4G128 (the
+ * reference's ActivationMode::int4).  graph_verifier_batch: 0, or 2..32 to capture the
+ * MTP chain + verifier of depth graph_verifier_batch - 1 as hipGraphs. */
+typedef struct gfxinfer_session_config {
+  size_t maximum_context_tokens;
+  uint32_t graph_verifier_batch;
+} gfxinfer_session_config;
+
+/* DecodeSessionSummary (qwen_runtime.h:31-37). */
+typedef struct gfxinfer_session_summary {
+  size_t arena_bytes;
+  size_t maximum_context_tokens;
+  size_t gdn_state_bytes;
+  size_t kv_cache_bytes;
+  size_t mtp_cache_bytes;
+} gfxinfer_session_summary;
+
+/* SpeculativeStepResult (qwen_runtime.h:39-45): token_count = accepted_drafts + 1
+ * tokens, the accepted drafts then the target's correction or bonus token. */
+typedef struct gfxinfer_speculative_result {
+  uint32_t tokens[32];
+  uint32_t token_count;
+  uint32_t proposed_drafts;
+  uint32_t accepted_drafts;
+} gfxinfer_speculative_result;
+
+typedef struct gfxinfer_session gfxinfer_session;
+
+/* QwenDecodeSession::create (qwen_runtime.cpp:943-1262). */
+int32_t gfxinfer_session_create(gfxinfer_model* model, const gfxinfer_session_config* config,
+                                gfxinfer_session** out);
+void gfxinfer_session_destroy(gfxinfer_session* session);
+/* QwenDecodeSession::greedy_step (qwen_runtime.cpp:1264-1318). */
+int32_t gfxinfer_session_greedy_step(gfxinfer_session* session, uint32_t input_token,
+                                     uint32_t* output_token);
+/* QwenDecodeSession::block_step (qwen_runtime.cpp:1320-1392): 1..32 tokens;
+ * output_tokens receives one target token per input. */
+int32_t gfxinfer_session_block_step(gfxinfer_session* session, const uint32_t* input_tokens,
+                                    size_t count, uint32_t* output_tokens);
+/* QwenDecodeSession::mtp_draft (qwen_runtime.cpp:1394-1419). */
+int32_t gfxinfer_session_mtp_draft(gfxinfer_session* session, uint32_t next_token,
+                                   uint32_t* output_token);
+/* QwenDecodeSession::speculative_step (qwen_runtime.cpp:1421-1544): draft_count 1..31. */
+int32_t gfxinfer_session_speculative_step(gfxinfer_session* session, uint32_t seed_token,
+                                          size_t draft_count,
+                                          gfxinfer_speculative_result* result);
+/* speculative_step with an acceptance override, for benchmarks on synthetic weights
+ * whose drafts never match: accepted_drafts = forced_accepted (0..draft_count) whatever
+ * the comparison says; everything else (proposals, verifier, rollback or state swap,
+ * MTP cache advance) runs as in speculative_step.  No reference counterpart. */
+int32_t gfxinfer_session_speculative_step_forced(gfxinfer_session* session,
+                                                 uint32_t seed_token, size_t draft_count,
+                                                 uint32_t forced_accepted,
+                                                 gfxinfer_speculative_result* result);
+/* speculative_step whose verifier checks the given host drafts instead of the MTP
+ * chain's (the chain still runs and advances the MTP cache).  Test hook for
+ * planted-acceptance checks on synthetic weights; no reference counterpart. */
+int32_t gfxinfer_session_speculative_step_planted(gfxinfer_session* session,
+                                                  uint32_t seed_token, size_t draft_count,
+                                                  const uint32_t* planted_drafts,
+                                                  gfxinfer_speculative_result* result);
+/* QwenDecodeSession::position / summary (qwen_runtime.cpp:1546-1552). */
+size_t gfxinfer_session_position(const gfxinfer_session* session);
+size_t gfxinfer_session_mtp_position(const gfxinfer_session* session);
+int32_t gfxinfer_session_get_summary(const gfxinfer_session* session,
+                                 gfxinfer_session_summary* out);
+/* Copies `bytes` bytes from offset `offset` of a named session buffer into host memory
+ * ("logits", "hidden", "selected", "drafts", "conv_states", "gdn_states",
+ * "key_caches", "value_caches", "mtp_key_cache", "mtp_value_cache", "mtp_hidden").
+ * No reference counterpart: a test accessor. */
+int32_t gfxinfer_session_copy_buffer(const gfxinfer_session* session, const char* name,
+                                     size_t offset, void* host, size_t bytes);
+/* Byte size of a named session buffer (0 if unknown). */
+size_t gfxinfer_session_buffer_bytes(const gfxinfer_session* session, const char* name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -219,3 +219,50 @@ def dequant_dot_gemv_packed(codes, fmt, ws, a, as16, N, K):
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ---- synthetic checkpoint generator -----------------------------------------
+# CPU restatement of the counter-based generator of gfxinfer_model_create_synthetic
+# (gfxinfer_amd/csrc/model.hip): key = splitmix64(seed ^ fnv1a64(name)); element i
+# is mean + float(n_i) * (sigma * 2^-16) in fp32, n_i = the sum of the twelve 16-bit
+# fields of splitmix64(key + 3i + j), j = 0..2, plus 6 - 6 * 65536 (an exact
+# Irwin-Hall(12) numerator).  Not a reference algorithm: it only has to agree with
+# the device generator, which the runtime tests check bit for bit.
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _splitmix64(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        z = x + np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def name_hash(name: str) -> int:
+    h = 1469598103934665603
+    for c in name.encode():
+        h ^= c
+        h = (h * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def synthetic_values(seed: int, name: str, count: int, sigma: float, mean: float,
+                     first: int = 0) -> np.ndarray:
+    key = _splitmix64(np.array([np.uint64(seed) ^ np.uint64(name_hash(name))], dtype=np.uint64))[0]
+    idx = np.arange(first, first + count, dtype=np.uint64)
+    total = np.zeros(count, dtype=np.int64)
+    with np.errstate(over="ignore"):
+        for j in range(3):
+            h = _splitmix64(key + np.uint64(3) * idx + np.uint64(j))
+            for shift in (0, 16, 32, 48):
+                total += ((h >> np.uint64(shift)) & np.uint64(0xFFFF)).astype(np.int64)
+    n = (total + 6 - 6 * 65536).astype(np.float32)
+    scale = np.float32(sigma) * np.float32(2.0 ** -16)
+    return (np.float32(mean) + n * scale).astype(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)).astype(np.uint16)

@@ -149,6 +149,8 @@ CASES = [
     (3, 8, 64, 640, 3), (3, 8, 64, 640, 16),
     (2, 4, 17408, 5120, 5), (2, 4, 5120, 17408, 5), (3, 4, 17408, 5120, 5),
     (2, 4, 17408, 5120, 1), (2, 4, 17408, 5120, 32), (2, 8, 17408, 5120, 1),
+    # down projection at verify batches: K = 17408 needs the LDS wave cap at 32 tokens
+    (2, 4, 5120, 17408, 32), (3, 4, 5120, 17408, 16), (2, 8, 5120, 17408, 32),
 ]
 
 
