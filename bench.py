@@ -104,6 +104,100 @@ def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16):
                 weight_bytes=sum(c.numel() for c in codes) + 2 * sum(s.numel() for s in scales))
 
 
+def _forced_acceptance(rng, depth):
+    """Seeded Bernoulli(0.85) per draft; accepted = index of the first failure."""
+    trials = rng.random(depth) < 0.85
+    return int(depth if trials.all() else int(trials.argmin()))
+
+
+def _matrix_bytes(model, names):
+    total = 0
+    for name in names:
+        v = model.find_tensor(name)
+        total += int(v.data_bytes) + int(v.auxiliary_bytes)
+    return total
+
+
+def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026):
+    """Full synthetic 27B-shaped model: hipGraph-captured MTP chain +
+    64-layer verifier of depth D, forced seeded 85 % Bernoulli acceptance, rollback or
+    state swap per round.  Emitted tok/s = sum(accepted + 1) / time, verified tok/s =
+    sum(D + 1) / time (the reference's evaluated target tokens)."""
+    import numpy as np
+    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, qwen38_27b_spec
+
+    spec = qwen38_27b_spec()
+    t0 = time.perf_counter()
+    model = SyntheticModel(spec, seed)
+    create_s = time.perf_counter() - t0
+    names = [t for t in _tensor_names(spec)]
+    mtp = [n for n in names if n.startswith("mtp.")]
+    verifier = [n for n in names if not n.startswith("mtp.") and "embed_tokens" not in n]
+    head = model.find_tensor("lm_head.weight")
+    head_bytes = int(head.data_bytes) + int(head.auxiliary_bytes)
+    verifier_bytes = _matrix_bytes(model, verifier)
+    proposal_bytes = _matrix_bytes(model, mtp) + head_bytes * spec.mtp_draft_vocabulary // spec.vocabulary_size
+    results = {}
+    try:
+        for depth in depths:
+            session = QwenDecodeSession(model, 4096, depth + 1)
+            rng = np.random.default_rng(seed + depth)
+            token = session.greedy_step(1)
+            for _ in range(warmup):
+                token = session.speculative_step_forced(token, depth, _forced_acceptance(rng, depth)).tokens[-1]
+            emitted = verified = 0
+            n = min(rounds, (4096 - session.position()) // (depth + 1) - 1)
+            t0 = time.perf_counter()
+            for _ in range(n):
+                r = session.speculative_step_forced(token, depth, _forced_acceptance(rng, depth))
+                emitted += len(r.tokens)
+                verified += depth + 1
+                token = r.tokens[-1]
+            elapsed = time.perf_counter() - t0
+            session.close()
+            round_bytes = verifier_bytes + depth * proposal_bytes
+            results[f"depth_{depth}"] = {
+                "rounds": n,
+                "ms_per_round": round(elapsed / n * 1e3, 4),
+                "emitted_tok_s": round(emitted / elapsed, 2),
+                "verified_tok_s": round(verified / elapsed, 2),
+                "acceptance": round((emitted - n) / (n * depth), 4),
+                "weight_bytes_per_round": round_bytes,
+                "weight_gbs": round(round_bytes * n / elapsed / 1e9, 1),
+                "weight_frac_of_hbm_peak": round(round_bytes * n / elapsed / 1e9 / HBM_PEAK_GBS, 4),
+            }
+    finally:
+        model.close()
+    return {"model_weight_bytes": verifier_bytes + proposal_bytes, "create_s": round(create_s, 3),
+            "verifier_weight_bytes": verifier_bytes, "proposal_weight_bytes": proposal_bytes,
+            **results}
+
+
+def _tensor_names(spec):
+    """Matrix and vector names of the synthetic checkpoint (converter naming)."""
+    names = ["lm_head.weight", "model.language_model.norm.weight"]
+    for i in range(spec.layer_count):
+        p = f"model.language_model.layers.{i}."
+        names += [p + s for s in ("input_layernorm.weight", "post_attention_layernorm.weight",
+                                  "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")]
+        if (i + 1) % spec.full_attention_interval == 0:
+            names += [p + "self_attn." + s for s in ("q_proj.weight", "k_proj.weight", "v_proj.weight",
+                                                     "o_proj.weight", "q_norm.weight", "k_norm.weight")]
+        else:
+            names += [p + "linear_attn." + s for s in ("in_proj_qkv.weight", "in_proj_z.weight",
+                                                       "in_proj_a.weight", "in_proj_b.weight",
+                                                       "conv1d.weight", "A_log", "dt_bias", "norm.weight",
+                                                       "out_proj.weight")]
+    names += ["mtp.fc.weight", "mtp.pre_fc_norm_embedding.weight", "mtp.pre_fc_norm_hidden.weight",
+              "mtp.norm.weight"]
+    p = "mtp.layers.0."
+    names += [p + s for s in ("input_layernorm.weight", "post_attention_layernorm.weight",
+                              "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")]
+    names += [p + "self_attn." + s for s in ("q_proj.weight", "k_proj.weight", "v_proj.weight",
+                                             "o_proj.weight", "q_norm.weight", "k_norm.weight")]
+    return names
+
+
 def cpu_baseline(rows=17408, cols=5120, repeats=5):
     """Oracle W3A8 quantize + dequant-dot GEMV on host cores."""
     import numpy as np
@@ -152,6 +246,8 @@ def main():
     ap.add_argument("--steps", type=int, default=8000)
     ap.add_argument("--warmup", type=int, default=800)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--verify-rounds", type=int, default=60)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -198,6 +294,8 @@ def main():
         },
         "reference_packed_gbps": round(codes_only / (r["ms_step"] * 1e-3) / 1e9, 2),
     }
+    if not args.no_verify:
+        out["verify"] = verify_bench(rounds=args.verify_rounds)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

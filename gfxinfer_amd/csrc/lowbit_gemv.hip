@@ -200,10 +200,28 @@ struct GemmArgs {
   const uint8_t* activations;
   const __half* activation_scales;
   int32_t* partials;
+  unsigned long long* argmax_keys;  // [batch][tiles] tile-local argmax keys, or null
+  uint32_t argmax_rows;             // rows >= this never win the argmax
   uint32_t columns;
   uint32_t groups;
   uint32_t batch;
 };
+
+// Orderable argmax key of logit v at row: the high word orders values (a total
+// order on floats with -0 folded into +0), the low word is ~row so that equal
+// values keep the lowest row, as the strict > scan of argmax_logits does
+// (qwen_ops.hip:768-807).  NaN and -inf never win and map to 0, the key of
+// "no candidate" (the reference then returns index 0).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t row, uint32_t limit) {
+  if (row >= limit || !(v > -INFINITY)) return 0ull;
+  uint32_t bits = __float_as_uint(v == 0.0F ? 0.0F : v);
+  bits = (bits & 0x80000000u) != 0 ? ~bits : (bits | 0x80000000u);
+  return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - row);
+}
+
+__device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
+  return key == 0ull ? 0u : 0xffffffffu - static_cast<uint32_t>(key);
+}
 
 // Dynamic LDS: one private region per wave holding the activations of the
 // wave's current chunk of groups for every live token ([batch][pitch]), already
@@ -486,7 +504,28 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       }
     }
   }
-  if (window != 0) return;
+  if (args.argmax_keys != nullptr) {
+    // Fused greedy argmax: the best of the tile's 16 rows per token (rows 4kb+r of
+    // lanes n, n+16, n+32, n+48), one key per (token, tile).
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned long long key = argmax_key(acc[t][r], tile * 16u + 4u * kb + r, args.argmax_rows);
+        best = key > best ? key : best;
+      }
+      unsigned long long other = __shfl_xor(best, 16);
+      best = other > best ? other : best;
+      other = __shfl_xor(best, 32);
+      best = other > best ? other : best;
+      const unsigned token = t * 16u + slot;
+      if (kb == 0 && window == 0 && token < batch) {
+        args.argmax_keys[static_cast<std::size_t>(token) * matrix.tiles + tile] = best;
+      }
+    }
+  }
+  if (window != 0 || matrix.output == nullptr) return;
 #pragma unroll
   for (int t = 0; t < NTB; ++t) {
     if (t * 16u + slot >= batch) continue;
@@ -523,6 +562,32 @@ __global__ __launch_bounds__(256) void row_gather_kernel(
   const int w = unpack_lane_code(Format, chunk, static_cast<unsigned>(column % 32));
   output[column] = to_half(static_cast<float>(w) *
                                 __half2float(scales[scale_offset(row, column / kGroup, groups)]));
+}
+
+// Second half of the fused argmax: the best tile key of each token row.
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long long* __restrict__ keys,
+                                                          uint32_t count,
+                                                          const uint32_t* __restrict__ token_ids,
+                                                          uint32_t* __restrict__ out) {
+  __shared__ unsigned long long partial[4];
+  const unsigned long long* row = keys + static_cast<std::size_t>(blockIdx.x) * count;
+  unsigned long long best = 0ull;
+  for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+    const unsigned long long k = row[i];
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) {
+    const unsigned long long other = __shfl_xor(best, offset);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (unsigned w = 1; w < blockDim.x / 64; ++w) best = partial[w] > best ? partial[w] : best;
+    const uint32_t index = argmax_key_row(best);
+    out[blockIdx.x] = token_ids != nullptr ? token_ids[index] : index;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -601,7 +666,8 @@ struct MatrixBinding {
 int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindings,
                    std::size_t count, int32_t activation_bits, const void* activations,
                    const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
-                   uint32_t batch, bool half_out, hipStream_t stream) {
+                   uint32_t batch, bool half_out, hipStream_t stream,
+                   unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W3G128 and W4G128");
   }
@@ -621,7 +687,8 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   for (std::size_t i = 0; i < count; ++i) {
     const MatrixBinding& b = bindings[i];
     if (b.weights == nullptr || b.scales == nullptr ||
-        (partials == nullptr && b.output == nullptr) || b.rows == 0 || b.rows % 16 != 0) {
+        (partials == nullptr && argmax_keys == nullptr && b.output == nullptr) || b.rows == 0 ||
+        b.rows % 16 != 0) {
       return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " matrix binding is invalid");
     }
     if (!aligned(b.weights, 16) || !aligned(b.scales, 8) ||
@@ -645,6 +712,8 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   args.activations = static_cast<const uint8_t*>(activations);
   args.activation_scales = reinterpret_cast<const __half*>(activation_scales);
   args.partials = partials;
+  args.argmax_keys = argmax_keys;
+  args.argmax_rows = argmax_rows;
   args.columns = static_cast<uint32_t>(columns);
   args.groups = static_cast<uint32_t>(columns / kGroup);
   args.batch = batch;
@@ -815,6 +884,34 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
   return gemm_entry("gfx950 fused INT4 GEMM", format, bindings, matrix_count, 4,
                     packed_activations, activation_scales, nullptr, columns, batch, false,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch) {
+  return ((rows + 15) / 16) * static_cast<std::size_t>(batch) * sizeof(unsigned long long);
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(
+    int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_weight_scales,
+    const uint8_t* packed_activations, const uint16_t* activation_scales, float* logits,
+    size_t rows, size_t columns, uint32_t batch, size_t argmax_rows, const uint32_t* token_ids,
+    void* workspace, size_t workspace_bytes, uint32_t* tokens, void* stream) {
+  if (tokens == nullptr || workspace == nullptr || argmax_rows == 0 || argmax_rows > rows ||
+      rows > 0xffffffffu || workspace_bytes < gfxinfer_gemm_argmax_workspace_bytes(rows, batch) ||
+      !aligned(workspace, 8)) {
+    return fail(GFXI_INVALID_ARGUMENT, "fused GEMM argmax needs tokens, 1 <= argmax rows <= rows "
+                                       "and an 8-byte aligned workspace of "
+                                       "gfxinfer_gemm_argmax_workspace_bytes() bytes");
+  }
+  const MatrixBinding binding{tiled_weights, tiled_weight_scales, logits, rows};
+  auto* keys = static_cast<unsigned long long*>(workspace);
+  auto s = static_cast<hipStream_t>(stream);
+  const int32_t status = gemm_entry("fused GEMM argmax", format, &binding, 1, 4, packed_activations,
+                                    activation_scales, nullptr, columns, batch, false, s, keys,
+                                    static_cast<uint32_t>(argmax_rows));
+  if (status != GFXI_OK) return status;
+  hipLaunchKernelGGL(argmax_keys_kernel, dim3(batch), dim3(256), 0, s, keys,
+                     static_cast<uint32_t>(rows / 16), token_ids, tokens);
+  return launch_status("fused GEMM argmax reduction launch failed");
 }
 
 extern "C" int32_t gfxinfer_launch_gfx950_i8_gemm(int32_t format, const uint8_t* tiled_weights,

@@ -5,6 +5,7 @@
 //
 // Reference semantics: src/kernels/qwen_ops.hip.  Shapes the reference bakes in
 // (48 value heads, 16 key heads, 24/4 attention heads x 256) are parameters here.
+#include <algorithm>
 #include <cmath>
 #include <limits>
 #include <string>
@@ -121,6 +122,66 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
 }
 
+// Register-resident variant for rows of up to kNormSlots * 16 * 128 elements (even
+// count): one workgroup of up to 16 waves per row, wave w owns 128-element slots
+// w, w + waves, ...; each lane keeps its two values per slot in registers, so the
+// row is read once, reduced once and (Quantize) each 128 group is one wave's A4
+// quantizer.  Same arithmetic per element as rms_norm_kernel.
+constexpr unsigned kNormSlots = 10;
+constexpr uint32_t kNormFastMax = kNormSlots * 16u * 128u;
+
+template <bool Residual, bool Quantize>
+__global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
+    const __half* __restrict__ input, const float* __restrict__ update,
+    __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
+    __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
+    uint32_t elements, float epsilon, bool unit_offset) {
+  __shared__ float scratch[16];
+  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
+  float x[kNormSlots][2];
+  float square = 0.0F;
+#pragma unroll
+  for (unsigned j = 0; j < kNormSlots; ++j) {
+    x[j][0] = 0.0F;
+    x[j][1] = 0.0F;
+    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    if (i < elements) {
+      const __half2 h = *reinterpret_cast<const __half2*>(input + base + i);
+      __half a = __low2half(h), b = __high2half(h);
+      if constexpr (Residual) {
+        const float2 u = *reinterpret_cast<const float2*>(update + base + i);
+        a = to_half(__half2float(a) + u.x);
+        b = to_half(__half2float(b) + u.y);
+        *reinterpret_cast<__half2*>(residual_out + base + i) = __halves2half2(a, b);
+      }
+      x[j][0] = __half2float(a);
+      x[j][1] = __half2float(b);
+      square = fmaf(x[j][0], x[j][0], square);
+      square = fmaf(x[j][1], x[j][1], square);
+    }
+  }
+  const float total = block_sum(square, scratch);
+  const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
+#pragma unroll
+  for (unsigned j = 0; j < kNormSlots; ++j) {
+    const uint32_t g = wave + j * waves;
+    const uint32_t i = g * 128u + 2u * lane;
+    if (g * 128u >= elements) break;  // wave-uniform
+    __half n0 = __float2half(0.0F), n1 = n0;
+    if (i < elements) {
+      n0 = to_half(x[j][0] * inverse * norm_scale(weight, i, unit_offset));
+      n1 = to_half(x[j][1] * inverse * norm_scale(weight, i + 1, unit_offset));
+      if (output != nullptr) *reinterpret_cast<__half2*>(output + base + i) = __halves2half2(n0, n1);
+    }
+    if constexpr (Quantize) {
+      const uint32_t groups = elements / 128u;
+      quantize_group_a4(n0, n1, codes + static_cast<std::size_t>(blockIdx.x) * (elements / 2) + g * 64u,
+                        scales + static_cast<std::size_t>(blockIdx.x) * groups + g, lane);
+    }
+  }
+}
+
 // qwen_ops.hip:65-106: two RMSNorms written side by side.
 __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
     const __half* __restrict__ left, const uint16_t* __restrict__ left_weight,
@@ -178,13 +239,21 @@ __global__ void float_to_half_kernel(const float* __restrict__ in, __half* __res
 // GDN causal depthwise conv (qwen_ops.hip:219-261).  Thread per channel.
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void gdn_conv_kernel(
+template <unsigned MaxTokens>
+__global__ __launch_bounds__(64) void gdn_conv_kernel(
     const float* __restrict__ projected, const uint16_t* __restrict__ weight,
     const __half* initial_state, __half* final_state,  // may alias (in-place update)
     __half* __restrict__ output, __half* __restrict__ appended_log, uint32_t channels,
     uint32_t tokens) {
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= channels) return;
+  // Every token's input is loaded up front (independent loads, one latency); the
+  // conv is a window over inputs, not a recurrence.
+  __half x[MaxTokens];
+#pragma unroll
+  for (unsigned t = 0; t < MaxTokens; ++t) {
+    if (t < tokens) x[t] = to_half(projected[static_cast<std::size_t>(t) * channels + c]);
+  }
   __half state[4];
   float w[4];
 #pragma unroll
@@ -192,16 +261,19 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(
     state[tap] = initial_state[static_cast<std::size_t>(c) * 4 + tap];
     w[tap] = bf16_to_float(weight[static_cast<std::size_t>(c) * 4 + tap]);
   }
-  for (uint32_t t = 0; t < tokens; ++t) {
-    state[0] = state[1];
-    state[1] = state[2];
-    state[2] = state[3];
-    state[3] = to_half(projected[static_cast<std::size_t>(t) * channels + c]);
-    if (appended_log != nullptr) appended_log[static_cast<std::size_t>(t) * channels + c] = state[3];
-    float conv = 0.0F;
 #pragma unroll
-    for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(state[tap]), w[tap], conv);
-    output[static_cast<std::size_t>(t) * channels + c] = to_half(silu(conv));
+  for (unsigned t = 0; t < MaxTokens; ++t) {
+    if (t < tokens) {
+      state[0] = state[1];
+      state[1] = state[2];
+      state[2] = state[3];
+      state[3] = x[t];
+      if (appended_log != nullptr) appended_log[static_cast<std::size_t>(t) * channels + c] = state[3];
+      float conv = 0.0F;
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(state[tap]), w[tap], conv);
+      output[static_cast<std::size_t>(t) * channels + c] = to_half(silu(conv));
+    }
   }
 #pragma unroll
   for (int tap = 0; tap < 4; ++tap) final_state[static_cast<std::size_t>(c) * 4 + tap] = state[tap];
@@ -596,6 +668,29 @@ int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_
   auto* ro = reinterpret_cast<__half*>(residual_out);
   auto* out = reinterpret_cast<__half*>(output);
   auto* sc = reinterpret_cast<__half*>(scales);
+  auto aligned = [](const void* p, std::uintptr_t a) {
+    return p == nullptr || reinterpret_cast<std::uintptr_t>(p) % a == 0;
+  };
+  if (e % 2 == 0 && e <= kNormFastMax && aligned(input, 4) && aligned(residual_out, 4) &&
+      aligned(output, 4) && aligned(update, 8)) {
+    const unsigned slots = (e + 127u) / 128u;
+    const unsigned waves = std::min(16u, slots);  // slots <= 16 * kNormSlots by kNormFastMax
+    const dim3 block(64u * waves);
+    if (residual && quantize) {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<true, true>), dim3(batch), block, 0, stream, in, update,
+                         ro, weight, out, codes, sc, e, epsilon, unit);
+    } else if (residual) {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<true, false>), dim3(batch), block, 0, stream, in,
+                         update, ro, weight, out, codes, sc, e, epsilon, unit);
+    } else if (quantize) {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<false, true>), dim3(batch), block, 0, stream, in,
+                         update, ro, weight, out, codes, sc, e, epsilon, unit);
+    } else {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<false, false>), dim3(batch), block, 0, stream, in,
+                         update, ro, weight, out, codes, sc, e, epsilon, unit);
+    }
+    return launch_status((std::string(name) + " launch failed").c_str());
+  }
   if (residual && quantize) {
     hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(batch), dim3(256), smem, stream, in, update, ro,
                        weight, out, codes, sc, e, epsilon, unit);
@@ -742,7 +837,10 @@ extern "C" int32_t gfxinfer_launch_gdn_conv_update_block(
     return fail(GFXI_INVALID_ARGUMENT, "invalid block GDN convolution arguments");
   }
   const auto c = static_cast<uint32_t>(channels);
-  hipLaunchKernelGGL(gdn_conv_kernel, dim3((c + 255) / 256), dim3(256), 0,
+  if (batch > kGdnMaxTokens) {
+    return fail(GFXI_INVALID_ARGUMENT, "block GDN convolution supports at most 32 tokens");
+  }
+  hipLaunchKernelGGL(gdn_conv_kernel<kGdnMaxTokens>, dim3((c + 63) / 64), dim3(64), 0,
                      static_cast<hipStream_t>(stream), projected_qkv, bf16_conv_weight,
                      reinterpret_cast<const __half*>(initial_conv_state),
                      reinterpret_cast<__half*>(final_conv_state), reinterpret_cast<__half*>(convolved_qkv),

@@ -161,6 +161,8 @@ struct gfxinfer_session {
   float *projected_main{}, *projected_z{}, *projected_a{}, *projected_b{}, *projected_k{};
   float *projected_v{}, *gdn_mixed{}, *mixer_update{}, *gate_output{}, *up_output{};
   float *mlp_update{}, *logits{}, *attention_workspace{};
+  void* argmax_keys{};
+  std::size_t argmax_keys_bytes{0};
   std::size_t attention_workspace_bytes{0};
   uint32_t *selected{}, *draft_tokens{}, *verify_drafts{}, *result{}, *graph_seed{};
   int32_t* graph_forced{};
@@ -213,6 +215,15 @@ struct gfxinfer_session {
     }
     return gfxinfer_launch_gfx950_i4_gemm_fused(first->format, bind.data(), n, act_codes,
                                                 act_scales, first->columns, batch, 0, stream);
+  }
+
+  // Head projection fused with greedy argmax (qwen_runtime.cpp:635-639, 859-866); the
+  // fp32 logits are kept only when the session was configured to keep them.
+  int32_t gemm_argmax(const Matrix& m, unsigned batch, std::size_t argmax_rows, uint32_t* tokens) {
+    return gfxinfer_launch_gfx950_i4_gemm_argmax(
+        m.format, m.weights, m.scales, act_codes, act_scales,
+        config.keep_logits != 0 ? logits : nullptr, m.rows, m.columns, batch, argmax_rows, nullptr,
+        argmax_keys, argmax_keys_bytes, tokens, stream);
   }
 
   int32_t gather(uint16_t* destination, uint32_t token, const uint32_t* indirect) {
@@ -334,9 +345,7 @@ struct gfxinfer_session {
       GFXI_TRY(layer_block(layers[i], current, next, batch, next_norm, device_position));
       std::swap(current, next);
     }
-    GFXI_TRY(gemm(lm_head, logits, batch));
-    return gfxinfer_launch_argmax_batch(logits, selected, spec.tokenizer_vocabulary_size, V, batch,
-                                        stream);
+    return gemm_argmax(lm_head, batch, spec.tokenizer_vocabulary_size, selected);
   }
 
   // qwen_runtime.cpp:546-640 enqueue_verifier_body: seed + D drafts (device ids).
@@ -370,9 +379,7 @@ struct gfxinfer_session {
                              output_token == nullptr));
     if (output_token == nullptr) return ok();
     GFXI_TRY(mlp_tail(mtp, mtp_input, mtp_hidden, mtp_final_norm, 1));
-    GFXI_TRY(gemm(draft_head, logits, 1));
-    return gfxinfer_launch_argmax_batch(logits, output_token, spec.mtp_draft_vocabulary, V, 1,
-                                        stream);
+    return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, output_token);
   }
 
   // The D proposals then the verifier with rollback logging (qwen_runtime.cpp:1448-1467,
@@ -685,6 +692,7 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
   const std::size_t max_k = std::max({s->I, 2 * s->H, s->attn_width, s->gdn_value});
   s->attention_workspace_bytes =
       gfxinfer_attention_workspace_bytes(kMaxBlock, sp.attention_head_count, ctx);
+  s->argmax_keys_bytes = gfxinfer_gemm_argmax_workspace_bytes(s->V, kMaxBlock);
   const std::size_t conv_bytes = s->gdn_layers * s->conv_state_elements() * 2;
   const std::size_t gdn_bytes = s->gdn_layers * s->gdn_state_elements() * 4;
   const std::size_t kv_bytes = s->attn_layers * ctx * s->kv_rows * 2;
@@ -716,6 +724,7 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
       {"up_output", reinterpret_cast<void**>(&s->up_output), B * s->I * 4},
       {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), B * s->H * 4},
       {"logits", reinterpret_cast<void**>(&s->logits), B * s->V * 4},
+      {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
       {"attention_workspace", reinterpret_cast<void**>(&s->attention_workspace),
        s->attention_workspace_bytes},
       {"selected", reinterpret_cast<void**>(&s->selected), B * 4},

@@ -61,7 +61,8 @@ class TensorView(ctypes.Structure):
 
 class SessionConfig(ctypes.Structure):
     """gfxinfer_session_config (qwen_runtime.h:23-29 DecodeSessionConfig)."""
-    _fields_ = [("maximum_context_tokens", ctypes.c_size_t), ("graph_verifier_batch", ctypes.c_uint32)]
+    _fields_ = [("maximum_context_tokens", ctypes.c_size_t), ("graph_verifier_batch", ctypes.c_uint32),
+                ("keep_logits", ctypes.c_int32)]
 
 
 class SessionSummary(ctypes.Structure):
@@ -136,9 +137,9 @@ class QwenDecodeSession:
     """QwenDecodeSession (qwen_runtime.h:47-77) over a SyntheticModel."""
 
     def __init__(self, model: SyntheticModel, maximum_context_tokens: int = 4096,
-                 graph_verifier_batch: int = 0):
+                 graph_verifier_batch: int = 0, keep_logits: bool = False):
         self.model = model
-        config = SessionConfig(maximum_context_tokens, graph_verifier_batch)
+        config = SessionConfig(maximum_context_tokens, graph_verifier_batch, int(keep_logits))
         handle = ctypes.c_void_p()
         check(lib().gfxinfer_session_create(model.handle, ctypes.byref(config), ctypes.byref(handle)))
         self._handle = handle

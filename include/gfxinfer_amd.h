@@ -131,6 +131,26 @@ int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
                                              uint32_t batch, int32_t sequential_w3,
                                              void* stream);
 
+/* Bytes of workspace gfxinfer_launch_gfx950_i4_gemm_argmax needs: one 8-byte key per
+ * (token, 16-row tile). */
+size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch);
+
+/* W{3,4}G128 x A4G128 projection fused with greedy argmax: tokens[b] = the row of the
+ * largest logit among rows [0, argmax_rows) (ties to the lowest row, NaN never wins,
+ * index 0 when nothing wins), remapped through token_ids when it is not NULL.  Replaces
+ * the LM-head projection + launch_argmax_batch pair of the verifier tail
+ * (qwen_runtime.cpp:635-639) and the draft head + launch_argmax_mapped pair of the MTP
+ * step (qwen_runtime.cpp:859-866) with two launches and no logits round trip; logits
+ * [batch, rows] are written too when `logits` is not NULL. */
+int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(int32_t format, const uint8_t* tiled_weights,
+                                              const uint16_t* tiled_weight_scales,
+                                              const uint8_t* packed_activations,
+                                              const uint16_t* activation_scales, float* logits,
+                                              size_t rows, size_t columns, uint32_t batch,
+                                              size_t argmax_rows, const uint32_t* token_ids,
+                                              void* workspace, size_t workspace_bytes,
+                                              uint32_t* tokens, void* stream);
+
 /* lowbit_gemv.h:147-157 (launch_gfx12_i8_gemm): W{3,4}G128 x A8G128 -> fp32.
  * The reference accepts W2/W4 only; W3 x A8 is added here. */
 int32_t gfxinfer_launch_gfx950_i8_gemm(int32_t format, const uint8_t* tiled_weights,

@@ -89,10 +89,13 @@ int32_t gfxinfer_model_copy_tensor(const gfxinfer_model* model, const char* name
 
 /* DecodeSessionConfig (qwen_runtime.h:23-29).  Activations are always A4G128 (the
  * reference's ActivationMode::int4).  graph_verifier_batch: 0, or 2..32 to capture the
- * MTP chain + verifier of depth graph_verifier_batch - 1 as hipGraphs. */
+ * MTP chain + verifier of depth graph_verifier_batch - 1 as hipGraphs.  keep_logits:
+ * non-zero also writes the fp32 logits of every head projection to the "logits" buffer
+ * (a test accessor; the argmax is fused into the projection either way). */
 typedef struct gfxinfer_session_config {
   size_t maximum_context_tokens;
   uint32_t graph_verifier_batch;
+  int32_t keep_logits;
 } gfxinfer_session_config;
 
 /* DecodeSessionSummary (qwen_runtime.h:31-37). */

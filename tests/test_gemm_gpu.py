@@ -251,3 +251,52 @@ def test_row_gather(device, gx, orc, fmt):
     idx = dev(np.array([rows + 5], np.uint32))  # out of range -> zeros (lowbit_gemv.hip:202-205)
     gx.launch_row_gather_tiled_indirect(fmt, dw, dws, out, idx, rows, cols)
     assert np.all(host(out, np.uint16) == 0)
+
+
+def _gemm_argmax(gx, fmt, p, rows, cols, batch, argmax_rows, ids=None, logits=True):
+    ws_bytes = gx.lib().gfxinfer_gemm_argmax_workspace_bytes(rows, batch)
+    work = empty((ws_bytes // 8,), np.uint64)
+    tokens = empty((batch,), np.uint32)
+    y = empty((batch, rows), np.float32) if logits else None
+    dids = dev(ids) if ids is not None else None
+    dw, dws, da, das = dev(p["tiled"]), dev(p["tscales"]), dev(p["acts"]), dev(p["as16"])
+    say("gemm argmax", fmt, rows, cols, batch, argmax_rows)
+    gx.check(gx.lib().gfxinfer_launch_gfx950_i4_gemm_argmax(
+        fmt, dw.data_ptr(), dws.data_ptr(), da.data_ptr(), das.data_ptr(),
+        None if y is None else y.data_ptr(), rows, cols, batch, argmax_rows,
+        None if dids is None else dids.data_ptr(), work.data_ptr(), ws_bytes, tokens.data_ptr(), None))
+    return host(tokens, np.uint32), (host(y) if y is not None else None)
+
+
+@pytest.mark.parametrize("fmt,rows,cols,batch,limit", [
+    (3, 1024, 256, 1, 1024), (3, 1024, 256, 5, 1000), (3, 4096, 640, 32, 4000), (2, 2048, 512, 17, 2048),
+    (3, 151936, 5120, 5, 151936)])
+def test_gemm_argmax_matches_logits_argmax(device, gx, orc, fmt, rows, cols, batch, limit):
+    """LM head + fused greedy argmax == argmax (ties to the lowest index) of the same
+    GEMM's logits, and the logits match the oracle epilogue."""
+    p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=rows + batch)
+    tokens, y = _gemm_argmax(gx, fmt, p, rows, cols, batch, limit)
+    want = np.empty(batch, np.uint32)
+    orc.lib().orc_argmax(orc.ptr(np.ascontiguousarray(y)), limit, rows, batch, None, orc.ptr(want))
+    assert np.array_equal(tokens, want)
+    if rows * cols <= 4096 * 640:
+        want_y = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+        assert np.abs(y - want_y).max() <= 2e-5 * max(1e-30, float(np.abs(want_y).max()))
+    tokens_only, _ = _gemm_argmax(gx, fmt, p, rows, cols, batch, limit, logits=False)
+    assert np.array_equal(tokens_only, tokens)
+
+
+def test_gemm_argmax_ties_limit_and_mapping(device, gx, orc):
+    """Every row a copy of one row: all logits tie, so the lowest row wins; the
+    shortlist limit and the token-id map (argmax_mapped) apply."""
+    fmt, rows, cols, batch = 3, 512, 256, 3
+    p = _problem(orc, gx, fmt, 4, 16, cols, batch, seed=9)  # activations only
+    w = np.repeat(orc.synthetic_values(3, "tie", cols, 0.02, 0.0)[None, :], rows, axis=0)
+    _, codes, scales = orc.quantize_group128(w, fmt)
+    tiled, tscales = gx.tile_group128(fmt, codes, scales, rows, cols)
+    q = dict(p, tiled=tiled, tscales=tscales)
+    tokens, y = _gemm_argmax(gx, fmt, q, rows, cols, batch, rows)
+    assert (y == y[:, :1]).all() and (tokens == 0).all()
+    ids = (np.arange(rows, dtype=np.uint32) * 7 + 3) % 100000
+    tokens, _ = _gemm_argmax(gx, fmt, q, rows, cols, batch, 100, ids=ids)
+    assert (tokens == ids[0]).all()

@@ -276,18 +276,20 @@ def test_gdn_restore_rejects_bad_accept(gx):
     assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
 
 
-def test_gdn_conv(device, gx, orc):
-    T = 32
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("T,in_place", [(32, False), (5, True), (1, True)])
+def test_gdn_conv(device, gx, orc, T, in_place):
+    rng = np.random.default_rng(5 + T)
     proj = rng.standard_normal((T, C)).astype(np.float32)
     w = _bf16(rng.standard_normal((C, 4)) * 0.5)
     s0 = _half(rng.standard_normal((C, 4)))
     want_f, want_o, want_l = np.empty_like(s0), np.empty((T, C), np.uint16), np.empty((T, C), np.uint16)
     orc.lib().orc_gdn_conv_update(orc.ptr(proj), orc.ptr(w), orc.ptr(s0), orc.ptr(want_f), orc.ptr(want_o),
                                   orc.ptr(want_l), C, T)
-    fin, out, log = empty((C, 4), np.uint16), empty((T, C), np.uint16), empty((T, C), np.uint16)
-    say("gdn conv")
-    gx.check(gx.lib().gfxinfer_launch_gdn_conv_update_block(D_(proj), D_(w), D_(s0),
+    out, log = empty((T, C), np.uint16), empty((T, C), np.uint16)
+    state = dev(s0)
+    fin = state if in_place else empty((C, 4), np.uint16)
+    say("gdn conv", T, "in place" if in_place else "")
+    gx.check(gx.lib().gfxinfer_launch_gdn_conv_update_block(D_(proj), D_(w), state.data_ptr(),
                                                             fin.data_ptr(), out.data_ptr(), log.data_ptr(), C, T, None))
     assert np.array_equal(host(fin, np.uint16), want_f)
     assert np.array_equal(host(log, np.uint16), want_l)
