@@ -542,6 +542,380 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
 }
 
 // ---------------------------------------------------------------------------
+// Direct-operand GEMM.
+//
+// Same arithmetic as lowbit_gemm_kernel (one 16x16x64 MFMA pair per group, GP
+// token windows, per-pack fp32 epilogue), but the B operands never touch LDS:
+// each lane loads the 16 (A4) or 32 (A8) activation bytes of its own (token,
+// group, lane block) straight from the L2-resident activation codes and expands
+// them in registers with the same masks as the W4 weights; the window mask of
+// group j is folded into the expansion masks.  Out-of-range tokens and groups
+// read zeros through the buffer descriptor.  A wave reuses its activation
+// registers for R consecutive 16-row tiles, so the L2 traffic per weight byte
+// falls by R; LDS only holds the final cross-wave reduction, so occupancy is set
+// by registers alone.  Workgroup = R tiles x W waves splitting K.
+// ---------------------------------------------------------------------------
+
+// Two packed-nibble dwords -> four operand registers (value 16*x), AND-ed with m.
+__device__ __forceinline__ i32x4 expand_nibbles_masked(unsigned x0, unsigned x1, unsigned m) {
+  i32x4 r;
+  r[0] = static_cast<int>((x0 << 4) & m);
+  r[1] = static_cast<int>(x0 & m);
+  r[2] = static_cast<int>((x1 << 4) & m);
+  r[3] = static_cast<int>(x1 & m);
+  return r;
+}
+
+template <int Format, int ABits, int GP, int NTB, int CH, int R, bool HalfOut, bool Partials>
+__global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args) {
+  constexpr unsigned LB = lane_bytes(Format);
+  constexpr unsigned WD = LB / 4;                     // weight dwords per lane per group
+  constexpr unsigned TPAD = 16 / GP;                  // token slots per window
+  constexpr unsigned CHG = CH * GP;                   // groups per chunk
+  constexpr unsigned AGB = ABits == 4 ? 64u : 128u;   // activation bytes per token per group
+  constexpr unsigned AD = ABits == 4 ? 4u : 8u;       // activation dwords per lane per group
+  constexpr float kInvF =
+      1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
+  constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
+  constexpr unsigned kOut = 0x80000000u;              // voffset that reads zeros
+
+  extern __shared__ __align__(16) uint8_t lds_all[];
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned waves = blockDim.x >> 6;
+
+  unsigned block = blockIdx.x;
+  unsigned index = 0;
+#pragma unroll
+  for (unsigned i = 1; i < 4; ++i) {
+    if (block >= args.tile_begin[i]) index = i;
+  }
+  const GemmMatrix matrix = args.matrix[index];
+  block -= args.tile_begin[index];
+  const unsigned tile0 = block * R;
+  const unsigned valid = min(static_cast<unsigned>(R), matrix.tiles - tile0);  // wave-uniform
+  const uint32_t groups = args.groups;
+  const uint32_t batch = args.batch;
+  const uint32_t rows = matrix.tiles * 16u;
+  const uint32_t row_bytes = ABits == 4 ? args.columns / 2 : args.columns;
+  const uint32_t tile_bytes = groups * 64u * LB;
+  const auto weights = buffer(matrix.weights + static_cast<std::size_t>(tile0) * tile_bytes,
+                              valid * tile_bytes);
+  const auto weight_scales =
+      buffer(matrix.scales + static_cast<std::size_t>(tile0) * groups * 16u, valid * groups * 32u);
+  const auto activations = buffer(args.activations, batch * row_bytes);
+  // Scale rows are read as aligned dwords; the range is rounded up to the enclosing
+  // dword (never past the page of the last scale) so that the last half is not
+  // dropped by the descriptor's per-dword range check.
+  const auto act_scales = buffer(args.activation_scales, (batch * groups * 2u + 3u) & ~3u);
+
+  const unsigned n = lane & 15u;
+  const unsigned kb = lane >> 4;
+  const unsigned slot = n % TPAD;
+  const unsigned window = n / TPAD;
+  const unsigned w_voffset = lane * LB;
+  const unsigned ws_voffset = (window * 16u + 4u * kb) * 2u;
+  // With one window (GP == 1) the activation loads run in quad-coalesced order
+  // (lanes 4m..4m+3 read the 64 contiguous bytes of token m) and ds_bpermute routes
+  // each dword to MFMA order (lane kb*16 + n holds token n, lane block kb): in MFMA
+  // order each quad would touch four token rows, i.e. four cache lines.
+  constexpr bool kCoalesced = GP == 1 && ABits == 4;
+  const unsigned load_token = kCoalesced ? lane >> 2 : slot;
+  const unsigned load_piece = kCoalesced ? lane & 3u : kb;
+  const int permute_from = static_cast<int>((n * 4u + kb) * 4u);
+  unsigned a_voffset[NTB], as_voffset[NTB];
+#pragma unroll
+  for (int t = 0; t < NTB; ++t) {
+    const unsigned token = t * 16u + load_token;  // >= batch lands past the buffer: zeros
+    a_voffset[t] = token * row_bytes + window * AGB + load_piece * (AGB / 4u);
+    as_voffset[t] = ((t * 16u + slot) * groups + window) * 2u;
+  }
+
+  const unsigned packs = (groups + GP - 1) / GP;
+  const unsigned pack_begin = packs * wave / waves;
+  const unsigned pack_end = packs * (wave + 1) / waves;
+
+  float acc[R][NTB][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < NTB; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][t][i] = 0.0F;
+
+  for (unsigned base = pack_begin; base < pack_end; base += CH) {
+    // 1) Loads of CH packs: activations + their scales (L2), weights + scales (HBM).
+    unsigned areg[CH][NTB][AD];
+    unsigned short asreg[CH][NTB];
+    unsigned wreg[R][CHG][WD];
+    u32x2 wsreg[R][CH];
+    // GP == 1: the activation scales of the chunk's CH groups, one load per token block
+    // (a token's scales are contiguous over groups but may start at an odd half, so
+    // the aligned dwords around them are loaded and shifted into place; entries past
+    // the chunk or the row are never used).
+    constexpr unsigned kScaleDwords = (CH + 1) / 2 + 1;
+    static_assert(kScaleDwords <= 4, "chunk too long for one scale load");
+    unsigned asrow[NTB][4];
+    unsigned as_odd[NTB];
+    if constexpr (GP == 1 && !Partials) {
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        const unsigned first = (t * 16u + slot) * groups + base;  // half index
+        as_odd[t] = first & 1u;
+        const unsigned off = t * 16u + slot < batch ? (first & ~1u) * 2u : kOut;
+        if constexpr (kScaleDwords == 2) {
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(act_scales, off, 0, 0);
+          asrow[t][0] = v[0];
+          asrow[t][1] = v[1];
+        } else if constexpr (kScaleDwords == 3) {
+          const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(act_scales, off, 0, 0);
+          asrow[t][0] = v[0];
+          asrow[t][1] = v[1];
+          asrow[t][2] = v[2];
+        } else {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(act_scales, off, 0, 0);
+          asrow[t][0] = v[0];
+          asrow[t][1] = v[1];
+          asrow[t][2] = v[2];
+          asrow[t][3] = v[3];
+        }
+      }
+    }
+#pragma unroll
+    for (unsigned ci = 0; ci < CH; ++ci) {
+      const unsigned pack = min(base + ci, pack_end - 1u);
+      const bool live = pack * GP + window < groups;
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        const unsigned off = live ? a_voffset[t] : kOut;
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(activations, off, pack * GP * AGB, 0);
+        areg[ci][t][0] = x[0];
+        areg[ci][t][1] = x[1];
+        areg[ci][t][2] = x[2];
+        areg[ci][t][3] = x[3];
+        if constexpr (ABits == 8) {
+          const u32x4 y =
+              __builtin_amdgcn_raw_buffer_load_b128(activations, off + 16u, pack * GP * AGB, 0);
+          areg[ci][t][4] = y[0];
+          areg[ci][t][5] = y[1];
+          areg[ci][t][6] = y[2];
+          areg[ci][t][7] = y[3];
+        }
+        if constexpr (!Partials && GP > 1) {
+          asreg[ci][t] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, live ? as_voffset[t] : kOut,
+                                                              pack * GP * 2u, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (unsigned j = 0; j < GP; ++j) {
+          const unsigned g_offset = r * tile_bytes + (pack * GP + j) * 64u * LB;
+          if constexpr (Format == GFXI_W3G128) {
+            const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
+            wreg[r][ci * GP + j][0] = w[0];
+            wreg[r][ci * GP + j][1] = w[1];
+            wreg[r][ci * GP + j][2] = w[2];
+          } else {
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(weights, w_voffset, g_offset, kStreaming);
+            wreg[r][ci * GP + j][0] = w[0];
+            wreg[r][ci * GP + j][1] = w[1];
+            wreg[r][ci * GP + j][2] = w[2];
+            wreg[r][ci * GP + j][3] = w[3];
+          }
+        }
+        if constexpr (!Partials) {
+          wsreg[r][ci] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, ws_voffset,
+                                                              r * groups * 32u + pack * GP * 32u, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kCoalesced) {
+      // Quad-coalesced load order -> MFMA lane order.
+#pragma unroll
+      for (unsigned ci = 0; ci < CH; ++ci)
+#pragma unroll
+        for (int t = 0; t < NTB; ++t)
+#pragma unroll
+          for (unsigned d = 0; d < 4; ++d) {
+            areg[ci][t][d] = static_cast<unsigned>(
+                __builtin_amdgcn_ds_bpermute(permute_from, static_cast<int>(areg[ci][t][d])));
+          }
+    }
+    if constexpr (GP == 1 && !Partials) {
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        unsigned row[kScaleDwords - 1];
+#pragma unroll
+        for (unsigned d = 0; d + 1 < kScaleDwords; ++d) {
+          row[d] = __builtin_amdgcn_alignbit(asrow[t][d + 1], asrow[t][d], as_odd[t] * 16u);
+        }
+#pragma unroll
+        for (unsigned ci = 0; ci < CH; ++ci) {
+          // group base + ci sits at half ci of the shifted row (or is past pack_end)
+          asreg[ci][t] = static_cast<unsigned short>(row[ci / 2] >> ((ci & 1u) * 16u));
+        }
+      }
+    }
+    // 2) Compute.
+#pragma unroll
+    for (unsigned ci = 0; ci < CH; ++ci) {
+      const unsigned pack = base + ci;
+      if (pack >= pack_end) break;
+      // B operands of every group of the pack: this lane's activations where its
+      // window is the group's, zeros elsewhere.
+      i32x4 b[GP][NTB][2];
+#pragma unroll
+      for (unsigned j = 0; j < GP; ++j) {
+        const unsigned on = (GP == 1 || window == j) ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) {
+          if constexpr (ABits == 4) {
+            b[j][t][0] = expand_nibbles_masked(areg[ci][t][0], areg[ci][t][1], 0xF0F0F0F0u & on);
+            b[j][t][1] = expand_nibbles_masked(areg[ci][t][2], areg[ci][t][3], 0xF0F0F0F0u & on);
+          } else {
+            const i32x4 p0 = permute_i8(areg[ci][t][0], areg[ci][t][1], areg[ci][t][2], areg[ci][t][3]);
+            const i32x4 p1 = permute_i8(areg[ci][t][4], areg[ci][t][5], areg[ci][t][6], areg[ci][t][7]);
+            const int m = static_cast<int>(on);
+            b[j][t][0] = i32x4{p0[0] & m, p0[1] & m, p0[2] & m, p0[3] & m};
+            b[j][t][1] = i32x4{p1[0] & m, p1[1] & m, p1[2] & m, p1[3] & m};
+          }
+        }
+      }
+      float as[NTB];
+      if constexpr (!Partials) {
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) as[t] = __half2float(__ushort_as_half(asreg[ci][t])) * kInvF;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (static_cast<unsigned>(r) >= valid) break;  // wave-uniform: short last block
+        i32x4 c[NTB];
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (unsigned j = 0; j < GP; ++j) {
+          if (pack * GP + j >= groups) break;  // wave-uniform: partial last pack
+          i32x4 a0, a1;
+          const unsigned* w = wreg[r][ci * GP + j];
+          if constexpr (Format == GFXI_W3G128) {
+            expand_w3(w[0], w[1], w[2], a0, a1);
+          } else {
+            a0 = expand_nibbles(w[0], w[1]);
+            a1 = expand_nibbles(w[2], w[3]);
+          }
+#pragma unroll
+          for (int t = 0; t < NTB; ++t) {
+            c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b[j][t][0], c[t], 0, 0, 0);
+            c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b[j][t][1], c[t], 0, 0, 0);
+          }
+        }
+        const unsigned g_c = pack * GP + window;
+        if constexpr (Partials) {
+#pragma unroll
+          for (int t = 0; t < NTB; ++t) {
+            const unsigned token = t * 16u + slot;
+            if (g_c < groups && token < batch) {
+              const std::size_t row0 =
+                  static_cast<std::size_t>(token) * rows + (tile0 + r) * 16u + 4u * kb;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) args.partials[(row0 + i) * groups + g_c] = c[t][i] >> kShift;
+            }
+          }
+        } else {
+          // Dead tokens and a missing last group hold exact zeros (and zero scales).
+          const u32x2 pw = wsreg[r][ci];
+          float ws[4];
+          ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] & 0xffffu)));
+          ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] >> 16)));
+          ws[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] & 0xffffu)));
+          ws[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] >> 16)));
+#pragma unroll
+          for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[r][t][i] = fmaf(static_cast<float>(c[t][i]), ws[i] * as[t], acc[r][t][i]);
+            }
+          }
+        }
+      }
+    }
+  }
+  if constexpr (Partials) return;
+
+  // Combine the GP windows of each token slot (lanes n, n+TPAD, ...).
+#pragma unroll
+  for (unsigned offset = TPAD; offset < 16u; offset <<= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < NTB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][t][i] += __shfl_xor(acc[r][t][i], static_cast<int>(offset));
+  }
+  if (waves > 1) {
+    constexpr unsigned kRegion = R * NTB * 4u * 64u * 4u;
+    float* mine = reinterpret_cast<float*>(lds_all + wave * kRegion);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < NTB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[((r * NTB + t) * 4 + i) * 64 + lane] = acc[r][t][i];
+    __syncthreads();
+    if (wave != 0) return;
+    for (unsigned w = 1; w < waves; ++w) {
+      const float* other = reinterpret_cast<const float*>(lds_all + w * kRegion);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < NTB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r][t][i] += other[((r * NTB + t) * 4 + i) * 64 + lane];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (static_cast<unsigned>(r) >= valid) break;
+    const unsigned tile = tile0 + r;
+    if (args.argmax_keys != nullptr) {
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+        unsigned long long best = 0ull;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const unsigned long long key = argmax_key(acc[r][t][i], tile * 16u + 4u * kb + i, args.argmax_rows);
+          best = key > best ? key : best;
+        }
+        unsigned long long other = __shfl_xor(best, 16);
+        best = other > best ? other : best;
+        other = __shfl_xor(best, 32);
+        best = other > best ? other : best;
+        const unsigned token = t * 16u + slot;
+        if (kb == 0 && window == 0 && token < batch) {
+          args.argmax_keys[static_cast<std::size_t>(token) * matrix.tiles + tile] = best;
+        }
+      }
+    }
+    if (window != 0 || matrix.output == nullptr) continue;
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+      if (t * 16u + slot >= batch) continue;
+      const std::size_t out = static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
+      if constexpr (HalfOut) {
+        __half* o = reinterpret_cast<__half*>(matrix.output) + out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = to_half(acc[r][t][i]);
+      } else {
+        float4 value = {acc[r][t][0], acc[r][t][1], acc[r][t][2], acc[r][t][3]};
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tiled row gather (lowbit_gemv.hip:191-231): out[c] = fp16(w(row,c) * ws(row,g)).
 // ---------------------------------------------------------------------------
 
@@ -619,8 +993,110 @@ unsigned choose_waves(uint32_t groups, unsigned gp) {
   return waves;
 }
 
+// GFXI_GEMM_KERNEL=lds selects the LDS-staged kernel (tuning knob); the default
+// is the direct-operand kernel.
+int kernel_override() {  // 0 default, 1 lds everywhere, 2 direct everywhere
+  static const int value = [] {
+    const char* text = std::getenv("GFXI_GEMM_KERNEL");
+    if (text == nullptr) return 0;
+    return std::string(text) == "lds" ? 1 : std::string(text) == "direct" ? 2 : 0;
+  }();
+  return value;
+}
+
+// GFXI_GEMM_ROWTILES (1 or 2) overrides the row tiles per workgroup (tuning knob).
+int rowtiles_override() {
+  static const int value = [] {
+    const char* text = std::getenv("GFXI_GEMM_ROWTILES");
+    const int v = text != nullptr ? std::atoi(text) : 0;
+    return v == 1 || v == 2 ? v : 0;
+  }();
+  return value;
+}
+
+// GFXI_GEMM_RESIDENT=0 disables the one-round residency cap on waves (tuning knob).
+bool resident_cap() {
+  static const bool value = [] {
+    const char* text = std::getenv("GFXI_GEMM_RESIDENT");
+    return text == nullptr || std::atoi(text) != 0;
+  }();
+  return value;
+}
+
+// Waves per workgroup: about ten groups of K per wave, but no more than lets every
+// workgroup of the grid be resident at once (a second partial round of
+// workgroups would double the time of a short kernel).
+unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, std::size_t lds_per_wave) {
+  unsigned want = choose_waves(groups, 1);
+  if (waves_override() != 0 || !resident_cap()) return want;
+  static int cus = [] {
+    int device = 0, count = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+      return 256;
+    }
+    return count;
+  }();
+  for (unsigned w = want; w >= 1; --w) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, static_cast<int>(64 * w),
+                                                     w > 1 ? w * lds_per_wave : 0) != hipSuccess) {
+      return want;
+    }
+    if (static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus) >= blocks) return w;
+  }
+  return want;
+}
+
+template <int Format, int ABits, bool HalfOut, bool Partials>
+void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipStream_t stream) {
+  const uint32_t batch = base_args.batch;
+  auto go = [&](auto kernel, unsigned r, unsigned ntb) {
+    GemmArgs args = base_args;
+    uint32_t blocks = 0;
+    for (unsigned i = 0; i < 4; ++i) {
+      args.tile_begin[i] = blocks;
+      // unused trailing slots repeat the last matrix with zero tiles
+      const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
+      if (used) blocks += (args.matrix[i].tiles + r - 1) / r;
+    }
+    args.tile_begin[4] = blocks;
+    const unsigned waves = resident_waves(reinterpret_cast<const void*>(kernel), args.groups, blocks,
+                                          r * ntb * 4u * 64u * 4u);
+    const std::size_t lds = static_cast<std::size_t>(waves) * r * ntb * 4u * 64u * 4u;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * waves), waves > 1 ? lds : 0, stream, args);
+  };
+  (void)total_tiles;
+  const int forced = rowtiles_override();
+  if (batch <= 4) {
+    go(lowbit_gemm_direct_kernel<Format, ABits, 4, 1, 3, 1, HalfOut, Partials>, 1, 1);
+  } else if (batch <= 8) {
+    go(lowbit_gemm_direct_kernel<Format, ABits, 2, 1, 5, 1, HalfOut, Partials>, 1, 1);
+  } else if (batch <= 16) {
+    if (forced == 1) {
+      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 6, 1, HalfOut, Partials>, 1, 1);
+    } else {
+      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 2, HalfOut, Partials>, 2, 1);
+    }
+  } else if constexpr (ABits == 8) {
+    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
+  } else if (forced == 1) {
+    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
+  } else {
+    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 3, 2, HalfOut, Partials>, 2, 2);
+  }
+}
+
 template <int Format, int ABits, bool HalfOut, bool Partials>
 void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
+  // Direct operands pay off from 9 tokens on (one token window, quad-coalesced
+  // activation loads, two row tiles per workgroup); up to 8 tokens the LDS-staged
+  // kernel with its packed token windows is as fast or faster.
+  const int forced = kernel_override();
+  if (forced == 2 || (forced == 0 && args.batch > 8)) {
+    launch_direct_kernel<Format, ABits, HalfOut, Partials>(args, total_tiles, stream);
+    return;
+  }
   const uint32_t batch = args.batch;
   auto go = [&](auto kernel, unsigned gp, unsigned ch, unsigned ntb) {
     unsigned waves = choose_waves(args.groups, 1);
