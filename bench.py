@@ -240,6 +240,52 @@ def cpu_baseline(rows=17408, cols=5120, repeats=5):
     }
 
 
+PROFILE = os.path.join(ROOT, "profiles", "gemv_w3a4_17408x5120_b5.txt")
+COPY_BYTES = 256 << 20
+
+
+def pmc_probe(launches=8, rows=17408, cols=5120, batch=5):
+    """Workload for the rocprofv3 --pmc passes: one device copy of COPY_BYTES (the
+    calibration kernel: it reads and writes exactly COPY_BYTES) and `launches` plain
+    launches of the headline GEMM on distinct weight buffers."""
+    import torch
+    import gfxinfer_amd as gx
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    fmt = gx.W3G128
+    w = torch.randn(rows, cols, device="cuda") * 0.02
+    codes = [torch.empty(gx.tile_bytes(fmt, rows, cols), dtype=torch.uint8, device="cuda") for _ in range(launches)]
+    scales = [torch.empty(rows * cols // 128, dtype=torch.int16, device="cuda") for _ in range(launches)]
+    for c, s in zip(codes, scales):
+        gx.launch_quantize_group128(fmt, w, rows, cols, c, s)
+    x = torch.randn(batch, cols, device="cuda").half()
+    a = torch.empty(batch, cols // 2, dtype=torch.uint8, device="cuda")
+    sa = torch.empty(batch, cols // 128, dtype=torch.int16, device="cuda")
+    y = torch.empty(batch, rows, device="cuda")
+    gx.launch_quantize_activation_i4(x, a, sa, cols, batch)
+    torch.cuda.synchronize()
+    for c, s in zip(codes, scales):
+        gx.launch_i4_gemm(fmt, c, s, a, sa, y, rows, cols, batch)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "gemm_launches": launches,
+                      "gemm_algorithmic_bytes": algorithmic_bytes(rows, cols, batch)}))
+
+
+def measured_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, or None."""
+    try:
+        for line in open(PROFILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1].split()[0])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +294,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--verify-rounds", type=int, default=60)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run the rocprofv3 --pmc workload (calibration copy + plain GEMM launches)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -255,6 +303,9 @@ def main():
         sys.exit(2)
     import gfxinfer_amd as gx
     gx.check(gx.lib().gfxinfer_require_gfx950_device(0))
+    if args.pmc_probe:
+        pmc_probe()
+        return
 
     r = gemv_bench(args.steps, args.warmup)
     nbytes = algorithmic_bytes(r["rows"], r["cols"], r["batch"])
@@ -287,7 +338,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemm_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "lowbit_gemm_kernel<W3,A4,GP=2>",
             "kernel_us": round(r["ms_gemm"] * 1e3, 3),
             "algorithmic_bytes": nbytes,

@@ -1,0 +1,98 @@
+"""Summaries of rocprofv3 CSV output for the committed profiles.
+
+    python -m gfxinfer_amd.rocprof_summary stats <dir> [--match NAME]...
+    python -m gfxinfer_amd.rocprof_summary pmc <fetch_dir> <write_dir> --kernel NAME \\
+        --copy NAME --copy-bytes N
+
+`stats` prints the kernel table of a --kernel-trace --stats run (calls, total,
+average, min, max per kernel).  `pmc` reads two --pmc runs (FETCH_SIZE, then
+WRITE_SIZE; both in KiB per dispatch), calibrates each counter on the copy kernel
+of known size (it reads and writes exactly N bytes) and prints the HBM bytes per
+dispatch of the named kernel.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+import statistics
+
+
+def _csv(directory: str, suffix: str) -> list[dict]:
+    paths = glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    rows: list[dict] = []
+    for p in paths:
+        with open(p) as f:
+            rows.extend(csv.DictReader(f))
+    return rows
+
+
+def short(name: str) -> str:
+    name = name.replace("void ", "").replace("gfx950::(anonymous namespace)::", "")
+    return name.split("(")[0]
+
+
+def stats(directory: str, match: list[str]) -> str:
+    rows = _csv(directory, "kernel_stats.csv")
+    lines = [f"{'calls':>7} {'total_us':>11} {'avg_us':>9} {'min_us':>9} {'max_us':>9}  kernel"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        if match and not any(m in r["Name"] for m in match):
+            continue
+        lines.append(f"{int(r['Calls']):7d} {float(r['TotalDurationNs']) / 1e3:11.1f} "
+                     f"{float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
+                     f"{float(r['MaxNs']) / 1e3:9.3f}  {short(r['Name'])}")
+    return "\n".join(lines)
+
+
+def _per_dispatch(directory: str, counter: str, needle: str) -> list[float]:
+    per: dict[int, float] = {}
+    for r in _csv(directory, "counter_collection.csv"):
+        if r["Counter_Name"] != counter or needle not in r["Kernel_Name"]:
+            continue
+        d = int(r["Dispatch_Id"])
+        per[d] = per.get(d, 0.0) + float(r["Counter_Value"])
+    return [per[d] for d in sorted(per)]
+
+
+def pmc(fetch_dir: str, write_dir: str, kernel: str, copy: str, copy_bytes: int) -> str:
+    out = []
+    total = 0.0
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        copy_kib = _per_dispatch(directory, counter, copy)
+        kern_kib = _per_dispatch(directory, counter, kernel)
+        if not copy_kib or not kern_kib:
+            raise SystemExit(f"{counter}: missing dispatches of {copy!r} or {kernel!r}")
+        factor = copy_bytes / max(copy_kib)  # bytes per counted KiB, from the copy
+        value = statistics.median(kern_kib) * factor
+        total += value
+        out.append(f"{counter}: copy {max(copy_kib):.0f} KiB for {copy_bytes} B -> factor "
+                   f"{factor:.1f} B per counted KiB; kernel median {statistics.median(kern_kib):.0f} KiB "
+                   f"over {len(kern_kib)} dispatches -> {value:.0f} B")
+    out.append(f"traffic_bytes_per_launch = {total:.0f}")
+    return "\n".join(out)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    a = sub.add_parser("stats")
+    a.add_argument("directory")
+    a.add_argument("--match", action="append", default=[])
+    b = sub.add_parser("pmc")
+    b.add_argument("fetch_dir")
+    b.add_argument("write_dir")
+    b.add_argument("--kernel", required=True)
+    b.add_argument("--copy", required=True)
+    b.add_argument("--copy-bytes", type=int, required=True)
+    args = ap.parse_args()
+    if args.cmd == "stats":
+        print(stats(args.directory, args.match))
+    else:
+        print(pmc(args.fetch_dir, args.write_dir, args.kernel, args.copy, args.copy_bytes))
+
+
+if __name__ == "__main__":
+    main()
