@@ -198,8 +198,9 @@ def _tensor_names(spec):
     return names
 
 
-def cpu_baseline(rows=17408, cols=5120, repeats=5):
-    """Oracle W3A8 quantize + dequant-dot GEMV on host cores."""
+def cpu_baseline(rows=17408, cols=5120, seconds=10.0):
+    """Oracle W3A8 quantize + dequant-dot GEMV on host cores: the
+    GEMV repeats for about `seconds` of CPU time and the median run is reported."""
     import numpy as np
     from oracle import oracle as O
 
@@ -214,10 +215,12 @@ def cpu_baseline(rows=17408, cols=5120, repeats=5):
     a, as16 = O.quantize_activation_i8(x16)
     O.dequant_dot_gemv_packed(codes, O.W3, scales, a, as16, rows, cols)  # warmup
     times = []
-    for _ in range(repeats):
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds or len(times) < 5:
         t0 = time.perf_counter()
         O.dequant_dot_gemv_packed(codes, O.W3, scales, a, as16, rows, cols)
         times.append(time.perf_counter() - t0)
+    repeats = len(times)
     gemv = sorted(times)[len(times) // 2]
     nbytes = algorithmic_bytes(rows, cols, 1, wbits=3, abits=8)
     model = "unknown"

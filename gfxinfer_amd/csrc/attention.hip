@@ -49,7 +49,10 @@ __device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
 __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   __shared__ __align__(16) _Float16 ks[kSplit][kD + kPad];  // K rows of the split
   __shared__ __align__(16) _Float16 vt[kD][kRow];           // V transposed: [d][position]
-  __shared__ __align__(16) _Float16 ps[4][16][kRow];        // per-wave P tile
+  // Per-wave P tile as an fp16 pair p = hi + lo (hi = fp16(p), lo = fp16(p - hi)): two
+  // f16 MFMAs then carry ~22 significant bits of p, close to the reference's fp32 P.V.
+  __shared__ __align__(16) _Float16 ps[4][16][kRow];
+  __shared__ __align__(16) _Float16 ps_lo[4][16][kRow];
 
   const unsigned split = blockIdx.x, hk = blockIdx.y;
   const uint64_t base = base_count_of(a);
@@ -130,7 +133,9 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
       for (unsigned j = 0; j < kTiles; ++j) {
         const float p = best == -INFINITY ? 0.0F : expf(sc[j][r] - best);
         total += p;
-        ps[wave][4 * kb + r][j * 16 + m] = static_cast<_Float16>(p);
+        const _Float16 hi = static_cast<_Float16>(p);
+        ps[wave][4 * kb + r][j * 16 + m] = hi;
+        ps_lo[wave][4 * kb + r][j * 16 + m] = static_cast<_Float16>(p - static_cast<float>(hi));
       }
       total += __shfl_xor(total, 1);
       total += __shfl_xor(total, 2);
@@ -140,15 +145,19 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
       sum[r] = total;
     }
     // O = P V: 8 tiles of 16 head dims, kSteps K-steps of 32 positions.
-    h8 pa[kSteps];
+    h8 pa[kSteps], pl[kSteps];
 #pragma unroll
-    for (unsigned s = 0; s < kSteps; ++s) pa[s] = *reinterpret_cast<const h8*>(&ps[wave][m][32 * s + 8 * kb]);
+    for (unsigned s = 0; s < kSteps; ++s) {
+      pa[s] = *reinterpret_cast<const h8*>(&ps[wave][m][32 * s + 8 * kb]);
+      pl[s] = *reinterpret_cast<const h8*>(&ps_lo[wave][m][32 * s + 8 * kb]);
+    }
 #pragma unroll
     for (int dj = 0; dj < 8; ++dj) {
       f4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (unsigned s = 0; s < kSteps; ++s) {
         const h8 vv = *reinterpret_cast<const h8*>(&vt[dj * 16 + m][32 * s + 8 * kb]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], vv, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[s], vv, acc, 0, 0, 0);
       }
 #pragma unroll

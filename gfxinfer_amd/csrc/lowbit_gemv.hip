@@ -230,10 +230,11 @@ __device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
 // chunk's activation scales as fp32 already multiplied by 1/F.  After the MFMA
 // loop the region holds the wave's partial sums for the cross-wave reduction.
 struct GemmLds {
-  uint32_t pitch;         // bytes per token row (chunk bytes + 16: rotates LDS banks)
-  uint32_t zero_offset;   // zero line
-  uint32_t scale_offset;  // fp32 scales [batch][chunk groups]
-  uint32_t region;        // bytes per wave
+  uint32_t pitch;          // bytes per token row (chunk bytes + 16: rotates LDS banks)
+  uint32_t zero_offset;    // zero line
+  uint32_t scale_offset;   // fp32 scales [batch][chunk groups]
+  uint32_t wscale_offset;  // fp16 weight scales of the chunk [chunk groups][16 rows]
+  uint32_t region;         // bytes per wave
 };
 
 __host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32_t batch, int abits,
@@ -243,7 +244,8 @@ __host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32
   l.pitch = chunk_groups * 128u + 16u;  // operand-ready int8: 128 bytes per token per group
   l.zero_offset = batch * l.pitch;
   l.scale_offset = l.zero_offset + 16u;
-  uint32_t region = l.scale_offset + batch * chunk_groups * 4u;
+  l.wscale_offset = (l.scale_offset + batch * chunk_groups * 4u + 15u) & ~15u;
+  uint32_t region = l.wscale_offset + chunk_groups * 32u;
   const uint32_t reduce = ntb * 4u * 64u * 4u;
   if (region < reduce) region = reduce;
   l.region = (region + 15u) & ~15u;
@@ -297,7 +299,6 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   const unsigned slot = n % TPAD;  // token slot of column n
   const unsigned window = n / TPAD;
   const unsigned w_voffset = lane * LB;
-  const unsigned ws_voffset = (window * 16u + 4u * kb) * 2u;
 
   const unsigned packs = (groups + GP - 1) / GP;
   const unsigned pack_begin = packs * wave / waves;
@@ -345,6 +346,14 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       stage[p] = __builtin_amdgcn_raw_buffer_load_b128(activations, token * row_bytes + rem * 16u,
                                                        g0 * AGB, 0);
     }
+    // The chunk's weight scales ([CHG groups][16 rows] fp16, contiguous in the tile):
+    // one coalesced 16-byte load per lane (lanes < 2 * CHG), staged through LDS, instead
+    // of one small scattered load per pack that would stall each pack's epilogue.
+    u32x4 wschunk = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (!Partials) {
+      wschunk = __builtin_amdgcn_raw_buffer_load_b128(weight_scales, lane < 2u * CHG ? lane * 16u : 0x80000000u,
+                                                      g0 * 32u, 0);
+    }
     if constexpr (!Partials) {
       // entry e < batch * CHG: scale of (token e / CHG, group g0 + e % CHG)
 #pragma unroll
@@ -357,7 +366,6 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     }
     // 2) Weights and weight scales of CH packs, all in flight together.
     unsigned wreg[CH][GP][WD];
-    u32x2 wsreg[CH];
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
       const unsigned pack = min(base + ci, pack_end - 1u);
@@ -376,9 +384,6 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
           wreg[ci][j][2] = w[2];
           wreg[ci][j][3] = w[3];
         }
-      }
-      if constexpr (!Partials) {
-        wsreg[ci] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, ws_voffset, pack * GP * 32u, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -410,6 +415,7 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
               __half2float(__ushort_as_half(stage_scale[it])) * kInvF;
         }
       }
+      if (lane < 2u * CHG) *reinterpret_cast<u32x4*>(lds + layout.wscale_offset + lane * 16u) = wschunk;
     }
     __builtin_amdgcn_sched_barrier(0);
     // 4) Compute.
@@ -455,7 +461,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
         }
       } else {
         // Columns of dead tokens or of a missing last group hold exact zeros.
-        const u32x2 pw = wsreg[ci];
+        const u32x2 pw = *reinterpret_cast<const u32x2*>(
+            lds + layout.wscale_offset + (min(g_c, groups - 1u) - g0) * 32u + 8u * kb);
         float ws[4];
         ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] & 0xffffu)));
         ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] >> 16)));

@@ -1,0 +1,254 @@
+"""Model-level CPU oracle: the reference's decode-session forward restated on top of
+the oracle ops (liboracle.so), for end-to-end parity of small synthetic models.
+
+TEST INFRASTRUCTURE ONLY (tests/ import it as the checker; the product never does).
+
+Follows src/qwen_runtime.cpp: embedding row gather (:576-600), first input norm
+(:602-606), layer blocks (:421-544: mixer, residual + post norm, gate/up, SwiGLU,
+down, residual + next layer's input norm), LM head + argmax over the tokenizer
+vocabulary (:635-639), and the MTP proposal (:715-867).  Activations are A4G128
+(ActivationMode::int4, :111-128): every projection quantizes its fp16 input, takes
+the exact per-group integer partials and the per-group fp32 epilogue.
+Weights are the synthetic checkpoint of gfxinfer_model_create_synthetic, regenerated
+with oracle.synthetic_values and quantized with the restated quantize_group128.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import oracle as O
+
+EPS = ctypes.c_float(1e-6)
+
+
+def _laws(name: str):
+    if name.endswith("conv1d.weight") or name.endswith("A_log") or name.endswith("dt_bias"):
+        return 0.0, 0.5
+    if name.endswith("linear_attn.norm.weight"):
+        return 1.0, 0.02
+    return 0.0, 0.02
+
+
+class Matrix:
+    def __init__(self, seed, name, fmt, rows, cols):
+        w = O.synthetic_values(seed, name, rows * cols, 0.02, 0.0).reshape(rows, cols)
+        status, codes, scales = O.quantize_group128(w, fmt)
+        assert status == 0
+        self.w = O.unpack_weights(codes, rows, cols, fmt)
+        self.ws16 = O.f32_to_f16_bits(scales)
+        self.rows, self.cols = rows, cols
+
+    def __call__(self, x16: np.ndarray) -> np.ndarray:
+        """fp16 [B, K] -> fp32 [B, N] through A4 activations (lowbit_gemv.hip:373-553)."""
+        packed, as16 = O.quantize_activation_i4(x16)
+        a = O.unpack_a4(packed, self.cols)
+        return O.gemm_epilogue(O.gemm_partials(self.w, a), self.ws16, as16)
+
+    def head(self, rows: int) -> "Matrix":
+        m = Matrix.__new__(Matrix)
+        m.w, m.ws16, m.rows, m.cols = self.w[:rows], self.ws16[:rows], rows, self.cols
+        return m
+
+
+class OracleModel:
+    def __init__(self, spec: dict, seed: int):
+        self.s = s = dict(spec)
+        self.seed = seed
+        H, I, hd = s["hidden_size"], s["intermediate_size"], s["attention_head_size"]
+        self.hd = hd
+        self.q_rows = 2 * s["attention_head_count"] * hd
+        self.kv_rows = s["kv_head_count"] * hd
+        self.gk = s["gdn_key_head_count"] * s["gdn_head_size"]
+        self.gv = s["gdn_value_head_count"] * s["gdn_head_size"]
+        self.C = 2 * self.gk + self.gv
+
+        def mat(name, fmt, rows, cols):
+            return Matrix(seed, name, fmt, rows, cols)
+
+        def vec(name, n):
+            mean, sigma = _laws(name)
+            return O.f32_to_bf16_bits(O.synthetic_values(seed, name, n, sigma, mean))
+
+        V = s["vocabulary_size"]
+        self.embed = mat("model.language_model.embed_tokens.weight", O.W4, V, H)
+        self.final_norm = vec("model.language_model.norm.weight", H)
+        self.lm_head = mat("lm_head.weight", O.W4, V, H)
+        self.layers = []
+        for i in range(s["layer_count"]):
+            p = f"model.language_model.layers.{i}."
+            fmt = O.W3 if i < s["w3_mlp_layers"] else O.W4
+            L = dict(attention=(i + 1) % s["full_attention_interval"] == 0,
+                     input_norm=vec(p + "input_layernorm.weight", H),
+                     post_norm=vec(p + "post_attention_layernorm.weight", H),
+                     gate=mat(p + "mlp.gate_proj.weight", fmt, I, H),
+                     up=mat(p + "mlp.up_proj.weight", fmt, I, H),
+                     down=mat(p + "mlp.down_proj.weight", fmt, H, I))
+            if L["attention"]:
+                self._attention(L, p)
+            else:
+                L.update(qkv=mat(p + "linear_attn.in_proj_qkv.weight", O.W4, self.C, H),
+                         z=mat(p + "linear_attn.in_proj_z.weight", O.W4, self.gv, H),
+                         a=mat(p + "linear_attn.in_proj_a.weight", O.W4, s["gdn_value_head_count"], H),
+                         b=mat(p + "linear_attn.in_proj_b.weight", O.W4, s["gdn_value_head_count"], H),
+                         conv=vec(p + "linear_attn.conv1d.weight", self.C * 4),
+                         a_log=vec(p + "linear_attn.A_log", s["gdn_value_head_count"]),
+                         dt_bias=vec(p + "linear_attn.dt_bias", s["gdn_value_head_count"]),
+                         gdn_norm=vec(p + "linear_attn.norm.weight", s["gdn_head_size"]),
+                         out=mat(p + "linear_attn.out_proj.weight", O.W4, H, self.gv))
+            self.layers.append(L)
+        self.mtp_fc = mat("mtp.fc.weight", O.W4, H, 2 * H)
+        self.mtp_pre_embedding_norm = vec("mtp.pre_fc_norm_embedding.weight", H)
+        self.mtp_pre_hidden_norm = vec("mtp.pre_fc_norm_hidden.weight", H)
+        self.mtp_final_norm = vec("mtp.norm.weight", H)
+        self.mtp = dict(attention=True, input_norm=vec("mtp.layers.0.input_layernorm.weight", H),
+                        post_norm=vec("mtp.layers.0.post_attention_layernorm.weight", H),
+                        gate=mat("mtp.layers.0.mlp.gate_proj.weight", O.W4, I, H),
+                        up=mat("mtp.layers.0.mlp.up_proj.weight", O.W4, I, H),
+                        down=mat("mtp.layers.0.mlp.down_proj.weight", O.W4, H, I))
+        self._attention(self.mtp, "mtp.layers.0.")
+        self.draft_head = self.lm_head.head(s["mtp_draft_vocabulary"])
+
+    def _attention(self, L, p):
+        s, H, hd = self.s, self.s["hidden_size"], self.hd
+        L.update(q=Matrix(self.seed, p + "self_attn.q_proj.weight", O.W4, self.q_rows, H),
+                 k=Matrix(self.seed, p + "self_attn.k_proj.weight", O.W4, self.kv_rows, H),
+                 v=Matrix(self.seed, p + "self_attn.v_proj.weight", O.W4, self.kv_rows, H),
+                 q_norm=O.f32_to_bf16_bits(O.synthetic_values(self.seed, p + "self_attn.q_norm.weight", hd, 0.02, 0.0)),
+                 k_norm=O.f32_to_bf16_bits(O.synthetic_values(self.seed, p + "self_attn.k_norm.weight", hd, 0.02, 0.0)),
+                 o=Matrix(self.seed, p + "self_attn.o_proj.weight", O.W4, H, s["attention_head_count"] * hd))
+
+
+def _p(a):
+    return O.ptr(np.ascontiguousarray(a))
+
+
+class OracleSession:
+    """Decode state of one sequence: conv/GDN states, K/V caches, positions."""
+
+    def __init__(self, model: OracleModel, capacity: int):
+        self.m = m = model
+        s = m.s
+        self.capacity = capacity
+        gdn_layers = sum(1 for L in m.layers if not L["attention"])
+        attn_layers = len(m.layers) - gdn_layers
+        Hv, d = s["gdn_value_head_count"], s["gdn_head_size"]
+        self.conv = [np.zeros((m.C, 4), np.uint16) for _ in range(gdn_layers)]
+        self.state = [np.zeros((Hv, d, d), np.float32) for _ in range(gdn_layers)]
+        self.kcache = [np.zeros((capacity, m.kv_rows), np.uint16) for _ in range(attn_layers)]
+        self.vcache = [np.zeros((capacity, m.kv_rows), np.uint16) for _ in range(attn_layers)]
+        self.mtp_k = np.zeros((capacity, m.kv_rows), np.uint16)
+        self.mtp_v = np.zeros((capacity, m.kv_rows), np.uint16)
+        self.position = 0
+        self.last_hidden = None
+
+    # ---- pieces ------------------------------------------------------------------
+    def _norm(self, x16, w):
+        out = np.empty_like(x16)
+        O.lib().orc_rms_norm(_p(x16), _p(w), O.ptr(out), x16.shape[1], x16.shape[0], EPS, 1)
+        return out
+
+    def _residual_norm(self, res16, upd, w):
+        r = np.empty_like(res16)
+        n = np.empty_like(res16)
+        O.lib().orc_residual_add_rms_norm(_p(res16), _p(upd), O.ptr(r), _p(w), O.ptr(n), res16.shape[1],
+                                          res16.shape[0], EPS, 1)
+        return r, n
+
+    def _attention_mixer(self, L, normed, kcache, vcache, position, stop_after_append=False):
+        m, s = self.m, self.m.s
+        T, hd = normed.shape[0], m.hd
+        q = L["q"](normed)
+        k = L["k"](normed)
+        v = L["v"](normed)
+        qn = np.empty((T, s["attention_head_count"], hd), np.uint16)
+        kn = np.empty((T, s["kv_head_count"], hd), np.uint16)
+        theta = ctypes.c_float(s["rope_theta"])
+        O.lib().orc_head_norm_rope(_p(q), 2 * hd, _p(L["q_norm"]), O.ptr(qn), s["attention_head_count"], hd,
+                                   s["rotary_size"], ctypes.c_uint64(position), T, theta)
+        O.lib().orc_head_norm_rope(_p(k), hd, _p(L["k_norm"]), O.ptr(kn), s["kv_head_count"], hd,
+                                   s["rotary_size"], ctypes.c_uint64(position), T, theta)
+        O.lib().orc_kv_append(O.ptr(kn), _p(v), O.ptr(kcache), O.ptr(vcache), position, m.kv_rows, T)
+        if stop_after_append:
+            return None
+        out = np.empty((T, s["attention_head_count"], hd), np.uint16)
+        O.lib().orc_gated_attention(O.ptr(qn), _p(q), O.ptr(kcache), O.ptr(vcache), O.ptr(out), position + 1, T,
+                                    s["attention_head_count"], s["kv_head_count"], hd,
+                                    ctypes.c_float(np.float32(1.0 / np.sqrt(hd))))
+        return L["o"](out.reshape(T, -1))
+
+    def _gdn_mixer(self, L, normed, index):
+        m, s = self.m, self.m.s
+        T = normed.shape[0]
+        proj = L["qkv"](normed)
+        z, a, b = L["z"](normed), L["a"](normed), L["b"](normed)
+        conv_out = np.empty((T, m.C), np.uint16)
+        final = np.empty_like(self.conv[index])
+        O.lib().orc_gdn_conv_update(_p(proj), _p(L["conv"]), O.ptr(self.conv[index]), O.ptr(final),
+                                    O.ptr(conv_out), None, m.C, T)
+        self.conv[index] = final
+        state = np.empty_like(self.state[index])
+        out = np.empty((T, m.gv), np.uint16)
+        O.lib().orc_gdn_recurrent(O.ptr(conv_out), _p(z), _p(a), _p(b), _p(L["a_log"]), _p(L["dt_bias"]),
+                                  _p(L["gdn_norm"]), O.ptr(self.state[index]), O.ptr(state), O.ptr(out), None,
+                                  None, None, T, s["gdn_key_head_count"], s["gdn_value_head_count"],
+                                  s["gdn_head_size"])
+        self.state[index] = state
+        return L["out"](out)
+
+    def _mlp(self, L, residual, mixer_update, next_norm):
+        post, post_normed = self._residual_norm(residual, mixer_update, L["post_norm"])
+        gate, up = L["gate"](post_normed), L["up"](post_normed)
+        act = np.empty(gate.shape, np.uint16)
+        O.lib().orc_silu_multiply(_p(gate), _p(up), O.ptr(act), gate.size)
+        return self._residual_norm(post, L["down"](act), next_norm)
+
+    # ---- QwenDecodeSession::block_step (qwen_runtime.cpp:1320-1392) --------------
+    def block_step(self, tokens):
+        m, s = self.m, self.m.s
+        T = len(tokens)
+        hidden = np.stack([self._gather(t) for t in tokens])
+        normed = self._norm(hidden, m.layers[0]["input_norm"])
+        gdn_i = attn_i = 0
+        for i, L in enumerate(m.layers):
+            next_norm = m.layers[i + 1]["input_norm"] if i + 1 < len(m.layers) else m.final_norm
+            if L["attention"]:
+                update = self._attention_mixer(L, normed, self.kcache[attn_i], self.vcache[attn_i], self.position)
+                attn_i += 1
+            else:
+                update = self._gdn_mixer(L, normed, gdn_i)
+                gdn_i += 1
+            hidden, normed = self._mlp(L, hidden, update, next_norm)
+        logits = m.lm_head(normed)
+        out = np.empty(T, np.uint32)
+        O.lib().orc_argmax(O.ptr(logits), s["tokenizer_vocabulary_size"], s["vocabulary_size"], T, None,
+                           O.ptr(out))
+        self.position += T
+        self.last_hidden = hidden[-1:].copy()
+        return [int(x) for x in out], logits
+
+    def _gather(self, token):
+        """launch_lowbit_row_gather: fp16(w(row, c) * ws(row, c/128)) (lowbit_gemv.hip:191-231)."""
+        m = self.m.embed
+        scales = O.f16_bits_to_f32(m.ws16[token]).repeat(128)
+        return O.f32_to_f16_bits(m.w[token].astype(np.float32) * scales)
+
+    # ---- launch_mtp_proposal (qwen_runtime.cpp:715-867) ---------------------------
+    def mtp_proposal(self, token, conditioning16, position):
+        m, s = self.m, self.m.s
+        H = s["hidden_size"]
+        emb = self._gather(token)[None, :]
+        concat = np.empty((1, 2 * H), np.uint16)
+        O.lib().orc_dual_rms_norm_concat(O.ptr(emb), _p(m.mtp_pre_embedding_norm), _p(conditioning16),
+                                         _p(m.mtp_pre_hidden_norm), O.ptr(concat), H, EPS, 1)
+        fc = m.mtp_fc(concat)
+        mtp_input = O.f32_to_f16_bits(fc)                  # launch_gfx12_i4_gemm_half
+        normed = self._norm(mtp_input, m.mtp["input_norm"])
+        update = self._attention_mixer(m.mtp, normed, self.mtp_k, self.mtp_v, position)
+        hidden, normed = self._mlp(m.mtp, mtp_input, update, m.mtp_final_norm)
+        logits = m.draft_head(normed)
+        out = np.empty(1, np.uint32)
+        O.lib().orc_argmax(O.ptr(logits), s["mtp_draft_vocabulary"], s["mtp_draft_vocabulary"], 1, None,
+                           O.ptr(out))
+        return int(out[0]), logits, hidden

@@ -1,0 +1,79 @@
+"""End-to-end parity of the GPU decode session against the model-level CPU oracle
+(oracle/model.py) on a small synthetic model of the same structure: logits of
+block steps (fresh state, then with K/V caches and GDN state carried over) and of an
+MTP proposal within the BASELINE logit tolerance 2e-2 absolute, greedy tokens equal
+wherever the oracle's top-1/top-2 margin exceeds twice that tolerance."""
+import numpy as np
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+SEED = 4321
+LOGIT_TOL = 2e-2
+
+
+def _spec():
+    from gfxinfer_amd.runtime import tiny_spec
+    return tiny_spec(full_attention_interval=2, gdn_key_head_count=4)
+
+
+@pytest.fixture(scope="module")
+def pair(device):
+    from gfxinfer_amd.runtime import SyntheticModel
+    from oracle.model import OracleModel
+    spec = _spec()
+    say("tiny model for oracle parity")
+    gpu = SyntheticModel(spec, SEED)
+    cpu = OracleModel(spec.as_dict(), SEED)
+    yield gpu, cpu
+    gpu.close()
+
+
+def _check_tokens(got, logits):
+    top2 = np.sort(logits, axis=1)[:, -2:]
+    margin = top2[:, 1] - top2[:, 0]
+    want = np.argmax(logits, axis=1)
+    sure = margin > 2 * LOGIT_TOL
+    assert sure.any()
+    assert np.array_equal(np.asarray(got)[sure], want[sure])
+
+
+def test_block_steps_match_oracle(pair):
+    from gfxinfer_amd.runtime import QwenDecodeSession
+    from oracle.model import OracleSession
+    gpu, cpu = pair
+    spec = _spec()
+    V, Vt = spec.vocabulary_size, spec.tokenizer_vocabulary_size
+    s = QwenDecodeSession(gpu, 64, 0, keep_logits=True)
+    o = OracleSession(cpu, 64)
+    for block in ([3, 141, 59, 26, 535], [897, 9, 32], [384]):
+        say("block", block)
+        got = s.block_step(block)
+        want, want_logits = o.block_step(block)
+        logits = s.buffer("logits", np.float32, len(block) * V).reshape(len(block), V)
+        err = np.abs(logits - want_logits).max()
+        assert err <= LOGIT_TOL, err
+        _check_tokens(got, want_logits[:, :Vt])
+    gdn = s.buffer("gdn_states", np.float32).reshape(len(o.state), *o.state[0].shape)
+    np.testing.assert_allclose(gdn, np.stack(o.state), rtol=5e-3, atol=5e-4)
+
+
+def test_mtp_proposal_matches_oracle(pair):
+    from gfxinfer_amd.runtime import QwenDecodeSession
+    from oracle.model import OracleSession
+    gpu, cpu = pair
+    spec = _spec()
+    s = QwenDecodeSession(gpu, 64, 0, keep_logits=True)
+    o = OracleSession(cpu, 64)
+    first = s.greedy_step(77)
+    want_first, _ = o.block_step([77])
+    assert first == want_first[0]
+    say("mtp draft")
+    draft = s.mtp_draft(first)
+    want_draft, want_logits, _ = o.mtp_proposal(first, o.last_hidden, 0)
+    logits = s.buffer("logits", np.float32, spec.mtp_draft_vocabulary)
+    err = np.abs(logits - want_logits[0]).max()
+    assert err <= LOGIT_TOL, err
+    _check_tokens([draft], want_logits)

@@ -321,7 +321,7 @@ def test_gdn_output_quantize(device, gx, orc):
 HQ, HKV, AD = 40, 8, 128
 
 
-@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 64), (32, 4065)])
+@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 64), (32, 4065), (5, 1), (32, 1), (3, 63), (8, 60)])
 def test_attention_matches_oracle(device, gx, orc, T, base):
     capacity = 4096 + 32
     rng = np.random.default_rng(T * 7 + base)
