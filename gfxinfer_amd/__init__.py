@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gdn_recurrent_decode_block": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, P, P]),
     "gfxinfer_launch_gdn_recurrent_window": (I32, [P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, P]),
     "gfxinfer_launch_gdn_output_quantize_i4": (I32, [P, P, P, P, P, P, U32, U32, U32, P]),
+    "gfxinfer_launch_gdn_conv_window": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, P]),
     "gfxinfer_launch_gdn_restore_prefix_all": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, U32, U32, P]),
     "gfxinfer_launch_qk_rms_norm_rope_block": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, ctypes.c_uint64, U32, F32, P]),
     "gfxinfer_launch_qk_rms_norm_rope_block_indirect_position": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, P, U32, F32, P]),

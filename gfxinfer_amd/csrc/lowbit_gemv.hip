@@ -340,11 +340,12 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     unsigned short stage_scale[kScaleIters];
 #pragma unroll
     for (unsigned p = 0; p < kMaxPieces; ++p) {
+      // Pieces of absent tokens read past the descriptor (zeros, no memory request).
       const unsigned i = p * 64u + lane;
-      const unsigned token = min(i / kRowPieces, batch - 1u);
+      const unsigned token = i / kRowPieces;
       const unsigned rem = i % kRowPieces;
-      stage[p] = __builtin_amdgcn_raw_buffer_load_b128(activations, token * row_bytes + rem * 16u,
-                                                       g0 * AGB, 0);
+      const unsigned off = i < total_pieces ? token * row_bytes + rem * 16u : 0x80000000u;
+      stage[p] = __builtin_amdgcn_raw_buffer_load_b128(activations, off, g0 * AGB, 0);
     }
     // The chunk's weight scales ([CHG groups][16 rows] fp16, contiguous in the tile):
     // one coalesced 16-byte load per lane (lanes < 2 * CHG), staged through LDS, instead
@@ -359,9 +360,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
 #pragma unroll
       for (unsigned it = 0; it < kScaleIters; ++it) {
         const unsigned e = it * 64u + lane;
-        const unsigned token = min(e / CHG, batch - 1u);
-        stage_scale[it] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, (token * groups + e % CHG) * 2u,
-                                                               g0 * 2u, 0);
+        const unsigned off = e < batch * CHG ? ((e / CHG) * groups + e % CHG) * 2u : 0x80000000u;
+        stage_scale[it] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, off, g0 * 2u, 0);
       }
     }
     // 2) Weights and weight scales of CH packs, all in flight together.

@@ -438,6 +438,202 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs args) {
   }
 }
 
+// Causal conv + gated delta rule over a window in one launch (the pair
+// gdn_conv_kernel -> gdn_recurrent_kernel with identical arithmetic).  Each
+// workgroup (value head h, 16 state columns) needs the conv outputs of the 2 x 128
+// query/key channels of its key head and of its own 16 value channels: it stages
+// fp16(projected) of those 272 channels for every token in LDS (independent loads),
+// computes the 4-tap conv + SiLU per (token, channel) in parallel, then normalizes
+// and runs the recurrence.  The query/key conv channels are shared by
+// value_heads/key_heads x 8 workgroups; the one with h % ratio == 0 and column block
+// 0 writes their final conv state and log, every workgroup writes those of its
+// value channels.  Conv states must not be updated in place (other workgroups may
+// still read the initial state).
+struct GdnWindowArgs {
+  const float* projected;       // [T][C] fp32 (C = 2*Hk*D + Hv*D)
+  const uint16_t* conv_weight;  // bf16 [C][4]
+  const __half* conv_initial;   // [C][4]
+  __half* conv_final;           // [C][4]
+  __half* conv_log;             // [T][C] or null
+  GdnArgs gdn;                  // .qkv unused
+};
+
+constexpr unsigned kWindowChannels = 2 * kGdnD + kGdnCols;  // 272
+
+__global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
+  constexpr unsigned D = kGdnD;
+  const GdnArgs& args = w.gdn;
+  __shared__ float qn[kGdnMaxTokens][D];
+  __shared__ float kn[kGdnMaxTokens][D];
+  __shared__ float vv[kGdnMaxTokens][kGdnCols];
+  __shared__ __half xs[kGdnMaxTokens + 3][kWindowChannels];  // x[t-3..T-1] per channel
+  __shared__ float cw[kWindowChannels][4];
+  __shared__ float decay_s[kGdnMaxTokens];
+  __shared__ float beta_s[kGdnMaxTokens];
+  __shared__ float tile[D][kGdnCols + 1];
+
+  const unsigned blocks_per_head = D / kGdnCols;
+  const unsigned h = blockIdx.x / blocks_per_head;
+  const unsigned cb = blockIdx.x - h * blocks_per_head;
+  const unsigned ratio = args.value_heads / args.key_heads;
+  const unsigned kh = h / ratio;
+  const unsigned T = args.tokens;
+  const std::size_t key_elements = static_cast<std::size_t>(args.key_heads) * D;
+  const std::size_t value_elements = static_cast<std::size_t>(args.value_heads) * D;
+  const std::size_t C = 2 * key_elements + value_elements;
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const bool owner = (h % ratio) == 0 && cb == 0;  // writes the shared q/k conv channels
+  const bool log_keys = args.key_log != nullptr && owner;
+
+  // Local channel j -> global channel: q of kh, k of kh, then 16 v columns of h.
+  auto channel = [&](unsigned j) -> std::size_t {
+    if (j < D) return static_cast<std::size_t>(kh) * D + j;
+    if (j < 2 * D) return key_elements + static_cast<std::size_t>(kh) * D + (j - D);
+    return 2 * key_elements + static_cast<std::size_t>(h) * D + cb * kGdnCols + (j - 2 * D);
+  };
+
+  // Stage 1: conv state (x[-3..-1] are taps 1..3 of the initial state), weights,
+  // and fp16(projected) of every token; log and final conv state by the owners.
+  for (unsigned j = tid; j < kWindowChannels; j += blockDim.x) {
+    const std::size_t c = channel(j);
+    const bool own = owner || j >= 2 * D;
+#pragma unroll
+    for (int tap = 0; tap < 4; ++tap) cw[j][tap] = bf16_to_float(w.conv_weight[c * 4 + tap]);
+    __half init[4];
+#pragma unroll
+    for (int tap = 0; tap < 4; ++tap) init[tap] = w.conv_initial[c * 4 + tap];
+    xs[0][j] = init[1];
+    xs[1][j] = init[2];
+    xs[2][j] = init[3];
+    if (own) {
+      // final state = the last four inputs x[T-4..T-1] (from the initial state when T < 4)
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) {
+        const int s = static_cast<int>(T) - 4 + tap;
+        const unsigned from_init = T + static_cast<unsigned>(tap);  // 1..3 when s < 0
+        const __half kept = from_init == 1u ? init[1] : (from_init == 2u ? init[2] : init[3]);
+        w.conv_final[c * 4 + tap] =
+            s >= 0 ? to_half(w.projected[static_cast<std::size_t>(s) * C + c]) : kept;
+      }
+    }
+  }
+  for (unsigned i = tid; i < T * kWindowChannels; i += blockDim.x) {
+    const unsigned t = i / kWindowChannels, j = i - t * kWindowChannels;
+    const std::size_t c = channel(j);
+    const __half x = to_half(w.projected[static_cast<std::size_t>(t) * C + c]);
+    xs[t + 3][j] = x;
+    if (w.conv_log != nullptr && (owner || j >= 2 * D)) w.conv_log[static_cast<std::size_t>(t) * C + c] = x;
+  }
+  // decay and beta per token (qwen_ops.hip:342-349).
+  if (tid < T) {
+    const float a_value = args.a[static_cast<std::size_t>(tid) * args.value_heads + h] +
+                          bf16_to_float(args.dt_bias[h]);
+    const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
+    const float g = -expf(bf16_to_float(args.a_log[h])) * softplus;
+    const float decay = expf(g);
+    decay_s[tid] = decay;
+    beta_s[tid] = 1.0F / (1.0F + expf(-args.b[static_cast<std::size_t>(tid) * args.value_heads + h]));
+    if (args.decay_log != nullptr && cb == 0) {
+      args.decay_log[static_cast<std::size_t>(tid) * args.value_heads + h] = decay;
+    }
+  }
+  // state tile [D rows][16 columns]
+  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
+    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
+    tile[r][c4 * 4 + 0] = v[0];
+    tile[r][c4 * 4 + 1] = v[1];
+    tile[r][c4 * 4 + 2] = v[2];
+    tile[r][c4 * 4 + 3] = v[3];
+  }
+  __syncthreads();
+
+  // Stage 2: conv + SiLU per (token, channel) -> fp16 -> float (gdn_conv_kernel order).
+  for (unsigned i = tid; i < T * kWindowChannels; i += blockDim.x) {
+    const unsigned t = i / kWindowChannels, j = i - t * kWindowChannels;
+    float conv = 0.0F;
+#pragma unroll
+    for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(xs[t + tap][j]), cw[j][tap], conv);
+    const float y = __half2float(to_half(silu(conv)));
+    if (j < D) {
+      qn[t][j] = y;
+    } else if (j < 2 * D) {
+      kn[t][j - D] = y;
+    } else {
+      vv[t][j - 2 * D] = y;
+    }
+  }
+  __syncthreads();
+
+  // Stage 3: normalized q (with the 1/sqrt(D) query scale) and k per token.
+  const float query_scale = 0.08838834764831845F;  // 1/sqrt(128), qwen_ops.hip:325
+  for (unsigned t = wave; t < T; t += 4) {
+    const float q0 = qn[t][2 * lane], q1 = qn[t][2 * lane + 1];
+    const float k0 = kn[t][2 * lane], k1 = kn[t][2 * lane + 1];
+    const float iq = rsqrtf(wave_sum(q0 * q0 + q1 * q1) + 1.0e-6F) * query_scale;
+    const float ik = rsqrtf(wave_sum(k0 * k0 + k1 * k1) + 1.0e-6F);
+    qn[t][2 * lane] = q0 * iq;
+    qn[t][2 * lane + 1] = q1 * iq;
+    kn[t][2 * lane] = k0 * ik;
+    kn[t][2 * lane + 1] = k1 * ik;
+    if (log_keys) {
+      float* kl = args.key_log + static_cast<std::size_t>(t) * key_elements + kh * D;
+      kl[2 * lane] = k0 * ik;
+      kl[2 * lane + 1] = k1 * ik;
+    }
+  }
+  __syncthreads();
+
+  // Stage 4: the recurrence (gdn_recurrent_kernel).
+  const unsigned ks = lane & 15u;
+  const unsigned col = wave * 4u + (lane >> 4);
+  float S[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
+  const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
+  for (unsigned t = 0; t < T; ++t) {
+    const float decay = decay_s[t], beta = beta_s[t];
+    float kv[8], qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kv[i] = kn[t][ks * 8 + i];
+      qv[i] = qn[t][ks * 8 + i];
+    }
+    float memory = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = S[i] * decay;
+      memory = fmaf(S[i], kv[i], memory);
+    }
+    memory = row16_sum(memory);
+    const float delta = (vv[t][col] - memory) * beta;
+    float o = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = fmaf(kv[i], delta, S[i]);
+      o = fmaf(S[i], qv[i], o);
+    }
+    o = row16_sum(o);
+    if (ks == 0) {
+      args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
+      if (args.delta_log != nullptr) {
+        args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tile[ks * 8 + i][col] = S[i];
+  __syncthreads();
+  float* final_state = args.final_state + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
+    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    f32x4 v = {tile[r][c4 * 4 + 0], tile[r][c4 * 4 + 1], tile[r][c4 * 4 + 2], tile[r][c4 * 4 + 3]};
+    *reinterpret_cast<f32x4*>(final_state + static_cast<std::size_t>(r) * D + c4 * 4) = v;
+  }
+}
+
 // Head RMSNorm * weight * SiLU(z) (qwen_ops.hip:386-409) of the mixed output,
 // optionally followed by the A4 quantizer (a head is exactly one 128 group).
 // One wave per (token, value head).
@@ -928,6 +1124,35 @@ extern "C" int32_t gfxinfer_launch_gdn_recurrent_window(
   hipLaunchKernelGGL(gdn_recurrent_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), args);
   return launch_status("GDN recurrent window launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_gdn_conv_window(
+    const float* projected_qkv, const uint16_t* bf16_conv_weight, const uint16_t* initial_conv_state,
+    uint16_t* final_conv_state, uint16_t* appended_log, const float* projected_a,
+    const float* projected_b, const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias,
+    const float* initial_recurrent_state, float* final_recurrent_state, float* mixed, float* key_log,
+    float* delta_log, float* decay_log, uint32_t batch, uint32_t key_heads, uint32_t value_heads,
+    uint32_t head_size, void* stream) {
+  if (projected_qkv == nullptr || bf16_conv_weight == nullptr || initial_conv_state == nullptr ||
+      final_conv_state == nullptr || final_conv_state == initial_conv_state ||
+      projected_a == nullptr || projected_b == nullptr || bf16_a_log == nullptr ||
+      bf16_dt_bias == nullptr || initial_recurrent_state == nullptr ||
+      final_recurrent_state == nullptr || mixed == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid fused GDN conv/window arguments (the conv state "
+                                       "cannot be updated in place)");
+  }
+  if (const int32_t s = gdn_check("fused GDN conv/window", batch, key_heads, value_heads, head_size);
+      s != GFXI_OK) {
+    return s;
+  }
+  GdnWindowArgs w{projected_qkv, bf16_conv_weight, reinterpret_cast<const __half*>(initial_conv_state),
+                  reinterpret_cast<__half*>(final_conv_state), reinterpret_cast<__half*>(appended_log),
+                  GdnArgs{nullptr, projected_a, projected_b, bf16_a_log, bf16_dt_bias,
+                          initial_recurrent_state, final_recurrent_state, mixed, key_log, delta_log,
+                          decay_log, batch, key_heads, value_heads}};
+  hipLaunchKernelGGL(gdn_window_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w);
+  return launch_status("fused GDN conv/window launch failed");
 }
 
 extern "C" int32_t gfxinfer_launch_gdn_restore_prefix_all(

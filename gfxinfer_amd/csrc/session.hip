@@ -306,19 +306,19 @@ struct gfxinfer_session {
                            {&L.a, projected_a},
                            {&L.b, projected_b}},
                           batch));
-      uint16_t* conv_state = conv_states + L.state_index * conv_state_elements();
-      float* state = gdn_states + L.state_index * gdn_state_elements();
-      uint16_t* conv_final = record_rollback
-                                 ? conv_snapshot + L.state_index * conv_state_elements()
-                                 : conv_state;
-      float* state_final =
-          record_rollback ? gdn_snapshot + L.state_index * gdn_state_elements() : state;
+      // The window always writes its final states into the snapshot buffers (the fused
+      // conv cannot update in place); the caller keeps them by swapping buffers, or,
+      // after a partial acceptance, replays the logged prefix onto the originals
+      // (qwen_runtime.cpp:484-511 selects the same buffers when recording).
+      const uint16_t* conv_state = conv_states + L.state_index * conv_state_elements();
+      const float* state = gdn_states + L.state_index * gdn_state_elements();
+      uint16_t* conv_final = conv_snapshot + L.state_index * conv_state_elements();
+      float* state_final = gdn_snapshot + L.state_index * gdn_state_elements();
       const std::size_t log_token = L.state_index * kMaxBlock;
-      GFXI_TRY(gfxinfer_launch_gdn_conv_update_block(
-          projected_main, L.conv, conv_state, conv_final, convolved,
-          record_rollback ? conv_log + log_token * channels : nullptr, channels, batch, stream));
-      GFXI_TRY(gfxinfer_launch_gdn_recurrent_window(
-          convolved, projected_a, projected_b, L.a_log, L.dt_bias, state, state_final, gdn_mixed,
+      GFXI_TRY(gfxinfer_launch_gdn_conv_window(
+          projected_main, L.conv, conv_state, conv_final,
+          record_rollback ? conv_log + log_token * channels : nullptr, projected_a, projected_b,
+          L.a_log, L.dt_bias, state, state_final, gdn_mixed,
           record_rollback ? key_log + log_token * gdn_key : nullptr,
           record_rollback ? delta_log + log_token * gdn_value : nullptr,
           record_rollback ? decay_log + log_token * spec.gdn_value_head_count : nullptr, batch,
@@ -566,6 +566,10 @@ struct gfxinfer_session {
     const auto batch = static_cast<unsigned>(count);
     for (unsigned i = 0; i < batch; ++i) GFXI_TRY(gather(hidden_a + i * H, tokens[i], nullptr));
     GFXI_TRY(decoder_stack(batch, nullptr));
+    // The windows wrote the advanced states into the snapshot buffers: keep them.
+    std::swap(conv_states, conv_snapshot);
+    std::swap(gdn_states, gdn_snapshot);
+    parity = !parity;
     if (auto e = hipMemcpyAsync(host_result, selected, count * 4, hipMemcpyDeviceToHost, stream);
         e != hipSuccess) {
       return hip_fail(e, "decode block token download failed");

@@ -283,6 +283,18 @@ int32_t gfxinfer_launch_gdn_output_quantize_i4(const float* mixed, const float* 
                                                uint32_t batch, uint32_t value_heads,
                                                uint32_t head_size, void* stream);
 
+/* gfxinfer_launch_gdn_conv_update_block followed by gfxinfer_launch_gdn_recurrent_window in one
+ * launch, with the same arithmetic and outputs (the convolved channels are not written out).
+ * No reference counterpart: the reference runs the two launches (qwen_runtime.cpp:502-518).
+ * The conv state cannot be updated in place (final_conv_state != initial_conv_state). */
+int32_t gfxinfer_launch_gdn_conv_window(
+    const float* projected_qkv, const uint16_t* bf16_conv_weight, const uint16_t* initial_conv_state,
+    uint16_t* final_conv_state, uint16_t* appended_log, const float* projected_a,
+    const float* projected_b, const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias,
+    const float* initial_recurrent_state, float* final_recurrent_state, float* mixed, float* key_log,
+    float* delta_log, float* decay_log, uint32_t batch, uint32_t key_heads, uint32_t value_heads,
+    uint32_t head_size, void* stream);
+
 /* qwen_ops.h launch_gdn_restore_prefix_all (qwen_ops.hip:1141-1179): replay the first
  * accepted_tokens (1..maximum_logged_tokens) logged tokens of every layer onto the pre-window
  * conv and recurrent states, bit-identical to running only those tokens.  Logs are

@@ -409,3 +409,44 @@ def test_argmax_ties_and_mapping(device, gx, orc):
     one = empty((1,), np.uint32)
     gx.check(L.gfxinfer_launch_argmax_mapped(D_(logits[2]), D_(ids), one.data_ptr(), 98304, None))
     assert int(host(one).view(np.uint32)[0]) == int(ids[np.argmax(logits[2, :98304])])
+
+
+@pytest.mark.parametrize("T", [1, 3, 5, 32])
+def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T):
+    """The fused conv + recurrence launch reproduces gdn_conv_update_block followed by
+    gdn_recurrent_window bit for bit (states, logs, unnormalized output)."""
+    rng = np.random.default_rng(70 + T)
+    proj = rng.standard_normal((T, C)).astype(np.float32)
+    w = _bf16(rng.standard_normal((C, 4)) * 0.5)
+    c0 = _half(rng.standard_normal((C, 4)))
+    a = rng.standard_normal((T, HV)).astype(np.float32)
+    b = rng.standard_normal((T, HV)).astype(np.float32)
+    a_log, dt = _bf16(rng.standard_normal(HV) * 0.5), _bf16(rng.standard_normal(HV) * 0.5)
+    s0 = (rng.standard_normal((HV, D, D)) * 0.1).astype(np.float32)
+    L = gx.lib()
+    dp, dw, dc0, da, db, dal, ddt, ds0 = (D_(x) for x in (proj, w, c0, a, b, a_log, dt, s0))
+    outs = []
+    for fused in (False, True):
+        cf = empty((C, 4), np.uint16)
+        clog = empty((T, C), np.uint16)
+        sf = empty((HV, D, D), np.float32)
+        mixed = empty((T, HV * D), np.float32)
+        kl, dl, yl = empty((T, HK * D), np.float32), empty((T, HV * D), np.float32), empty((T, HV), np.float32)
+        say("gdn conv window", T, "fused" if fused else "two launches")
+        if fused:
+            gx.check(L.gfxinfer_launch_gdn_conv_window(dp, dw, dc0, cf.data_ptr(), clog.data_ptr(), da, db, dal, ddt,
+                                                       ds0, sf.data_ptr(), mixed.data_ptr(), kl.data_ptr(),
+                                                       dl.data_ptr(), yl.data_ptr(), T, HK, HV, D, None))
+        else:
+            conv = empty((T, C), np.uint16)
+            gx.check(L.gfxinfer_launch_gdn_conv_update_block(dp, dw, dc0, cf.data_ptr(), conv.data_ptr(),
+                                                             clog.data_ptr(), C, T, None))
+            gx.check(L.gfxinfer_launch_gdn_recurrent_window(conv.data_ptr(), da, db, dal, ddt, ds0, sf.data_ptr(),
+                                                            mixed.data_ptr(), kl.data_ptr(), dl.data_ptr(),
+                                                            yl.data_ptr(), T, HK, HV, D, None))
+        outs.append([host(x) for x in (cf, clog, sf, mixed, kl, dl, yl)])
+    for got, want in zip(outs[1], outs[0]):
+        assert np.array_equal(got, want)
+    # the conv state cannot be updated in place
+    assert L.gfxinfer_launch_gdn_conv_window(dp, dw, dc0, dc0, None, da, db, dal, ddt, ds0, ds0, ds0, None, None,
+                                             None, T, HK, HV, D, None) == gx.INVALID_ARGUMENT
