@@ -61,6 +61,8 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_quantize_activation_i4": (I32, [P, P, P, SZ, U32, P]),
     "gfxinfer_launch_quantize_activation_i8": (I32, [P, P, P, SZ, U32, P]),
     "gfxinfer_launch_gfx950_i4_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, I32, P]),
+    "gfxinfer_launch_gfx950_i4_gemm_split": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, U32, P]),
+    "gfxinfer_gemm_split_count": (U32, [SZ, SZ, U32]),
     "gfxinfer_launch_gfx950_i4_gemm_half": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, I32, P]),
     "gfxinfer_launch_gfx950_i4_gemm_fused": (I32, [I32, P, SZ, P, P, SZ, U32, I32, P]),
     "gfxinfer_launch_gfx950_i8_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, P]),
@@ -74,6 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_residual_add_rms_norm_batch": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_rms_norm_quantize_i4": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_residual_add_rms_norm_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, U32, F32, I32, P]),
+    "gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes": (I32, [P, P, U32, P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_dual_rms_norm_concat": (I32, [P, P, P, P, P, SZ, F32, I32, P]),
     "gfxinfer_launch_silu_multiply": (I32, [P, P, P, SZ, P]),
     "gfxinfer_launch_silu_multiply_quantize_i4": (I32, [P, P, P, P, SZ, U32, P]),
@@ -196,6 +199,15 @@ def launch_quantize_group128(fmt, weights, rows, columns, codes, scales, flag=No
 
 def launch_i4_gemm(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
     check(lib().gfxinfer_launch_gfx950_i4_gemm(fmt, _p(w), _p(ws), _p(a), _p(as_), _p(out), rows, columns, batch, 1, _stream(stream)))
+
+
+def launch_i4_gemm_split(fmt, w, ws, a, as_, planes, rows, columns, batch, splits, stream=None):
+    """Split-K GEMM: `splits` fp32 planes [splits, batch, rows] whose sum is the product."""
+    check(lib().gfxinfer_launch_gfx950_i4_gemm_split(fmt, _p(w), _p(ws), _p(a), _p(as_), _p(planes), rows, columns, batch, splits, _stream(stream)))
+
+
+def gemm_split_count(rows, columns, batch):
+    return int(lib().gfxinfer_gemm_split_count(rows, columns, batch))
 
 
 def launch_i4_gemm_half(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):

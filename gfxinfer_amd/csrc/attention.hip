@@ -124,10 +124,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
         sc[j][r] = s;
         best = fmaxf(best, s);
       }
-      best = fmaxf(best, __shfl_xor(best, 1));
-      best = fmaxf(best, __shfl_xor(best, 2));
-      best = fmaxf(best, __shfl_xor(best, 4));
-      best = fmaxf(best, __shfl_xor(best, 8));
+      best = row16_max(best);
       float total = 0.0F;
 #pragma unroll
       for (unsigned j = 0; j < kTiles; ++j) {
@@ -137,10 +134,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
         ps[wave][4 * kb + r][j * 16 + m] = hi;
         ps_lo[wave][4 * kb + r][j * 16 + m] = static_cast<_Float16>(p - static_cast<float>(hi));
       }
-      total += __shfl_xor(total, 1);
-      total += __shfl_xor(total, 2);
-      total += __shfl_xor(total, 4);
-      total += __shfl_xor(total, 8);
+      total = row16_sum(total);
       mx[r] = best;
       sum[r] = total;
     }

@@ -33,6 +33,53 @@ __device__ __forceinline__ __half to_half(float x) {
   return __float2half(x);
 }
 
+// Cross-lane reductions through DPP lane moves (VALU, no LDS round trip as
+// __shfl_xor's ds_bpermute takes).  DPP controls: quad_perm [1,0,3,2] (lane ^ 1),
+// quad_perm [2,3,0,1] (lane ^ 2), row_half_mirror (lane i <-> 7 - i within 8 lanes),
+// row_mirror (lane i <-> 15 - i within 16 lanes).  After the two quad steps every
+// lane of a quad holds the quad's value, so the mirrors pair equal partials exactly
+// as xor 4 and xor 8 would: the 16-lane results are bit-identical to the xor tree.
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// Sum / maximum over the 16 lanes of each row, in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<kDppXor1>(v);
+  v += dpp_move<kDppXor2>(v);
+  v += dpp_move<kDppHalfMirror>(v);
+  v += dpp_move<kDppMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<kDppXor1>(v));
+  v = fmaxf(v, dpp_move<kDppXor2>(v));
+  v = fmaxf(v, dpp_move<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_move<kDppMirror>(v));
+  return v;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wave-wide sum / maximum (all 64 lanes active), wave-uniform result:
+// (row0 + row1) + (row2 + row3) of the row sums.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 // Signed quantization level of value at scale (quantization.cpp:29-56: encode_value
 // then decode_value), clamped to the format's range.
 template <int Format>

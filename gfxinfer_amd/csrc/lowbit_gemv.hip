@@ -30,12 +30,6 @@ using u32x2 = unsigned __attribute__((ext_vector_type(2)));
 // scales are bit-identical to the reference.
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float wave_max(float value) {
-#pragma unroll
-  for (int offset = 32; offset != 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
-  return value;
-}
-
 template <int Bits>
 __global__ __launch_bounds__(256) void quantize_activation_kernel(
     const __half2* __restrict__ input, uint8_t* __restrict__ output, __half* __restrict__ scales,
@@ -205,7 +199,23 @@ struct GemmArgs {
   uint32_t columns;
   uint32_t groups;
   uint32_t batch;
+  // Split-K: workgroup b computes split b % splits of the packs of K for tile (block)
+  // b / splits and writes fp32 plane `split` ([splits][batch][rows] per matrix); the
+  // consumer sums the planes in plane order.  1 = one plane, the plain product.
+  uint32_t splits;
 };
+
+// Packs [begin, end) of this wave: split `split` of `splits` equal ranges of the
+// matrix's packs, then wave `wave` of `waves` equal pieces of that range.
+struct PackRange {
+  unsigned begin, end;
+};
+__device__ __forceinline__ PackRange wave_packs(unsigned packs, unsigned split, unsigned splits,
+                                                unsigned wave, unsigned waves) {
+  const unsigned first = packs * split / splits;
+  const unsigned span = packs * (split + 1) / splits - first;
+  return {first + span * wave / waves, first + span * (wave + 1) / waves};
+}
 
 // Orderable argmax key of logit v at row: the high word orders values (a total
 // order on floats with -0 folded into +0), the low word is ~row so that equal
@@ -276,7 +286,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   uint8_t* lds = lds_all + wave * layout.region;
 
   // Matrix selection for fused launches.
-  unsigned tile = blockIdx.x;
+  const unsigned split = blockIdx.x % args.splits;
+  unsigned tile = blockIdx.x / args.splits;
   unsigned index = 0;
 #pragma unroll
   for (unsigned i = 1; i < 4; ++i) {
@@ -300,9 +311,9 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   const unsigned window = n / TPAD;
   const unsigned w_voffset = lane * LB;
 
-  const unsigned packs = (groups + GP - 1) / GP;
-  const unsigned pack_begin = packs * wave / waves;
-  const unsigned pack_end = packs * (wave + 1) / waves;
+  const PackRange range = wave_packs((groups + GP - 1) / GP, split, args.splits, wave, waves);
+  const unsigned pack_begin = range.begin;
+  const unsigned pack_end = range.end;
 
   // LDS byte offset of this lane's B operand for group j of a pack, token block t
   // (relative to the pack's first group); lanes outside the window read zeros.
@@ -364,6 +375,11 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
         stage_scale[it] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, off, g0 * 2u, 0);
       }
     }
+    // Keep these small loads ahead of the weight stream: loads complete in issue
+    // order, so staging them then waits for them alone (a weight-scale load moved
+    // behind the weights would make the staging, and so every MFMA, wait for the
+    // whole chunk).
+    __builtin_amdgcn_sched_barrier(0);
     // 2) Weights and weight scales of CH packs, all in flight together.
     unsigned wreg[CH][GP][WD];
 #pragma unroll
@@ -533,10 +549,12 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     }
   }
   if (window != 0 || matrix.output == nullptr) return;
+  const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
 #pragma unroll
   for (int t = 0; t < NTB; ++t) {
     if (t * 16u + slot >= batch) continue;
-    const std::size_t out = static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
+    const std::size_t out =
+        plane + static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
     if constexpr (HalfOut) {
       __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
@@ -591,7 +609,8 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
   const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const unsigned waves = blockDim.x >> 6;
 
-  unsigned block = blockIdx.x;
+  const unsigned split = blockIdx.x % args.splits;
+  unsigned block = blockIdx.x / args.splits;
   unsigned index = 0;
 #pragma unroll
   for (unsigned i = 1; i < 4; ++i) {
@@ -638,9 +657,9 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
     as_voffset[t] = ((t * 16u + slot) * groups + window) * 2u;
   }
 
-  const unsigned packs = (groups + GP - 1) / GP;
-  const unsigned pack_begin = packs * wave / waves;
-  const unsigned pack_end = packs * (wave + 1) / waves;
+  const PackRange range = wave_packs((groups + GP - 1) / GP, split, args.splits, wave, waves);
+  const unsigned pack_begin = range.begin;
+  const unsigned pack_end = range.end;
 
   float acc[R][NTB][4];
 #pragma unroll
@@ -688,6 +707,8 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
         }
       }
     }
+    // Activations (L2) of all CH packs first, then the weight stream (HBM): loads
+    // complete in issue order, so routing the activations waits for them alone.
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
       const unsigned pack = min(base + ci, pack_end - 1u);
@@ -713,6 +734,11 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
                                                               pack * GP * 2u, 0);
         }
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (unsigned ci = 0; ci < CH; ++ci) {
+      const unsigned pack = min(base + ci, pack_end - 1u);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -882,6 +908,7 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
           for (int i = 0; i < 4; ++i) acc[r][t][i] += other[((r * NTB + t) * 4 + i) * 64 + lane];
     }
   }
+  const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (static_cast<unsigned>(r) >= valid) break;
@@ -909,7 +936,8 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
       if (t * 16u + slot >= batch) continue;
-      const std::size_t out = static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
+      const std::size_t out =
+          plane + static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
       if constexpr (HalfOut) {
         __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
@@ -990,6 +1018,7 @@ int waves_override() {
 }
 
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per CU (and per workgroup)
+constexpr uint32_t kMaxSplits = 8;            // split-K planes per GEMM
 
 unsigned choose_waves(uint32_t groups, unsigned gp) {
   if (const int forced = waves_override(); forced != 0) return static_cast<unsigned>(forced);
@@ -1068,10 +1097,12 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
       if (used) blocks += (args.matrix[i].tiles + r - 1) / r;
     }
     args.tile_begin[4] = blocks;
-    const unsigned waves = resident_waves(reinterpret_cast<const void*>(kernel), args.groups, blocks,
-                                          r * ntb * 4u * 64u * 4u);
+    const unsigned waves =
+        resident_waves(reinterpret_cast<const void*>(kernel), args.groups / args.splits,
+                       blocks * args.splits, r * ntb * 4u * 64u * 4u);
     const std::size_t lds = static_cast<std::size_t>(waves) * r * ntb * 4u * 64u * 4u;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * waves), waves > 1 ? lds : 0, stream, args);
+    hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), waves > 1 ? lds : 0,
+                       stream, args);
   };
   (void)total_tiles;
   const int forced = rowtiles_override();
@@ -1106,15 +1137,15 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
   }
   const uint32_t batch = args.batch;
   auto go = [&](auto kernel, unsigned gp, unsigned ch, unsigned ntb) {
-    unsigned waves = choose_waves(args.groups, 1);
+    unsigned waves = choose_waves(args.groups / args.splits, 1);
     if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
     const GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
     // A workgroup may hold at most the CU's 160 KiB of LDS (32 tokens x 136 groups
     // would otherwise ask for 8 x 21 KiB).
     const unsigned lds_waves = kLdsBytes / layout.region;
     if (waves > lds_waves) waves = lds_waves;
-    hipLaunchKernelGGL(kernel, dim3(total_tiles), dim3(64 * waves), layout.region * waves, stream,
-                       args, layout);
+    hipLaunchKernelGGL(kernel, dim3(total_tiles * args.splits), dim3(64 * waves),
+                       layout.region * waves, stream, args, layout);
   };
   // CH = packs per load chunk: about ten groups of weights in flight per wave.
   if (batch <= 4) {
@@ -1150,7 +1181,8 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
                    std::size_t count, int32_t activation_bits, const void* activations,
                    const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
                    uint32_t batch, bool half_out, hipStream_t stream,
-                   unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0) {
+                   unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0,
+                   uint32_t splits = 1) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W3G128 and W4G128");
   }
@@ -1164,6 +1196,13 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   }
   if (!aligned(activations, 16)) {
     return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " requires 16-byte aligned activations");
+  }
+  if (splits == 0 || splits > kMaxSplits || splits > columns / kGroup ||
+      (splits > 1 && (half_out || partials != nullptr || argmax_keys != nullptr))) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " split count must be in [1, " +
+                                           std::to_string(kMaxSplits) +
+                                           "], at most K/128, and 1 for fp16, partial or argmax "
+                                           "outputs");
   }
   GemmArgs args{};
   uint64_t tiles = 0;
@@ -1200,6 +1239,10 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   args.columns = static_cast<uint32_t>(columns);
   args.groups = static_cast<uint32_t>(columns / kGroup);
   args.batch = batch;
+  args.splits = splits;
+  if (tiles * splits > std::numeric_limits<uint32_t>::max() / 2) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " grid is too large");
+  }
   const auto total = static_cast<uint32_t>(tiles);
   if (partials != nullptr) {
     if (activation_bits == 4) dispatch_gemm<4, false, true>(format, args, total, stream);
@@ -1331,6 +1374,38 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm(int32_t format, const uint8_t*
   return gemm_entry("gfx950 INT4 GEMM", format, &binding, 1, 4, packed_activations,
                     activation_scales, nullptr, columns, batch, false,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" uint32_t gfxinfer_gemm_split_count(size_t rows, size_t columns, uint32_t batch) {
+  // Enough workgroups to fill the chip about four times over (a grid below that
+  // leaves CUs idle or runs a partial second round), each split keeping at least
+  // eight groups of K; the chosen kernel handles 2 row tiles per workgroup above
+  // 8 tokens.  GFXI_GEMM_SPLIT_TARGET overrides the target (tuning knob).
+  static const uint64_t target = [] {
+    const char* text = std::getenv("GFXI_GEMM_SPLIT_TARGET");
+    const long v = text != nullptr ? std::atol(text) : 0;
+    return v > 0 ? static_cast<uint64_t>(v) : uint64_t{1024};
+  }();
+  if (rows == 0 || columns < kGroup || batch == 0) return 1;
+  const uint64_t tiles = (rows + 15) / 16;
+  const uint64_t blocks = batch > 8 ? (tiles + 1) / 2 : tiles;
+  uint64_t splits = (target + blocks - 1) / blocks;
+  splits = std::min<uint64_t>(splits, kMaxSplits);
+  splits = std::min<uint64_t>(splits, columns / kGroup / 8);
+  return static_cast<uint32_t>(std::max<uint64_t>(splits, 1));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_split(int32_t format, const uint8_t* tiled_weights,
+                                                        const uint16_t* tiled_weight_scales,
+                                                        const uint8_t* packed_activations,
+                                                        const uint16_t* activation_scales,
+                                                        float* output_planes, size_t rows,
+                                                        size_t columns, uint32_t batch,
+                                                        uint32_t splits, void* stream) {
+  const MatrixBinding binding{tiled_weights, tiled_weight_scales, output_planes, rows};
+  return gemm_entry("gfx950 split-K INT4 GEMM", format, &binding, 1, 4, packed_activations,
+                    activation_scales, nullptr, columns, batch, false,
+                    static_cast<hipStream_t>(stream), nullptr, 0, splits);
 }
 
 extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_half(int32_t format, const uint8_t* tiled_weights,

@@ -24,27 +24,6 @@ __device__ __forceinline__ float bf16_to_float(uint16_t value) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
 
-__device__ __forceinline__ float wave_sum(float value) {
-#pragma unroll
-  for (int offset = 32; offset != 0; offset >>= 1) value += __shfl_xor(value, offset);
-  return value;
-}
-
-__device__ __forceinline__ float wave_max(float value) {
-#pragma unroll
-  for (int offset = 32; offset != 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
-  return value;
-}
-
-// Sum over the 16 lanes of a row (lanes l, l^1, ..., l^8).
-__device__ __forceinline__ float row16_sum(float value) {
-  value += __shfl_xor(value, 1);
-  value += __shfl_xor(value, 2);
-  value += __shfl_xor(value, 4);
-  value += __shfl_xor(value, 8);
-  return value;
-}
-
 // Block-wide sum for blockDim.x <= 1024 (all threads receive the result).
 __device__ float block_sum(float value, float* scratch) {
   value = wave_sum(value);
@@ -87,7 +66,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
     const __half* __restrict__ input, const float* __restrict__ update,
     __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
     __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
-    uint32_t elements, float epsilon, bool unit_offset) {
+    uint32_t elements, float epsilon, bool unit_offset, uint32_t planes, uint64_t plane_stride) {
   extern __shared__ __align__(16) uint8_t smem[];
   __half* row = reinterpret_cast<__half*>(smem);           // [elements] staged values
   float* scratch = reinterpret_cast<float*>(smem + ((elements * 2 + 15) & ~15u));
@@ -96,7 +75,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
     __half v = input[base + i];
     if constexpr (Residual) {
-      v = to_half(__half2float(v) + update[base + i]);
+      float u = update[base + i];
+      for (uint32_t p = 1; p < planes; ++p) u += update[p * plane_stride + base + i];
+      v = to_half(__half2float(v) + u);
       residual_out[base + i] = v;
     }
     row[i] = v;
@@ -122,35 +103,67 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
 }
 
-// Register-resident variant for rows of up to kNormSlots * 16 * 128 elements (even
+// Register-resident variant for rows of up to Slots * 16 * 128 elements (even
 // count): one workgroup of up to 16 waves per row, wave w owns 128-element slots
 // w, w + waves, ...; each lane keeps its two values per slot in registers, so the
 // row is read once, reduced once and (Quantize) each 128 group is one wave's A4
-// quantizer.  Same arithmetic per element as rms_norm_kernel.
+// quantizer.  Every global load (row, weights, all update planes) is issued before
+// the first use.  The update is the sum of `planes` fp32 planes `plane_stride`
+// apart, added in plane order (the split-K GEMM's output).  Same arithmetic per
+// element as rms_norm_kernel.
 constexpr unsigned kNormSlots = 10;
+constexpr unsigned kNormPlaneSlots = 3;  // split-update variant: rows up to 6144
+constexpr unsigned kNormMaxPlanes = 8;
 constexpr uint32_t kNormFastMax = kNormSlots * 16u * 128u;
 
-template <bool Residual, bool Quantize>
+template <bool Residual, bool Quantize, unsigned Slots, unsigned MaxPlanes>
 __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     const __half* __restrict__ input, const float* __restrict__ update,
     __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
     __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
-    uint32_t elements, float epsilon, bool unit_offset) {
+    uint32_t elements, float epsilon, bool unit_offset, uint32_t planes, uint64_t plane_stride) {
   __shared__ float scratch[16];
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
-  float x[kNormSlots][2];
+  // 1) Loads.  Dead slots read element 0 (always valid) and are ignored.
+  uint32_t hin[Slots];
+  uint32_t wpair[Slots];  // the two bf16 weights of each lane's pair
+  float2 upd[Slots][MaxPlanes];
+#pragma unroll
+  for (unsigned j = 0; j < Slots; ++j) {
+    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    const uint32_t at = i < elements ? i : 0u;
+    hin[j] = *reinterpret_cast<const uint32_t*>(input + base + at);
+    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+    if constexpr (Residual) {
+#pragma unroll
+      for (unsigned p = 0; p < MaxPlanes; ++p) {
+        if (p < planes) {
+          upd[j][p] = *reinterpret_cast<const float2*>(update + p * plane_stride + base + at);
+        }
+      }
+    }
+  }
+  // 2) Residual add (fp16 rounding of the sum), squares.
+  float x[Slots][2];
   float square = 0.0F;
 #pragma unroll
-  for (unsigned j = 0; j < kNormSlots; ++j) {
+  for (unsigned j = 0; j < Slots; ++j) {
     x[j][0] = 0.0F;
     x[j][1] = 0.0F;
     const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
     if (i < elements) {
-      const __half2 h = *reinterpret_cast<const __half2*>(input + base + i);
-      __half a = __low2half(h), b = __high2half(h);
+      __half a = __ushort_as_half(static_cast<unsigned short>(hin[j] & 0xffffu));
+      __half b = __ushort_as_half(static_cast<unsigned short>(hin[j] >> 16));
       if constexpr (Residual) {
-        const float2 u = *reinterpret_cast<const float2*>(update + base + i);
+        float2 u = upd[j][0];
+#pragma unroll
+        for (unsigned p = 1; p < MaxPlanes; ++p) {
+          if (p < planes) {
+            u.x += upd[j][p].x;
+            u.y += upd[j][p].y;
+          }
+        }
         a = to_half(__half2float(a) + u.x);
         b = to_half(__half2float(b) + u.y);
         *reinterpret_cast<__half2*>(residual_out + base + i) = __halves2half2(a, b);
@@ -164,14 +177,16 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
   const float total = block_sum(square, scratch);
   const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
 #pragma unroll
-  for (unsigned j = 0; j < kNormSlots; ++j) {
+  for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t g = wave + j * waves;
     const uint32_t i = g * 128u + 2u * lane;
     if (g * 128u >= elements) break;  // wave-uniform
     __half n0 = __float2half(0.0F), n1 = n0;
     if (i < elements) {
-      n0 = to_half(x[j][0] * inverse * norm_scale(weight, i, unit_offset));
-      n1 = to_half(x[j][1] * inverse * norm_scale(weight, i + 1, unit_offset));
+      const float w0 = bf16_to_float(static_cast<uint16_t>(wpair[j] & 0xffffu));
+      const float w1 = bf16_to_float(static_cast<uint16_t>(wpair[j] >> 16));
+      n0 = to_half(x[j][0] * inverse * (unit_offset ? w0 + 1.0F : w0));
+      n1 = to_half(x[j][1] * inverse * (unit_offset ? w1 + 1.0F : w1));
       if (output != nullptr) *reinterpret_cast<__half2*>(output + base + i) = __halves2half2(n0, n1);
     }
     if constexpr (Quantize) {
@@ -492,62 +507,112 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
     return 2 * key_elements + static_cast<std::size_t>(h) * D + cb * kGdnCols + (j - 2 * D);
   };
 
-  // Stage 1: conv state (x[-3..-1] are taps 1..3 of the initial state), weights,
-  // and fp16(projected) of every token; log and final conv state by the owners.
-  for (unsigned j = tid; j < kWindowChannels; j += blockDim.x) {
-    const std::size_t c = channel(j);
-    const bool own = owner || j >= 2 * D;
+  // Stage 1: every global load is issued before the first use (one memory latency):
+  // the state tile, fp16(projected) of the 272 channels per token as 4-channel runs,
+  // a/b of the head, the conv weights and the initial conv state.
+  constexpr unsigned kQuads = kWindowChannels / 4;                        // 68
+  constexpr unsigned kTileLoads = D * (kGdnCols / 4) / 256;                // 2
+  constexpr unsigned kInputLoads = (kGdnMaxTokens * kQuads + 255) / 256;   // 9
+  const unsigned quads = T * kQuads;
+  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  f32x4 tv[kTileLoads];
 #pragma unroll
-    for (int tap = 0; tap < 4; ++tap) cw[j][tap] = bf16_to_float(w.conv_weight[c * 4 + tap]);
-    __half init[4];
+  for (unsigned u = 0; u < kTileLoads; ++u) {
+    const unsigned i = tid + u * 256, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    tv[u] = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
+  }
+  f32x4 xv[kInputLoads];
 #pragma unroll
-    for (int tap = 0; tap < 4; ++tap) init[tap] = w.conv_initial[c * 4 + tap];
-    xs[0][j] = init[1];
-    xs[1][j] = init[2];
-    xs[2][j] = init[3];
-    if (own) {
-      // final state = the last four inputs x[T-4..T-1] (from the initial state when T < 4)
+  for (unsigned u = 0; u < kInputLoads; ++u) {
+    const unsigned i = tid + u * 256;
+    if (i < quads) {
+      const unsigned t = i / kQuads, q = i - t * kQuads;
+      xv[u] = *reinterpret_cast<const f32x4*>(w.projected + static_cast<std::size_t>(t) * C +
+                                              channel(q * 4));
+    }
+  }
+  float a_in = 0.0F, b_in = 0.0F;
+  if (tid < T) {
+    a_in = args.a[static_cast<std::size_t>(tid) * args.value_heads + h];
+    b_in = args.b[static_cast<std::size_t>(tid) * args.value_heads + h];
+  }
+  uint16_t wv[2][4];
+  __half iv[2][4];
+#pragma unroll
+  for (unsigned u = 0; u < 2; ++u) {
+    const unsigned j = tid + u * 256;
+    if (j < kWindowChannels) {
+      const std::size_t c = channel(j);
 #pragma unroll
       for (int tap = 0; tap < 4; ++tap) {
-        const int s = static_cast<int>(T) - 4 + tap;
-        const unsigned from_init = T + static_cast<unsigned>(tap);  // 1..3 when s < 0
-        const __half kept = from_init == 1u ? init[1] : (from_init == 2u ? init[2] : init[3]);
-        w.conv_final[c * 4 + tap] =
-            s >= 0 ? to_half(w.projected[static_cast<std::size_t>(s) * C + c]) : kept;
+        wv[u][tap] = w.conv_weight[c * 4 + tap];
+        iv[u][tap] = w.conv_initial[c * 4 + tap];
       }
     }
   }
-  for (unsigned i = tid; i < T * kWindowChannels; i += blockDim.x) {
-    const unsigned t = i / kWindowChannels, j = i - t * kWindowChannels;
-    const std::size_t c = channel(j);
-    const __half x = to_half(w.projected[static_cast<std::size_t>(t) * C + c]);
-    xs[t + 3][j] = x;
-    if (w.conv_log != nullptr && (owner || j >= 2 * D)) w.conv_log[static_cast<std::size_t>(t) * C + c] = x;
+
+#pragma unroll
+  for (unsigned u = 0; u < kTileLoads; ++u) {
+    const unsigned i = tid + u * 256, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[r][c4 * 4 + e] = tv[u][e];
+  }
+#pragma unroll
+  for (unsigned u = 0; u < kInputLoads; ++u) {
+    const unsigned i = tid + u * 256;
+    if (i < quads) {
+      const unsigned t = i / kQuads, q = i - t * kQuads;
+      uint32_t bits[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const __half x = to_half(xv[u][e]);
+        xs[t + 3][q * 4 + e] = x;
+        bits[e] = __half_as_ushort(x);
+      }
+      if (w.conv_log != nullptr && (owner || q * 4 >= 2 * D)) {
+        const uint2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+        *reinterpret_cast<uint2*>(w.conv_log + static_cast<std::size_t>(t) * C + channel(q * 4)) =
+            packed;
+      }
+    }
+  }
+#pragma unroll
+  for (unsigned u = 0; u < 2; ++u) {
+    const unsigned j = tid + u * 256;
+    if (j < kWindowChannels) {
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) cw[j][tap] = bf16_to_float(wv[u][tap]);
+      xs[0][j] = iv[u][1];
+      xs[1][j] = iv[u][2];
+      xs[2][j] = iv[u][3];
+    }
   }
   // decay and beta per token (qwen_ops.hip:342-349).
   if (tid < T) {
-    const float a_value = args.a[static_cast<std::size_t>(tid) * args.value_heads + h] +
-                          bf16_to_float(args.dt_bias[h]);
+    const float a_value = a_in + bf16_to_float(args.dt_bias[h]);
     const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
     const float g = -expf(bf16_to_float(args.a_log[h])) * softplus;
     const float decay = expf(g);
     decay_s[tid] = decay;
-    beta_s[tid] = 1.0F / (1.0F + expf(-args.b[static_cast<std::size_t>(tid) * args.value_heads + h]));
+    beta_s[tid] = 1.0F / (1.0F + expf(-b_in));
     if (args.decay_log != nullptr && cb == 0) {
       args.decay_log[static_cast<std::size_t>(tid) * args.value_heads + h] = decay;
     }
   }
-  // state tile [D rows][16 columns]
-  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
-  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
-    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
-    const f32x4 v = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
-    tile[r][c4 * 4 + 0] = v[0];
-    tile[r][c4 * 4 + 1] = v[1];
-    tile[r][c4 * 4 + 2] = v[2];
-    tile[r][c4 * 4 + 3] = v[3];
-  }
   __syncthreads();
+
+  // Final conv state = the last four inputs x[T-4..T-1] = xs[T-1..T+2] (xs[0..2]
+  // hold the initial state's taps 1..3 when T < 4), written by the channel owners.
+  for (unsigned j = tid; j < kWindowChannels; j += blockDim.x) {
+    if (owner || j >= 2 * D) {
+      const std::size_t c = channel(j);
+      uint32_t bits[4];
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) bits[tap] = __half_as_ushort(xs[T - 1 + tap][j]);
+      *reinterpret_cast<uint2*>(w.conv_final + c * 4) = {bits[0] | (bits[1] << 16),
+                                                         bits[2] | (bits[3] << 16)};
+    }
+  }
 
   // Stage 2: conv + SiLU per (token, channel) -> fp16 -> float (gdn_conv_kernel order).
   for (unsigned i = tid; i < T * kWindowChannels; i += blockDim.x) {
@@ -847,15 +912,46 @@ __global__ __launch_bounds__(256) void argmax_kernel(
 
 bool valid_epsilon(float epsilon) { return std::isfinite(epsilon) && epsilon > 0.0F; }
 
+template <bool Residual, bool Quantize>
+void launch_norm(bool fast, unsigned per_wave_slots, uint32_t planes, dim3 block, std::size_t smem,
+                 uint32_t batch, hipStream_t stream, const __half* in, const float* update,
+                 __half* ro, const uint16_t* weight, __half* out, uint8_t* codes, __half* sc,
+                 uint32_t e, float epsilon, bool unit, uint64_t plane_stride) {
+  if (fast && per_wave_slots <= kNormPlaneSlots && (planes == 1 || Residual)) {
+    if (planes == 1) {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, 1>), dim3(batch),
+                         block, 0, stream, in, update, ro, weight, out, codes, sc, e, epsilon, unit,
+                         planes, plane_stride);
+    } else {
+      hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots,
+                                               Residual ? kNormMaxPlanes : 1>),
+                         dim3(batch), block, 0, stream, in, update, ro, weight, out, codes, sc, e,
+                         epsilon, unit, planes, plane_stride);
+    }
+  } else if (fast && planes == 1) {
+    hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormSlots, 1>), dim3(batch), block,
+                       0, stream, in, update, ro, weight, out, codes, sc, e, epsilon, unit, planes,
+                       plane_stride);
+  } else {
+    hipLaunchKernelGGL((rms_norm_kernel<Residual, Quantize>), dim3(batch), dim3(256), smem, stream,
+                       in, update, ro, weight, out, codes, sc, e, epsilon, unit, planes,
+                       plane_stride);
+  }
+}
+
+// planes > 1 (residual only): the update is the sum of `planes` fp32 planes of
+// [batch][elements], one after the other.
 int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_t* input,
                    const float* update, uint16_t* residual_out, const uint16_t* weight,
                    uint16_t* output, uint8_t* codes, uint16_t* scales, std::size_t elements,
-                   uint32_t batch, float epsilon, bool unit, hipStream_t stream) {
+                   uint32_t batch, float epsilon, bool unit, hipStream_t stream,
+                   uint32_t planes = 1) {
   if (input == nullptr || weight == nullptr || elements == 0 || batch == 0 ||
       !valid_epsilon(epsilon) || elements > (1u << 20) ||
       (residual && (update == nullptr || residual_out == nullptr)) ||
       (!quantize && output == nullptr) ||
-      (quantize && (codes == nullptr || scales == nullptr || elements % 128 != 0))) {
+      (quantize && (codes == nullptr || scales == nullptr || elements % 128 != 0)) ||
+      planes == 0 || planes > kNormMaxPlanes || (planes > 1 && !residual)) {
     return fail(GFXI_INVALID_ARGUMENT, std::string("invalid ") + name + " arguments");
   }
   const auto e = static_cast<uint32_t>(elements);
@@ -867,38 +963,26 @@ int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_
   auto aligned = [](const void* p, std::uintptr_t a) {
     return p == nullptr || reinterpret_cast<std::uintptr_t>(p) % a == 0;
   };
-  if (e % 2 == 0 && e <= kNormFastMax && aligned(input, 4) && aligned(residual_out, 4) &&
-      aligned(output, 4) && aligned(update, 8)) {
-    const unsigned slots = (e + 127u) / 128u;
-    const unsigned waves = std::min(16u, slots);  // slots <= 16 * kNormSlots by kNormFastMax
-    const dim3 block(64u * waves);
-    if (residual && quantize) {
-      hipLaunchKernelGGL((rms_norm_rows_kernel<true, true>), dim3(batch), block, 0, stream, in, update,
-                         ro, weight, out, codes, sc, e, epsilon, unit);
-    } else if (residual) {
-      hipLaunchKernelGGL((rms_norm_rows_kernel<true, false>), dim3(batch), block, 0, stream, in,
-                         update, ro, weight, out, codes, sc, e, epsilon, unit);
-    } else if (quantize) {
-      hipLaunchKernelGGL((rms_norm_rows_kernel<false, true>), dim3(batch), block, 0, stream, in,
-                         update, ro, weight, out, codes, sc, e, epsilon, unit);
-    } else {
-      hipLaunchKernelGGL((rms_norm_rows_kernel<false, false>), dim3(batch), block, 0, stream, in,
-                         update, ro, weight, out, codes, sc, e, epsilon, unit);
-    }
-    return launch_status((std::string(name) + " launch failed").c_str());
-  }
+  const bool fast = e % 2 == 0 && e <= kNormFastMax && aligned(input, 4) &&
+                    aligned(residual_out, 4) && aligned(output, 4) && aligned(update, 8) &&
+                    aligned(weight, 4);
+  const unsigned slots = (e + 127u) / 128u;
+  const unsigned waves = std::min(16u, slots);  // slots <= 16 * kNormSlots on the fast path
+  const unsigned per_wave = (slots + waves - 1) / waves;
+  const dim3 block(64u * waves);
+  const uint64_t stride = static_cast<uint64_t>(batch) * e;
   if (residual && quantize) {
-    hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(batch), dim3(256), smem, stream, in, update, ro,
-                       weight, out, codes, sc, e, epsilon, unit);
+    launch_norm<true, true>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+                            weight, out, codes, sc, e, epsilon, unit, stride);
   } else if (residual) {
-    hipLaunchKernelGGL((rms_norm_kernel<true, false>), dim3(batch), dim3(256), smem, stream, in, update, ro,
-                       weight, out, codes, sc, e, epsilon, unit);
+    launch_norm<true, false>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+                             weight, out, codes, sc, e, epsilon, unit, stride);
   } else if (quantize) {
-    hipLaunchKernelGGL((rms_norm_kernel<false, true>), dim3(batch), dim3(256), smem, stream, in, update, ro,
-                       weight, out, codes, sc, e, epsilon, unit);
+    launch_norm<false, true>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+                             weight, out, codes, sc, e, epsilon, unit, stride);
   } else {
-    hipLaunchKernelGGL((rms_norm_kernel<false, false>), dim3(batch), dim3(256), smem, stream, in, update,
-                       ro, weight, out, codes, sc, e, epsilon, unit);
+    launch_norm<false, false>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+                              weight, out, codes, sc, e, epsilon, unit, stride);
   }
   return launch_status((std::string(name) + " launch failed").c_str());
 }
@@ -955,6 +1039,17 @@ extern "C" int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4(
   return norm_entry("fused residual/RMSNorm/A4", true, true, residual, update, residual_output,
                     bf16_weight, normalized_output, packed_output, scales, elements, batch,
                     epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+    const uint16_t* residual, const float* update_planes, uint32_t planes,
+    uint16_t* residual_output, const uint16_t* bf16_weight, uint16_t* normalized_output,
+    uint8_t* packed_output, uint16_t* scales, size_t elements, uint32_t batch, float epsilon,
+    int32_t add_unit_offset, void* stream) {
+  return norm_entry("fused residual(planes)/RMSNorm/A4", true, true, residual, update_planes,
+                    residual_output, bf16_weight, normalized_output, packed_output, scales,
+                    elements, batch, epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream),
+                    planes);
 }
 
 extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
@@ -1144,6 +1239,17 @@ extern "C" int32_t gfxinfer_launch_gdn_conv_window(
   if (const int32_t s = gdn_check("fused GDN conv/window", batch, key_heads, value_heads, head_size);
       s != GFXI_OK) {
     return s;
+  }
+  // 4-channel vector accesses: 16-byte inputs and states, 8-byte conv states and log.
+  const auto misaligned = [](const void* p, std::uintptr_t a) {
+    return p != nullptr && reinterpret_cast<std::uintptr_t>(p) % a != 0;
+  };
+  if (misaligned(projected_qkv, 16) || misaligned(initial_recurrent_state, 16) ||
+      misaligned(final_recurrent_state, 16) || misaligned(final_conv_state, 8) ||
+      misaligned(appended_log, 8)) {
+    return fail(GFXI_INVALID_ARGUMENT,
+                "fused GDN conv/window needs 16-byte aligned fp32 inputs and states and 8-byte "
+                "aligned conv state and log");
   }
   GdnWindowArgs w{projected_qkv, bf16_conv_weight, reinterpret_cast<const __half*>(initial_conv_state),
                   reinterpret_cast<__half*>(final_conv_state), reinterpret_cast<__half*>(appended_log),

@@ -28,6 +28,7 @@ namespace gfx950 {
 namespace {
 
 constexpr unsigned kMaxBlock = 32;  // qwen_runtime.cpp:40 kMaximumBlock
+constexpr std::size_t kMaxPlanes = 8;  // split-K planes of a projection (GEMM entry limit)
 
 struct Matrix {
   int32_t format{0};
@@ -161,6 +162,8 @@ struct gfxinfer_session {
   float *projected_main{}, *projected_z{}, *projected_a{}, *projected_b{}, *projected_k{};
   float *projected_v{}, *gdn_mixed{}, *mixer_update{}, *gate_output{}, *up_output{};
   float *mlp_update{}, *logits{}, *attention_workspace{};
+  // Split-K plane counts of the last projections into mixer_update / mlp_update.
+  uint32_t mixer_planes = 1, mlp_planes = 1;
   void* argmax_keys{};
   std::size_t argmax_keys_bytes{0};
   std::size_t attention_workspace_bytes{0};
@@ -198,6 +201,14 @@ struct gfxinfer_session {
   int32_t gemm(const Matrix& m, float* out, unsigned batch) {
     return gfxinfer_launch_gfx950_i4_gemm(m.format, m.weights, m.scales, act_codes, act_scales,
                                           out, m.rows, m.columns, batch, 0, stream);
+  }
+  // [hidden, K] projections that feed a residual RMSNorm: split-K planes when the
+  // plain grid would leave the GPU underfilled; the norm sums them.
+  int32_t gemm_planes(const Matrix& m, float* out, unsigned batch, uint32_t& planes) {
+    planes = gfxinfer_gemm_split_count(m.rows, m.columns, batch);
+    return gfxinfer_launch_gfx950_i4_gemm_split(m.format, m.weights, m.scales, act_codes,
+                                                act_scales, out, m.rows, m.columns, batch, planes,
+                                                stream);
   }
   int32_t gemm_fused(std::initializer_list<std::pair<const Matrix*, float*>> list,
                      unsigned batch) {
@@ -274,23 +285,23 @@ struct gfxinfer_session {
     }
     GFXI_TRY(gfxinfer_launch_quantize_activation_i4(attention_output, act_codes, act_scales,
                                                     attn_width, batch, stream));
-    return gemm(L.o, mixer_update, batch);
+    return gemm_planes(L.o, mixer_update, batch, mixer_planes);
   }
 
   // MLP half of a layer (qwen_runtime.cpp:512-543): residual + post norm -> A4,
   // gate/up, SwiGLU -> A4, down, residual + next norm -> A4 (+ optional fp16 norm).
   int32_t mlp_tail(const Layer& L, const uint16_t* input, uint16_t* output,
                    const uint16_t* next_norm, unsigned batch) {
-    GFXI_TRY(gfxinfer_launch_residual_add_rms_norm_quantize_i4(
-        input, mixer_update, post_attention, L.post_norm, nullptr, act_codes, act_scales, H,
-        batch, spec.rms_norm_epsilon, 1, stream));
+    GFXI_TRY(gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+        input, mixer_update, mixer_planes, post_attention, L.post_norm, nullptr, act_codes,
+        act_scales, H, batch, spec.rms_norm_epsilon, 1, stream));
     GFXI_TRY(gemm_fused({{&L.gate, gate_output}, {&L.up, up_output}}, batch));
     GFXI_TRY(gfxinfer_launch_silu_multiply_quantize_i4(gate_output, up_output, act_codes,
                                                        act_scales, I, batch, stream));
-    GFXI_TRY(gemm(L.down, mlp_update, batch));
-    return gfxinfer_launch_residual_add_rms_norm_quantize_i4(
-        post_attention, mlp_update, output, next_norm, nullptr, act_codes, act_scales, H, batch,
-        spec.rms_norm_epsilon, 1, stream);
+    GFXI_TRY(gemm_planes(L.down, mlp_update, batch, mlp_planes));
+    return gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+        post_attention, mlp_update, mlp_planes, output, next_norm, nullptr, act_codes, act_scales,
+        H, batch, spec.rms_norm_epsilon, 1, stream);
   }
 
   // qwen_runtime.cpp:421-544 launch_layer_block.
@@ -327,7 +338,7 @@ struct gfxinfer_session {
                                                       act_codes, act_scales, batch,
                                                       spec.gdn_value_head_count,
                                                       spec.gdn_head_size, stream));
-      GFXI_TRY(gemm(L.out, mixer_update, batch));
+      GFXI_TRY(gemm_planes(L.out, mixer_update, batch, mixer_planes));
     }
     return mlp_tail(L, input, output, next_norm, batch);
   }
@@ -723,10 +734,10 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
       {"projected_k", reinterpret_cast<void**>(&s->projected_k), B * s->kv_rows * 4},
       {"projected_v", reinterpret_cast<void**>(&s->projected_v), B * s->kv_rows * 4},
       {"gdn_mixed", reinterpret_cast<void**>(&s->gdn_mixed), B * s->gdn_value * 4},
-      {"mixer_update", reinterpret_cast<void**>(&s->mixer_update), B * s->H * 4},
+      {"mixer_update", reinterpret_cast<void**>(&s->mixer_update), kMaxPlanes * B * s->H * 4},
       {"gate_output", reinterpret_cast<void**>(&s->gate_output), B * s->I * 4},
       {"up_output", reinterpret_cast<void**>(&s->up_output), B * s->I * 4},
-      {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), B * s->H * 4},
+      {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), kMaxPlanes * B * s->H * 4},
       {"logits", reinterpret_cast<void**>(&s->logits), B * s->V * 4},
       {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
       {"attention_workspace", reinterpret_cast<void**>(&s->attention_workspace),

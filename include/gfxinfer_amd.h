@@ -104,6 +104,24 @@ int32_t gfxinfer_launch_gfx950_i4_gemm(int32_t format, const uint8_t* tiled_weig
                                        size_t rows, size_t columns, uint32_t batch,
                                        int32_t sequential_w3, void* stream);
 
+/* No reference counterpart (split-K form of gfxinfer_launch_gfx950_i4_gemm for
+ * matrices with few 16-row tiles, e.g. the [hidden, K] down/output projections):
+ * writes `splits` fp32 planes [splits][batch][rows]; plane s holds the part of the
+ * product over the s-th of `splits` equal ranges of K's groups, and the product is
+ * the sum of the planes in plane order (the residual RMSNorm entry
+ * gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes consumes them).
+ * splits in [1, 8] and at most K/128. */
+int32_t gfxinfer_launch_gfx950_i4_gemm_split(int32_t format, const uint8_t* tiled_weights,
+                                             const uint16_t* tiled_weight_scales,
+                                             const uint8_t* packed_activations,
+                                             const uint16_t* activation_scales,
+                                             float* output_planes, size_t rows, size_t columns,
+                                             uint32_t batch, uint32_t splits, void* stream);
+
+/* The split count gfxinfer_launch_gfx950_i4_gemm_split is fastest with for a shape
+ * (1 when the plain grid already fills the GPU). */
+uint32_t gfxinfer_gemm_split_count(size_t rows, size_t columns, uint32_t batch);
+
 /* lowbit_gemv.h:113-126 (launch_gfx12_i4_gemm_half): fp16 output [batch, rows]. */
 int32_t gfxinfer_launch_gfx950_i4_gemm_half(int32_t format, const uint8_t* tiled_weights,
                                             const uint16_t* tiled_weight_scales,
@@ -224,6 +242,15 @@ int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4(
     const uint16_t* bf16_weight, uint16_t* normalized_output, uint8_t* packed_output,
     uint16_t* scales, size_t elements, uint32_t batch, float epsilon, int32_t add_unit_offset,
     void* stream);
+
+/* No reference counterpart: gfxinfer_launch_residual_add_rms_norm_quantize_i4 with the
+ * update given as `planes` (1..8) fp32 planes [planes][batch][elements], summed in
+ * plane order (the output of gfxinfer_launch_gfx950_i4_gemm_split). */
+int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+    const uint16_t* residual, const float* update_planes, uint32_t planes,
+    uint16_t* residual_output, const uint16_t* bf16_weight, uint16_t* normalized_output,
+    uint8_t* packed_output, uint16_t* scales, size_t elements, uint32_t batch, float epsilon,
+    int32_t add_unit_offset, void* stream);
 
 /* qwen_ops.h:33-42 launch_dual_rms_norm_concat: [norm(left) | norm(right)]. */
 int32_t gfxinfer_launch_dual_rms_norm_concat(const uint16_t* left, const uint16_t* left_bf16_weight,

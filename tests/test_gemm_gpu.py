@@ -176,6 +176,43 @@ def test_gemm_partials_bit_exact_and_output(device, gx, orc, fmt, abits, rows, c
     assert np.abs(got - want_y).max() <= 2e-5 * scale
 
 
+@pytest.mark.parametrize("fmt,rows,cols,batch,splits", [
+    (2, 5120, 17408, 5, 4), (2, 5120, 17408, 32, 4), (3, 5120, 17408, 5, 8), (3, 5120, 6144, 5, 4),
+    (3, 5120, 6144, 16, 3), (2, 5120, 5120, 9, 5), (2, 64, 640, 1, 5), (3, 64, 640, 32, 2),
+    (2, 48, 1024, 7, 8),
+])
+def test_gemm_split_planes_sum_to_product(device, gx, orc, fmt, rows, cols, batch, splits):
+    """Split-K planes: plane s = the epilogue over the s-th of `splits` equal pack ranges
+    of K; their sum in plane order is the product (same 2e-5 bar as the plain GEMM)."""
+    p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=rows * 3 + cols + batch + splits)
+    want = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+    planes = empty((splits, batch, rows), np.float32)
+    say("gemm split", fmt, rows, cols, batch, splits)
+    gx.launch_i4_gemm_split(fmt, dev(p["tiled"]), dev(p["tscales"]), dev(p["acts"]), dev(p["as16"]),
+                            planes, rows, cols, batch, splits)
+    got = host(planes)
+    total = got[0].copy()
+    for s in range(1, splits):
+        total += got[s]
+    scale = float(np.abs(want).max())
+    assert np.abs(total - want).max() <= 2e-5 * scale
+    # each plane is exactly its own K range: planes of disjoint ranges are not all alike
+    groups = cols // 128
+    if splits <= groups:
+        assert not np.array_equal(got[0], got[-1])
+
+
+def test_gemm_split_rejects_bad_counts(device, gx):
+    z = empty((8,), np.uint8)
+    L = gx.lib()
+    for splits in (0, 9, 6):  # 6 > K/128 = 5
+        rc = L.gfxinfer_launch_gfx950_i4_gemm_split(2, z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr(),
+                                                     z.data_ptr(), 16, 640, 1, splits, None)
+        assert rc == gx.INVALID_ARGUMENT
+    assert 1 <= gx.gemm_split_count(5120, 17408, 5) <= 8
+    assert gx.gemm_split_count(34816, 5120, 5) == 1
+
+
 def test_gemm_half_output(device, gx, orc):
     fmt, rows, cols, batch = 2, 5120, 10240, 1  # mtp.fc shape
     p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=21)

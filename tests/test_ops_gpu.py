@@ -110,6 +110,52 @@ def test_residual_add_rms_norm_and_fused_quantize(device, gx, orc, batch):
     assert np.array_equal(host(codes), c) and np.array_equal(host(scales, np.uint16), s)
 
 
+@pytest.mark.parametrize("n,batch,planes", [(5120, 5, 4), (5120, 32, 8), (5120, 1, 2), (6144, 3, 3),
+                                            (10240, 2, 4), (640, 7, 5), (5120, 4, 1)])
+def test_residual_norm_sums_update_planes(device, gx, orc, n, batch, planes):
+    """Planes entry == the plain fused entry on the fp32 sum of the planes taken in
+    plane order (bit-exact: same additions, same kernel arithmetic); the residual is
+    the oracle's one-rounding add of that sum."""
+    rng = np.random.default_rng(n + batch * 7 + planes)
+    res = _half(rng.standard_normal((batch, n)))
+    upd = (rng.standard_normal((planes, batch, n)) * 0.5).astype(np.float32)
+    total = upd[0].copy()
+    for p in range(1, planes):
+        total += upd[p]
+    w = _bf16(np.round(rng.standard_normal(n) * 64) / 1024)
+    want_r = np.empty_like(res)
+    want_n = np.empty_like(res)
+    orc.lib().orc_residual_add_rms_norm(orc.ptr(res), orc.ptr(total), orc.ptr(want_r), orc.ptr(w), orc.ptr(want_n),
+                                        n, batch, EPS, 1)
+    L = gx.lib()
+    dr, dw = dev(res), dev(w)
+    outs = []
+    for update, count, fn in ((dev(upd), planes, "planes"), (dev(total), 1, "plain")):
+        ro, no = empty((batch, n), np.uint16), empty((batch, n), np.uint16)
+        codes, scales = empty((batch, n // 2), np.uint8), empty((batch, n // 128), np.uint16)
+        say("residual norm", fn, n, batch, planes)
+        if fn == "planes":
+            gx.check(L.gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+                dr.data_ptr(), update.data_ptr(), count, ro.data_ptr(), dw.data_ptr(), no.data_ptr(),
+                codes.data_ptr(), scales.data_ptr(), n, batch, EPS, 1, None))
+        else:
+            gx.check(L.gfxinfer_launch_residual_add_rms_norm_quantize_i4(
+                dr.data_ptr(), update.data_ptr(), ro.data_ptr(), dw.data_ptr(), no.data_ptr(),
+                codes.data_ptr(), scales.data_ptr(), n, batch, EPS, 1, None))
+        outs.append([host(ro, np.uint16), host(no, np.uint16), host(codes), host(scales, np.uint16)])
+    assert np.array_equal(outs[0][0], want_r)
+    assert _close16(outs[0][1], want_n)
+    if n <= 16 * 3 * 128:  # both calls take the register-resident kernel
+        for a, b in zip(outs[0], outs[1]):
+            assert np.array_equal(a, b)
+    else:  # planes beyond 6144 elements take the generic kernel (other reduction order)
+        assert np.array_equal(outs[0][0], outs[1][0]) and _close16(outs[0][1], outs[1][1])
+    bad = L.gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+        dr.data_ptr(), dr.data_ptr(), 9, dr.data_ptr(), dw.data_ptr(), dr.data_ptr(), dr.data_ptr(),
+        dr.data_ptr(), n, batch, EPS, 1, None)
+    assert bad == gx.INVALID_ARGUMENT
+
+
 def test_dual_rms_norm_concat(device, gx, orc):
     n = 5120
     rng = np.random.default_rng(3)
