@@ -122,6 +122,8 @@ __global__ __launch_bounds__(256) void quantize_group128_kernel(
 constexpr int kBufferWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit data format
 constexpr int kStreaming = 2;             // nt: weights are read exactly once
 
+typedef __attribute__((address_space(3))) void lds_void;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
                                            kBufferWord3);
@@ -234,10 +236,14 @@ __device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
 }
 
 // Dynamic LDS: one private region per wave holding the activations of the
-// wave's current chunk of groups for every live token ([batch][pitch]), already
-// expanded to MFMA operand bytes ([group][lane block kb][K-step h][16 bytes]),
-// a 16-byte zero line read by lanes outside a group's token window, and the
-// chunk's activation scales as fp32 already multiplied by 1/F.  After the MFMA
+// wave's current chunk of groups for every live token ([batch][pitch]), a 16-byte
+// zero line read by lanes outside a group's token window, and the chunk's
+// activation scales as fp32 already multiplied by 1/F.  A4 activations arrive as
+// packed nibbles straight from memory (buffer_load_dwordx4 ... lds, one 16-byte
+// piece per lane at LDS base + 16 * lane; a zero piece pads each token row, which
+// rotates the LDS banks of consecutive tokens) and are expanded to MFMA operand
+// bytes when read; A8 activations are staged through registers already permuted
+// to operand order ([group][lane block kb][K-step h][16 bytes]).  After the MFMA
 // loop the region holds the wave's partial sums for the cross-wave reduction.
 struct GemmLds {
   uint32_t pitch;          // bytes per token row (chunk bytes + 16: rotates LDS banks)
@@ -250,9 +256,14 @@ struct GemmLds {
 __host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32_t batch, int abits,
                                                     uint32_t ntb) {
   GemmLds l{};
-  (void)abits;
-  l.pitch = chunk_groups * 128u + 16u;  // operand-ready int8: 128 bytes per token per group
+  // A4: 64 packed bytes per token per group + a zero piece; A8: 128 operand bytes + 16
+  l.pitch = abits == 4 ? chunk_groups * 64u + 16u : chunk_groups * 128u + 16u;
   l.zero_offset = batch * l.pitch;
+  if (abits == 4) {
+    // whole DMA instructions: 64 pieces of 16 bytes each
+    const uint32_t pieces = batch * (l.pitch / 16u);
+    l.zero_offset = (pieces + 63u) / 64u * 1024u;
+  }
   l.scale_offset = l.zero_offset + 16u;
   l.wscale_offset = (l.scale_offset + batch * chunk_groups * 4u + 15u) & ~15u;
   uint32_t region = l.wscale_offset + chunk_groups * 32u;
@@ -275,6 +286,7 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   constexpr float kInvF =
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
+  constexpr bool kDma = ABits == 4;  // A4 pieces go straight from memory to LDS
 
   extern __shared__ __align__(16) uint8_t lds_all[];
 
@@ -323,8 +335,9 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
       const unsigned token = t * 16u + slot;
-      b_offset[j][t] = (window == j && token < batch) ? token * layout.pitch + j * 128u + kb * 32u
-                                                       : 0xffffffffu;
+      b_offset[j][t] = (window == j && token < batch)
+                           ? token * layout.pitch + j * (kDma ? 64u : 128u) + kb * (kDma ? 16u : 32u)
+                           : 0xffffffffu;
     }
   }
   if (lane < 4) reinterpret_cast<uint32_t*>(lds + layout.zero_offset)[lane] = 0u;
@@ -339,7 +352,9 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   constexpr unsigned kPieces = AGB / 16;  // 16-byte source pieces per token per group
   constexpr unsigned kRowPieces = CHG * kPieces;
   constexpr unsigned kMaxTokens = TPAD * NTB;  // batch capacity of this variant
-  constexpr unsigned kMaxPieces = (kMaxTokens * kRowPieces + 63u) / 64u;
+  constexpr unsigned kDmaRow = kRowPieces + 1; // pieces per token row incl. the zero pad
+  constexpr unsigned kMaxPieces = kDma ? 1u : (kMaxTokens * kRowPieces + 63u) / 64u;
+  constexpr unsigned kMaxDma = (kMaxTokens * kDmaRow + 63u) / 64u;
   const auto act_scales = buffer(args.activation_scales, batch * groups * 2u);
   for (unsigned base = pack_begin; base < pack_end; base += CH) {
     const unsigned g0 = base * GP;
@@ -349,8 +364,26 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     u32x4 stage[kMaxPieces];
     constexpr unsigned kScaleIters = (kMaxTokens * CHG + 63u) / 64u;
     unsigned short stage_scale[kScaleIters];
+    if constexpr (kDma) {
+      // Piece i = (token i / kDmaRow, piece i % kDmaRow) lands at LDS byte 16 * i =
+      // token * pitch + 16 * piece; the pad piece and absent tokens read zeros.
+      const unsigned dma_pieces = batch * kDmaRow;
+#pragma unroll
+      for (unsigned p = 0; p < kMaxDma; ++p) {
+        if (p * 64u >= dma_pieces) break;  // wave-uniform
+        const unsigned i = p * 64u + lane;
+        const unsigned token = i / kDmaRow;
+        const unsigned rem = i - token * kDmaRow;
+        const unsigned off = (i < dma_pieces && rem < kRowPieces) ? token * row_bytes + rem * 16u : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(activations, (lds_void*)(lds + p * 1024u),
+                                                 16, off, g0 * AGB, 0, 0);
+      }
+      // Nothing moves above the DMA: the explicit wait below counts the loads after it.
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (unsigned p = 0; p < kMaxPieces; ++p) {
+      if constexpr (kDma) break;
       // Pieces of absent tokens read past the descriptor (zeros, no memory request).
       const unsigned i = p * 64u + lane;
       const unsigned token = i / kRowPieces;
@@ -403,10 +436,19 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kDma) {
+      // The compiler does not order LDS reads after buffer->LDS loads: wait here
+      // until only the loads issued after the DMA (weight-scale chunk, activation
+      // scales, weights) may still be in flight; loads complete in issue order.
+      constexpr unsigned kAfter = (Partials ? 0u : 1u + kScaleIters) + CH * GP;
+      static_assert(kAfter <= 63, "vmcnt holds at most 63");
+      __builtin_amdgcn_s_waitcnt(static_cast<int>((kAfter & 15u) | ((kAfter >> 4) << 14) | (7u << 4) | (15u << 8)));
+    }
     // 3) Expand the activations into operand bytes and stage them (and the
     //    scales) into this wave's LDS region.
 #pragma unroll
     for (unsigned p = 0; p < kMaxPieces; ++p) {
+      if constexpr (kDma) break;
       const unsigned i = p * 64u + lane;
       if (i < total_pieces) {
         const unsigned token = i / kRowPieces;
@@ -456,9 +498,17 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
 #pragma unroll
         for (int t = 0; t < NTB; ++t) {
           const bool on = b_offset[j][t] != 0xffffffffu;
-          const uint32_t off = on ? b_offset[j][t] + ci * GP * 128u : layout.zero_offset;
-          const i32x4 b0 = *reinterpret_cast<const i32x4*>(lds + off);
-          const i32x4 b1 = *reinterpret_cast<const i32x4*>(lds + (on ? off + 16u : off));
+          i32x4 b0, b1;
+          if constexpr (kDma) {
+            const uint32_t off = on ? b_offset[j][t] + ci * GP * 64u : layout.zero_offset;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(lds + off);
+            b0 = expand_nibbles(x[0], x[1]);
+            b1 = expand_nibbles(x[2], x[3]);
+          } else {
+            const uint32_t off = on ? b_offset[j][t] + ci * GP * 128u : layout.zero_offset;
+            b0 = *reinterpret_cast<const i32x4*>(lds + off);
+            b1 = *reinterpret_cast<const i32x4*>(lds + (on ? off + 16u : off));
+          }
           c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c[t], 0, 0, 0);
           c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c[t], 0, 0, 0);
         }
@@ -1029,13 +1079,14 @@ unsigned choose_waves(uint32_t groups, unsigned gp) {
   return waves;
 }
 
-// GFXI_GEMM_KERNEL=lds selects the LDS-staged kernel (tuning knob); the default
-// is the direct-operand kernel.
+// GFXI_GEMM_KERNEL=lds|direct forces one kernel family (tuning knob).  The default
+// is the LDS-staged kernel up to 8 tokens and the direct-operand kernel above.
 int kernel_override() {  // 0 default, 1 lds everywhere, 2 direct everywhere
   static const int value = [] {
     const char* text = std::getenv("GFXI_GEMM_KERNEL");
     if (text == nullptr) return 0;
-    return std::string(text) == "lds" ? 1 : std::string(text) == "direct" ? 2 : 0;
+    const std::string v(text);
+    return v == "lds" ? 1 : v == "direct" ? 2 : 0;
   }();
   return value;
 }
