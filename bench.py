@@ -297,6 +297,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--verify-rounds", type=int, default=60)
+    ap.add_argument("--verify-depths", default="4,31",
+                    help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the rocprofv3 --pmc workload (calibration copy + plain GEMM launches)")
     args = ap.parse_args()
@@ -349,7 +351,8 @@ def main():
         "reference_packed_gbps": round(codes_only / (r["ms_step"] * 1e-3) / 1e9, 2),
     }
     if not args.no_verify:
-        out["verify"] = verify_bench(rounds=args.verify_rounds)
+        depths = tuple(int(d) for d in args.verify_depths.split(",") if d)
+        out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

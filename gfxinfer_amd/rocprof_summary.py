@@ -4,8 +4,13 @@
     python -m gfxinfer_amd.rocprof_summary pmc <fetch_dir> <write_dir> --kernel NAME \\
         --copy NAME --copy-bytes N
 
+    python -m gfxinfer_amd.rocprof_summary rounds <dir> --marker NAME --rounds N
+
 `stats` prints the kernel table of a --kernel-trace --stats run (calls, total,
-average, min, max per kernel).  `pmc` reads two --pmc runs (FETCH_SIZE, then
+average, min, max per kernel).  `rounds` reads the kernel trace of such a run and
+prints, for the last N rounds (a round starts at each dispatch of the marker
+kernel), the span per round, the GPU-busy time per round and each kernel's time
+and dispatch count per round.  `pmc` reads two --pmc runs (FETCH_SIZE, then
 WRITE_SIZE; both in KiB per dispatch), calibrates each counter on the copy kernel
 of known size (it reads and writes exactly N bytes) and prints the HBM bytes per
 dispatch of the named kernel.
@@ -44,6 +49,27 @@ def stats(directory: str, match: list[str]) -> str:
         lines.append(f"{int(r['Calls']):7d} {float(r['TotalDurationNs']) / 1e3:11.1f} "
                      f"{float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
                      f"{float(r['MaxNs']) / 1e3:9.3f}  {short(r['Name'])}")
+    return "\n".join(lines)
+
+
+def rounds(directory: str, marker: str, count: int) -> str:
+    rows = sorted(_csv(directory, "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if marker in r["Kernel_Name"]]
+    if len(starts) < count:
+        raise SystemExit(f"only {len(starts)} dispatches of {marker!r}")
+    window = rows[starts[-count]:]
+    total: dict[str, float] = {}
+    calls: dict[str, int] = {}
+    for r in window:
+        name = short(r["Kernel_Name"])
+        total[name] = total.get(name, 0.0) + (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        calls[name] = calls.get(name, 0) + 1
+    span = (int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])) / 1e3
+    lines = [f"rounds {count}: span {span / count:.1f} us/round, GPU busy {sum(total.values()) / count:.1f} "
+             f"us/round, {len(window) / count:.1f} dispatches/round",
+             f"{'us/round':>9} {'calls/round':>11} {'avg_us':>8}  kernel"]
+    for name, t in sorted(total.items(), key=lambda kv: -kv[1]):
+        lines.append(f"{t / count:9.1f} {calls[name] / count:11.1f} {t / calls[name]:8.2f}  {name}")
     return "\n".join(lines)
 
 
@@ -87,9 +113,15 @@ def main() -> None:
     b.add_argument("--kernel", required=True)
     b.add_argument("--copy", required=True)
     b.add_argument("--copy-bytes", type=int, required=True)
+    c = sub.add_parser("rounds")
+    c.add_argument("directory")
+    c.add_argument("--marker", required=True)
+    c.add_argument("--rounds", type=int, required=True)
     args = ap.parse_args()
     if args.cmd == "stats":
         print(stats(args.directory, args.match))
+    elif args.cmd == "rounds":
+        print(rounds(args.directory, args.marker, args.rounds))
     else:
         print(pmc(args.fetch_dir, args.write_dir, args.kernel, args.copy, args.copy_bytes))
 
