@@ -104,6 +104,17 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_model_weight_bytes": (SZ, [P]),
     "gfxinfer_model_find_tensor": (I32, [P, ctypes.c_char_p, P]),
     "gfxinfer_model_copy_tensor": (I32, [P, ctypes.c_char_p, I32, P, SZ]),
+    "gfxinfer_artifact_open": (I32, [ctypes.c_char_p, I32, P]),
+    "gfxinfer_artifact_close": (None, [P]),
+    "gfxinfer_artifact_get_identity": (I32, [P, P]),
+    "gfxinfer_artifact_tensor_count": (SZ, [P]),
+    "gfxinfer_artifact_tensor_at": (I32, [P, SZ, P]),
+    "gfxinfer_artifact_find": (I32, [P, ctypes.c_char_p, P]),
+    "gfxinfer_artifact_bytes": (P, [P, ctypes.c_uint64, ctypes.c_uint64]),
+    "gfxinfer_crc64_ecma": (ctypes.c_uint64, [ctypes.c_uint64, P, SZ]),
+    "gfxinfer_retile_gfx12_for_gfx950": (I32, [I32, P, SZ, P]),
+    "gfxinfer_model_create_from_artifact": (I32, [P, ctypes.c_char_p, I32, I32, P]),
+    "gfxinfer_model_write_artifact": (I32, [P, ctypes.c_char_p, ctypes.c_char_p, P, SZ]),
     "gfxinfer_session_create": (I32, [P, P, P]),
     "gfxinfer_session_destroy": (None, [P]),
     "gfxinfer_session_greedy_step": (I32, [P, U32, P]),

@@ -301,25 +301,26 @@ int32_t generate(gfxinfer_model& m, uint64_t seed) {
 
 }  // namespace
 
-extern "C" int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* spec, uint64_t seed,
-                                                   int32_t device, gfxinfer_model** out) {
-  if (spec == nullptr || out == nullptr) {
-    return fail(GFXI_INVALID_ARGUMENT, "model creation needs a spec and an output handle");
-  }
+namespace gfx950 {
+
+int32_t allocate_model(const gfxinfer_model_spec& spec, int32_t device, std::vector<Tensor> tensors,
+                       gfxinfer_model** out) {
   *out = nullptr;
-  if (int32_t s = validate_spec(*spec); s != GFXI_OK) return s;
+  if (int32_t s = validate_spec(spec); s != GFXI_OK) return s;
   if (int32_t s = gfxinfer_require_gfx950_device(device); s != GFXI_OK) return s;
   if (auto e = hipSetDevice(device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
   auto m = new gfxinfer_model();
-  m->spec = *spec;
+  m->spec = spec;
   m->device = device;
-  m->tensors = model_tensors(*spec);
+  m->tensors = std::move(tensors);
   std::size_t cursor = 0;
   for (std::size_t i = 0; i < m->tensors.size(); ++i) {
     auto& t = m->tensors[i];
     m->index.emplace(t.name, i);
     if (t.format == kBf16) {
       t.data_bytes = t.rows * t.columns * 2;
+    } else if (t.format == kI32) {
+      t.data_bytes = t.rows * t.columns * 4;
     } else {
       t.data_bytes = t.rows * t.columns * (t.format == GFXI_W3G128 ? 3 : 4) / 8;
       t.auxiliary_bytes = t.rows * (t.columns / kGroup) * 2;
@@ -341,10 +342,29 @@ extern "C" int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* sp
              e2 != hipSuccess) {
     m->arena = nullptr;
     status = hip_fail(e2, "weight arena allocation failed");
-  } else {
-    status = generate(*m, seed);
   }
   if (status != GFXI_OK) {
+    gfxinfer_model_destroy(m);
+    return status;
+  }
+  *out = m;
+  return ok();
+}
+
+}  // namespace gfx950
+
+extern "C" int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* spec, uint64_t seed,
+                                                   int32_t device, gfxinfer_model** out) {
+  if (spec == nullptr || out == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "model creation needs a spec and an output handle");
+  }
+  *out = nullptr;
+  gfxinfer_model* m = nullptr;
+  if (const int32_t status = allocate_model(*spec, device, model_tensors(*spec), &m);
+      status != GFXI_OK) {
+    return status;
+  }
+  if (const int32_t status = generate(*m, seed); status != GFXI_OK) {
     gfxinfer_model_destroy(m);
     return status;
   }

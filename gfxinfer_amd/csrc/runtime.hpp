@@ -14,7 +14,8 @@
 
 namespace gfx950 {
 
-constexpr int32_t kBf16 = 0;  // tensor format tag of bf16 vectors / small matrices
+constexpr int32_t kBf16 = 0;   // tensor format tag of bf16 vectors / small matrices
+constexpr int32_t kI32 = -1;   // tensor format tag of int32 vectors (draft-head token ids)
 
 // One named tensor of the weight arena (engine.h:47-60 DeviceTensorView).
 struct Tensor {
@@ -41,6 +42,10 @@ inline bool is_attention_layer(const gfxinfer_model_spec& spec, uint32_t layer) 
 std::vector<Tensor> model_tensors(const gfxinfer_model_spec& spec);
 // Checks the shape constraints the kernels rely on; returns GFXI_OK or the error.
 int32_t validate_spec(const gfxinfer_model_spec& spec);
+// Lays the tensors out in one 256-byte-aligned device arena (engine.cpp:166-205) and
+// creates the compute stream; the arena is left unfilled.
+int32_t allocate_model(const gfxinfer_model_spec& spec, int32_t device, std::vector<Tensor> tensors,
+                       gfxinfer_model** out);
 
 // FNV-1a of a tensor name: the per-tensor key of the synthetic generator.
 inline uint64_t name_hash(const std::string& name) {

@@ -141,6 +141,7 @@ struct gfxinfer_session {
   std::vector<Layer> layers;
   Layer mtp;
   Matrix embedding, lm_head, draft_head, mtp_fc;
+  const uint32_t* draft_token_ids{nullptr};  // draft-head row -> token id (null: identity)
   const uint16_t* final_norm{nullptr};
   const uint16_t* mtp_pre_embedding_norm{nullptr};
   const uint16_t* mtp_pre_hidden_norm{nullptr};
@@ -230,10 +231,11 @@ struct gfxinfer_session {
 
   // Head projection fused with greedy argmax (qwen_runtime.cpp:635-639, 859-866); the
   // fp32 logits are kept only when the session was configured to keep them.
-  int32_t gemm_argmax(const Matrix& m, unsigned batch, std::size_t argmax_rows, uint32_t* tokens) {
+  int32_t gemm_argmax(const Matrix& m, unsigned batch, std::size_t argmax_rows, uint32_t* tokens,
+                      const uint32_t* token_ids = nullptr) {
     return gfxinfer_launch_gfx950_i4_gemm_argmax(
         m.format, m.weights, m.scales, act_codes, act_scales,
-        config.keep_logits != 0 ? logits : nullptr, m.rows, m.columns, batch, argmax_rows, nullptr,
+        config.keep_logits != 0 ? logits : nullptr, m.rows, m.columns, batch, argmax_rows, token_ids,
         argmax_keys, argmax_keys_bytes, tokens, stream);
   }
 
@@ -390,7 +392,7 @@ struct gfxinfer_session {
                              output_token == nullptr));
     if (output_token == nullptr) return ok();
     GFXI_TRY(mlp_tail(mtp, mtp_input, mtp_hidden, mtp_final_norm, 1));
-    return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, output_token);
+    return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, output_token, draft_token_ids);
   }
 
   // The D proposals then the verifier with rollback logging (qwen_runtime.cpp:1448-1467,
@@ -697,10 +699,23 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
     delete s;
     return fail(GFXI_CORRUPT_ARTIFACT, "model lacks a tensor the decode session needs");
   }
-  // The MTP draft head is the LM head's first rows (qwen_runtime.cpp:994-1008); in the
-  // tile layout a row prefix is a byte prefix of codes and scales.
-  s->draft_head = s->lm_head;
-  s->draft_head.rows = sp.mtp_draft_vocabulary;
+  // The MTP draft head (qwen_runtime.cpp:994-1008): the converter's ranked rows
+  // "mtp.draft_head.weight" with their token ids when the model has them, else the LM
+  // head's first rows (in the tile layout a row prefix is a byte prefix of codes and
+  // scales) with the identity map.
+  if (const Tensor* ids = model->find("mtp.draft_head_token_ids"); ids != nullptr) {
+    bool absent = false;
+    s->draft_head = bind_matrix(*model, "mtp.draft_head.weight", absent);
+    if (absent || ids->format != kI32 || ids->columns != s->draft_head.rows ||
+        s->draft_head.rows != sp.mtp_draft_vocabulary) {
+      delete s;
+      return fail(GFXI_CORRUPT_ARTIFACT, "MTP draft head and token ids do not match the spec");
+    }
+    s->draft_token_ids = static_cast<const uint32_t*>(model->data(ids));
+  } else {
+    s->draft_head = s->lm_head;
+    s->draft_head.rows = sp.mtp_draft_vocabulary;
+  }
 
   // Arena (qwen_runtime.cpp:1117-1184).
   const std::size_t B = kMaxBlock, ctx = config->maximum_context_tokens;

@@ -84,8 +84,92 @@ class SpeculativeStepResult:
     accepted_drafts: int
 
 
+class ArtifactIdentity(ctypes.Structure):
+    """gfxinfer_artifact_identity (artifact.h:35-40 ArtifactIdentity)."""
+    _fields_ = [("target_arch", ctypes.c_char * 16), ("model_id", ctypes.c_char * 32),
+                ("weights_id", ctypes.c_char * 32), ("recipe_id", ctypes.c_char * 64)]
+
+
+class ArtifactTensor(ctypes.Structure):
+    """gfxinfer_artifact_tensor (artifact.h:42-55 TensorDescriptor)."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_uint16), ("quantization", ctypes.c_uint16),
+                ("rank", ctypes.c_uint16), ("flags", ctypes.c_uint16), ("alignment", ctypes.c_uint32),
+                ("dimensions", ctypes.c_uint64 * 4), ("data_offset", ctypes.c_uint64),
+                ("data_bytes", ctypes.c_uint64), ("aux_offset", ctypes.c_uint64),
+                ("aux_bytes", ctypes.c_uint64), ("data_crc64", ctypes.c_uint64)]
+
+    @property
+    def shape(self) -> tuple:
+        return tuple(int(self.dimensions[i]) for i in range(self.rank))
+
+
+class Artifact:
+    """A mapped, validated .gfxi file (ArtifactView, artifact.h:81-120)."""
+
+    def __init__(self, path: str, verify_checksums: bool = True):
+        handle = ctypes.c_void_p()
+        check(lib().gfxinfer_artifact_open(str(path).encode(), int(verify_checksums), ctypes.byref(handle)))
+        self._handle = handle
+
+    def close(self):
+        if self._handle is not None:
+            lib().gfxinfer_artifact_close(self._handle)
+            self._handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def identity(self) -> dict:
+        ident = ArtifactIdentity()
+        check(lib().gfxinfer_artifact_get_identity(self._handle, ctypes.byref(ident)))
+        return {k: getattr(ident, k).decode() for k in ("target_arch", "model_id", "weights_id", "recipe_id")}
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(int(lib().gfxinfer_artifact_tensor_count(self._handle))):
+            t = ArtifactTensor()
+            check(lib().gfxinfer_artifact_tensor_at(self._handle, i, ctypes.byref(t)))
+            out.append(t)
+        return out
+
+    def find(self, name: str) -> ArtifactTensor:
+        t = ArtifactTensor()
+        check(lib().gfxinfer_artifact_find(self._handle, name.encode(), ctypes.byref(t)))
+        return t
+
+    def payload(self, t: ArtifactTensor, auxiliary: bool = False) -> np.ndarray:
+        offset, n = (t.aux_offset, t.aux_bytes) if auxiliary else (t.data_offset, t.data_bytes)
+        ptr = lib().gfxinfer_artifact_bytes(self._handle, offset, n)
+        if ptr is None:
+            raise GfxinferError(1, "payload outside the artifact")
+        return np.frombuffer((ctypes.c_uint8 * n).from_address(ptr), np.uint8).copy()
+
+
+def crc64_ecma(data: bytes, state: int = 0) -> int:
+    """CRC-64/ECMA-182 (artifact.cpp:187-213)."""
+    buf = np.frombuffer(bytes(data), np.uint8)
+    return int(lib().gfxinfer_crc64_ecma(state, buf.ctypes.data if len(buf) else None, len(buf)))
+
+
+def retile_gfx12_for_gfx950(fmt: int, gfx12_codes: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(gfx12_codes, np.uint8)
+    out = np.empty_like(src)
+    check(lib().gfxinfer_retile_gfx12_for_gfx950(fmt, src.ctypes.data, src.nbytes, out.ctypes.data))
+    return out
+
+
 class SyntheticModel:
-    """Seeded synthetic checkpoint on one device (Engine::create equivalent)."""
+    """Seeded synthetic checkpoint on one device (Engine::create equivalent), or, with
+    from_artifact(), the weights of a .gfxi artifact."""
 
     def __init__(self, spec: ModelSpec, seed: int, device: int = 0):
         self.spec = spec
@@ -93,6 +177,23 @@ class SyntheticModel:
         handle = ctypes.c_void_p()
         check(lib().gfxinfer_model_create_synthetic(ctypes.byref(spec), seed, device, ctypes.byref(handle)))
         self._handle = handle
+
+    @classmethod
+    def from_artifact(cls, spec: ModelSpec, path: str, verify_checksums: bool = True, device: int = 0):
+        self = cls.__new__(cls)
+        self.spec = spec
+        self.seed = None
+        handle = ctypes.c_void_p()
+        check(lib().gfxinfer_model_create_from_artifact(ctypes.byref(spec), str(path).encode(),
+                                                        int(verify_checksums), device, ctypes.byref(handle)))
+        self._handle = handle
+        return self
+
+    def write_artifact(self, path: str, weights_id: str, draft_rows=None):
+        rows = None if draft_rows is None else np.ascontiguousarray(draft_rows, np.uint32)
+        check(lib().gfxinfer_model_write_artifact(self.handle, str(path).encode(), weights_id.encode(),
+                                                  None if rows is None else rows.ctypes.data,
+                                                  0 if rows is None else len(rows)))
 
     @property
     def handle(self):

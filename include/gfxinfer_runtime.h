@@ -68,7 +68,7 @@ size_t gfxinfer_model_weight_bytes(const gfxinfer_model* model);
 
 /* DeviceTensorView (engine.h:47-60).  format: GFXI_W3G128 / GFXI_W4G128 for tiled
  * matrices (data = tiled codes, auxiliary = tiled fp16 scales), 0 for bf16 vectors
- * (data = bf16 values, auxiliary = NULL). */
+ * (data = bf16 values, auxiliary = NULL), -1 for int32 vectors (draft-head token ids). */
 typedef struct gfxinfer_tensor_view {
   int32_t format;
   uint64_t rows;
@@ -86,6 +86,83 @@ int32_t gfxinfer_model_find_tensor(const gfxinfer_model* model, const char* name
  * of `bytes` bytes.  No reference counterpart: a test accessor. */
 int32_t gfxinfer_model_copy_tensor(const gfxinfer_model* model, const char* name,
                                    int32_t auxiliary, void* host, size_t bytes);
+
+/* ---- .gfxi artifacts (artifact.h, artifact.cpp; converter.cpp) --------------------
+ * The reference's file format: 256-byte header, 128-byte directory entries, name table,
+ * 256-byte aligned payloads, CRC-64/ECMA-182 over the manifest and every tensor's data.
+ * target_arch "gfx1200": the reference converter's recipe (gfx12 tile order; W3
+ * fragments are re-packed while loading); "gfx950": this library's recipe (loads as
+ * plain copies). */
+typedef struct gfxinfer_artifact gfxinfer_artifact;
+
+/* ArtifactIdentity (artifact.h:35-40), NUL-padded as on disk. */
+typedef struct gfxinfer_artifact_identity {
+  char target_arch[16];
+  char model_id[32];
+  char weights_id[32];
+  char recipe_id[64];
+} gfxinfer_artifact_identity;
+
+/* TensorDescriptor (artifact.h:42-55).  dtype: 1 u8, 2 i32, 3 f16, 4 bf16, 5 f32;
+ * quantization: 0 none, 1 W2G128, 2 W3G128, 3 W4G128, 4 W8G128, 5 FP8 rows.  `name`
+ * stays valid until the artifact is closed; offsets are file offsets. */
+typedef struct gfxinfer_artifact_tensor {
+  const char* name;
+  uint16_t dtype;
+  uint16_t quantization;
+  uint16_t rank;
+  uint16_t flags;
+  uint32_t alignment;
+  uint64_t dimensions[4];
+  uint64_t data_offset;
+  uint64_t data_bytes;
+  uint64_t aux_offset;
+  uint64_t aux_bytes;
+  uint64_t data_crc64;
+} gfxinfer_artifact_tensor;
+
+/* ArtifactView::open (artifact.cpp:264-411): maps the file and validates magic,
+ * version, byte order, section bounds, names, alignment, payload overlap and (when
+ * verify_checksums is non-zero) every checksum.  GFXI_IO_ERROR, GFXI_CORRUPT_ARTIFACT
+ * or GFXI_UNSUPPORTED on failure, as the reference. */
+int32_t gfxinfer_artifact_open(const char* path, int32_t verify_checksums, gfxinfer_artifact** out);
+void gfxinfer_artifact_close(gfxinfer_artifact* artifact);
+int32_t gfxinfer_artifact_get_identity(const gfxinfer_artifact* artifact, gfxinfer_artifact_identity* out);
+size_t gfxinfer_artifact_tensor_count(const gfxinfer_artifact* artifact);
+int32_t gfxinfer_artifact_tensor_at(const gfxinfer_artifact* artifact, size_t index,
+                                    gfxinfer_artifact_tensor* out);
+/* ArtifactView::find (artifact.cpp:413-417). */
+int32_t gfxinfer_artifact_find(const gfxinfer_artifact* artifact, const char* name,
+                               gfxinfer_artifact_tensor* out);
+/* ArtifactView::data / auxiliary (artifact.cpp:419-425): `bytes` bytes of the mapped
+ * file at `offset`, or NULL outside the file. */
+const void* gfxinfer_artifact_bytes(const gfxinfer_artifact* artifact, uint64_t offset, uint64_t bytes);
+/* crc64_ecma_update (artifact.cpp:191-213). */
+uint64_t gfxinfer_crc64_ecma(uint64_t state, const void* bytes, size_t count);
+
+/* No reference counterpart: converts codes in the reference's gfx12 tile order
+ * (quantization.cpp:253-318, the "gfx1200" recipe) to the gfx950 tile layout (W3
+ * fragments re-packed, W4 copied); the loader's conversion, on the host.  `bytes` is a
+ * multiple of the 32-column fragment (12 B W3, 16 B W4); scales need no conversion. */
+int32_t gfxinfer_retile_gfx12_for_gfx950(int32_t format, const uint8_t* gfx12_codes, size_t bytes,
+                                         uint8_t* gfx950_codes);
+
+/* Engine::create from an artifact (engine.cpp:62-209) for the spec's shapes: every
+ * tensor of the converter's naming is required; matrices take the artifact's W3/W4
+ * quantization, the rest bf16; an "mtp.draft_head.weight" + "mtp.draft_head_token_ids"
+ * pair (converter.cpp:252-302) becomes the MTP draft head with its token-id map. */
+int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec* spec, const char* path,
+                                            int32_t verify_checksums, int32_t device,
+                                            gfxinfer_model** out);
+/* No reference counterpart (the reference writes artifacts only from safetensors): writes
+ * the model's arena as a gfx950-recipe artifact (identity gfx950 / qwen3.8-27b /
+ * weights_id / "gfx950-tile16x128-w3w4-bf16") through a temporary file and rename.
+ * With draft_count > 0 (a multiple of 16) it also writes the converter's MTP draft head
+ * (converter.cpp:252-302): LM-head rows draft_rows[0..draft_count) as
+ * "mtp.draft_head.weight" and the row ids as "mtp.draft_head_token_ids". */
+int32_t gfxinfer_model_write_artifact(const gfxinfer_model* model, const char* path,
+                                      const char* weights_id, const uint32_t* draft_rows,
+                                      size_t draft_count);
 
 /* DecodeSessionConfig (qwen_runtime.h:23-29).  Activations are always A4G128 (the
  * reference's ActivationMode::int4).  graph_verifier_batch: 0, or 2..32 to capture the

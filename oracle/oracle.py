@@ -51,7 +51,64 @@ def ref_lib() -> ctypes.CDLL | None:
         _ref.ref_dequantize_group128.argtypes = [P, P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, P]
         _ref.ref_packed_row_bytes.restype = ctypes.c_size_t
         _ref.ref_packed_row_bytes.argtypes = [ctypes.c_int, ctypes.c_size_t]
+        _ref.ref_tile_group128_for_gfx12.restype = ctypes.c_int
+        _ref.ref_tile_group128_for_gfx12.argtypes = [P, P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, P, P]
+        _ref.ref_write_artifact.restype = ctypes.c_int
+        _ref.ref_write_artifact.argtypes = [ctypes.c_char_p] * 5 + [ctypes.c_size_t] + [P] * 9
+        _ref.ref_open_artifact.restype = ctypes.c_int
+        _ref.ref_open_artifact.argtypes = [ctypes.c_char_p, ctypes.c_int, P]
+        _ref.ref_crc64_ecma.restype = ctypes.c_uint64
+        _ref.ref_crc64_ecma.argtypes = [P, ctypes.c_size_t]
     return _ref
+
+
+def ref_write_artifact(path: str, identity: tuple, tensors: list) -> int:
+    """The reference ArtifactWriter::write (artifact.cpp:427-545) on `tensors`: dicts with
+    name, dtype, quantization, dims, data (bytes-like), aux (bytes-like or None)."""
+    R = ref_lib()
+    n = len(tensors)
+    keep = []
+    def arr(values, ctype):
+        a = (ctype * len(values))(*values)
+        keep.append(a)
+        return ctypes.cast(a, P)
+    names = [t["name"].encode() for t in tensors]
+    name_arr = (ctypes.c_char_p * n)(*names)
+    dims = []
+    for t in tensors:
+        d = list(t["dims"]) + [0] * (4 - len(t["dims"]))
+        dims += d
+    datas = [np.ascontiguousarray(np.frombuffer(bytes(t["data"]), np.uint8)) for t in tensors]
+    auxs = [None if t.get("aux") is None else np.ascontiguousarray(np.frombuffer(bytes(t["aux"]), np.uint8))
+            for t in tensors]
+    keep += datas + [a for a in auxs if a is not None]
+    data_ptrs = (P * n)(*[d.ctypes.data for d in datas])
+    aux_ptrs = (P * n)(*[None if a is None else a.ctypes.data for a in auxs])
+    return R.ref_write_artifact(
+        str(path).encode(), *[x.encode() for x in identity], n, ctypes.cast(name_arr, P),
+        arr([t["dtype"] for t in tensors], ctypes.c_int), arr([t["quantization"] for t in tensors], ctypes.c_int),
+        arr([len(t["dims"]) for t in tensors], ctypes.c_int), arr(dims, ctypes.c_uint64),
+        ctypes.cast(data_ptrs, P), arr([d.nbytes for d in datas], ctypes.c_uint64),
+        ctypes.cast(aux_ptrs, P), arr([0 if a is None else a.nbytes for a in auxs], ctypes.c_uint64))
+
+
+def ref_open_artifact(path: str, verify: bool = True) -> tuple:
+    """The reference ArtifactView::open: (status code, tensor count)."""
+    count = ctypes.c_size_t(0)
+    rc = ref_lib().ref_open_artifact(str(path).encode(), int(verify), ctypes.byref(count))
+    return rc, count.value
+
+
+def ref_tile_gfx12(codes: np.ndarray, scales: np.ndarray, rows: int, cols: int, fmt: int):
+    """The reference tile_group128_for_gfx12 (quantization.cpp:253-318)."""
+    out_codes = np.empty(codes.size, np.uint8)
+    out_scales = np.empty(scales.size, np.float32)
+    rc = ref_lib().ref_tile_group128_for_gfx12(ptr(np.ascontiguousarray(codes, np.uint8)),
+                                               ptr(np.ascontiguousarray(scales, np.float32)),
+                                               rows, cols, fmt, ptr(out_codes), ptr(out_scales))
+    if rc != 0:
+        raise RuntimeError(f"reference gfx12 tiling failed: {rc}")
+    return out_codes, out_scales
 
 
 P = ctypes.c_void_p

@@ -1,0 +1,165 @@
+"""Loading models from .gfxi artifacts on the GPU.
+
+- gfx950 recipe: a synthetic model written by the library and loaded back is the same
+  model byte for byte and gives the same tokens and logits; the reference reader
+  (oracle/_ref, where built) accepts the file.
+- gfx1200 recipe: the same synthetic weights quantized, gfx12-tiled and written by the
+  reference's own code (quantizer, tile_group128_for_gfx12, ArtifactWriter) load into
+  the identical gfx950 arena.
+- The converter's MTP draft head (ranked LM-head rows + token ids) drives the MTP
+  proposal through the token-id map.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+SEED = 77
+
+
+def _spec():
+    from gfxinfer_amd.runtime import tiny_spec
+    return tiny_spec(full_attention_interval=2, gdn_key_head_count=4)
+
+
+@pytest.fixture(scope="module")
+def model(device):
+    from gfxinfer_amd.runtime import SyntheticModel
+    say("synthetic model for artifacts")
+    m = SyntheticModel(_spec(), SEED)
+    yield m
+    m.close()
+
+
+def _names(path):
+    from gfxinfer_amd.runtime import Artifact
+    with Artifact(path) as a:
+        return [(t.name.decode(), t.quantization, t.shape) for t in a.tensors()]
+
+
+def _same_arena(a, b, names):
+    for name, quant, _ in names:
+        assert np.array_equal(a.tensor_bytes(name), b.tensor_bytes(name)), name
+        if quant != 0:
+            assert np.array_equal(a.tensor_bytes(name, True), b.tensor_bytes(name, True)), name
+
+
+def _outputs(model):
+    """Verifier tokens and logits of one 4-token block, and one greedy step's MTP proposal."""
+    from gfxinfer_amd.runtime import QwenDecodeSession
+    spec = model.spec
+    s = QwenDecodeSession(model, 64, 0, keep_logits=True)
+    try:
+        tokens = s.block_step([5, 77, 301, 9])
+        logits = s.buffer("logits", np.float32, 4 * spec.vocabulary_size)
+    finally:
+        s.close()
+    s = QwenDecodeSession(model, 64, 0, keep_logits=True)
+    try:
+        first = s.greedy_step(42)
+        draft = s.mtp_draft(first)
+        draft_logits = s.buffer("logits", np.float32, spec.mtp_draft_vocabulary)
+    finally:
+        s.close()
+    return tokens + [first, draft], logits, draft_logits
+
+
+def test_gfx950_artifact_round_trip(model, orc, tmp_path):
+    from gfxinfer_amd.runtime import Artifact, SyntheticModel
+    path = tmp_path / "tiny_gfx950.gfxi"
+    say("write gfx950 artifact")
+    model.write_artifact(path, "synthetic-77")
+    names = _names(path)
+    with Artifact(path) as a:
+        ident = a.identity()
+        assert (ident["target_arch"], ident["weights_id"]) == ("gfx950", "synthetic-77")
+        conv = [t for t in a.tensors() if t.name.decode().endswith("conv1d.weight")][0]
+        assert conv.rank == 3 and conv.dimensions[1] == 1
+    if orc.ref_lib() is not None:
+        assert orc.ref_open_artifact(path, True) == (0, len(names))
+    say("load gfx950 artifact")
+    loaded = SyntheticModel.from_artifact(_spec(), path)
+    try:
+        _same_arena(model, loaded, names)
+        say("sessions on both models")
+        want, got = _outputs(model), _outputs(loaded)
+    finally:
+        loaded.close()
+    assert got[0] == want[0]
+    assert np.array_equal(got[1], want[1]) and np.array_equal(got[2], want[2])
+
+
+def test_gfx1200_artifact_from_reference_writer(model, orc, tmp_path):
+    if orc.ref_lib() is None:
+        pytest.skip("oracle/_ref (the reference quantizer, tiler and writer) is not built")
+    from gfxinfer_amd.runtime import SyntheticModel
+    ours = tmp_path / "tiny_gfx950.gfxi"
+    model.write_artifact(ours, "synthetic-77")
+    tensors = []
+    for name, quant, shape in _names(ours):
+        if quant == 0:
+            dtype = 4
+            data, aux = model.tensor_bytes(name).tobytes(), None
+        else:
+            dtype = 1
+            rows, cols = shape
+            w = orc.synthetic_values(SEED, name, rows * cols, 0.02, 0.0).reshape(rows, cols)
+            status, codes, scales = orc.ref_quantize_group128(w, quant)
+            assert status == 0
+            tiled, tscales = orc.ref_tile_gfx12(codes, scales, rows, cols, quant)
+            data, aux = tiled.tobytes(), orc.f32_to_f16_bits(tscales).tobytes()
+        tensors.append(dict(name=name, dtype=dtype, quantization=quant, dims=shape, data=data, aux=aux))
+    path = tmp_path / "tiny_gfx1200.gfxi"
+    say("reference writer: gfx1200 artifact of", len(tensors), "tensors")
+    assert orc.ref_write_artifact(path, ("gfx1200", "qwen3.8-27b", "synthetic-77", "reference-gfx12"),
+                                  tensors) == 0
+    say("load gfx1200 artifact")
+    loaded = SyntheticModel.from_artifact(_spec(), path)
+    try:
+        _same_arena(model, loaded, _names(ours))
+    finally:
+        loaded.close()
+
+
+def test_draft_head_artifact_uses_token_ids(model, tmp_path):
+    from gfxinfer_amd.runtime import SyntheticModel
+    spec = _spec()
+    n = spec.mtp_draft_vocabulary
+    rng = np.random.default_rng(5)
+    # (a) the same candidate rows in another order: the proposal is unchanged
+    perm = rng.permutation(n).astype(np.uint32)
+    path = tmp_path / "draft_perm.gfxi"
+    say("artifact with a permuted draft head")
+    model.write_artifact(path, "synthetic-77", draft_rows=perm)
+    loaded = SyntheticModel.from_artifact(spec, path)
+    try:
+        assert np.array_equal(loaded.tensor_bytes("mtp.draft_head_token_ids").view(np.uint32), perm)
+        want, got = _outputs(model), _outputs(loaded)
+    finally:
+        loaded.close()
+    assert got[0] == want[0]
+    assert np.array_equal(got[2], want[2][perm])  # the draft logits come in the artifact's row order
+    # (b) other rows: the proposal is ids[argmax of the draft head's own logits]
+    rows = rng.choice(spec.vocabulary_size, n, replace=False).astype(np.uint32)
+    path = tmp_path / "draft_other.gfxi"
+    model.write_artifact(path, "synthetic-77", draft_rows=rows)
+    loaded = SyntheticModel.from_artifact(spec, path)
+    try:
+        got = _outputs(loaded)
+    finally:
+        loaded.close()
+    draft, logits = got[0][-1], got[2]
+    assert draft == int(rows[int(np.argmax(logits))])
+
+
+def test_load_rejects_mismatched_spec(model, tmp_path):
+    from gfxinfer_amd import GfxinferError
+    from gfxinfer_amd.runtime import SyntheticModel, tiny_spec
+    path = tmp_path / "tiny.gfxi"
+    model.write_artifact(path, "synthetic-77")
+    with pytest.raises(GfxinferError) as e:
+        SyntheticModel.from_artifact(tiny_spec(full_attention_interval=2, gdn_key_head_count=2), path)
+    assert e.value.code == 3  # corrupt_artifact: shape does not match the spec
