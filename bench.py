@@ -104,6 +104,103 @@ def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16):
                 weight_bytes=sum(c.numel() for c in codes) + 2 * sum(s.numel() for s in scales))
 
 
+def verify_gemm_bench(batches=(5, 16, 32), copies=4, reps=20):
+    """one dense decoder block's projection set in W3A4 (q/k/v from
+    hidden 5120 with 40 Q / 8 KV heads x 128, o, SwiGLU MLP 5120 -> 17408 -> 5120) at
+    k + 1 = 5, 16, 32 rows, launched the way the verifier launches them (q/k/v and
+    gate/up fused into one grid each, o and down as split-K planes), and the W4 LM head
+    [151936, 5120] with the fused greedy argmax.  Each launch is timed alone under graph
+    replay over rotating weight copies (the block's weights x copies exceed the 256 MB
+    Infinity Cache); one JSON line per (projection, rows)."""
+    import ctypes
+    import torch
+    import gfxinfer_amd as gx
+
+    H, I, V = 5120, 17408, 151936
+    w3, w4 = gx.W3G128, gx.W4G128
+
+    def matrix(fmt, rows, cols, n):
+        w = torch.randn(rows, cols, device="cuda") * 0.02
+        c0 = torch.empty(gx.tile_bytes(fmt, rows, cols), dtype=torch.uint8, device="cuda")
+        s0 = torch.empty(rows * cols // 128, dtype=torch.int16, device="cuda")
+        gx.launch_quantize_group128(fmt, w, rows, cols, c0, s0)
+        del w
+        return [(c0, s0)] + [(c0.clone(), s0.clone()) for _ in range(n - 1)]
+
+    torch.manual_seed(0x5EED)
+    mats = {"q": (w3, H, H), "k": (w3, 1024, H), "v": (w3, 1024, H), "o": (w3, H, H),
+            "gate": (w3, I, H), "up": (w3, I, H), "down": (w3, H, I)}
+    weights = {name: matrix(f, r, c, copies) for name, (f, r, c) in mats.items()}
+    head = matrix(w4, V, H, 1)[0]
+    out = []
+    stream = torch.cuda.Stream()
+    for batch in batches:
+        acts = {}
+        for cols in (H, I):
+            x = torch.randn(batch, cols, device="cuda").half()
+            a = torch.empty(batch, cols // 2, dtype=torch.uint8, device="cuda")
+            sa = torch.empty(batch, cols // 128, dtype=torch.int16, device="cuda")
+            gx.launch_quantize_activation_i4(x, a, sa, cols, batch)
+            acts[cols] = (a, sa)
+        ys = {name: torch.empty(8, batch, r, device="cuda") for name, (_, r, _) in mats.items()}
+        keys_bytes = int(gx.lib().gfxinfer_gemm_argmax_workspace_bytes(V, batch))
+        keys = torch.empty(keys_bytes, dtype=torch.uint8, device="cuda")
+        tokens = torch.empty(batch, dtype=torch.int32, device="cuda")
+
+        def fused(names, i, s):
+            a, sa = acts[H]
+            gx.launch_i4_gemm_fused(w3, [(weights[n][i][0], weights[n][i][1], ys[n], mats[n][1]) for n in names],
+                                    a, sa, H, batch, stream=s)
+
+        def split(name, i, s):
+            f, r, c = mats[name]
+            a, sa = acts[c]
+            gx.launch_i4_gemm_split(f, weights[name][i][0], weights[name][i][1], a, sa, ys[name], r, c, batch,
+                                    gx.gemm_split_count(r, c, batch), stream=s)
+
+        def lm_head(i, s):
+            a, sa = acts[H]
+            gx.check(gx.lib().gfxinfer_launch_gfx950_i4_gemm_argmax(
+                w4, head[0].data_ptr(), head[1].data_ptr(), a.data_ptr(), sa.data_ptr(), None, V, H, batch,
+                V, None, keys.data_ptr(), keys_bytes, tokens.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
+
+        cases = [("qkv", ("q", "k", "v"), lambda i, s: fused(("q", "k", "v"), i, s)),
+                 ("o", ("o",), lambda i, s: split("o", i, s)),
+                 ("gate_up", ("gate", "up"), lambda i, s: fused(("gate", "up"), i, s)),
+                 ("down", ("down",), lambda i, s: split("down", i, s)),
+                 ("lm_head_argmax", None, lm_head)]
+        for label, names, fn in cases:
+            n = copies if names is not None else 1
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(stream):
+                for i in range(n):
+                    fn(i, stream)
+                stream.synchronize()
+                with torch.cuda.graph(g, stream=stream):
+                    for i in range(n):
+                        fn(i, stream)
+                for _ in range(3):
+                    g.replay()
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+            if names is None:
+                nbytes = algorithmic_bytes(V, H, batch, wbits=4)
+            else:
+                nbytes = sum(algorithmic_bytes(mats[m][1], mats[m][2], batch) for m in names)
+            line = {"verify_gemm": label, "rows": batch, "us": round(us, 3), "bytes": nbytes,
+                    "gbs": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            out.append(line)
+            print(json.dumps(line), flush=True)
+    return out
+
+
 def _forced_acceptance(rng, depth):
     """Seeded Bernoulli(0.85) per draft; accepted = index of the first failure."""
     trials = rng.random(depth) < 0.85
@@ -301,6 +398,10 @@ def main():
                     help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the rocprofv3 --pmc workload (calibration copy + plain GEMM launches)")
+    ap.add_argument("--probe-rows", type=int, default=17408, help="--pmc-probe GEMM rows")
+    ap.add_argument("--probe-batch", type=int, default=5, help="--pmc-probe GEMM tokens")
+    ap.add_argument("--verify-gemms", action="store_true",
+                    help="time BASELINE config 3 (one block's projections + LM head argmax at 5/16/32 rows)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -309,7 +410,10 @@ def main():
     import gfxinfer_amd as gx
     gx.check(gx.lib().gfxinfer_require_gfx950_device(0))
     if args.pmc_probe:
-        pmc_probe()
+        pmc_probe(rows=args.probe_rows, batch=args.probe_batch)
+        return
+    if args.verify_gemms:
+        verify_gemm_bench()
         return
 
     r = gemv_bench(args.steps, args.warmup)

@@ -5,6 +5,8 @@
         --copy NAME --copy-bytes N
 
     python -m gfxinfer_amd.rocprof_summary rounds <dir> --marker NAME --rounds N
+    python -m gfxinfer_amd.rocprof_summary counters <dir>... --kernel NAME [--us T]
+    python -m gfxinfer_amd.rocprof_summary shapes <dir> [--match NAME]...
 
 `stats` prints the kernel table of a --kernel-trace --stats run (calls, total,
 average, min, max per kernel).  `rounds` reads the kernel trace of such a run and
@@ -13,7 +15,14 @@ kernel), the span per round, the GPU-busy time per round and each kernel's time
 and dispatch count per round.  `pmc` reads two --pmc runs (FETCH_SIZE, then
 WRITE_SIZE; both in KiB per dispatch), calibrates each counter on the copy kernel
 of known size (it reads and writes exactly N bytes) and prints the HBM bytes per
-dispatch of the named kernel.
+dispatch of the named kernel.  `shapes` splits a --kernel-trace run by launch
+shape (kernel, grid, workgroup) and prints each shape's dispatch count and median and
+minimum duration.  `counters` prints the per-dispatch median of every
+counter that --pmc runs collected for the named kernel and, given the kernel's mean
+duration T (from a --kernel-trace run), the derived figures: MFMA busy fraction
+(SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x T x 2.4 GHz), average DRAM read latency
+(TCC_EA0_RDREQ_LEVEL / TCC_EA0_RDREQ, TCC cycles) and average DRAM reads in flight
+(TCC_EA0_RDREQ_LEVEL / (T x 2.4 GHz), 128-byte requests).
 """
 from __future__ import annotations
 
@@ -101,6 +110,48 @@ def pmc(fetch_dir: str, write_dir: str, kernel: str, copy: str, copy_bytes: int)
     return "\n".join(out)
 
 
+def shapes(directory: str, match: list[str]) -> str:
+    groups: dict[tuple, list[float]] = {}
+    for r in _csv(directory, "kernel_trace.csv"):
+        if match and not any(m in r["Kernel_Name"] for m in match):
+            continue
+        wg = int(r["Workgroup_Size_X"])
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // wg, wg)
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"{'workgroups':>10} {'threads':>7} {'calls':>6} {'median_us':>9} {'min_us':>8}  kernel"]
+    for (name, wgs, wg), v in sorted(groups.items()):
+        lines.append(f"{wgs:10d} {wg:7d} {len(v):6d} {statistics.median(v):9.2f} {min(v):8.2f}  {name}")
+    return "\n".join(lines)
+
+
+SIMDS = 1024          # 256 CUs x 4 SIMDs
+CLOCK_GHZ = 2.4       # MI355X peak engine clock
+
+
+def counters(directories: list[str], kernel: str, us: float | None) -> str:
+    names: set[str] = set()
+    for d in directories:
+        names.update(r["Counter_Name"] for r in _csv(d, "counter_collection.csv") if kernel in r["Kernel_Name"])
+    med: dict[str, float] = {}
+    lines = []
+    for name in sorted(names):
+        values = []
+        for d in directories:
+            values += _per_dispatch(d, name, kernel)
+        med[name] = statistics.median(values)
+        lines.append(f"{name:36s} median {med[name]:.6g} over {len(values)} dispatches")
+    if us:
+        cycles = us * 1e3 * CLOCK_GHZ
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+            lines.append(f"mfma_busy_fraction = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / (SIMDS * cycles):.4f}  "
+                         f"(kernel {us} us)")
+        if "TCC_EA0_RDREQ_LEVEL_sum" in med and "TCC_EA0_RDREQ_sum" in med:
+            lines.append(f"dram_read_latency_cycles = {med['TCC_EA0_RDREQ_LEVEL_sum'] / med['TCC_EA0_RDREQ_sum']:.0f}")
+            inflight = med["TCC_EA0_RDREQ_LEVEL_sum"] / cycles
+            lines.append(f"dram_reads_in_flight = {inflight:.0f} ({inflight * 128 / 1e6:.2f} MB)")
+    return "\n".join(lines)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -117,7 +168,20 @@ def main() -> None:
     c.add_argument("directory")
     c.add_argument("--marker", required=True)
     c.add_argument("--rounds", type=int, required=True)
+    d = sub.add_parser("counters")
+    d.add_argument("directories", nargs="+")
+    d.add_argument("--kernel", required=True)
+    d.add_argument("--us", type=float, default=None)
+    e = sub.add_parser("shapes")
+    e.add_argument("directory")
+    e.add_argument("--match", action="append", default=[])
     args = ap.parse_args()
+    if args.cmd == "shapes":
+        print(shapes(args.directory, args.match))
+        return
+    if args.cmd == "counters":
+        print(counters(args.directories, args.kernel, args.us))
+        return
     if args.cmd == "stats":
         print(stats(args.directory, args.match))
     elif args.cmd == "rounds":

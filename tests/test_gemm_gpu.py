@@ -151,6 +151,8 @@ CASES = [
     (2, 4, 17408, 5120, 1), (2, 4, 17408, 5120, 32), (2, 8, 17408, 5120, 1),
     # down projection at verify batches: K = 17408 needs the LDS wave cap at 32 tokens
     (2, 4, 5120, 17408, 32), (3, 4, 5120, 17408, 16), (2, 8, 5120, 17408, 32),
+    # 9-32 tokens (LDS-ring kernel): workgroups of 4 or 8 tiles with a short last one
+    (2, 4, 48, 256, 13), (3, 4, 112, 384, 32), (3, 4, 16480, 5120, 32), (2, 4, 34816, 5120, 24),
 ]
 
 
