@@ -1023,17 +1023,28 @@ __global__ __launch_bounds__(256) void row_gather_kernel(
                                 __half2float(scales[scale_offset(row, column / kGroup, groups)]));
 }
 
-// Second half of the fused argmax: the best tile key of each token row.
-__global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long long* __restrict__ keys,
-                                                          uint32_t count,
-                                                          const uint32_t* __restrict__ token_ids,
-                                                          uint32_t* __restrict__ out) {
-  __shared__ unsigned long long partial[4];
+// Second half of the fused argmax: the best tile key of each token row.  One
+// 1024-thread workgroup per row; every thread issues all its loads (up to
+// kArgmaxLoads keys, coalesced across the workgroup) before the first comparison,
+// so a row of up to 16384 tiles costs one memory round trip instead of a chain.
+constexpr unsigned kArgmaxThreads = 1024;
+constexpr unsigned kArgmaxLoads = 16;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_keys_kernel(
+    const unsigned long long* __restrict__ keys, uint32_t count, const uint32_t* __restrict__ token_ids,
+    uint32_t* __restrict__ out) {
+  __shared__ unsigned long long partial[kArgmaxThreads / 64];
   const unsigned long long* row = keys + static_cast<std::size_t>(blockIdx.x) * count;
   unsigned long long best = 0ull;
-  for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-    const unsigned long long k = row[i];
-    best = k > best ? k : best;
+  for (uint32_t base = 0; base < count; base += kArgmaxThreads * kArgmaxLoads) {
+    unsigned long long k[kArgmaxLoads];
+#pragma unroll
+    for (unsigned u = 0; u < kArgmaxLoads; ++u) {
+      const uint32_t i = base + u * kArgmaxThreads + threadIdx.x;
+      k[u] = i < count ? row[i] : 0ull;
+    }
+#pragma unroll
+    for (unsigned u = 0; u < kArgmaxLoads; ++u) best = k[u] > best ? k[u] : best;
   }
 #pragma unroll
   for (int offset = 32; offset != 0; offset >>= 1) {
@@ -1043,7 +1054,7 @@ __global__ __launch_bounds__(256) void argmax_keys_kernel(const unsigned long lo
   if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (unsigned w = 1; w < blockDim.x / 64; ++w) best = partial[w] > best ? partial[w] : best;
+    for (unsigned w = 1; w < kArgmaxThreads / 64; ++w) best = partial[w] > best ? partial[w] : best;
     const uint32_t index = argmax_key_row(best);
     out[blockIdx.x] = token_ids != nullptr ? token_ids[index] : index;
   }
@@ -1518,7 +1529,7 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(
                                     activation_scales, nullptr, columns, batch, false, s, keys,
                                     static_cast<uint32_t>(argmax_rows));
   if (status != GFXI_OK) return status;
-  hipLaunchKernelGGL(argmax_keys_kernel, dim3(batch), dim3(256), 0, s, keys,
+  hipLaunchKernelGGL(argmax_keys_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, keys,
                      static_cast<uint32_t>(rows / 16), token_ids, tokens);
   return launch_status("fused GEMM argmax reduction launch failed");
 }

@@ -309,7 +309,9 @@ def _gemm_argmax(gx, fmt, p, rows, cols, batch, argmax_rows, ids=None, logits=Tr
 
 @pytest.mark.parametrize("fmt,rows,cols,batch,limit", [
     (3, 1024, 256, 1, 1024), (3, 1024, 256, 5, 1000), (3, 4096, 640, 32, 4000), (2, 2048, 512, 17, 2048),
-    (3, 151936, 5120, 5, 151936)])
+    (3, 151936, 5120, 5, 151936),
+    # 17000 tiles: more keys per row than one pass of the reduction's loads holds
+    (3, 272000, 128, 2, 271990)])
 def test_gemm_argmax_matches_logits_argmax(device, gx, orc, fmt, rows, cols, batch, limit):
     """LM head + fused greedy argmax == argmax (ties to the lowest index) of the same
     GEMM's logits, and the logits match the oracle epilogue."""
