@@ -207,16 +207,54 @@ struct GemmArgs {
   uint32_t splits;
 };
 
-// Packs [begin, end) of this wave: split `split` of `splits` equal ranges of the
-// matrix's packs, then wave `wave` of `waves` equal pieces of that range.
-struct PackRange {
-  unsigned begin, end;
+// Canonical summation over K.  Every GEMM variant adds the int32 group partials the
+// same way, so an output depends only on (row, token, K, splits): not on the batch,
+// the kernel family or the launch shape, and a block of tokens gives each token
+// exactly what a one-token step gives it (as the reference's sequential epilogue does).
+//   * K's groups form quads of 4 consecutive groups; split s of S owns quads
+//     [Q s / S, Q (s + 1) / S) of the Q quads;
+//   * a split is cut into range_count(its groups) ranges of whole quads (range r of
+//     R: quads [Qs r / R, Qs (r + 1) / R) of the split's Qs quads);
+//   * in a range, stream j = group mod 4 accumulates fmaf(float(partial), ws * as,
+//     acc_j) over its groups in increasing order, and the range sums to
+//     (acc_0 + acc_1) + (acc_2 + acc_3);
+//   * a split's output is ((range_0 + range_1) + range_2) + ... in range order.
+// A kernel may give a wave several consecutive ranges; a chunk of loads always holds
+// whole quads, so each pack's stream is known at compile time.
+struct GroupRange {
+  unsigned begin, end;  // groups [begin, end)
 };
-__device__ __forceinline__ PackRange wave_packs(unsigned packs, unsigned split, unsigned splits,
-                                                unsigned wave, unsigned waves) {
-  const unsigned first = packs * split / splits;
-  const unsigned span = packs * (split + 1) / splits - first;
-  return {first + span * wave / waves, first + span * (wave + 1) / waves};
+
+__host__ __device__ inline unsigned quad_count(unsigned groups) { return (groups + 3u) / 4u; }
+
+__host__ __device__ inline GroupRange split_groups(unsigned groups, unsigned split, unsigned splits) {
+  const unsigned q = quad_count(groups);
+  const unsigned b = 4u * (q * split / splits), e = 4u * (q * (split + 1u) / splits);
+  return {b < groups ? b : groups, e < groups ? e : groups};
+}
+
+__host__ __device__ inline unsigned range_count(unsigned groups_in_split) {
+  const unsigned r = (groups_in_split + 9u) / 10u;  // about ten groups per range
+  return r < 1u ? 1u : (r > 16u ? 16u : r);
+}
+
+__host__ __device__ inline GroupRange canonical_range(unsigned groups, unsigned split, unsigned splits,
+                                                      unsigned range, unsigned ranges) {
+  const unsigned q = quad_count(groups);
+  const unsigned qs = q * split / splits, qn = q * (split + 1u) / splits - qs;
+  const unsigned b = 4u * (qs + qn * range / ranges), e = 4u * (qs + qn * (range + 1u) / ranges);
+  return {b < groups ? b : groups, e < groups ? e : groups};
+}
+
+// Fewest ranges of any split of a launch: a workgroup has at most that many waves.
+inline unsigned min_range_count(unsigned groups, unsigned splits) {
+  unsigned m = 16u;
+  for (unsigned s = 0; s < splits; ++s) {
+    const GroupRange g = split_groups(groups, s, splits);
+    const unsigned r = range_count(g.end - g.begin);
+    m = r < m ? r : m;
+  }
+  return m;
 }
 
 // Orderable argmax key of logit v at row: the high word orders values (a total
@@ -244,13 +282,14 @@ __device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
 // rotates the LDS banks of consecutive tokens) and are expanded to MFMA operand
 // bytes when read; A8 activations are staged through registers already permuted
 // to operand order ([group][lane block kb][K-step h][16 bytes]).  After the MFMA
-// loop the region holds the wave's partial sums for the cross-wave reduction.
+// loop the range values wait in their own area for the ordered sum of the split.
 struct GemmLds {
-  uint32_t pitch;          // bytes per token row (chunk bytes + 16: rotates LDS banks)
-  uint32_t zero_offset;    // zero line
-  uint32_t scale_offset;   // fp32 scales [batch][chunk groups]
-  uint32_t wscale_offset;  // fp16 weight scales of the chunk [chunk groups][16 rows]
-  uint32_t region;         // bytes per wave
+  uint32_t pitch;           // bytes per token row (chunk bytes + 16: rotates LDS banks)
+  uint32_t zero_offset;     // zero line
+  uint32_t scale_offset;    // fp32 scales [batch][chunk groups]
+  uint32_t wscale_offset;   // fp16 weight scales of the chunk [chunk groups][16 rows]
+  uint32_t region;          // bytes per wave
+  uint32_t results_offset;  // after the wave regions: [ranges][NTB][4][64] fp32 range values
 };
 
 __host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32_t batch, int abits,
@@ -287,6 +326,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
   constexpr bool kDma = ABits == 4;  // A4 pieces go straight from memory to LDS
+  constexpr unsigned NS = 4 / GP;    // accumulator sets per lane: streams (group mod 4) / GP
+  static_assert(CH * GP % 4 == 0 || GP == 4, "a chunk holds whole quads of groups");
 
   extern __shared__ __align__(16) uint8_t lds_all[];
 
@@ -323,9 +364,11 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   const unsigned window = n / TPAD;
   const unsigned w_voffset = lane * LB;
 
-  const PackRange range = wave_packs((groups + GP - 1) / GP, split, args.splits, wave, waves);
-  const unsigned pack_begin = range.begin;
-  const unsigned pack_end = range.end;
+  // This wave's ranges of the canonical K partition (waves <= ranges).
+  const GroupRange own = split_groups(groups, split, args.splits);
+  const unsigned ranges = range_count(own.end - own.begin);
+  const unsigned range_begin = ranges * wave / waves;
+  const unsigned range_end = ranges * (wave + 1u) / waves;
 
   // LDS byte offset of this lane's B operand for group j of a pack, token block t
   // (relative to the pack's first group); lanes outside the window read zeros.
@@ -342,12 +385,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   }
   if (lane < 4) reinterpret_cast<uint32_t*>(lds + layout.zero_offset)[lane] = 0u;
 
-  float acc[NTB][4];
-#pragma unroll
-  for (int t = 0; t < NTB; ++t) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0F;
-  }
+  float acc[NS][NTB][4];  // stream sets of the current range
+  float total[NTB][4];    // the range value (one range) or the split's sum
 
   constexpr unsigned kPieces = AGB / 16;  // 16-byte source pieces per token per group
   constexpr unsigned kRowPieces = CHG * kPieces;
@@ -356,6 +395,16 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   constexpr unsigned kMaxPieces = kDma ? 1u : (kMaxTokens * kRowPieces + 63u) / 64u;
   constexpr unsigned kMaxDma = (kMaxTokens * kDmaRow + 63u) / 64u;
   const auto act_scales = buffer(args.activation_scales, batch * groups * 2u);
+  for (unsigned range = range_begin; range < range_end; ++range) {
+  const GroupRange span = canonical_range(groups, split, args.splits, range, ranges);
+  const unsigned pack_begin = span.begin / GP;
+  const unsigned pack_end = (span.end + GP - 1u) / GP;
+#pragma unroll
+  for (unsigned q = 0; q < NS; ++q)
+#pragma unroll
+    for (int t = 0; t < NTB; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[q][t][r] = 0.0F;
   for (unsigned base = pack_begin; base < pack_end; base += CH) {
     const unsigned g0 = base * GP;
     // 1) Activation pieces of this chunk (L2-resident), loaded first.  Piece i
@@ -542,38 +591,61 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
           const float as = scales[token * CHG + gl];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            acc[t][r] = fmaf(static_cast<float>(c[t][r]), ws[r] * as, acc[t][r]);
+            // stream of group g_c (chunks start on quads): set ((ci * GP) mod 4) / GP
+            float& a = acc[((ci * GP) & 3u) / GP][t][r];
+            a = fmaf(static_cast<float>(c[t][r]), ws[r] * as, a);
           }
         }
       }
     }
   }
-  if constexpr (Partials) return;
-
-  // Combine the GP windows of each token slot (lanes n, n+TPAD, ...).
-#pragma unroll
-  for (unsigned offset = TPAD; offset < 16u; offset <<= 1) {
-#pragma unroll
-    for (int t = 0; t < NTB; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] += __shfl_xor(acc[t][r], static_cast<int>(offset));
-    }
-  }
-  if (waves > 1) {
-    float* mine = reinterpret_cast<float*>(lds);  // this wave's region is free now
+  if constexpr (!Partials) {
+    // The range value (acc_0 + acc_1) + (acc_2 + acc_3).  Stream j lives in set j / GP
+    // of the lanes of window j % GP: GP = 4 adds windows (0 + 1) and (2 + 3), then the
+    // two sums; GP = 2 adds windows 0 + 1 in each set, then the sets; GP = 1 adds sets.
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mine[(t * 4 + r) * 64 + lane] = acc[t][r];
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (GP == 4) {
+          float v = acc[0][t][r] + __shfl_xor(acc[0][t][r], 4);
+          total[t][r] = v + __shfl_xor(v, 8);
+        } else if constexpr (GP == 2) {
+          const float v01 = acc[0][t][r] + __shfl_xor(acc[0][t][r], 8);
+          const float v23 = acc[1][t][r] + __shfl_xor(acc[1][t][r], 8);
+          total[t][r] = v01 + v23;
+        } else {
+          total[t][r] = (acc[0][t][r] + acc[1][t][r]) + (acc[2][t][r] + acc[3][t][r]);
+        }
+      }
     }
-    __syncthreads();
-    if (wave != 0) return;
-    for (unsigned w = 1; w < waves; ++w) {
-      const float* other = reinterpret_cast<const float*>(lds_all + w * layout.region);
+    if (ranges > 1) {
+      float* slot_out = reinterpret_cast<float*>(lds_all + layout.results_offset) + range * NTB * 4u * 64u;
 #pragma unroll
       for (int t = 0; t < NTB; ++t) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] += other[(t * 4 + r) * 64 + lane];
+        for (int r = 0; r < 4; ++r) slot_out[(t * 4 + r) * 64 + lane] = total[t][r];
+      }
+    }
+  }
+  }  // ranges
+  if constexpr (Partials) return;
+
+  if (ranges > 1) {
+    // The split's value: range values added in range order.
+    __syncthreads();
+    if (wave != 0) return;
+    const float* results = reinterpret_cast<const float*>(lds_all + layout.results_offset);
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total[t][r] = results[(t * 4 + r) * 64 + lane];
+    }
+    for (unsigned rg = 1; rg < ranges; ++rg) {
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) total[t][r] += results[(rg * NTB * 4u + t * 4 + r) * 64 + lane];
       }
     }
   }
@@ -585,7 +657,7 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       unsigned long long best = 0ull;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const unsigned long long key = argmax_key(acc[t][r], tile * 16u + 4u * kb + r, args.argmax_rows);
+        const unsigned long long key = argmax_key(total[t][r], tile * 16u + 4u * kb + r, args.argmax_rows);
         best = key > best ? key : best;
       }
       unsigned long long other = __shfl_xor(best, 16);
@@ -608,9 +680,9 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     if constexpr (HalfOut) {
       __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = to_half(acc[t][r]);
+      for (int r = 0; r < 4; ++r) o[r] = to_half(total[t][r]);
     } else {
-      float4 value = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+      float4 value = {total[t][0], total[t][1], total[t][2], total[t][3]};
       *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
     }
   }
@@ -641,8 +713,12 @@ __device__ __forceinline__ i32x4 expand_nibbles_masked(unsigned x0, unsigned x1,
   return r;
 }
 
+// Waves per workgroup of the direct kernel: the stream sets of the canonical
+// summation need up to ~190 VGPRs at 32 tokens, so a workgroup stops at eight waves.
+constexpr unsigned kDirectMaxWaves = 8;
+
 template <int Format, int ABits, int GP, int NTB, int CH, int R, bool HalfOut, bool Partials>
-__global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args) {
+__global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kernel(GemmArgs args) {
   constexpr unsigned LB = lane_bytes(Format);
   constexpr unsigned WD = LB / 4;                     // weight dwords per lane per group
   constexpr unsigned TPAD = 16 / GP;                  // token slots per window
@@ -653,6 +729,8 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
   constexpr unsigned kOut = 0x80000000u;              // voffset that reads zeros
+  constexpr unsigned NS = 4 / GP;  // accumulator sets per lane: streams (group mod 4) / GP
+  static_assert(CH * GP % 4 == 0 || GP == 4, "a chunk holds whole quads of groups");
 
   extern __shared__ __align__(16) uint8_t lds_all[];
   const unsigned lane = threadIdx.x & 63u;
@@ -707,17 +785,26 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
     as_voffset[t] = ((t * 16u + slot) * groups + window) * 2u;
   }
 
-  const PackRange range = wave_packs((groups + GP - 1) / GP, split, args.splits, wave, waves);
-  const unsigned pack_begin = range.begin;
-  const unsigned pack_end = range.end;
+  // This wave's ranges of the canonical K partition (waves <= ranges).
+  const GroupRange own = split_groups(groups, split, args.splits);
+  const unsigned ranges = range_count(own.end - own.begin);
+  const unsigned range_begin = ranges * wave / waves;
+  const unsigned range_end = ranges * (wave + 1u) / waves;
 
-  float acc[R][NTB][4];
+  float acc[NS][R][NTB][4];  // stream sets of the current range
+  float total[R][NTB][4];    // the range value (one range) or the split's sum
+  for (unsigned range = range_begin; range < range_end; ++range) {
+  const GroupRange span = canonical_range(groups, split, args.splits, range, ranges);
+  const unsigned pack_begin = span.begin / GP;
+  const unsigned pack_end = (span.end + GP - 1u) / GP;
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (unsigned q = 0; q < NS; ++q)
 #pragma unroll
-    for (int t = 0; t < NTB; ++t)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[r][t][i] = 0.0F;
+      for (int t = 0; t < NTB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[q][r][t][i] = 0.0F;
 
   for (unsigned base = pack_begin; base < pack_end; base += CH) {
     // 1) Loads of CH packs: activations + their scales (L2), weights + scales (HBM).
@@ -918,44 +1005,67 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
           for (int t = 0; t < NTB; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              acc[r][t][i] = fmaf(static_cast<float>(c[t][i]), ws[i] * as[t], acc[r][t][i]);
+              // stream of group g_c (chunks start on quads): set ((ci * GP) mod 4) / GP
+              float& a = acc[((ci * GP) & 3u) / GP][r][t][i];
+              a = fmaf(static_cast<float>(c[t][i]), ws[i] * as[t], a);
             }
           }
         }
       }
     }
   }
-  if constexpr (Partials) return;
-
-  // Combine the GP windows of each token slot (lanes n, n+TPAD, ...).
-#pragma unroll
-  for (unsigned offset = TPAD; offset < 16u; offset <<= 1) {
+  if constexpr (!Partials) {
+    // The range value (acc_0 + acc_1) + (acc_2 + acc_3); stream j lives in set j / GP
+    // of the lanes of window j % GP (as in lowbit_gemm_kernel).
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int t = 0; t < NTB; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][t][i] += __shfl_xor(acc[r][t][i], static_cast<int>(offset));
-  }
-  if (waves > 1) {
-    constexpr unsigned kRegion = R * NTB * 4u * 64u * 4u;
-    float* mine = reinterpret_cast<float*>(lds_all + wave * kRegion);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < NTB; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mine[((r * NTB + t) * 4 + i) * 64 + lane] = acc[r][t][i];
-    __syncthreads();
-    if (wave != 0) return;
-    for (unsigned w = 1; w < waves; ++w) {
-      const float* other = reinterpret_cast<const float*>(lds_all + w * kRegion);
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (GP == 4) {
+            const float v = acc[0][r][t][i] + __shfl_xor(acc[0][r][t][i], 4);
+            total[r][t][i] = v + __shfl_xor(v, 8);
+          } else if constexpr (GP == 2) {
+            const float v01 = acc[0][r][t][i] + __shfl_xor(acc[0][r][t][i], 8);
+            const float v23 = acc[1][r][t][i] + __shfl_xor(acc[1][r][t][i], 8);
+            total[r][t][i] = v01 + v23;
+          } else {
+            total[r][t][i] = (acc[0][r][t][i] + acc[1][r][t][i]) + (acc[2][r][t][i] + acc[3][r][t][i]);
+          }
+        }
+    if (ranges > 1) {
+      float* out = reinterpret_cast<float*>(lds_all) + range * R * NTB * 4u * 64u;
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < NTB; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][t][i] += other[((r * NTB + t) * 4 + i) * 64 + lane];
+          for (int i = 0; i < 4; ++i) out[((r * NTB + t) * 4 + i) * 64 + lane] = total[r][t][i];
+    }
+  }
+  }  // ranges
+  if constexpr (Partials) return;
+  if (ranges > 1) {
+    // The split's value: range values added in range order.
+    __syncthreads();
+    if (wave != 0) return;
+    const float* results = reinterpret_cast<const float*>(lds_all);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < NTB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) total[r][t][i] = results[((r * NTB + t) * 4 + i) * 64 + lane];
+    for (unsigned rg = 1; rg < ranges; ++rg) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < NTB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            total[r][t][i] += results[(((rg * R + r) * NTB + t) * 4 + i) * 64 + lane];
+          }
     }
   }
   const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
@@ -969,7 +1079,7 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
         unsigned long long best = 0ull;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const unsigned long long key = argmax_key(acc[r][t][i], tile * 16u + 4u * kb + i, args.argmax_rows);
+          const unsigned long long key = argmax_key(total[r][t][i], tile * 16u + 4u * kb + i, args.argmax_rows);
           best = key > best ? key : best;
         }
         unsigned long long other = __shfl_xor(best, 16);
@@ -991,9 +1101,9 @@ __global__ __launch_bounds__(1024) void lowbit_gemm_direct_kernel(GemmArgs args)
       if constexpr (HalfOut) {
         __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = to_half(acc[r][t][i]);
+        for (int i = 0; i < 4; ++i) o[i] = to_half(total[r][t][i]);
       } else {
-        float4 value = {acc[r][t][0], acc[r][t][1], acc[r][t][2], acc[r][t][3]};
+        float4 value = {total[r][t][0], total[r][t][1], total[r][t][2], total[r][t][3]};
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
       }
     }
@@ -1124,7 +1234,7 @@ bool resident_cap() {
 // Waves per workgroup: about ten groups of K per wave, but no more than lets every
 // workgroup of the grid be resident at once (a second partial round of
 // workgroups would double the time of a short kernel).
-unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, std::size_t lds_per_wave) {
+unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, std::size_t lds_bytes) {
   unsigned want = choose_waves(groups, 1);
   if (waves_override() != 0 || !resident_cap()) return want;
   static int cus = [] {
@@ -1138,7 +1248,7 @@ unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, st
   for (unsigned w = want; w >= 1; --w) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, static_cast<int>(64 * w),
-                                                     w > 1 ? w * lds_per_wave : 0) != hipSuccess) {
+                                                     lds_bytes) != hipSuccess) {
       return want;
     }
     if (static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus) >= blocks) return w;
@@ -1159,22 +1269,28 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
       if (used) blocks += (args.matrix[i].tiles + r - 1) / r;
     }
     args.tile_begin[4] = blocks;
-    const unsigned waves =
-        resident_waves(reinterpret_cast<const void*>(kernel), args.groups / args.splits,
-                       blocks * args.splits, r * ntb * 4u * 64u * 4u);
-    const std::size_t lds = static_cast<std::size_t>(waves) * r * ntb * 4u * 64u * 4u;
-    hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), waves > 1 ? lds : 0,
-                       stream, args);
+    unsigned max_ranges = 1;
+    for (unsigned sp = 0; sp < args.splits; ++sp) {
+      const GroupRange g = split_groups(args.groups, sp, args.splits);
+      max_ranges = std::max(max_ranges, range_count(g.end - g.begin));
+    }
+    // range values of the canonical K partition, summed in order at the end
+    const std::size_t lds = max_ranges > 1 ? static_cast<std::size_t>(max_ranges) * r * ntb * 4u * 64u * 4u : 0;
+    const unsigned waves = std::min(
+        {resident_waves(reinterpret_cast<const void*>(kernel), args.groups / args.splits, blocks * args.splits,
+                        lds),
+         min_range_count(args.groups, args.splits), kDirectMaxWaves});
+    hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), lds, stream, args);
   };
   (void)total_tiles;
   const int forced = rowtiles_override();
   if (batch <= 4) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 4, 1, 3, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 8) {
-    go(lowbit_gemm_direct_kernel<Format, ABits, 2, 1, 5, 1, HalfOut, Partials>, 1, 1);
+    go(lowbit_gemm_direct_kernel<Format, ABits, 2, 1, 6, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 16) {
     if (forced == 1) {
-      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 6, 1, HalfOut, Partials>, 1, 1);
+      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 1, HalfOut, Partials>, 1, 1);
     } else {
       go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 2, HalfOut, Partials>, 2, 1);
     }
@@ -1183,7 +1299,7 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
   } else if (forced == 1) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
   } else {
-    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 3, 2, HalfOut, Partials>, 2, 2);
+    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 2, HalfOut, Partials>, 2, 2);
   }
 }
 
@@ -1199,25 +1315,36 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
   }
   const uint32_t batch = args.batch;
   auto go = [&](auto kernel, unsigned gp, unsigned ch, unsigned ntb) {
-    unsigned waves = choose_waves(args.groups / args.splits, 1);
+    // One wave per range of the canonical K partition (at most the fewest ranges of
+    // any split), within the register and LDS limits.
+    unsigned waves = std::min(choose_waves(args.groups / args.splits, 1),
+                              min_range_count(args.groups, args.splits));
     if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
-    const GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
+    GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
+    unsigned max_ranges = 1;
+    for (unsigned sp = 0; sp < args.splits; ++sp) {
+      const GroupRange g = split_groups(args.groups, sp, args.splits);
+      max_ranges = std::max(max_ranges, range_count(g.end - g.begin));
+    }
+    const uint32_t results = max_ranges > 1 ? max_ranges * ntb * 4u * 64u * 4u : 0u;
     // A workgroup may hold at most the CU's 160 KiB of LDS (32 tokens x 136 groups
     // would otherwise ask for 8 x 21 KiB).
-    const unsigned lds_waves = kLdsBytes / layout.region;
+    const unsigned lds_waves = (kLdsBytes - results) / layout.region;
     if (waves > lds_waves) waves = lds_waves;
+    layout.results_offset = layout.region * waves;
     hipLaunchKernelGGL(kernel, dim3(total_tiles * args.splits), dim3(64 * waves),
-                       layout.region * waves, stream, args, layout);
+                       layout.results_offset + results, stream, args, layout);
   };
-  // CH = packs per load chunk: about ten groups of weights in flight per wave.
+  // CH = packs per load chunk: about ten groups of weights in flight per wave, whole
+  // quads of groups per chunk.
   if (batch <= 4) {
     go(lowbit_gemm_kernel<Format, ABits, 4, 1, 3, HalfOut, Partials>, 4, 3, 1);
   } else if (batch <= 8) {
-    go(lowbit_gemm_kernel<Format, ABits, 2, 1, 5, HalfOut, Partials>, 2, 5, 1);
+    go(lowbit_gemm_kernel<Format, ABits, 2, 1, 6, HalfOut, Partials>, 2, 6, 1);
   } else if (batch <= 16) {
-    go(lowbit_gemm_kernel<Format, ABits, 1, 1, 6, HalfOut, Partials>, 1, 6, 1);
+    go(lowbit_gemm_kernel<Format, ABits, 1, 1, 8, HalfOut, Partials>, 1, 8, 1);
   } else {
-    go(lowbit_gemm_kernel<Format, ABits, 1, 2, 5, HalfOut, Partials>, 1, 5, 2);
+    go(lowbit_gemm_kernel<Format, ABits, 1, 2, 4, HalfOut, Partials>, 1, 4, 2);
   }
 }
 
@@ -1439,19 +1566,21 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm(int32_t format, const uint8_t*
 }
 
 extern "C" uint32_t gfxinfer_gemm_split_count(size_t rows, size_t columns, uint32_t batch) {
-  // Enough workgroups to fill the chip about four times over (a grid below that
-  // leaves CUs idle or runs a partial second round), each split keeping at least
-  // eight groups of K; the chosen kernel handles 2 row tiles per workgroup above
-  // 8 tokens.  GFXI_GEMM_SPLIT_TARGET overrides the target (tuning knob).
+  // Enough row-tile x split workgroups to fill the chip about four times over (a grid
+  // below that leaves CUs idle or runs a partial second round), each split keeping at
+  // least eight groups of K.  The count depends on the shape only, never on the batch:
+  // the split is part of the summation order, so a block of tokens and one-token
+  // steps must use the same one.  GFXI_GEMM_SPLIT_TARGET overrides the target (tuning
+  // knob; it changes the summation order of split GEMMs).
   static const uint64_t target = [] {
     const char* text = std::getenv("GFXI_GEMM_SPLIT_TARGET");
     const long v = text != nullptr ? std::atol(text) : 0;
     return v > 0 ? static_cast<uint64_t>(v) : uint64_t{1024};
   }();
-  if (rows == 0 || columns < kGroup || batch == 0) return 1;
+  (void)batch;
+  if (rows == 0 || columns < kGroup) return 1;
   const uint64_t tiles = (rows + 15) / 16;
-  const uint64_t blocks = batch > 8 ? (tiles + 1) / 2 : tiles;
-  uint64_t splits = (target + blocks - 1) / blocks;
+  uint64_t splits = (target + tiles - 1) / tiles;
   splits = std::min<uint64_t>(splits, kMaxSplits);
   splits = std::min<uint64_t>(splits, columns / kGroup / 8);
   return static_cast<uint32_t>(std::max<uint64_t>(splits, 1));

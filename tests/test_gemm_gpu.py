@@ -204,6 +204,34 @@ def test_gemm_split_planes_sum_to_product(device, gx, orc, fmt, rows, cols, batc
         assert not np.array_equal(got[0], got[-1])
 
 
+@pytest.mark.parametrize("fmt,rows,cols", [(2, 640, 5120), (3, 512, 17408), (2, 48, 640), (3, 96, 1280)])
+def test_gemm_is_batch_invariant(device, gx, orc, fmt, rows, cols):
+    """Every kernel variant sums K in one canonical order, so token i of a batch of B
+    gets bit for bit what it gets alone (what makes a verify block equal one-token
+    steps), for the plain product and for split-K planes."""
+    p = _problem(orc, gx, fmt, 4, rows, cols, 32, seed=rows + cols + fmt)
+    acts, as16 = p["acts"], p["as16"]
+    dw, dws = dev(p["tiled"]), dev(p["tscales"])
+    splits = gx.gemm_split_count(rows, cols, 1)
+    for b in (2, 5, 32):
+        assert gx.gemm_split_count(rows, cols, b) == splits
+    ref = ref_planes = None
+    for batch in (32, 1, 2, 3, 4, 5, 7, 8, 9, 13, 16, 17, 24, 31):
+        da, das = dev(np.ascontiguousarray(acts[:batch])), dev(np.ascontiguousarray(as16[:batch]))
+        y = empty((batch, rows), np.float32)
+        say("gemm batch invariance", fmt, rows, cols, batch)
+        gx.launch_i4_gemm(fmt, dw, dws, da, das, y, rows, cols, batch)
+        planes = empty((splits, batch, rows), np.float32)
+        gx.launch_i4_gemm_split(fmt, dw, dws, da, das, planes, rows, cols, batch, splits)
+        if ref is None:
+            ref, ref_planes = host(y), host(planes)
+            want = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+            assert np.abs(ref - want).max() <= 2e-5 * float(np.abs(want).max())
+            continue
+        assert np.array_equal(host(y), ref[:batch]), batch
+        assert np.array_equal(host(planes), ref_planes[:, :batch]), batch
+
+
 def test_gemm_split_rejects_bad_counts(device, gx):
     z = empty((8,), np.uint8)
     L = gx.lib()

@@ -71,18 +71,26 @@ def test_synthetic_weights_match_cpu_generator(tiny, gx, orc, name):
     assert np.array_equal(tiny.tensor_bytes(name, auxiliary=True).view(np.uint16), tscales)
 
 
-def test_block_step_equals_serial(tiny):
-    tokens = [5, 17, 900, 3, 42]
+@pytest.mark.parametrize("count", [5, 9, 17, 32])
+def test_block_step_equals_serial(tiny, count):
+    """cli/main.cpp:880-887: a block of tokens gives the tokens and the state that
+    one-token steps give, bit for bit, at every block size."""
+    tokens = [int(t) for t in np.random.default_rng(count).integers(0, 1000, count)]
     serial = _session(tiny)
-    say("serial greedy steps")
+    say("serial greedy steps", count)
     outs = [serial.greedy_step(t) for t in tokens]
     block = _session(tiny)
-    say("block step")
+    say("block step", count)
     assert block.block_step(tokens) == outs
     assert block.position() == serial.position() == len(tokens)
-    a = serial.buffer("gdn_states", np.float32)
-    b = block.buffer("gdn_states", np.float32)
-    np.testing.assert_allclose(a, b, rtol=1e-3, atol=1e-4)
+    for name in ("gdn_states", "conv_states", "hidden"):
+        a, b = serial.buffer(name), block.buffer(name)
+        if name == "hidden":  # the last token's row
+            row = a.size // 32
+            a, b = a[:row], b[(count - 1) * row:count * row]
+        assert np.array_equal(a, b), name
+    for name in ("key_caches", "value_caches"):  # the written positions
+        assert np.array_equal(_kv_prefix(serial, name, count), _kv_prefix(block, name, count)), name
 
 
 def _kv_prefix(session, name, positions, ctx=256):
