@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_residual_add_rms_norm_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes": (I32, [P, P, U32, P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_dual_rms_norm_concat": (I32, [P, P, P, P, P, SZ, F32, I32, P]),
+    "gfxinfer_launch_dual_rms_norm_concat_batch": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_silu_multiply": (I32, [P, P, P, SZ, P]),
     "gfxinfer_launch_silu_multiply_quantize_i4": (I32, [P, P, P, P, SZ, U32, P]),
     "gfxinfer_launch_float_to_half": (I32, [P, P, SZ, P]),
@@ -128,6 +129,12 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_session_get_summary": (I32, [P, P]),
     "gfxinfer_session_copy_buffer": (I32, [P, ctypes.c_char_p, SZ, P, SZ]),
     "gfxinfer_session_buffer_bytes": (SZ, [P, ctypes.c_char_p]),
+    "gfxinfer_session_prefill": (I32, [P, P, SZ, I32, P]),
+    "gfxinfer_session_generate": (I32, [P, P, SZ, P, P, P, P]),
+    "gfxinfer_depth_policy_create": (I32, [U32, P]),
+    "gfxinfer_depth_policy_destroy": (None, [P]),
+    "gfxinfer_depth_policy_choose": (U32, [P, U32]),
+    "gfxinfer_depth_policy_record": (I32, [P, U32, U32, ctypes.c_double]),
 }
 
 

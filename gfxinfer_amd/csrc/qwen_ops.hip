@@ -203,10 +203,12 @@ __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
     const __half* __restrict__ right, const uint16_t* __restrict__ right_weight,
     __half* __restrict__ output, uint32_t elements, float epsilon, bool unit_offset) {
   __shared__ float scratch[16];
+  // Row blockIdx.y of [rows][elements] inputs -> row blockIdx.y of [rows][2 * elements].
+  const std::size_t row = blockIdx.y;
   const bool second = blockIdx.x != 0;
-  const __half* input = second ? right : left;
+  const __half* input = (second ? right : left) + row * elements;
   const uint16_t* weight = second ? right_weight : left_weight;
-  output += second ? elements : 0;
+  output += row * 2u * elements + (second ? elements : 0);
   float square = 0.0F;
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
     const float f = __half2float(input[i]);
@@ -1067,6 +1069,23 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
                      reinterpret_cast<__half*>(concatenated_output), static_cast<uint32_t>(elements),
                      epsilon, add_unit_offset != 0);
   return launch_status("dual RMSNorm/concat launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat_batch(
+    const uint16_t* left, const uint16_t* left_bf16_weight, const uint16_t* right,
+    const uint16_t* right_bf16_weight, uint16_t* concatenated_output, size_t elements, uint32_t batch,
+    float epsilon, int32_t add_unit_offset, void* stream) {
+  if (left == nullptr || left_bf16_weight == nullptr || right == nullptr ||
+      right_bf16_weight == nullptr || concatenated_output == nullptr || elements == 0 ||
+      elements > (1u << 30) || batch == 0 || batch > 65535 || !valid_epsilon(epsilon)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid batched dual RMSNorm/concat arguments");
+  }
+  hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const __half*>(left), left_bf16_weight,
+                     reinterpret_cast<const __half*>(right), right_bf16_weight,
+                     reinterpret_cast<__half*>(concatenated_output), static_cast<uint32_t>(elements),
+                     epsilon, add_unit_offset != 0);
+  return launch_status("batched dual RMSNorm/concat launch failed");
 }
 
 // ---- SwiGLU -----------------------------------------------------------------

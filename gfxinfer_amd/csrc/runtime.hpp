@@ -77,3 +77,21 @@ struct gfxinfer_model {
     return t->auxiliary_bytes == 0 ? nullptr : arena + t->auxiliary_offset;
   }
 };
+
+// Online MTP depth selection by emitted tokens per millisecond (the policy behind
+// gfxinfer_depth_policy_*; gfxinfer_session_generate uses it with adaptive_depth).
+struct gfxinfer_depth_policy {
+  struct Candidate {
+    uint32_t depth;
+    uint32_t rounds;
+    double tokens;  // exponential average of tokens emitted per round
+    double ms;      // exponential average of milliseconds per round
+  };
+  std::vector<Candidate> candidates;
+  uint64_t round{0};
+  uint32_t probe{0};  // next candidate to re-measure
+
+  explicit gfxinfer_depth_policy(uint32_t maximum_depth);
+  uint32_t choose(uint32_t limit);
+  bool record(uint32_t depth, uint32_t emitted, double milliseconds);
+};

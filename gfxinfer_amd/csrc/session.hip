@@ -11,7 +11,9 @@
 // result record instead of the drafts and target tokens.
 #include <algorithm>
 #include <array>
+#include <chrono>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -158,6 +160,7 @@ struct gfxinfer_session {
 
   uint16_t *hidden_a{}, *hidden_b{}, *post_attention{}, *mtp_hidden{}, *target_hidden_snapshot{};
   uint16_t *mtp_concat{}, *mtp_input{}, *convolved{}, *query{}, *key{}, *attention_output{};
+  uint16_t* mtp_conditioning{};  // [32][H] target hidden states of a batched MTP update
   uint8_t* act_codes{};
   uint16_t* act_scales{};
   float *projected_main{}, *projected_z{}, *projected_a{}, *projected_b{}, *projected_k{};
@@ -393,6 +396,136 @@ struct gfxinfer_session {
     if (output_token == nullptr) return ok();
     GFXI_TRY(mlp_tail(mtp, mtp_input, mtp_hidden, mtp_final_norm, 1));
     return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, output_token, draft_token_ids);
+  }
+
+  // The MTP K/V update of mtp_proposal(token, ..., nullptr) for `count` consecutive
+  // cache entries at once: entry position + i from tokens[i] and conditioning row i
+  // (mtp_conditioning).  Every kernel computes each row as the one-token path does.
+  int32_t mtp_sync(const uint32_t* tokens, unsigned count, std::size_t position) {
+    for (unsigned i = 0; i < count; ++i) GFXI_TRY(gather(hidden_b + i * H, tokens[i], nullptr));
+    GFXI_TRY(gfxinfer_launch_dual_rms_norm_concat_batch(hidden_b, mtp_pre_embedding_norm, mtp_conditioning,
+                                                        mtp_pre_hidden_norm, mtp_concat, H, count,
+                                                        spec.rms_norm_epsilon, 1, stream));
+    GFXI_TRY(gfxinfer_launch_quantize_activation_i4(mtp_concat, act_codes, act_scales, 2 * H, count,
+                                                    stream));
+    GFXI_TRY(gfxinfer_launch_gfx950_i4_gemm_half(mtp_fc.format, mtp_fc.weights, mtp_fc.scales,
+                                                 act_codes, act_scales, mtp_input, mtp_fc.rows,
+                                                 mtp_fc.columns, count, 0, stream));
+    GFXI_TRY(gfxinfer_launch_rms_norm_quantize_i4(mtp_input, mtp.input_norm, nullptr, act_codes,
+                                                  act_scales, H, count, spec.rms_norm_epsilon, 1,
+                                                  stream));
+    return attention_mixer(mtp, mtp_key_cache, mtp_value_cache, count, position, nullptr, true);
+  }
+
+  // Chunked prefill: the target over the prompt in blocks of up to kMaxBlock tokens
+  // and, with sync_mtp, the MTP cache over the same positions (entry j from token j + 1
+  // and the target hidden state of position j), the state the serial loop of
+  // cli/main.cpp:1055-1069 (greedy_step(p0); then mtp_draft(p_i) and greedy_step(p_i))
+  // leaves.
+  int32_t prefill(const uint32_t* tokens, std::size_t count, bool sync_mtp, uint32_t* next) {
+    if (tokens == nullptr || next == nullptr || count == 0 ||
+        count > config.maximum_context_tokens - current_position ||
+        (sync_mtp && current_position != 0 && mtp_position + 1 != current_position) ||
+        (sync_mtp && current_position == 0 && mtp_position != 0)) {
+      return fail(GFXI_INVALID_ARGUMENT,
+                  "prefill needs 1..context tokens and a fresh or MTP-aligned session");
+    }
+    uint32_t outputs[kMaxBlock];
+    for (std::size_t a = 0; a < count; a += kMaxBlock) {
+      const auto T = static_cast<unsigned>(std::min<std::size_t>(kMaxBlock, count - a));
+      const bool previous = current_position != 0;  // a hidden state for position a - 1
+      if (sync_mtp && previous) {
+        if (auto e = hipMemcpyAsync(mtp_conditioning, last_hidden, H * 2, hipMemcpyDeviceToDevice, stream);
+            e != hipSuccess) {
+          return hip_fail(e, "prefill conditioning copy failed");
+        }
+      }
+      GFXI_TRY(block(tokens + a, T, outputs));
+      *next = outputs[T - 1];
+      if (!sync_mtp) continue;
+      const unsigned entries = previous ? T : T - 1;
+      if (entries == 0) continue;
+      if (T > 1) {
+        if (auto e = hipMemcpyAsync(mtp_conditioning + (previous ? H : 0), hidden_a, (T - 1) * H * 2,
+                                    hipMemcpyDeviceToDevice, stream);
+            e != hipSuccess) {
+          return hip_fail(e, "prefill conditioning copy failed");
+        }
+      }
+      GFXI_TRY(mtp_sync(tokens + a + (previous ? 0 : 1), entries, mtp_position));
+      GFXI_TRY(sync("prefill MTP cache update failed"));
+      mtp_position += entries;
+    }
+    return ok();
+  }
+
+  // cli/main.cpp:1023-1120 generate, without the tokenizer.
+  int32_t generate(const uint32_t* prompt, std::size_t count, const gfxinfer_generate_config& cfg,
+                   uint32_t* output, std::size_t* output_count, gfxinfer_generate_stats* stats) {
+    if (prompt == nullptr || output == nullptr || output_count == nullptr || count == 0 ||
+        cfg.maximum_tokens == 0 || cfg.draft_count >= kMaxBlock ||
+        (cfg.stop_count != 0 && cfg.stop_tokens == nullptr) ||
+        count + cfg.maximum_tokens > config.maximum_context_tokens - current_position) {
+      return fail(GFXI_INVALID_ARGUMENT,
+                  "generate needs a prompt, 1+ output tokens, 0..31 drafts and prompt + output "
+                  "within the session context");
+    }
+    using clock = std::chrono::steady_clock;
+    const auto elapsed_ms = [](clock::time_point a, clock::time_point b) {
+      return std::chrono::duration<double, std::milli>(b - a).count();
+    };
+    const auto stop = [&](uint32_t token) {
+      for (uint32_t i = 0; i < cfg.stop_count; ++i) {
+        if (cfg.stop_tokens[i] == token) return true;
+      }
+      return false;
+    };
+    gfxinfer_generate_stats st{};
+    st.prompt_tokens = count;
+    const auto start = clock::now();
+    uint32_t next = 0;
+    GFXI_TRY(prefill(prompt, count, cfg.draft_count != 0, &next));
+    const auto first = clock::now();
+    std::size_t produced = 0;
+    output[produced++] = next;
+    std::unique_ptr<gfxinfer_depth_policy> policy;
+    if (cfg.adaptive_depth != 0 && cfg.draft_count != 0) {
+      policy = std::make_unique<gfxinfer_depth_policy>(cfg.draft_count);
+    }
+    while (produced < cfg.maximum_tokens && !stop(next)) {
+      if (cfg.draft_count == 0 || cfg.maximum_tokens - produced == 1) {
+        GFXI_TRY(block(&next, 1, &next));  // greedy_step
+        output[produced++] = next;
+        continue;
+      }
+      const auto room = static_cast<uint32_t>(
+          std::min<std::size_t>(cfg.draft_count, cfg.maximum_tokens - produced - 1));
+      const uint32_t depth = policy ? policy->choose(room) : room;
+      gfxinfer_speculative_result r{};
+      const auto round_start = clock::now();
+      GFXI_TRY(speculative(next, depth, -1, nullptr, &r));
+      if (policy) policy->record(depth, r.token_count, elapsed_ms(round_start, clock::now()));
+      st.proposed_drafts += r.proposed_drafts;
+      st.accepted_drafts += r.accepted_drafts;
+      ++st.speculative_rounds;
+      bool terminal = false;
+      for (uint32_t i = 0; i < r.token_count && produced < cfg.maximum_tokens; ++i) {
+        output[produced++] = r.tokens[i];
+        ++st.speculative_emitted;
+        next = r.tokens[i];
+        if (stop(next)) {
+          terminal = true;
+          break;
+        }
+      }
+      if (terminal) break;
+    }
+    st.output_tokens = produced;
+    st.prefill_ms = elapsed_ms(start, first);
+    st.decode_ms = elapsed_ms(first, clock::now());
+    *output_count = produced;
+    if (stats != nullptr) *stats = st;
+    return ok();
   }
 
   // The D proposals then the verifier with rollback logging (qwen_runtime.cpp:1448-1467,
@@ -733,8 +866,9 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
       {"post_attention", reinterpret_cast<void**>(&s->post_attention), B * s->H * 2},
       {"mtp_hidden", reinterpret_cast<void**>(&s->mtp_hidden), s->H * 2},
       {"target_hidden_snapshot", reinterpret_cast<void**>(&s->target_hidden_snapshot), s->H * 2},
-      {"mtp_concat", reinterpret_cast<void**>(&s->mtp_concat), 2 * s->H * 2},
-      {"mtp_input", reinterpret_cast<void**>(&s->mtp_input), s->H * 2},
+      {"mtp_concat", reinterpret_cast<void**>(&s->mtp_concat), B * 2 * s->H * 2},
+      {"mtp_input", reinterpret_cast<void**>(&s->mtp_input), B * s->H * 2},
+      {"mtp_conditioning", reinterpret_cast<void**>(&s->mtp_conditioning), B * s->H * 2},
       {"convolved", reinterpret_cast<void**>(&s->convolved), B * s->channels * 2},
       {"query", reinterpret_cast<void**>(&s->query), B * s->attn_width * 2},
       {"key", reinterpret_cast<void**>(&s->key), B * s->kv_rows * 2},
@@ -843,6 +977,21 @@ extern "C" int32_t gfxinfer_session_block_step(gfxinfer_session* session,
                                                uint32_t* output_tokens) {
   GFXI_TRY(enter(session));
   return session->block(input_tokens, count, output_tokens);
+}
+
+extern "C" int32_t gfxinfer_session_prefill(gfxinfer_session* session, const uint32_t* tokens,
+                                            size_t count, int32_t sync_mtp, uint32_t* next_token) {
+  GFXI_TRY(enter(session));
+  return session->prefill(tokens, count, sync_mtp != 0, next_token);
+}
+
+extern "C" int32_t gfxinfer_session_generate(gfxinfer_session* session, const uint32_t* prompt,
+                                             size_t prompt_count, const gfxinfer_generate_config* config,
+                                             uint32_t* output, size_t* output_count,
+                                             gfxinfer_generate_stats* stats) {
+  GFXI_TRY(enter(session));
+  if (config == nullptr) return fail(GFXI_INVALID_ARGUMENT, "generate needs a configuration");
+  return session->generate(prompt, prompt_count, *config, output, output_count, stats);
 }
 
 extern "C" int32_t gfxinfer_session_greedy_step(gfxinfer_session* session, uint32_t input_token,

@@ -10,7 +10,9 @@ libgfxinfer_amd.so; this module only marshals arguments.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -18,6 +20,22 @@ import numpy as np
 from . import GfxinferError, check, lib
 
 U32 = ctypes.c_uint32
+
+# Handles still open at interpreter exit are closed by atexit (sessions before the
+# models they use), while the HIP runtime is intact: a destructor run during the
+# interpreter's final teardown would call into an already-finalized runtime.
+_LIVE_SESSIONS: "weakref.WeakSet" = weakref.WeakSet()
+_LIVE_OTHERS: "weakref.WeakSet" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_handles() -> None:
+    for group in (_LIVE_SESSIONS, _LIVE_OTHERS):
+        for obj in list(group):
+            try:
+                obj.close()
+            except Exception:
+                pass
 
 
 class ModelSpec(ctypes.Structure):
@@ -82,6 +100,49 @@ class SpeculativeStepResult:
     tokens: list[int]
     proposed_drafts: int
     accepted_drafts: int
+
+
+class GenerateConfig(ctypes.Structure):
+    _fields_ = [("maximum_tokens", ctypes.c_uint32), ("draft_count", ctypes.c_uint32),
+                ("adaptive_depth", ctypes.c_int32), ("stop_tokens", ctypes.c_void_p),
+                ("stop_count", ctypes.c_uint32)]
+
+
+class GenerateStats(ctypes.Structure):
+    _fields_ = [("prompt_tokens", ctypes.c_size_t), ("output_tokens", ctypes.c_size_t),
+                ("speculative_rounds", ctypes.c_size_t), ("proposed_drafts", ctypes.c_size_t),
+                ("accepted_drafts", ctypes.c_size_t), ("speculative_emitted", ctypes.c_size_t),
+                ("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class DepthPolicy:
+    """Online MTP depth selection (gfxinfer_depth_policy_*)."""
+
+    def __init__(self, maximum_depth: int):
+        handle = ctypes.c_void_p()
+        check(lib().gfxinfer_depth_policy_create(maximum_depth, ctypes.byref(handle)))
+        self._handle = handle
+        _LIVE_OTHERS.add(self)
+
+    def choose(self, limit: int) -> int:
+        return int(lib().gfxinfer_depth_policy_choose(self._handle, limit))
+
+    def record(self, depth: int, emitted: int, milliseconds: float) -> None:
+        check(lib().gfxinfer_depth_policy_record(self._handle, depth, emitted, milliseconds))
+
+    def close(self):
+        if self._handle is not None:
+            lib().gfxinfer_depth_policy_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class ArtifactIdentity(ctypes.Structure):
@@ -177,6 +238,7 @@ class SyntheticModel:
         handle = ctypes.c_void_p()
         check(lib().gfxinfer_model_create_synthetic(ctypes.byref(spec), seed, device, ctypes.byref(handle)))
         self._handle = handle
+        _LIVE_OTHERS.add(self)
 
     @classmethod
     def from_artifact(cls, spec: ModelSpec, path: str, verify_checksums: bool = True, device: int = 0):
@@ -187,6 +249,7 @@ class SyntheticModel:
         check(lib().gfxinfer_model_create_from_artifact(ctypes.byref(spec), str(path).encode(),
                                                         int(verify_checksums), device, ctypes.byref(handle)))
         self._handle = handle
+        _LIVE_OTHERS.add(self)
         return self
 
     def write_artifact(self, path: str, weights_id: str, draft_rows=None):
@@ -244,6 +307,7 @@ class QwenDecodeSession:
         handle = ctypes.c_void_p()
         check(lib().gfxinfer_session_create(model.handle, ctypes.byref(config), ctypes.byref(handle)))
         self._handle = handle
+        _LIVE_SESSIONS.add(self)
 
     def close(self):
         if self._handle is not None:
@@ -294,6 +358,28 @@ class QwenDecodeSession:
         check(lib().gfxinfer_session_speculative_step_planted(self._handle, seed, len(arr), arr.ctypes.data,
                                                               ctypes.byref(r)))
         return self._result(r)
+
+    def prefill(self, tokens, sync_mtp: bool = True) -> int:
+        """Chunked prefill; returns the greedy token after the last prompt token."""
+        arr = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = U32()
+        check(lib().gfxinfer_session_prefill(self._handle, arr.ctypes.data, len(arr), int(sync_mtp),
+                                             ctypes.byref(out)))
+        return out.value
+
+    def generate(self, prompt, maximum_tokens: int, draft_count: int = 0, adaptive_depth: bool = False,
+                 stop_tokens=()):
+        """The reference CLI generate loop; returns (tokens, stats dict)."""
+        arr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        stops = np.ascontiguousarray(stop_tokens, dtype=np.uint32)
+        cfg = GenerateConfig(maximum_tokens, draft_count, int(adaptive_depth),
+                             stops.ctypes.data if len(stops) else None, len(stops))
+        out = np.zeros(maximum_tokens, np.uint32)
+        count = ctypes.c_size_t()
+        stats = GenerateStats()
+        check(lib().gfxinfer_session_generate(self._handle, arr.ctypes.data, len(arr), ctypes.byref(cfg),
+                                              out.ctypes.data, ctypes.byref(count), ctypes.byref(stats)))
+        return [int(x) for x in out[:count.value]], stats.as_dict()
 
     def position(self) -> int:
         return int(lib().gfxinfer_session_position(self._handle))

@@ -259,6 +259,17 @@ int32_t gfxinfer_launch_dual_rms_norm_concat(const uint16_t* left, const uint16_
                                              uint16_t* concatenated_output, size_t elements,
                                              float epsilon, int32_t add_unit_offset, void* stream);
 
+/* No reference counterpart: launch_dual_rms_norm_concat over `batch` rows ([batch][elements]
+ * inputs, [batch][2 * elements] output), for the batched MTP cache update of a chunked
+ * prefill; each row is computed exactly as the single-row launcher computes it. */
+int32_t gfxinfer_launch_dual_rms_norm_concat_batch(const uint16_t* left,
+                                                   const uint16_t* left_bf16_weight,
+                                                   const uint16_t* right,
+                                                   const uint16_t* right_bf16_weight,
+                                                   uint16_t* concatenated_output, size_t elements,
+                                                   uint32_t batch, float epsilon,
+                                                   int32_t add_unit_offset, void* stream);
+
 /* qwen_ops.h:44-49 launch_silu_multiply: fp16(silu(g) * u); elements % 128 == 0. */
 int32_t gfxinfer_launch_silu_multiply(const float* gate, const float* up, uint16_t* output,
                                       size_t elements, void* stream);

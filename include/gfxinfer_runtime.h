@@ -242,6 +242,63 @@ int32_t gfxinfer_session_copy_buffer(const gfxinfer_session* session, const char
 /* Byte size of a named session buffer (0 if unknown). */
 size_t gfxinfer_session_buffer_bytes(const gfxinfer_session* session, const char* name);
 
+/* Chunked prefill.  The reference prefills a prompt with one greedy_step per token and,
+ * when MTP is on, an mtp_draft per token from the second on (cli/main.cpp:1055-1069);
+ * this runs the target over the prompt in blocks of up to 32 tokens and, with
+ * sync_mtp != 0, advances the MTP K/V cache over the same positions in batches (entry j
+ * from token j + 1 and the target's hidden state at position j), leaving the target,
+ * GDN, KV and MTP cache state and the positions as that serial loop leaves them.
+ * *next_token = the greedy token after the last prompt token.  Requires a fresh
+ * session or, with sync_mtp, an aligned one (mtp_position + 1 == position).  No
+ * reference counterpart (the reference roadmap's "fast prefill", README.md:211-218). */
+int32_t gfxinfer_session_prefill(gfxinfer_session* session, const uint32_t* tokens, size_t count,
+                                 int32_t sync_mtp, uint32_t* next_token);
+
+/* Online MTP depth selection ("Online MTP depth selection based on accepted tokens
+ * per millisecond", docs/ROADMAP.md:51; not implemented by the reference).  The
+ * policy keeps, per candidate depth {1, 2, 3, 4, 6, 8, 12, 16, 24, 31} up to
+ * maximum_depth, exponential averages (weight 1/4) of tokens emitted per round and of
+ * milliseconds per round; choose() returns the first untried candidate within
+ * `limit`, else the one with the most tokens per millisecond, except that every 16th
+ * round it re-measures one of the other candidates within `limit`, in turn.  Host
+ * only, deterministic. */
+typedef struct gfxinfer_depth_policy gfxinfer_depth_policy;
+int32_t gfxinfer_depth_policy_create(uint32_t maximum_depth, gfxinfer_depth_policy** out);
+void gfxinfer_depth_policy_destroy(gfxinfer_depth_policy* policy);
+uint32_t gfxinfer_depth_policy_choose(gfxinfer_depth_policy* policy, uint32_t limit);
+int32_t gfxinfer_depth_policy_record(gfxinfer_depth_policy* policy, uint32_t depth,
+                                     uint32_t emitted_tokens, double milliseconds);
+
+/* The generate loop of the reference CLI (cli/main.cpp:1023-1120) without the
+ * tokenizer: prefill the prompt, then greedy steps (draft_count == 0) or speculative
+ * rounds of depth min(draft_count, tokens still wanted - 1) (or the depth policy's
+ * choice, adaptive_depth != 0) until maximum_tokens tokens are out or a stop token
+ * was emitted.  The first output token is the prefill's greedy token. */
+typedef struct gfxinfer_generate_config {
+  uint32_t maximum_tokens;       /* >= 1; prompt + maximum_tokens <= the session context */
+  uint32_t draft_count;          /* 0..31 */
+  int32_t adaptive_depth;        /* non-zero: online depth selection up to draft_count */
+  const uint32_t* stop_tokens;   /* end-of-turn ids (the reference's 248044, 248046) */
+  uint32_t stop_count;
+} gfxinfer_generate_config;
+
+typedef struct gfxinfer_generate_stats {
+  size_t prompt_tokens;
+  size_t output_tokens;
+  size_t speculative_rounds;
+  size_t proposed_drafts;
+  size_t accepted_drafts;
+  size_t speculative_emitted;
+  double prefill_ms;             /* time to first token */
+  double decode_ms;              /* after the first token */
+} gfxinfer_generate_stats;
+
+/* output: capacity config->maximum_tokens; *output_count = tokens written. */
+int32_t gfxinfer_session_generate(gfxinfer_session* session, const uint32_t* prompt,
+                                  size_t prompt_count, const gfxinfer_generate_config* config,
+                                  uint32_t* output, size_t* output_count,
+                                  gfxinfer_generate_stats* stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -170,6 +170,32 @@ def test_dual_rms_norm_concat(device, gx, orc):
     assert _close16(host(out, np.uint16), want)
 
 
+@pytest.mark.parametrize("batch", [1, 7, 32])
+def test_dual_rms_norm_concat_batch_rows_equal_single(device, gx, orc, batch):
+    """Each row of the batched launcher is bit-identical to the single-row launcher on
+    that row (the batched MTP cache update of a chunked prefill relies on it)."""
+    n = 5120
+    rng = np.random.default_rng(30 + batch)
+    left, right = _half(rng.standard_normal((batch, n))), _half(rng.standard_normal((batch, n)) * 3)
+    lw, rw = _bf16(rng.standard_normal(n) * 0.05), _bf16(rng.standard_normal(n) * 0.05)
+    dl, dr, dlw, drw = D_(left), D_(right), D_(lw), D_(rw)
+    out = empty((batch, 2 * n), np.uint16)
+    say("dual_rms_norm_concat_batch", batch)
+    gx.check(gx.lib().gfxinfer_launch_dual_rms_norm_concat_batch(dl, dlw, dr, drw, out.data_ptr(), n, batch,
+                                                                 EPS, 1, None))
+    got = host(out, np.uint16)
+    one = empty((2 * n,), np.uint16)
+    for r in (0, batch // 2, batch - 1):
+        gx.check(gx.lib().gfxinfer_launch_dual_rms_norm_concat(
+            dl + r * n * 2, dlw, dr + r * n * 2, drw, one.data_ptr(), n, EPS, 1, None))
+        assert np.array_equal(got[r], host(one, np.uint16))
+        want = np.empty(2 * n, np.uint16)
+        orc.lib().orc_dual_rms_norm_concat(orc.ptr(np.ascontiguousarray(left[r])), orc.ptr(lw),
+                                           orc.ptr(np.ascontiguousarray(right[r])), orc.ptr(rw),
+                                           orc.ptr(want), n, EPS, 1)
+        assert _close16(got[r], want)
+
+
 @pytest.mark.parametrize("batch", [1, 5, 32])
 def test_silu_multiply_quantize(device, gx, orc, batch):
     n = 17408
