@@ -211,26 +211,25 @@ struct GemmArgs {
 // same way, so an output depends only on (row, token, K, splits): not on the batch,
 // the kernel family or the launch shape, and a block of tokens gives each token
 // exactly what a one-token step gives it (as the reference's sequential epilogue does).
-//   * K's groups form quads of 4 consecutive groups; split s of S owns quads
-//     [Q s / S, Q (s + 1) / S) of the Q quads;
-//   * a split is cut into range_count(its groups) ranges of whole quads (range r of
-//     R: quads [Qs r / R, Qs (r + 1) / R) of the split's Qs quads);
-//   * in a range, stream j = group mod 4 accumulates fmaf(float(partial), ws * as,
-//     acc_j) over its groups in increasing order, and the range sums to
-//     (acc_0 + acc_1) + (acc_2 + acc_3);
+//   * split s of S owns groups [G s / S, G (s + 1) / S) of the G groups;
+//   * a split of n groups [b, b + n) is cut into R = range_count(n) ranges, range r
+//     holding groups [b + n r / R, b + n (r + 1) / R);
+//   * a range's value is v = fmaf(float(partial_g), ws_g * as_g, v) over its groups g
+//     in increasing order, from v = 0 (partial_g: the group's exact int32 MFMA sum;
+//     ws_g, as_g: the row's fp16 weight scale and the token's activation scale times
+//     1/F, as fp32);
 //   * a split's output is ((range_0 + range_1) + range_2) + ... in range order.
-// A kernel may give a wave several consecutive ranges; a chunk of loads always holds
-// whole quads, so each pack's stream is known at compile time.
+// A kernel may give a wave several consecutive ranges.  Load chunks start at the
+// range's first group and hold CH packs of GP groups; the MFMA pair of a pack leaves
+// group pg + w in the lanes of token window w, and add_pack folds the pack's groups
+// into the value held by the window-0 lanes in group order.  Groups past the range's
+// end are skipped.
 struct GroupRange {
   unsigned begin, end;  // groups [begin, end)
 };
 
-__host__ __device__ inline unsigned quad_count(unsigned groups) { return (groups + 3u) / 4u; }
-
 __host__ __device__ inline GroupRange split_groups(unsigned groups, unsigned split, unsigned splits) {
-  const unsigned q = quad_count(groups);
-  const unsigned b = 4u * (q * split / splits), e = 4u * (q * (split + 1u) / splits);
-  return {b < groups ? b : groups, e < groups ? e : groups};
+  return {groups * split / splits, groups * (split + 1u) / splits};
 }
 
 __host__ __device__ inline unsigned range_count(unsigned groups_in_split) {
@@ -240,10 +239,23 @@ __host__ __device__ inline unsigned range_count(unsigned groups_in_split) {
 
 __host__ __device__ inline GroupRange canonical_range(unsigned groups, unsigned split, unsigned splits,
                                                       unsigned range, unsigned ranges) {
-  const unsigned q = quad_count(groups);
-  const unsigned qs = q * split / splits, qn = q * (split + 1u) / splits - qs;
-  const unsigned b = 4u * (qs + qn * range / ranges), e = 4u * (qs + qn * (range + 1u) / ranges);
-  return {b < groups ? b : groups, e < groups ? e : groups};
+  const GroupRange own = split_groups(groups, split, splits);
+  const unsigned n = own.end - own.begin;
+  return {own.begin + n * range / ranges, own.begin + n * (range + 1u) / ranges};
+}
+
+// v <- the pack's groups added to v in order: the lane's own group (window 0) and
+// then windows 1 .. GP - 1 of the same token slot, moved in from lanes + w * TPAD of
+// the 16-lane row (DPP row_shl; lanes of other windows compute values never used).
+template <unsigned GP, unsigned TPAD>
+__device__ __forceinline__ float add_pack(float v, float c, float p) {
+  v = fmaf(c, p, v);
+  if constexpr (GP >= 2) v = fmaf(dpp_move<0x100 + TPAD>(c), dpp_move<0x100 + TPAD>(p), v);
+  if constexpr (GP == 4) {
+    v = fmaf(dpp_move<0x100 + 2 * TPAD>(c), dpp_move<0x100 + 2 * TPAD>(p), v);
+    v = fmaf(dpp_move<0x100 + 3 * TPAD>(c), dpp_move<0x100 + 3 * TPAD>(p), v);
+  }
+  return v;
 }
 
 // Fewest ranges of any split of a launch: a workgroup has at most that many waves.
@@ -326,8 +338,6 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
   constexpr bool kDma = ABits == 4;  // A4 pieces go straight from memory to LDS
-  constexpr unsigned NS = 4 / GP;    // accumulator sets per lane: streams (group mod 4) / GP
-  static_assert(CH * GP % 4 == 0 || GP == 4, "a chunk holds whole quads of groups");
 
   extern __shared__ __align__(16) uint8_t lds_all[];
 
@@ -385,8 +395,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   }
   if (lane < 4) reinterpret_cast<uint32_t*>(lds + layout.zero_offset)[lane] = 0u;
 
-  float acc[NS][NTB][4];  // stream sets of the current range
-  float total[NTB][4];    // the range value (one range) or the split's sum
+  float acc[NTB * 4];    // value of the current range: [token block * 4 + row]
+  float total[NTB][4];   // the range value (one range) or the split's sum
 
   constexpr unsigned kPieces = AGB / 16;  // 16-byte source pieces per token per group
   constexpr unsigned kRowPieces = CHG * kPieces;
@@ -397,16 +407,9 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   const auto act_scales = buffer(args.activation_scales, batch * groups * 2u);
   for (unsigned range = range_begin; range < range_end; ++range) {
   const GroupRange span = canonical_range(groups, split, args.splits, range, ranges);
-  const unsigned pack_begin = span.begin / GP;
-  const unsigned pack_end = (span.end + GP - 1u) / GP;
 #pragma unroll
-  for (unsigned q = 0; q < NS; ++q)
-#pragma unroll
-    for (int t = 0; t < NTB; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[q][t][r] = 0.0F;
-  for (unsigned base = pack_begin; base < pack_end; base += CH) {
-    const unsigned g0 = base * GP;
+  for (unsigned m = 0; m < NTB * 4; ++m) acc[m] = 0.0F;
+  for (unsigned g0 = span.begin; g0 < span.end; g0 += CHG) {
     // 1) Activation pieces of this chunk (L2-resident), loaded first.  Piece i
     //    is token i / kRowPieces, bytes (i % kRowPieces) * 16 of the chunk.
     const unsigned total_pieces = batch * kRowPieces;
@@ -466,10 +469,10 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     unsigned wreg[CH][GP][WD];
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
-      const unsigned pack = min(base + ci, pack_end - 1u);
 #pragma unroll
       for (unsigned j = 0; j < GP; ++j) {
-        const unsigned g_offset = (pack * GP + j) * 64u * LB;  // past the end -> zeros
+        // groups past the range's end load its last group again (never used)
+        const unsigned g_offset = min(g0 + ci * GP + j, span.end - 1u) * 64u * LB;
         if constexpr (Format == GFXI_W3G128) {
           const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
           wreg[ci][j][0] = w[0];
@@ -528,15 +531,14 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
     // 4) Compute.
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
-      const unsigned pack = base + ci;
-      if (pack >= pack_end) break;
+      const unsigned pg = g0 + ci * GP;  // the pack's first group
+      if (pg >= span.end) break;
       i32x4 c[NTB];
 #pragma unroll
       for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
 #pragma unroll
       for (unsigned j = 0; j < GP; ++j) {
-        const unsigned g = pack * GP + j;
-        if (g >= groups) break;  // wave-uniform: partial last pack
+        if (pg + j >= span.end) break;  // wave-uniform: partial last pack of the range
         i32x4 a0, a1;
         if constexpr (Format == GFXI_W3G128) {
           expand_w3(wreg[ci][j][0], wreg[ci][j][1], wreg[ci][j][2], a0, a1);
@@ -563,61 +565,46 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
         }
       }
       // Epilogue: lane holds rows 4*kb + r of column n = (token slot, group g_c).
-      const unsigned g_c = pack * GP + window;
+      const unsigned g_c = pg + window;
       if constexpr (Partials) {
 #pragma unroll
         for (int t = 0; t < NTB; ++t) {
           const unsigned token = t * 16u + slot;
-          if (g_c < groups && token < batch) {
+          if (g_c < span.end && token < batch) {
             const std::size_t row0 = static_cast<std::size_t>(token) * rows + tile * 16u + 4u * kb;
 #pragma unroll
             for (int r = 0; r < 4; ++r) args.partials[(row0 + r) * groups + g_c] = c[t][r] >> kShift;
           }
         }
       } else {
-        // Columns of dead tokens or of a missing last group hold exact zeros.
+        // Columns of dead tokens or of a group past the range hold exact zeros.
         const u32x2 pw = *reinterpret_cast<const u32x2*>(
-            lds + layout.wscale_offset + (min(g_c, groups - 1u) - g0) * 32u + 8u * kb);
+            lds + layout.wscale_offset + (min(g_c, span.end - 1u) - g0) * 32u + 8u * kb);
         float ws[4];
         ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] & 0xffffu)));
         ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] >> 16)));
         ws[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] & 0xffffu)));
         ws[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[1] >> 16)));
         const float* scales = reinterpret_cast<const float*>(lds + layout.scale_offset);
-        const unsigned gl = min(g_c, groups - 1u) - g0;
+        const unsigned gl = min(g_c, span.end - 1u) - g0;
 #pragma unroll
         for (int t = 0; t < NTB; ++t) {
           const unsigned token = min(t * 16u + slot, batch - 1u);
           const float as = scales[token * CHG + gl];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            // stream of group g_c (chunks start on quads): set ((ci * GP) mod 4) / GP
-            float& a = acc[((ci * GP) & 3u) / GP][t][r];
-            a = fmaf(static_cast<float>(c[t][r]), ws[r] * as, a);
+            acc[t * 4 + r] = add_pack<GP, TPAD>(acc[t * 4 + r], static_cast<float>(c[t][r]), ws[r] * as);
           }
         }
       }
     }
   }
   if constexpr (!Partials) {
-    // The range value (acc_0 + acc_1) + (acc_2 + acc_3).  Stream j lives in set j / GP
-    // of the lanes of window j % GP: GP = 4 adds windows (0 + 1) and (2 + 3), then the
-    // two sums; GP = 2 adds windows 0 + 1 in each set, then the sets; GP = 1 adds sets.
+    // The range value, valid in the lanes of window 0 (the only ones stored).
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (GP == 4) {
-          float v = acc[0][t][r] + __shfl_xor(acc[0][t][r], 4);
-          total[t][r] = v + __shfl_xor(v, 8);
-        } else if constexpr (GP == 2) {
-          const float v01 = acc[0][t][r] + __shfl_xor(acc[0][t][r], 8);
-          const float v23 = acc[1][t][r] + __shfl_xor(acc[1][t][r], 8);
-          total[t][r] = v01 + v23;
-        } else {
-          total[t][r] = (acc[0][t][r] + acc[1][t][r]) + (acc[2][t][r] + acc[3][t][r]);
-        }
-      }
+      for (int r = 0; r < 4; ++r) total[t][r] = acc[t * 4 + r];
     }
     if (ranges > 1) {
       float* slot_out = reinterpret_cast<float*>(lds_all + layout.results_offset) + range * NTB * 4u * 64u;
@@ -729,8 +716,6 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
       1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
   constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
   constexpr unsigned kOut = 0x80000000u;              // voffset that reads zeros
-  constexpr unsigned NS = 4 / GP;  // accumulator sets per lane: streams (group mod 4) / GP
-  static_assert(CH * GP % 4 == 0 || GP == 4, "a chunk holds whole quads of groups");
 
   extern __shared__ __align__(16) uint8_t lds_all[];
   const unsigned lane = threadIdx.x & 63u;
@@ -791,22 +776,14 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
   const unsigned range_begin = ranges * wave / waves;
   const unsigned range_end = ranges * (wave + 1u) / waves;
 
-  float acc[NS][R][NTB][4];  // stream sets of the current range
-  float total[R][NTB][4];    // the range value (one range) or the split's sum
+  float acc[R * NTB * 4];   // value of the current range: [(tile, token block) * 4 + row]
+  float total[R][NTB][4];   // the range value (one range) or the split's sum
   for (unsigned range = range_begin; range < range_end; ++range) {
   const GroupRange span = canonical_range(groups, split, args.splits, range, ranges);
-  const unsigned pack_begin = span.begin / GP;
-  const unsigned pack_end = (span.end + GP - 1u) / GP;
 #pragma unroll
-  for (unsigned q = 0; q < NS; ++q)
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < NTB; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[q][r][t][i] = 0.0F;
+  for (unsigned m = 0; m < R * NTB * 4; ++m) acc[m] = 0.0F;
 
-  for (unsigned base = pack_begin; base < pack_end; base += CH) {
+  for (unsigned g0 = span.begin; g0 < span.end; g0 += CHG) {
     // 1) Loads of CH packs: activations + their scales (L2), weights + scales (HBM).
     unsigned areg[CH][NTB][AD];
     unsigned short asreg[CH][NTB];
@@ -823,7 +800,7 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     if constexpr (GP == 1 && !Partials) {
 #pragma unroll
       for (int t = 0; t < NTB; ++t) {
-        const unsigned first = (t * 16u + slot) * groups + base;  // half index
+        const unsigned first = (t * 16u + slot) * groups + g0;  // half index
         as_odd[t] = first & 1u;
         const unsigned off = t * 16u + slot < batch ? (first & ~1u) * 2u : kOut;
         if constexpr (kScaleDwords == 2) {
@@ -848,19 +825,20 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     // complete in issue order, so routing the activations waits for them alone.
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
-      const unsigned pack = min(base + ci, pack_end - 1u);
-      const bool live = pack * GP + window < groups;
+      // a pack past the range's end loads its last group again (never used)
+      const unsigned pg = min(g0 + ci * GP, span.end - 1u);
+      const bool live = pg + window < span.end;
 #pragma unroll
       for (int t = 0; t < NTB; ++t) {
         const unsigned off = live ? a_voffset[t] : kOut;
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(activations, off, pack * GP * AGB, 0);
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(activations, off, pg * AGB, 0);
         areg[ci][t][0] = x[0];
         areg[ci][t][1] = x[1];
         areg[ci][t][2] = x[2];
         areg[ci][t][3] = x[3];
         if constexpr (ABits == 8) {
           const u32x4 y =
-              __builtin_amdgcn_raw_buffer_load_b128(activations, off + 16u, pack * GP * AGB, 0);
+              __builtin_amdgcn_raw_buffer_load_b128(activations, off + 16u, pg * AGB, 0);
           areg[ci][t][4] = y[0];
           areg[ci][t][5] = y[1];
           areg[ci][t][6] = y[2];
@@ -868,19 +846,19 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
         }
         if constexpr (!Partials && GP > 1) {
           asreg[ci][t] = __builtin_amdgcn_raw_buffer_load_b16(act_scales, live ? as_voffset[t] : kOut,
-                                                              pack * GP * 2u, 0);
+                                                              pg * 2u, 0);
         }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
-      const unsigned pack = min(base + ci, pack_end - 1u);
+      const unsigned pg = min(g0 + ci * GP, span.end - 1u);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
 #pragma unroll
         for (unsigned j = 0; j < GP; ++j) {
-          const unsigned g_offset = r * tile_bytes + (pack * GP + j) * 64u * LB;
+          const unsigned g_offset = r * tile_bytes + min(pg + j, span.end - 1u) * 64u * LB;
           if constexpr (Format == GFXI_W3G128) {
             const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
             wreg[r][ci * GP + j][0] = w[0];
@@ -896,7 +874,7 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
         }
         if constexpr (!Partials) {
           wsreg[r][ci] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, ws_voffset,
-                                                              r * groups * 32u + pack * GP * 32u, 0);
+                                                              r * groups * 32u + pg * 32u, 0);
         }
       }
     }
@@ -923,7 +901,7 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
         }
 #pragma unroll
         for (unsigned ci = 0; ci < CH; ++ci) {
-          // group base + ci sits at half ci of the shifted row (or is past pack_end)
+          // group g0 + ci sits at half ci of the shifted row (or is past the range)
           asreg[ci][t] = static_cast<unsigned short>(row[ci / 2] >> ((ci & 1u) * 16u));
         }
       }
@@ -931,8 +909,8 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     // 2) Compute.
 #pragma unroll
     for (unsigned ci = 0; ci < CH; ++ci) {
-      const unsigned pack = base + ci;
-      if (pack >= pack_end) break;
+      const unsigned pg = g0 + ci * GP;  // the pack's first group
+      if (pg >= span.end) break;
       // B operands of every group of the pack: this lane's activations where its
       // window is the group's, zeros elsewhere.
       i32x4 b[GP][NTB][2];
@@ -966,7 +944,7 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
         for (int t = 0; t < NTB; ++t) c[t] = i32x4{0, 0, 0, 0};
 #pragma unroll
         for (unsigned j = 0; j < GP; ++j) {
-          if (pack * GP + j >= groups) break;  // wave-uniform: partial last pack
+          if (pg + j >= span.end) break;  // wave-uniform: partial last pack of the range
           i32x4 a0, a1;
           const unsigned* w = wreg[r][ci * GP + j];
           if constexpr (Format == GFXI_W3G128) {
@@ -981,12 +959,12 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
             c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b[j][t][1], c[t], 0, 0, 0);
           }
         }
-        const unsigned g_c = pack * GP + window;
+        const unsigned g_c = pg + window;
         if constexpr (Partials) {
 #pragma unroll
           for (int t = 0; t < NTB; ++t) {
             const unsigned token = t * 16u + slot;
-            if (g_c < groups && token < batch) {
+            if (g_c < span.end && token < batch) {
               const std::size_t row0 =
                   static_cast<std::size_t>(token) * rows + (tile0 + r) * 16u + 4u * kb;
 #pragma unroll
@@ -1005,9 +983,8 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
           for (int t = 0; t < NTB; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              // stream of group g_c (chunks start on quads): set ((ci * GP) mod 4) / GP
-              float& a = acc[((ci * GP) & 3u) / GP][r][t][i];
-              a = fmaf(static_cast<float>(c[t][i]), ws[i] * as[t], a);
+              float& a = acc[(r * NTB + t) * 4 + i];
+              a = add_pack<GP, TPAD>(a, static_cast<float>(c[t][i]), ws[i] * as[t]);
             }
           }
         }
@@ -1015,25 +992,13 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     }
   }
   if constexpr (!Partials) {
-    // The range value (acc_0 + acc_1) + (acc_2 + acc_3); stream j lives in set j / GP
-    // of the lanes of window j % GP (as in lowbit_gemm_kernel).
+    // The range value, valid in the lanes of window 0 (the only ones stored).
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int t = 0; t < NTB; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if constexpr (GP == 4) {
-            const float v = acc[0][r][t][i] + __shfl_xor(acc[0][r][t][i], 4);
-            total[r][t][i] = v + __shfl_xor(v, 8);
-          } else if constexpr (GP == 2) {
-            const float v01 = acc[0][r][t][i] + __shfl_xor(acc[0][r][t][i], 8);
-            const float v23 = acc[1][r][t][i] + __shfl_xor(acc[1][r][t][i], 8);
-            total[r][t][i] = v01 + v23;
-          } else {
-            total[r][t][i] = (acc[0][r][t][i] + acc[1][r][t][i]) + (acc[2][r][t][i] + acc[3][r][t][i]);
-          }
-        }
+        for (int i = 0; i < 4; ++i) total[r][t][i] = acc[(r * NTB + t) * 4 + i];
     if (ranges > 1) {
       float* out = reinterpret_cast<float*>(lds_all) + range * R * NTB * 4u * 64u;
 #pragma unroll
@@ -1292,14 +1257,14 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
     if (forced == 1) {
       go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 1, HalfOut, Partials>, 1, 1);
     } else {
-      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 2, HalfOut, Partials>, 2, 1);
+      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 5, 2, HalfOut, Partials>, 2, 1);
     }
   } else if constexpr (ABits == 8) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
   } else if (forced == 1) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
   } else {
-    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 2, HalfOut, Partials>, 2, 2);
+    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 5, 2, HalfOut, Partials>, 2, 2);
   }
 }
 
@@ -1337,10 +1302,8 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
   };
   // CH = packs per load chunk: about ten groups of weights in flight per wave, whole
   // quads of groups per chunk.
-  if (batch <= 4) {
-    go(lowbit_gemm_kernel<Format, ABits, 4, 1, 3, HalfOut, Partials>, 4, 3, 1);
-  } else if (batch <= 8) {
-    go(lowbit_gemm_kernel<Format, ABits, 2, 1, 6, HalfOut, Partials>, 2, 6, 1);
+  if (batch <= 8) {
+    go(lowbit_gemm_kernel<Format, ABits, 2, 1, 5, HalfOut, Partials>, 2, 5, 1);
   } else if (batch <= 16) {
     go(lowbit_gemm_kernel<Format, ABits, 1, 1, 8, HalfOut, Partials>, 1, 8, 1);
   } else {

@@ -380,6 +380,42 @@ void orc_gemm_epilogue(const int32_t* partials, const uint16_t* ws16, const uint
   }
 }
 
+/* The epilogue above with K cut into splits and ranges, the summation order of
+ * gfxinfer_amd's GEMMs: split s of S owns groups [G s / S, G (s + 1) / S); a split
+ * of n groups is cut into R = clamp(ceil(n / 10), 1, 16) ranges, range r holding
+ * groups [b + n r / R, b + n (r + 1) / R); each range is the sequential epilogue
+ * over its groups from 0, and plane s = ((range_0 + range_1) + range_2) + ...
+ * With R = S = 1 this is orc_gemm_epilogue exactly.  out: fp32 [S, batch, rows]. */
+static unsigned range_count(unsigned n) {
+  unsigned r = (n + 9u) / 10u;
+  return r < 1u ? 1u : (r > 16u ? 16u : r);
+}
+
+void orc_gemm_epilogue_ranges(const int32_t* partials, const uint16_t* ws16, const uint16_t* as16,
+                              size_t rows, size_t columns, unsigned batch, unsigned splits, float* out) {
+  const unsigned groups = (unsigned)(columns / GROUP);
+#pragma omp parallel for schedule(static)
+  for (long long n = 0; n < (long long)rows; ++n) {
+    for (unsigned b = 0; b < batch; ++b) {
+      const int32_t* p = partials + ((size_t)b * rows + (size_t)n) * groups;
+      for (unsigned s = 0; s < splits; ++s) {
+        const unsigned begin = groups * s / splits, count = groups * (s + 1u) / splits - begin;
+        const unsigned ranges = range_count(count);
+        float plane = 0.0f;
+        for (unsigned r = 0; r < ranges; ++r) {
+          float value = 0.0f;
+          for (unsigned g = begin + count * r / ranges; g < begin + count * (r + 1u) / ranges; ++g) {
+            const float scale = h2f(ws16[(size_t)n * groups + g]) * h2f(as16[(size_t)b * groups + g]);
+            value = fmaf((float)p[g], scale, value);
+          }
+          plane = r == 0 ? value : plane + value;
+        }
+        out[((size_t)s * batch + b) * rows + (size_t)n] = plane;
+      }
+    }
+  }
+}
+
 /* src/cli/main.cpp:1468-1495 over every row. */
 void orc_dequant_dot_gemv(const int8_t* w, const float* ws, const int8_t* a, const uint16_t* as16,
                           size_t rows, size_t columns, unsigned batch, float* out) {

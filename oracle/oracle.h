@@ -58,6 +58,11 @@ void orc_gemm_partials(const int8_t* w, const int8_t* a, size_t rows, size_t col
 /* y[b,n] = fmaf(float(P[b,n,g]), ws16(n,g) * as16(b,g), y) over g in order. */
 void orc_gemm_epilogue(const int32_t* partials, const uint16_t* ws16, const uint16_t* as16,
                        size_t rows, size_t columns, unsigned batch, float* out);
+/* The same epilogue with K cut into splits and ranges (the library's GEMM order):
+ * plane s = ranges of split s, each a sequential epilogue, added in range order.
+ * out: fp32 [splits, B, N]; splits = 1, one range = orc_gemm_epilogue. */
+void orc_gemm_epilogue_ranges(const int32_t* partials, const uint16_t* ws16, const uint16_t* as16,
+                              size_t rows, size_t columns, unsigned batch, unsigned splits, float* out);
 /* Dequant-dot GEMV of the reference harness check (src/cli/main.cpp:1468-1495):
  * y[b,n] = fma chain over k of (w(n,k)*ws(n,g)) * (a(b,k)*as(b,g)).  OpenMP over rows. */
 void orc_dequant_dot_gemv(const int8_t* w, const float* ws, const int8_t* a, const uint16_t* as16,

@@ -131,6 +131,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_unpack_a4": (None, [P, SZ, U, P]),
         "orc_gemm_partials": (None, [P, P, SZ, SZ, U, P]),
         "orc_gemm_epilogue": (None, [P, P, P, SZ, SZ, U, P]),
+        "orc_gemm_epilogue_ranges": (None, [P, P, P, SZ, SZ, U, U, P]),
         "orc_dequant_dot_gemv": (None, [P, P, P, P, SZ, SZ, U, P]),
         "orc_dequant_dot_gemv_packed": (None, [P, I, P, P, P, SZ, SZ, U, P]),
         "orc_max_threads": (I, []),
@@ -260,6 +261,19 @@ def gemm_epilogue(partials: np.ndarray, ws16: np.ndarray, as16: np.ndarray) -> n
     B, N, G = partials.shape
     out = np.empty((B, N), dtype=np.float32)
     lib().orc_gemm_epilogue(ptr(partials), ptr(ws16), ptr(as16), N, G * GROUP, B, ptr(out))
+    return out
+
+
+def gemm_epilogue_ranges(partials: np.ndarray, ws16: np.ndarray, as16: np.ndarray,
+                         splits: int = 1) -> np.ndarray:
+    """fp32 [splits, B, N]: the epilogue cut into splits and ranges of K, the order in
+    which the library's GEMMs add the group partials (splits = 1 -> [1, B, N])."""
+    partials = np.ascontiguousarray(partials, dtype=np.int32)
+    ws16 = np.ascontiguousarray(ws16, dtype=np.uint16)
+    as16 = np.ascontiguousarray(as16, dtype=np.uint16)
+    B, N, G = partials.shape
+    out = np.empty((splits, B, N), dtype=np.float32)
+    lib().orc_gemm_epilogue_ranges(ptr(partials), ptr(ws16), ptr(as16), N, G * GROUP, B, splits, ptr(out))
     return out
 
 

@@ -1,8 +1,10 @@
 """GPU parity of the packed low-bit path against the CPU oracle, through the C ABI.
 
 Bars: integer codes, scales and per-group int32 partial sums bit-exact; fp32
-GEMM outputs within 2e-5 of max|y| of the oracle's sequential epilogue (the
-reference harness accepts 0.008*max(1,|y|), src/cli/main.cpp:1499).
+GEMM outputs bit-exact against the oracle's epilogue cut into the library's K ranges
+(orc_gemm_epilogue_ranges; one range is the reference's sequential epilogue itself),
+and within 2e-5 of max|y| of the uncut sequential epilogue (the reference harness
+accepts 0.008*max(1,|y|), src/cli/main.cpp:1499).
 """
 from __future__ import annotations
 
@@ -174,6 +176,7 @@ def test_gemm_partials_bit_exact_and_output(device, gx, orc, fmt, abits, rows, c
     else:
         gx.launch_i8_gemm(fmt, dw, dws, da, das, y, rows, cols, batch)
     got = host(y)
+    assert np.array_equal(got, orc.gemm_epilogue_ranges(want_P, p["ws16"], p["as16"])[0])
     scale = max(1e-30, float(np.abs(want_y).max()))
     assert np.abs(got - want_y).max() <= 2e-5 * scale
 
@@ -187,12 +190,14 @@ def test_gemm_split_planes_sum_to_product(device, gx, orc, fmt, rows, cols, batc
     """Split-K planes: plane s = the epilogue over the s-th of `splits` equal pack ranges
     of K; their sum in plane order is the product (same 2e-5 bar as the plain GEMM)."""
     p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=rows * 3 + cols + batch + splits)
-    want = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+    P = orc.gemm_partials(p["wint"], p["aint"])
+    want = orc.gemm_epilogue(P, p["ws16"], p["as16"])
     planes = empty((splits, batch, rows), np.float32)
     say("gemm split", fmt, rows, cols, batch, splits)
     gx.launch_i4_gemm_split(fmt, dev(p["tiled"]), dev(p["tscales"]), dev(p["acts"]), dev(p["as16"]),
                             planes, rows, cols, batch, splits)
     got = host(planes)
+    assert np.array_equal(got, orc.gemm_epilogue_ranges(P, p["ws16"], p["as16"], splits))
     total = got[0].copy()
     for s in range(1, splits):
         total += got[s]
@@ -246,11 +251,14 @@ def test_gemm_split_rejects_bad_counts(device, gx):
 def test_gemm_half_output(device, gx, orc):
     fmt, rows, cols, batch = 2, 5120, 10240, 1  # mtp.fc shape
     p = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=21)
-    want = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
+    P = orc.gemm_partials(p["wint"], p["aint"])
+    want = orc.gemm_epilogue(P, p["ws16"], p["as16"])
     y = empty((batch, rows), np.uint16)
     say("gemm half", rows, cols)
     gx.launch_i4_gemm_half(fmt, dev(p["tiled"]), dev(p["tscales"]), dev(p["acts"]), dev(p["as16"]), y, rows, cols, batch)
     got = host(y, np.uint16).view(np.float16).astype(np.float32)
+    exact = orc.gemm_epilogue_ranges(P, p["ws16"], p["as16"])[0]
+    assert np.array_equal(got, exact.astype(np.float16).astype(np.float32))
     ref16 = want.astype(np.float16).astype(np.float32)
     assert np.abs(got - ref16).max() <= 2e-5 * np.abs(want).max() + np.abs(ref16).max() * 2 ** -10
 
@@ -267,15 +275,15 @@ def test_gemm_fused_four_matrices(device, gx, orc):
         w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
         _, codes, scales = orc.quantize_group128(w, fmt)
         tiled, ts = gx.tile_group128(fmt, codes, scales, rows, cols)
-        wants.append(orc.gemm_epilogue(orc.gemm_partials(orc.unpack_weights(codes, rows, cols, fmt), aint),
-                                       orc.f32_to_f16_bits(scales), as16))
+        P = orc.gemm_partials(orc.unpack_weights(codes, rows, cols, fmt), aint)
+        wants.append(orc.gemm_epilogue_ranges(P, orc.f32_to_f16_bits(scales), as16)[0])
         out = empty((batch, rows), np.float32)
         outs.append(out)
         mats.append((dev(tiled), dev(ts), out, rows))
     say("gemm fused")
     gx.launch_i4_gemm_fused(fmt, mats, dev(acts), dev(as16), cols, batch)
     for out, want in zip(outs, wants):
-        assert np.abs(host(out) - want).max() <= 2e-5 * np.abs(want).max()
+        assert np.array_equal(host(out), want)
 
 
 def test_quantize_then_gemm_matches_float_reference(device, gx, orc):

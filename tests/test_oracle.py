@@ -175,6 +175,45 @@ def test_gemm_epilogue_is_one_rounding_per_group(orc):
             assert y[b, n] == acc
 
 
+def _fma32(p, scale, acc):
+    exact = fractions.Fraction(int(p)) * fractions.Fraction(float(scale)) + fractions.Fraction(float(acc))
+    return np.float32(float(exact))
+
+
+@pytest.mark.parametrize("groups,splits", [(1, 1), (7, 1), (10, 1), (11, 1), (40, 1), (136, 1), (200, 1),
+                                           (40, 4), (136, 4), (48, 3), (5, 5), (23, 2)])
+def test_gemm_epilogue_ranges_brute_force(orc, groups, splits):
+    """The library's K order, from its definition: split s = groups [G s/S, G(s+1)/S),
+    R = clamp(ceil(n/10), 1, 16) ranges [b + n r/R, b + n(r+1)/R), each a sequential
+    epilogue from 0, added in range order; one range is the reference epilogue itself."""
+    rng = np.random.default_rng(groups * 10 + splits)
+    B, N = 2, 3
+    P = rng.integers(-3584, 3585, size=(B, N, groups), dtype=np.int32)
+    ws16 = (rng.uniform(0.002, 0.08, size=(N, groups))).astype(np.float16).view(np.uint16)
+    as16 = (rng.uniform(0.01, 0.5, size=(B, groups))).astype(np.float16).view(np.uint16)
+    got = orc.gemm_epilogue_ranges(P, ws16, as16, splits)
+    assert got.shape == (splits, B, N)
+    ws = ws16.view(np.float16).astype(np.float32)
+    as_ = as16.view(np.float16).astype(np.float32)
+    for b in range(B):
+        for n in range(N):
+            for s in range(splits):
+                lo, hi = groups * s // splits, groups * (s + 1) // splits
+                count = hi - lo
+                ranges = min(16, max(1, -(-count // 10)))
+                plane = np.float32(0)
+                for r in range(ranges):
+                    value = np.float32(0)
+                    for g in range(lo + count * r // ranges, lo + count * (r + 1) // ranges):
+                        value = _fma32(P[b, n, g], np.float32(ws[n, g] * as_[b, g]), value)
+                    plane = value if r == 0 else np.float32(plane + value)
+                assert got[s, b, n] == plane, (s, b, n)
+    if splits == 1 and groups <= 10:
+        assert np.array_equal(got[0], orc.gemm_epilogue(P, ws16, as16))
+    total = got.sum(axis=0, dtype=np.float64)
+    assert np.allclose(total, orc.gemm_epilogue(P, ws16, as16), rtol=1e-5, atol=1e-6)
+
+
 def test_dequant_dot_gemv_close_to_exact(orc):
     rng = np.random.default_rng(5)
     w = (rng.standard_normal((32, 512)) * 0.02).astype(np.float32)
