@@ -476,8 +476,12 @@ struct GdnWindowArgs {
 };
 
 constexpr unsigned kWindowChannels = 2 * kGdnD + kGdnCols;  // 272
+// Sixteen waves share the loads, the conv and the norms; waves 0-3 (16 columns x 16
+// row slices) run the recurrence, whose arithmetic is the same at any workgroup size.
+constexpr unsigned kWindowThreads = 1024;
+constexpr unsigned kWindowRecurrenceWaves = kGdnCols / 4;
 
-__global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
+__global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArgs w) {
   constexpr unsigned D = kGdnD;
   const GdnArgs& args = w.gdn;
   __shared__ float qn[kGdnMaxTokens][D];
@@ -512,21 +516,26 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
   // Stage 1: every global load is issued before the first use (one memory latency):
   // the state tile, fp16(projected) of the 272 channels per token as 4-channel runs,
   // a/b of the head, the conv weights and the initial conv state.
-  constexpr unsigned kQuads = kWindowChannels / 4;                        // 68
-  constexpr unsigned kTileLoads = D * (kGdnCols / 4) / 256;                // 2
-  constexpr unsigned kInputLoads = (kGdnMaxTokens * kQuads + 255) / 256;   // 9
+  constexpr unsigned NT = kWindowThreads;
+  constexpr unsigned kQuads = kWindowChannels / 4;                           // 68
+  constexpr unsigned kTileQuads = D * (kGdnCols / 4);                         // 512
+  constexpr unsigned kTileLoads = (kTileQuads + NT - 1) / NT;                 // 1
+  constexpr unsigned kInputLoads = (kGdnMaxTokens * kQuads + NT - 1) / NT;    // 3
+  constexpr unsigned kChannelLoads = (kWindowChannels + NT - 1) / NT;         // 1
   const unsigned quads = T * kQuads;
   const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
   f32x4 tv[kTileLoads];
 #pragma unroll
   for (unsigned u = 0; u < kTileLoads; ++u) {
-    const unsigned i = tid + u * 256, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
-    tv[u] = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
+    const unsigned i = tid + u * NT, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    if (i < kTileQuads) {
+      tv[u] = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
+    }
   }
   f32x4 xv[kInputLoads];
 #pragma unroll
   for (unsigned u = 0; u < kInputLoads; ++u) {
-    const unsigned i = tid + u * 256;
+    const unsigned i = tid + u * NT;
     if (i < quads) {
       const unsigned t = i / kQuads, q = i - t * kQuads;
       xv[u] = *reinterpret_cast<const f32x4*>(w.projected + static_cast<std::size_t>(t) * C +
@@ -538,11 +547,11 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
     a_in = args.a[static_cast<std::size_t>(tid) * args.value_heads + h];
     b_in = args.b[static_cast<std::size_t>(tid) * args.value_heads + h];
   }
-  uint16_t wv[2][4];
-  __half iv[2][4];
+  uint16_t wv[kChannelLoads][4];
+  __half iv[kChannelLoads][4];
 #pragma unroll
-  for (unsigned u = 0; u < 2; ++u) {
-    const unsigned j = tid + u * 256;
+  for (unsigned u = 0; u < kChannelLoads; ++u) {
+    const unsigned j = tid + u * NT;
     if (j < kWindowChannels) {
       const std::size_t c = channel(j);
 #pragma unroll
@@ -555,13 +564,15 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
 
 #pragma unroll
   for (unsigned u = 0; u < kTileLoads; ++u) {
-    const unsigned i = tid + u * 256, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    const unsigned i = tid + u * NT, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    if (i < kTileQuads) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tile[r][c4 * 4 + e] = tv[u][e];
+      for (int e = 0; e < 4; ++e) tile[r][c4 * 4 + e] = tv[u][e];
+    }
   }
 #pragma unroll
   for (unsigned u = 0; u < kInputLoads; ++u) {
-    const unsigned i = tid + u * 256;
+    const unsigned i = tid + u * NT;
     if (i < quads) {
       const unsigned t = i / kQuads, q = i - t * kQuads;
       uint32_t bits[4];
@@ -579,8 +590,8 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
     }
   }
 #pragma unroll
-  for (unsigned u = 0; u < 2; ++u) {
-    const unsigned j = tid + u * 256;
+  for (unsigned u = 0; u < kChannelLoads; ++u) {
+    const unsigned j = tid + u * NT;
     if (j < kWindowChannels) {
 #pragma unroll
       for (int tap = 0; tap < 4; ++tap) cw[j][tap] = bf16_to_float(wv[u][tap]);
@@ -635,7 +646,7 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
 
   // Stage 3: normalized q (with the 1/sqrt(D) query scale) and k per token.
   const float query_scale = 0.08838834764831845F;  // 1/sqrt(128), qwen_ops.hip:325
-  for (unsigned t = wave; t < T; t += 4) {
+  for (unsigned t = wave; t < T; t += NT / 64) {
     const float q0 = qn[t][2 * lane], q1 = qn[t][2 * lane + 1];
     const float k0 = kn[t][2 * lane], k1 = kn[t][2 * lane + 1];
     const float iq = rsqrtf(wave_sum(q0 * q0 + q1 * q1) + 1.0e-6F) * query_scale;
@@ -652,46 +663,64 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(GdnWindowArgs w) {
   }
   __syncthreads();
 
-  // Stage 4: the recurrence (gdn_recurrent_kernel).
+  // Stage 4: the recurrence (gdn_recurrent_kernel), on waves 0-3; each token's key
+  // and query slices are read from LDS one token ahead.
   const unsigned ks = lane & 15u;
   const unsigned col = wave * 4u + (lane >> 4);
+  const bool recurrent = wave < kWindowRecurrenceWaves;
   float S[8];
+  if (recurrent) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
-  const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
-  for (unsigned t = 0; t < T; ++t) {
-    const float decay = decay_s[t], beta = beta_s[t];
-    float kv[8], qv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kv[i] = kn[t][ks * 8 + i];
-      qv[i] = qn[t][ks * 8 + i];
-    }
-    float memory = 0.0F;
+    for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
+    const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
+    float kv_next[8], qv_next[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      S[i] = S[i] * decay;
-      memory = fmaf(S[i], kv[i], memory);
+      kv_next[i] = kn[0][ks * 8 + i];
+      qv_next[i] = qn[0][ks * 8 + i];
     }
-    memory = row16_sum(memory);
-    const float delta = (vv[t][col] - memory) * beta;
-    float o = 0.0F;
+    for (unsigned t = 0; t < T; ++t) {
+      const float decay = decay_s[t], beta = beta_s[t];
+      float kv[8], qv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      S[i] = fmaf(kv[i], delta, S[i]);
-      o = fmaf(S[i], qv[i], o);
-    }
-    o = row16_sum(o);
-    if (ks == 0) {
-      args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
-      if (args.delta_log != nullptr) {
-        args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
+      for (int i = 0; i < 8; ++i) {
+        kv[i] = kv_next[i];
+        qv[i] = qv_next[i];
+      }
+      const unsigned tn = t + 1 < T ? t + 1 : t;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kv_next[i] = kn[tn][ks * 8 + i];
+        qv_next[i] = qn[tn][ks * 8 + i];
+      }
+      float memory = 0.0F;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        S[i] = S[i] * decay;
+        memory = fmaf(S[i], kv[i], memory);
+      }
+      memory = row16_sum(memory);
+      const float delta = (vv[t][col] - memory) * beta;
+      float o = 0.0F;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        S[i] = fmaf(kv[i], delta, S[i]);
+        o = fmaf(S[i], qv[i], o);
+      }
+      o = row16_sum(o);
+      if (ks == 0) {
+        args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
+        if (args.delta_log != nullptr) {
+          args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
+        }
       }
     }
-  }
+  }  // recurrent
   __syncthreads();
+  if (recurrent) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) tile[ks * 8 + i][col] = S[i];
+    for (int i = 0; i < 8; ++i) tile[ks * 8 + i][col] = S[i];
+  }
   __syncthreads();
   float* final_state = args.final_state + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
   for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
@@ -1275,7 +1304,7 @@ extern "C" int32_t gfxinfer_launch_gdn_conv_window(
                   GdnArgs{nullptr, projected_a, projected_b, bf16_a_log, bf16_dt_bias,
                           initial_recurrent_state, final_recurrent_state, mixed, key_log, delta_log,
                           decay_log, batch, key_heads, value_heads}};
-  hipLaunchKernelGGL(gdn_window_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(256), 0,
+  hipLaunchKernelGGL(gdn_window_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(kWindowThreads), 0,
                      static_cast<hipStream_t>(stream), w);
   return launch_status("fused GDN conv/window launch failed");
 }
