@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gdn_restore_prefix_all": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, U32, U32, P]),
     "gfxinfer_launch_qk_rms_norm_rope_block": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, ctypes.c_uint64, U32, F32, P]),
     "gfxinfer_launch_qk_rms_norm_rope_block_indirect_position": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, P, U32, F32, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_kv_append_block": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, P, P, P, SZ, ctypes.c_uint64, U32, F32, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_kv_append_block_indirect_position": (I32, [P, P, P, SZ, SZ, P, P, P, SZ, SZ, SZ, SZ, P, P, P, SZ, P, U32, F32, P]),
     "gfxinfer_launch_kv_append_block": (I32, [P, P, P, P, SZ, SZ, U32, SZ, P]),
     "gfxinfer_launch_kv_append_block_indirect_position": (I32, [P, P, P, P, P, SZ, U32, SZ, P]),
     "gfxinfer_launch_argmax_batch": (I32, [P, P, SZ, SZ, U32, P]),
@@ -97,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_attention_workspace_bytes": (SZ, [U32, U32, SZ]),
     "gfxinfer_launch_gated_attention_decode_block": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_gated_attention_decode_block_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position": (I32, [P, P, P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
     # include/gfxinfer_runtime.h
     "gfxinfer_model_spec_qwen38_27b": (None, [P]),
     "gfxinfer_model_create_synthetic": (I32, [P, ctypes.c_uint64, I32, P]),

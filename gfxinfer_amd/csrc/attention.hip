@@ -180,9 +180,13 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
 }
 
 // Merge the splits of each (token, q head) and apply the sigmoid gate.  One
-// wave per (token, head); lane owns head dims 2l, 2l+1.
+// wave per (token, head); lane owns head dims 2l, 2l+1.  With codes set, the wave
+// also quantizes its head (one 128 group) to A4G128 as quantize_activation_i4 does
+// on the fp16 output row ([T][Hq * 128] -> codes [T][Hq * 64], scales [T][Hq]).
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, const float* __restrict__ gate,
-                                                                __half* __restrict__ output) {
+                                                                __half* __restrict__ output,
+                                                                uint8_t* __restrict__ codes,
+                                                                __half* __restrict__ scales) {
   const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (linear >= a.tokens * a.q_heads) return;
   const unsigned lane = threadIdx.x & 63u;
@@ -205,15 +209,20 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   const float g0 = 1.0F / (1.0F + expf(-g[2 * lane]));
   const float g1 = 1.0F / (1.0F + expf(-g[2 * lane + 1]));
   __half* out = output + static_cast<std::size_t>(linear) * kD + 2 * lane;
-  out[0] = to_half(o0 / total * g0);
-  out[1] = to_half(o1 / total * g1);
+  const __half h0 = to_half(o0 / total * g0), h1 = to_half(o1 / total * g1);
+  out[0] = h0;
+  out[1] = h1;
+  if (codes != nullptr) {
+    quantize_group_a4(h0, h1, codes + static_cast<std::size_t>(linear) * (kD / 2), scales + linear, lane);
+  }
 }
 
 int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t* key_cache,
                         const uint16_t* value_cache, uint16_t* output, uint64_t base_count,
                         const uint64_t* indirect, size_t capacity, uint32_t batch, uint32_t q_heads,
                         uint32_t kv_heads, uint32_t head_size, float* workspace,
-                        size_t workspace_bytes, hipStream_t stream);
+                        size_t workspace_bytes, hipStream_t stream, uint8_t* codes = nullptr,
+                        uint16_t* scales = nullptr);
 
 }  // namespace
 }  // namespace gfx950
@@ -232,7 +241,11 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
                         const uint16_t* value_cache, uint16_t* output, uint64_t base_count,
                         const uint64_t* indirect, size_t capacity, uint32_t batch, uint32_t q_heads,
                         uint32_t kv_heads, uint32_t head_size, float* workspace,
-                        size_t workspace_bytes, hipStream_t stream) {
+                        size_t workspace_bytes, hipStream_t stream, uint8_t* codes,
+                        uint16_t* scales) {
+  if ((codes == nullptr) != (scales == nullptr)) {
+    return fail(GFXI_INVALID_ARGUMENT, "A4 codes and scales of the attention output go together");
+  }
   if (query == nullptr || gate == nullptr || key_cache == nullptr || value_cache == nullptr ||
       output == nullptr || workspace == nullptr || batch == 0 || batch > 32 || q_heads == 0 ||
       kv_heads == 0 || q_heads % kv_heads != 0 || head_size != kD || capacity == 0 ||
@@ -254,7 +267,7 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
   const uint32_t total = batch * q_heads;
   hipLaunchKernelGGL(attention_combine_kernel, dim3((total + 3) / 4), dim3(256), 0, stream, args, gate,
-                     reinterpret_cast<__half*>(output));
+                     reinterpret_cast<__half*>(output), codes, reinterpret_cast<__half*>(scales));
   return launch_status("gated attention combine launch failed");
 }
 }  // namespace
@@ -278,4 +291,28 @@ extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_indirect_positio
   return attention_entry(query, gate, key_cache, value_cache, output, 0, base_position, capacity, batch,
                          q_heads, kv_heads, head_size, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, size_t base_token_count, size_t capacity,
+    uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (codes == nullptr) return fail(GFXI_INVALID_ARGUMENT, "A4 codes of the attention output are null");
+  return attention_entry(query, gate, key_cache, value_cache, output, base_token_count, nullptr, capacity,
+                         batch, q_heads, kv_heads, head_size, workspace, workspace_bytes,
+                         static_cast<hipStream_t>(stream), codes, scales);
+}
+
+extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, const uint64_t* base_position, size_t capacity,
+    uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (base_position == nullptr || codes == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "indirect position or A4 codes of the attention output are null");
+  }
+  return attention_entry(query, gate, key_cache, value_cache, output, 0, base_position, capacity, batch,
+                         q_heads, kv_heads, head_size, workspace, workspace_bytes,
+                         static_cast<hipStream_t>(stream), codes, scales);
 }

@@ -80,6 +80,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// One wave quantizes 128 fp16 values (two per lane) to A4G128 exactly as
+// quantize_activation_i4 (lowbit_gemv.hip:373-407) does.
+__device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_t* codes,
+                                                  __half* scale_out, unsigned lane) {
+  const float x0 = __half2float(x0h), x1 = __half2float(x1h);
+  const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  const __half scale16 = to_half(maximum == 0.0F ? 1.0F : maximum / 7.0F);
+  const float scale = __half2float(scale16);
+  const int low = max(-7, min(7, __float2int_rn(x0 / scale)));
+  const int high = max(-7, min(7, __float2int_rn(x1 / scale)));
+  codes[lane] = static_cast<uint8_t>((low & 0x0f) | ((high & 0x0f) << 4));
+  if (lane == 0) *scale_out = scale16;
+}
+
 // Signed quantization level of value at scale (quantization.cpp:29-56: encode_value
 // then decode_value), clamped to the format's range.
 template <int Format>

@@ -1187,18 +1187,19 @@ int rowtiles_override() {
   return value;
 }
 
-// GFXI_GEMM_RESIDENT=0 disables the one-round residency cap on waves (tuning knob).
+// GFXI_GEMM_RESIDENT=1 caps the direct kernel's waves per workgroup so that the whole
+// grid is resident at once (tuning knob, off by default: with one wave per range of
+// the canonical K order the uncapped grids measured equal or faster).
 bool resident_cap() {
   static const bool value = [] {
     const char* text = std::getenv("GFXI_GEMM_RESIDENT");
-    return text == nullptr || std::atoi(text) != 0;
+    return text != nullptr && std::atoi(text) != 0;
   }();
   return value;
 }
 
-// Waves per workgroup: about ten groups of K per wave, but no more than lets every
-// workgroup of the grid be resident at once (a second partial round of
-// workgroups would double the time of a short kernel).
+// Waves per workgroup: about ten groups of K per wave; with the residency cap on, no
+// more than lets every workgroup of the grid be resident at once.
 unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, std::size_t lds_bytes) {
   unsigned want = choose_waves(groups, 1);
   if (waves_override() != 0 || !resident_cap()) return want;

@@ -36,19 +36,6 @@ __device__ float block_sum(float value, float* scratch) {
   return total;
 }
 
-// One wave quantizes 128 fp16 values (two per lane) to A4G128 exactly as
-// quantize_activation_i4 (lowbit_gemv.hip:373-407) does.
-__device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_t* codes,
-                                                  __half* scale_out, unsigned lane) {
-  const float x0 = __half2float(x0h), x1 = __half2float(x1h);
-  const float maximum = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const __half scale16 = to_half(maximum == 0.0F ? 1.0F : maximum / 7.0F);
-  const float scale = __half2float(scale16);
-  const int low = max(-7, min(7, __float2int_rn(x0 / scale)));
-  const int high = max(-7, min(7, __float2int_rn(x1 / scale)));
-  codes[lane] = static_cast<uint8_t>((low & 0x0f) | ((high & 0x0f) << 4));
-  if (lane == 0) *scale_out = scale16;
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm family (qwen_ops.hip:31-106, 176-217).  One workgroup per row.
@@ -835,6 +822,11 @@ struct RopeArgs {
   uint64_t base_position;
   const uint64_t* indirect_position;
   float theta;
+  // Optional K/V cache append ([capacity][key_heads * D], rows base + t): the key
+  // head waves also store their fp16 key row and the fp16 value row of their head.
+  const float* value_input;  // [T][key_heads * D] or null (no append)
+  __half* key_cache;
+  __half* value_cache;
 };
 
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
@@ -869,8 +861,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
     const float rotated = lane < half ? -partner : partner;
     v0 = fmaf(n0, cosf(angle), rotated * sinf(angle));
   }
-  out[lane] = to_half(v0);
-  out[lane + 64] = to_half(n1);
+  const __half h0 = to_half(v0), h1 = to_half(n1);
+  out[lane] = h0;
+  out[lane + 64] = h1;
+  if (is_key && a.value_input != nullptr) {
+    const std::size_t row = (static_cast<std::size_t>(base + t) * count + head) * D;
+    const float* value = a.value_input + (static_cast<std::size_t>(t) * count + head) * D;
+    a.key_cache[row + lane] = h0;
+    a.key_cache[row + lane + 64] = h1;
+    a.value_cache[row + lane] = to_half(value[lane]);
+    a.value_cache[row + lane + 64] = to_half(value[lane + 64]);
+  }
 }
 
 // K (fp16) and V (fp32 -> fp16) rows into the contiguous cache at the (device)
@@ -1344,7 +1345,14 @@ int32_t rope_entry(const float* query_input, const uint16_t* query_weight, uint1
                    size_t query_heads, size_t query_stride, const float* key_input,
                    const uint16_t* key_weight, uint16_t* key_output, size_t key_heads,
                    size_t key_stride, size_t head_size, size_t rotary, uint64_t base,
-                   const uint64_t* indirect, uint32_t batch, float theta, hipStream_t stream) {
+                   const uint64_t* indirect, uint32_t batch, float theta, hipStream_t stream,
+                   const float* value_input = nullptr, uint16_t* key_cache = nullptr,
+                   uint16_t* value_cache = nullptr, size_t capacity = 0) {
+  if (value_input != nullptr &&
+      (key_cache == nullptr || value_cache == nullptr ||
+       (indirect == nullptr && (base > capacity || batch > capacity - base)))) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid fused K/V cache append arguments");
+  }
   if (query_input == nullptr || query_weight == nullptr || query_output == nullptr ||
       key_input == nullptr || key_weight == nullptr || key_output == nullptr || query_heads == 0 ||
       key_heads == 0 || head_size != 128 || rotary == 0 || rotary > 64 || rotary % 2 != 0 ||
@@ -1357,7 +1365,8 @@ int32_t rope_entry(const float* query_input, const uint16_t* query_weight, uint1
              reinterpret_cast<__half*>(key_output), static_cast<uint32_t>(query_heads),
              static_cast<uint32_t>(query_stride), static_cast<uint32_t>(key_heads),
              static_cast<uint32_t>(key_stride), static_cast<uint32_t>(rotary), batch, base, indirect,
-             theta};
+             theta, value_input, reinterpret_cast<__half*>(key_cache),
+             reinterpret_cast<__half*>(value_cache)};
   const uint32_t waves = static_cast<uint32_t>(query_heads + key_heads) * batch;
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, a);
   return launch_status("Q/K RMSNorm/RoPE launch failed");
@@ -1402,6 +1411,36 @@ extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
   return rope_entry(query_input, query_bf16_weight, query_output, query_head_count, query_input_stride,
                     key_input, key_bf16_weight, key_output, key_head_count, key_input_stride, head_size,
                     rotary_size, 0, base_position, batch, rope_theta, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, const float* value_input,
+    uint16_t* key_cache, uint16_t* value_cache, size_t capacity, uint64_t base_position,
+    uint32_t batch, float rope_theta, void* stream) {
+  if (value_input == nullptr) return fail(GFXI_INVALID_ARGUMENT, "fused K/V append needs the value rows");
+  return rope_entry(query_input, query_bf16_weight, query_output, query_head_count, query_input_stride,
+                    key_input, key_bf16_weight, key_output, key_head_count, key_input_stride, head_size,
+                    rotary_size, base_position, nullptr, batch, rope_theta,
+                    static_cast<hipStream_t>(stream), value_input, key_cache, value_cache, capacity);
+}
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_block_indirect_position(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, const float* value_input,
+    uint16_t* key_cache, uint16_t* value_cache, size_t capacity, const uint64_t* base_position,
+    uint32_t batch, float rope_theta, void* stream) {
+  if (value_input == nullptr || base_position == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "fused K/V append needs the value rows and a position");
+  }
+  return rope_entry(query_input, query_bf16_weight, query_output, query_head_count, query_input_stride,
+                    key_input, key_bf16_weight, key_output, key_head_count, key_input_stride, head_size,
+                    rotary_size, 0, base_position, batch, rope_theta, static_cast<hipStream_t>(stream),
+                    value_input, key_cache, value_cache, capacity);
 }
 
 extern "C" int32_t gfxinfer_launch_kv_append_block(const uint16_t* key, const float* value,

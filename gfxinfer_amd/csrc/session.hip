@@ -259,37 +259,35 @@ struct gfxinfer_session {
                           bool stop_after_append) {
     GFXI_TRY(gemm_fused({{&L.q, projected_main}, {&L.k, projected_k}, {&L.v, projected_v}}, batch));
     const std::size_t hd = spec.attention_head_size;
+    // Q/K norm + RoPE and the K/V cache append of the block in one launch (the
+    // reference's launch pair, bit for bit).
     if (device_position == nullptr) {
-      GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_block(
+      GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
           projected_main, L.q_norm, query, spec.attention_head_count, 2 * hd, projected_k,
-          L.k_norm, key, spec.kv_head_count, hd, hd, spec.rotary_size, position, batch,
-          spec.rope_theta, stream));
-      GFXI_TRY(gfxinfer_launch_kv_append_block(key, projected_v, key_cache, value_cache, position,
-                                               config.maximum_context_tokens, batch, kv_rows,
-                                               stream));
+          L.k_norm, key, spec.kv_head_count, hd, hd, spec.rotary_size, projected_v, key_cache,
+          value_cache, config.maximum_context_tokens, position, batch, spec.rope_theta, stream));
     } else {
-      GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
+      GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_block_indirect_position(
           projected_main, L.q_norm, query, spec.attention_head_count, 2 * hd, projected_k,
-          L.k_norm, key, spec.kv_head_count, hd, hd, spec.rotary_size, device_position, batch,
-          spec.rope_theta, stream));
-      GFXI_TRY(gfxinfer_launch_kv_append_block_indirect_position(
-          key, projected_v, key_cache, value_cache, device_position,
-          config.maximum_context_tokens, batch, kv_rows, stream));
+          L.k_norm, key, spec.kv_head_count, hd, hd, spec.rotary_size, projected_v, key_cache,
+          value_cache, config.maximum_context_tokens, device_position, batch, spec.rope_theta,
+          stream));
     }
     if (stop_after_append) return ok();
+    // Attention with the o projection's A4 quantizer in its combine launch.
     if (device_position == nullptr) {
-      GFXI_TRY(gfxinfer_launch_gated_attention_decode_block(
-          query, projected_main, key_cache, value_cache, attention_output, position + 1,
-          config.maximum_context_tokens, batch, spec.attention_head_count, spec.kv_head_count,
-          spec.attention_head_size, attention_workspace, attention_workspace_bytes, stream));
+      GFXI_TRY(gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+          query, projected_main, key_cache, value_cache, attention_output, act_codes, act_scales,
+          position + 1, config.maximum_context_tokens, batch, spec.attention_head_count,
+          spec.kv_head_count, spec.attention_head_size, attention_workspace,
+          attention_workspace_bytes, stream));
     } else {
-      GFXI_TRY(gfxinfer_launch_gated_attention_decode_block_indirect_position(
-          query, projected_main, key_cache, value_cache, attention_output, device_position,
-          config.maximum_context_tokens, batch, spec.attention_head_count, spec.kv_head_count,
-          spec.attention_head_size, attention_workspace, attention_workspace_bytes, stream));
+      GFXI_TRY(gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position(
+          query, projected_main, key_cache, value_cache, attention_output, act_codes, act_scales,
+          device_position, config.maximum_context_tokens, batch, spec.attention_head_count,
+          spec.kv_head_count, spec.attention_head_size, attention_workspace,
+          attention_workspace_bytes, stream));
     }
-    GFXI_TRY(gfxinfer_launch_quantize_activation_i4(attention_output, act_codes, act_scales,
-                                                    attn_width, batch, stream));
     return gemm_planes(L.o, mixer_update, batch, mixer_planes);
   }
 

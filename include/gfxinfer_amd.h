@@ -361,6 +361,28 @@ int32_t gfxinfer_launch_qk_rms_norm_rope_block_indirect_position(
     size_t key_input_stride, size_t head_size, size_t rotary_size,
     const uint64_t* base_position, uint32_t batch, float rope_theta, void* stream);
 
+/* Q/K RMSNorm + RoPE followed by the K/V cache append of the same block in one launch:
+ * the outputs of gfxinfer_launch_qk_rms_norm_rope_block, and the caches
+ * ([capacity][key_head_count * head_size]) as gfxinfer_launch_kv_append_block leaves them
+ * for key = key_output and value = value_input ([batch][key_head_count * head_size] fp32),
+ * bit for bit.  No reference counterpart (the reference launches the pair,
+ * qwen_runtime.cpp:439-468). */
+int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, const float* value_input,
+    uint16_t* key_cache, uint16_t* value_cache, size_t capacity, uint64_t base_position,
+    uint32_t batch, float rope_theta, void* stream);
+/* The same with the base position read from device memory (graph-capture variant). */
+int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_block_indirect_position(
+    const float* query_input, const uint16_t* query_bf16_weight, uint16_t* query_output,
+    size_t query_head_count, size_t query_input_stride, const float* key_input,
+    const uint16_t* key_bf16_weight, uint16_t* key_output, size_t key_head_count,
+    size_t key_input_stride, size_t head_size, size_t rotary_size, const float* value_input,
+    uint16_t* key_cache, uint16_t* value_cache, size_t capacity, const uint64_t* base_position,
+    uint32_t batch, float rope_theta, void* stream);
+
 /* qwen_ops.h launch_kv_append_block: K (fp16) and V (fp32 -> fp16) rows of `batch` tokens into
  * caches [capacity][kv_elements] at position..position+batch-1. */
 int32_t gfxinfer_launch_kv_append_block(const uint16_t* key, const float* value,
@@ -403,6 +425,24 @@ int32_t gfxinfer_launch_gated_attention_decode_block_indirect_position(
     const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
     uint16_t* output, const uint64_t* base_position, size_t capacity, uint32_t batch,
     uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* Attention followed by the A4G128 quantizer of its output in the same launch: output as
+ * gfxinfer_launch_gated_attention_decode_block writes it, and codes [batch, q_heads * 64] /
+ * fp16 scales [batch, q_heads] as gfxinfer_launch_quantize_activation_i4 makes them from
+ * that output (each 128-wide head is one group), bit for bit.  No reference counterpart
+ * (the reference quantizes the attention output in a launch of its own inside the o
+ * projection's matrix() call, qwen_runtime.cpp:471-481 and :116-120). */
+int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, size_t base_token_count, size_t capacity,
+    uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream);
+/* The same with base_token_count = *base_position + 1 read from device memory. */
+int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, const uint64_t* base_position, size_t capacity,
+    uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
     size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -425,6 +425,53 @@ def test_attention_matches_oracle(device, gx, orc, T, base):
     assert np.array_equal(host(out2, np.uint16), host(out, np.uint16))
 
 
+@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 1)])
+def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base):
+    """Attention with the A4 quantizer in its combine launch == attention followed by
+    gfxinfer_launch_quantize_activation_i4 on its fp16 output: same output, codes and
+    scales bit for bit (direct and device position)."""
+    capacity = 2048
+    rng = np.random.default_rng(T + base)
+    q = _half(rng.standard_normal((T, HQ, AD)))
+    gate = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
+    kc = np.zeros((capacity, HKV, AD), np.uint16)
+    vc = np.zeros((capacity, HKV, AD), np.uint16)
+    n = base + T - 1
+    kc[:n] = _half(rng.standard_normal((n, HKV, AD)))
+    vc[:n] = _half(rng.standard_normal((n, HKV, AD)))
+    L = gx.lib()
+    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, capacity)
+    work = empty((wb // 4,), np.float32)
+    out = empty((T, HQ, AD), np.uint16)
+    codes, scales = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ), np.uint16)
+    dq, dg, dk, dv = D_(q), D_(gate), D_(kc), D_(vc)
+    say("attention then quantizer", T, base)
+    gx.check(L.gfxinfer_launch_gated_attention_decode_block(dq, dg, dk, dv, out.data_ptr(), base, capacity, T, HQ,
+                                                            HKV, AD, work.data_ptr(), wb, None))
+    gx.check(L.gfxinfer_launch_quantize_activation_i4(out.data_ptr(), codes.data_ptr(), scales.data_ptr(),
+                                                      HQ * AD, T, None))
+    want = [host(out, np.uint16), host(codes), host(scales, np.uint16)]
+    pos = dev(np.array([base - 1], np.uint64))
+    for indirect in (False, True):
+        out2 = empty((T, HQ, AD), np.uint16)
+        codes2, scales2 = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ), np.uint16)
+        say("attention + quantizer", T, base, indirect)
+        if indirect:
+            gx.check(L.gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position(
+                dq, dg, dk, dv, out2.data_ptr(), codes2.data_ptr(), scales2.data_ptr(), pos.data_ptr(), capacity,
+                T, HQ, HKV, AD, work.data_ptr(), wb, None))
+        else:
+            gx.check(L.gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+                dq, dg, dk, dv, out2.data_ptr(), codes2.data_ptr(), scales2.data_ptr(), base, capacity,
+                T, HQ, HKV, AD, work.data_ptr(), wb, None))
+        assert np.array_equal(host(out2, np.uint16), want[0])
+        assert np.array_equal(host(codes2), want[1])
+        assert np.array_equal(host(scales2, np.uint16), want[2])
+    assert L.gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+        dq, dg, dk, dv, out.data_ptr(), codes.data_ptr(), None, base, capacity, T, HQ, HKV, AD, work.data_ptr(), wb,
+        None) == gx.INVALID_ARGUMENT
+
+
 def test_qk_norm_rope_and_kv_append(device, gx, orc):
     T, rot, theta, base = 5, 32, np.float32(1e7), 1234
     rng = np.random.default_rng(8)
@@ -458,6 +505,51 @@ def test_qk_norm_rope_and_kv_append(device, gx, orc):
     assert np.array_equal(host(vc, np.uint16)[base:base + T], _half(val))
     assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), cap - 2, cap,
                                              T, HKV * AD, None) == gx.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("T,base", [(5, 1234), (32, 7), (1, 2047)])
+def test_fused_rope_kv_append_equals_the_pair(device, gx, T, base):
+    """Q/K norm + RoPE with the K/V cache append in one launch == the two launches: the
+    same q/k outputs and the same cache rows, bit for bit (direct and device position);
+    the cache outside the block is untouched."""
+    rot, theta, cap = 32, np.float32(1e7), 2048
+    rng = np.random.default_rng(80 + T)
+    qin = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
+    kin = rng.standard_normal((T, HKV, AD)).astype(np.float32)
+    qw, kw = _bf16(rng.standard_normal(AD) * 0.1), _bf16(rng.standard_normal(AD) * 0.1)
+    val = rng.standard_normal((T, HKV * AD)).astype(np.float32)
+    fill = rng.integers(0, 65536, (cap, HKV * AD), dtype=np.uint16)
+    L = gx.lib()
+    qo, ko = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
+    kc, vc = dev(fill), dev(fill)
+    say("rope + kv append pair", T, base)
+    gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD,
+                                                      D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD,
+                                                      rot, base, T, theta, None))
+    gx.check(L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), base, cap,
+                                               T, HKV * AD, None))
+    want = [host(x, np.uint16) for x in (qo, ko, kc, vc)]
+    pos = dev(np.array([base], np.uint64))
+    for indirect in (False, True):
+        qo2, ko2 = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
+        kc2, vc2 = dev(fill), dev(fill)
+        say("fused rope + kv append", T, base, indirect)
+        if indirect:
+            gx.check(L.gfxinfer_launch_qk_rms_norm_rope_kv_append_block_indirect_position(
+                D_(qin), D_(qw), qo2.data_ptr(), HQ, 2 * AD, D_(kin), D_(kw), ko2.data_ptr(), HKV, AD, AD, rot,
+                D_(val), kc2.data_ptr(), vc2.data_ptr(), cap, pos.data_ptr(), T, theta, None))
+        else:
+            gx.check(L.gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
+                D_(qin), D_(qw), qo2.data_ptr(), HQ, 2 * AD, D_(kin), D_(kw), ko2.data_ptr(), HKV, AD, AD, rot,
+                D_(val), kc2.data_ptr(), vc2.data_ptr(), cap, base, T, theta, None))
+        for got, exp in zip((qo2, ko2, kc2, vc2), want):
+            assert np.array_equal(host(got, np.uint16), exp)
+    assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
+        D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD, D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD, rot,
+        D_(val), kc.data_ptr(), vc.data_ptr(), cap, cap - T + 1, T, theta, None) == gx.INVALID_ARGUMENT
+    assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_block(
+        D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD, D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD, rot,
+        None, kc.data_ptr(), vc.data_ptr(), cap, base, T, theta, None) == gx.INVALID_ARGUMENT
 
 
 def test_argmax_ties_and_mapping(device, gx, orc):
