@@ -207,6 +207,57 @@ __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
   }
 }
 
+// Register-resident form of dual_rms_norm_kernel for even rows of up to Slots * 16 *
+// 128 elements (the MTP conditioning norms): sixteen waves, lane pairs in 128-element
+// slots as in rms_norm_rows_kernel, every load issued before the first use.  Same
+// per-element arithmetic as dual_rms_norm_kernel; the sum of squares runs in the slot
+// order of rms_norm_rows_kernel.
+template <unsigned Slots>
+__global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(
+    const __half* __restrict__ left, const uint16_t* __restrict__ left_weight,
+    const __half* __restrict__ right, const uint16_t* __restrict__ right_weight,
+    __half* __restrict__ output, uint32_t elements, float epsilon, bool unit_offset) {
+  __shared__ float scratch[16];
+  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const std::size_t row = blockIdx.y;
+  const bool second = blockIdx.x != 0;
+  const __half* input = (second ? right : left) + row * elements;
+  const uint16_t* weight = second ? right_weight : left_weight;
+  output += row * 2u * elements + (second ? elements : 0);
+  uint32_t hin[Slots], wpair[Slots];
+#pragma unroll
+  for (unsigned j = 0; j < Slots; ++j) {
+    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    const uint32_t at = i < elements ? i : 0u;
+    hin[j] = *reinterpret_cast<const uint32_t*>(input + at);
+    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+  }
+  float x[Slots][2];
+  float square = 0.0F;
+#pragma unroll
+  for (unsigned j = 0; j < Slots; ++j) {
+    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    x[j][0] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] & 0xffffu)));
+    x[j][1] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] >> 16)));
+    if (i < elements) {
+      square = fmaf(x[j][0], x[j][0], square);
+      square = fmaf(x[j][1], x[j][1], square);
+    }
+  }
+  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + epsilon);
+#pragma unroll
+  for (unsigned j = 0; j < Slots; ++j) {
+    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    if (i < elements) {
+      const float w0 = bf16_to_float(static_cast<uint16_t>(wpair[j] & 0xffffu));
+      const float w1 = bf16_to_float(static_cast<uint16_t>(wpair[j] >> 16));
+      const __half n0 = to_half(x[j][0] * inverse * (unit_offset ? w0 + 1.0F : w0));
+      const __half n1 = to_half(x[j][1] * inverse * (unit_offset ? w1 + 1.0F : w1));
+      *reinterpret_cast<__half2*>(output + i) = __halves2half2(n0, n1);
+    }
+  }
+}
+
 // qwen_ops.hip:108-163: fp16(silu(g) * u), then the A4 quantizer.  One wave per
 // (token, group of 128).
 template <bool Quantize>
@@ -1084,6 +1135,28 @@ extern "C" int32_t gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
                     planes);
 }
 
+namespace {
+bool aligned4(const void* pointer) { return reinterpret_cast<std::uintptr_t>(pointer) % 4 == 0; }
+
+// Rows of up to 3 * 16 * 128 even elements with 4-byte aligned rows take the
+// register-resident kernel, others the strided one.
+void launch_dual_norm(const uint16_t* left, const uint16_t* lw, const uint16_t* right, const uint16_t* rw,
+                      uint16_t* out, std::size_t elements, uint32_t batch, float epsilon, bool unit,
+                      hipStream_t stream) {
+  const bool rows = elements % 2 == 0 && elements <= 3u * 16u * 128u && aligned4(left) && aligned4(right) &&
+                    aligned4(lw) && aligned4(rw) && aligned4(out);
+  if (rows) {
+    hipLaunchKernelGGL(dual_rms_norm_rows_kernel<3>, dim3(2, batch), dim3(1024), 0, stream,
+                       reinterpret_cast<const __half*>(left), lw, reinterpret_cast<const __half*>(right), rw,
+                       reinterpret_cast<__half*>(out), static_cast<uint32_t>(elements), epsilon, unit);
+  } else {
+    hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), 0, stream,
+                       reinterpret_cast<const __half*>(left), lw, reinterpret_cast<const __half*>(right), rw,
+                       reinterpret_cast<__half*>(out), static_cast<uint32_t>(elements), epsilon, unit);
+  }
+}
+}  // namespace
+
 extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
     const uint16_t* left, const uint16_t* left_bf16_weight, const uint16_t* right,
     const uint16_t* right_bf16_weight, uint16_t* concatenated_output, size_t elements,
@@ -1093,11 +1166,8 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
       elements > (1u << 30) || !valid_epsilon(epsilon)) {
     return fail(GFXI_INVALID_ARGUMENT, "invalid dual RMSNorm/concat arguments");
   }
-  hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     reinterpret_cast<const __half*>(left), left_bf16_weight,
-                     reinterpret_cast<const __half*>(right), right_bf16_weight,
-                     reinterpret_cast<__half*>(concatenated_output), static_cast<uint32_t>(elements),
-                     epsilon, add_unit_offset != 0);
+  launch_dual_norm(left, left_bf16_weight, right, right_bf16_weight, concatenated_output, elements, 1,
+                   epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
   return launch_status("dual RMSNorm/concat launch failed");
 }
 
@@ -1110,11 +1180,8 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat_batch(
       elements > (1u << 30) || batch == 0 || batch > 65535 || !valid_epsilon(epsilon)) {
     return fail(GFXI_INVALID_ARGUMENT, "invalid batched dual RMSNorm/concat arguments");
   }
-  hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     reinterpret_cast<const __half*>(left), left_bf16_weight,
-                     reinterpret_cast<const __half*>(right), right_bf16_weight,
-                     reinterpret_cast<__half*>(concatenated_output), static_cast<uint32_t>(elements),
-                     epsilon, add_unit_offset != 0);
+  launch_dual_norm(left, left_bf16_weight, right, right_bf16_weight, concatenated_output, elements, batch,
+                   epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
   return launch_status("batched dual RMSNorm/concat launch failed");
 }
 

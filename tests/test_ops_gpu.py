@@ -156,9 +156,9 @@ def test_residual_norm_sums_update_planes(device, gx, orc, n, batch, planes):
     assert bad == gx.INVALID_ARGUMENT
 
 
-def test_dual_rms_norm_concat(device, gx, orc):
-    n = 5120
-    rng = np.random.default_rng(3)
+@pytest.mark.parametrize("n", [5120, 130, 129, 7168])  # register-resident rows; odd / long: strided
+def test_dual_rms_norm_concat(device, gx, orc, n):
+    rng = np.random.default_rng(3 + n)
     left, right = _half(rng.standard_normal(n)), _half(rng.standard_normal(n) * 3)
     lw, rw = _bf16(rng.standard_normal(n) * 0.05), _bf16(rng.standard_normal(n) * 0.05)
     want = np.empty(2 * n, np.uint16)
