@@ -194,16 +194,35 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   const uint64_t count = base_count_of(a) + t;
   const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
   const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
-  float best = -INFINITY;
-  for (unsigned s = 0; s < used; ++s) best = fmaxf(best, ml[2 * s]);
-  float o0 = 0.0F, o1 = 0.0F, total = 0.0F;
   const float* po = a.partial_o + static_cast<std::size_t>(linear) * a.splits * kD + 2 * lane;
-  for (unsigned s = 0; s < used; ++s) {
-    const float w = expf(ml[2 * s] - best);
-    total = fmaf(ml[2 * s + 1], w, total);
-    const float2 v = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD);
-    o0 = fmaf(v.x, w, o0);
-    o1 = fmaf(v.y, w, o1);
+  // Splits in batches of kBatch with every load of a batch issued before its first use
+  // (a long context has hundreds of splits); the sums still run in split order.
+  constexpr unsigned kBatch = 8;
+  float best = -INFINITY;
+  for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
+    float m[kBatch];
+#pragma unroll
+    for (unsigned k = 0; k < kBatch; ++k) m[k] = s0 + k < used ? ml[2 * (s0 + k)] : -INFINITY;
+#pragma unroll
+    for (unsigned k = 0; k < kBatch; ++k) best = fmaxf(best, m[k]);
+  }
+  float o0 = 0.0F, o1 = 0.0F, total = 0.0F;
+  for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
+    float2 mls[kBatch], v[kBatch];
+#pragma unroll
+    for (unsigned k = 0; k < kBatch; ++k) {
+      const unsigned s = s0 + k < used ? s0 + k : s0;
+      mls[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
+      v[k] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD);
+    }
+#pragma unroll
+    for (unsigned k = 0; k < kBatch; ++k) {
+      if (s0 + k >= used) break;
+      const float w = expf(mls[k].x - best);
+      total = fmaf(mls[k].y, w, total);
+      o0 = fmaf(v[k].x, w, o0);
+      o1 = fmaf(v[k].y, w, o1);
+    }
   }
   const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
   const float g0 = 1.0F / (1.0F + expf(-g[2 * lane]));
