@@ -265,7 +265,7 @@ def packed_row_bytes(fmt: int, columns: int) -> int:
 
 
 def tile_bytes(fmt: int, rows: int, columns: int) -> int:
-    return rows * columns * (3 if fmt == W3G128 else 4) // 8
+    return rows * columns * {W2G128: 2, W3G128: 3}.get(fmt, 4) // 8
 
 
 def tile_group128(fmt, packed_codes, scales, rows, columns):

@@ -10,10 +10,11 @@
 // (converter.cpp:345-393): codes in the gfx12 tile order [16-row tile][group][32-column
 // K-step][row][fragment] and fp16 scales [tile][group][16].  That fragment order is the
 // gfx950 lane order (lane = K-step * 16 + row), and W4 fragments are the same nibble
-// bytes, so only W3 fragments differ: the gfx12 recipe packs the 32 codes of a
-// fragment sequentially (3 bits each, least significant first, code = value + 4); the
-// gfx950 layout re-packs them so that each MFMA operand register expands with one
-// shift and mask.  target_arch "gfx950" artifacts (written here) hold the gfx950
+// bytes, so only W3 and W2 fragments differ: the gfx12 recipe packs the 32 codes of a
+// W3 fragment sequentially (3 bits each, least significant first, code = value + 4)
+// and keeps W2 fragments as the packed row bytes (four 2-bit codes per byte, lowest
+// column first, code = (value + 3) / 2); the gfx950 layout re-packs both so that each
+// MFMA operand register expands with one shift and mask.  target_arch "gfx950" artifacts (written here) hold the gfx950
 // layout and load as plain copies.
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -364,6 +365,29 @@ void repack_w3_fragment(const uint8_t* gfx12, uint8_t* gfx950) {
   pack_lane_chunk(GFXI_W3G128, values, gfx950);
 }
 
+// One gfx12 W2 fragment (8 bytes: the packed row bytes of 32 columns,
+// quantization.cpp:99-103, 300-307) -> the gfx950 lane chunk.
+void repack_w2_fragment(const uint8_t* gfx12, uint8_t* gfx950) {
+  int8_t values[32];
+  for (unsigned item = 0; item < 32; ++item) {
+    const unsigned code = (static_cast<unsigned>(gfx12[item / 4]) >> ((item & 3u) * 2u)) & 3u;
+    values[item] = static_cast<int8_t>(2 * static_cast<int>(code) - 3);
+  }
+  pack_lane_chunk(GFXI_W2G128, values, gfx950);
+}
+
+void repack_fragment(int32_t format, const uint8_t* gfx12, uint8_t* gfx950) {
+  if (format == GFXI_W2G128) {
+    repack_w2_fragment(gfx12, gfx950);
+  } else {
+    repack_w3_fragment(gfx12, gfx950);
+  }
+}
+
+uint64_t code_bits(int32_t format) {
+  return format == GFXI_W2G128 ? 2 : (format == GFXI_W3G128 ? 3 : 4);
+}
+
 struct Staging {
   uint8_t* host{nullptr};
   std::size_t bytes{0};
@@ -372,9 +396,12 @@ struct Staging {
   }
 };
 
+// repack_format: 0 (plain copy), or the W2 / W3 format whose gfx12 fragments are
+// re-packed on the way.
 int32_t upload(gfxinfer_model& m, void* device, const uint8_t* source, std::size_t bytes,
-               bool repack_w3, Staging& staging) {
-  // Chunks of whole 768-byte W3 (tile, group) blocks through pinned staging memory.
+               int32_t repack_format, Staging& staging) {
+  // Chunks of whole (tile, group) blocks (512 B for W2, 768 B for W3) through pinned
+  // staging memory.
   constexpr std::size_t kChunk = 768u * 65536u;  // 48 MiB
   if (staging.host == nullptr) {
     if (auto e = hipHostMalloc(reinterpret_cast<void**>(&staging.host), kChunk); e != hipSuccess) {
@@ -385,11 +412,12 @@ int32_t upload(gfxinfer_model& m, void* device, const uint8_t* source, std::size
   }
   for (std::size_t done = 0; done < bytes; done += kChunk) {
     const std::size_t n = std::min(kChunk, bytes - done);
-    if (repack_w3) {
+    if (repack_format != 0) {
+      const std::size_t fb = lane_bytes(repack_format);
 #pragma omp parallel for schedule(static)
-      for (long long f = 0; f < static_cast<long long>(n / 12); ++f) {
-        repack_w3_fragment(source + done + static_cast<std::size_t>(f) * 12,
-                           staging.host + static_cast<std::size_t>(f) * 12);
+      for (long long f = 0; f < static_cast<long long>(n / fb); ++f) {
+        repack_fragment(repack_format, source + done + static_cast<std::size_t>(f) * fb,
+                        staging.host + static_cast<std::size_t>(f) * fb);
       }
     } else {
       std::memcpy(staging.host, source + done, n);
@@ -415,15 +443,17 @@ uint64_t element_count(const gfxinfer_artifact_tensor& t) {
 
 extern "C" int32_t gfxinfer_retile_gfx12_for_gfx950(int32_t format, const uint8_t* gfx12_codes,
                                                     size_t bytes, uint8_t* gfx950_codes) {
-  if (gfx12_codes == nullptr || gfx950_codes == nullptr ||
-      (format != GFXI_W3G128 && format != GFXI_W4G128) || bytes % lane_bytes(format) != 0) {
-    return fail(GFXI_INVALID_ARGUMENT, "gfx12 re-tiling needs W3/W4 codes of whole 32-column fragments");
+  if (gfx12_codes == nullptr || gfx950_codes == nullptr || !valid_weight_format(format) ||
+      bytes % lane_bytes(format) != 0) {
+    return fail(GFXI_INVALID_ARGUMENT, "gfx12 re-tiling needs W2/W3/W4 codes of whole 32-column fragments");
   }
   if (format == GFXI_W4G128) {
     std::memmove(gfx950_codes, gfx12_codes, bytes);
     return ok();
   }
-  for (std::size_t f = 0; f < bytes / 12; ++f) repack_w3_fragment(gfx12_codes + f * 12, gfx950_codes + f * 12);
+  // Each fragment is read whole before its chunk is written (in place is fine).
+  const std::size_t fb = lane_bytes(format);
+  for (std::size_t f = 0; f < bytes / fb; ++f) repack_fragment(format, gfx12_codes + f * fb, gfx950_codes + f * fb);
   return ok();
 }
 
@@ -488,12 +518,12 @@ extern "C" int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec
         return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " is not an int32 vector");
       }
     } else {
-      if (e.quantization != GFXI_W3G128 && e.quantization != GFXI_W4G128) {
+      if (!valid_weight_format(e.quantization)) {
         return fail(GFXI_UNSUPPORTED, "tensor " + t.name + " uses a quantization the gfx950 GEMM "
-                                      "does not run (W3G128 and W4G128 only)");
+                                      "does not run (W2G128, W3G128 and W4G128 only)");
       }
-      t.format = e.quantization;  // the artifact's recipe decides W3 or W4
-      const uint64_t bits = t.format == GFXI_W3G128 ? 3 : 4;
+      t.format = e.quantization;  // the artifact's recipe decides W2, W3 or W4
+      const uint64_t bits = code_bits(t.format);
       if (e.dtype != kDtypeU8 || e.rank != 2 || e.dimensions[0] != t.rows ||
           e.dimensions[1] != t.columns || e.data_bytes != count * bits / 8 ||
           e.aux_bytes != t.rows * (t.columns / kGroup) * 2) {
@@ -512,10 +542,10 @@ extern "C" int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec
   for (std::size_t k = 0; k < m->tensors.size() && status == GFXI_OK; ++k) {
     const Tensor& t = m->tensors[k];
     const auto& e = *source[k];
-    const bool repack = gfx12 && t.format == GFXI_W3G128;
+    const int32_t repack = gfx12 && (t.format == GFXI_W2G128 || t.format == GFXI_W3G128) ? t.format : 0;
     status = upload(*m, m->data(&t), a->map + e.data_offset, e.data_bytes, repack, staging);
     if (status == GFXI_OK && t.auxiliary_bytes != 0) {
-      status = upload(*m, m->auxiliary(&t), a->map + e.aux_offset, e.aux_bytes, false, staging);
+      status = upload(*m, m->auxiliary(&t), a->map + e.aux_offset, e.aux_bytes, 0, staging);
     }
   }
   if (status != GFXI_OK) {
@@ -628,7 +658,7 @@ extern "C" int32_t gfxinfer_model_write_artifact(const gfxinfer_model* model, co
     hd.format = lm->format;
     hd.rows = draft_count;
     hd.columns = lm->columns;
-    hd.data_bytes = draft_count * lm->columns * (lm->format == GFXI_W3G128 ? 3 : 4) / 8;
+    hd.data_bytes = draft_count * lm->columns * code_bits(lm->format) / 8;
     hd.auxiliary_bytes = draft_count * groups * 2;
     head_codes.resize(hd.data_bytes);
     head_scales.resize(hd.auxiliary_bytes);

@@ -29,9 +29,14 @@ int32_t launch_status(const char* context) {
 
 namespace {
 
-// Reference packed storage (src/quantization.cpp:126-150): W3 groups are three
-// 16-byte bit planes, W4 is two codes per byte with the even column low.
+// Reference packed storage (src/quantization.cpp:94-150): W2 is four codes per byte
+// from the low bits, W3 groups are three 16-byte bit planes, W4 is two codes per
+// byte with the even column low.
 int reference_packed_weight(int32_t format, const uint8_t* row, std::size_t column) {
+  if (format == GFXI_W2G128) {
+    const unsigned code = (row[column / 4] >> ((column & 3u) * 2u)) & 3u;
+    return 2 * static_cast<int>(code) - 3;  // quantization.cpp:50
+  }
   if (format == GFXI_W3G128) {
     const std::size_t group = column / kGroup, local = column % kGroup;
     unsigned code = 0;
@@ -85,7 +90,7 @@ extern "C" int32_t gfxinfer_tile_group128_for_gfx950(int32_t format, const uint8
                                                      size_t columns, uint8_t* tiled_codes,
                                                      uint16_t* tiled_scales_f16) {
   if (!valid_weight_format(format)) {
-    return fail(GFXI_UNSUPPORTED, "gfx950 tiling supports W3G128 and W4G128");
+    return fail(GFXI_UNSUPPORTED, "gfx950 tiling supports W2G128, W3G128 and W4G128");
   }
   if (packed_codes == nullptr || scales == nullptr || tiled_codes == nullptr ||
       tiled_scales_f16 == nullptr || rows == 0 || rows % 16 != 0 || columns == 0 ||
@@ -123,7 +128,7 @@ extern "C" int32_t gfxinfer_untile_group128_for_gfx950(int32_t format, const uin
                                                        size_t rows, size_t columns,
                                                        int8_t* weights, uint16_t* scales_f16) {
   if (!valid_weight_format(format)) {
-    return fail(GFXI_UNSUPPORTED, "gfx950 layout supports W3G128 and W4G128");
+    return fail(GFXI_UNSUPPORTED, "gfx950 layout supports W2G128, W3G128 and W4G128");
   }
   if (tiled_codes == nullptr || weights == nullptr || rows == 0 || rows % 16 != 0 ||
       columns == 0 || columns % kGroup != 0) {

@@ -101,7 +101,20 @@ __device__ __forceinline__ int encode_level(float value, float scale) {
   const float normalized = scale == 0.0F ? 0.0F : value / scale;
   const float rounded = rintf(normalized);
   int q = static_cast<int>(fminf(fmaxf(rounded, -2147483648.0F), 2147483520.0F));
-  if constexpr (Format == GFXI_W3G128) {
+  if constexpr (Format == GFXI_W2G128) {
+    // nearest_w2 (quantization.cpp:15-27): first of {-3, -1, 1, 3} with the smallest
+    // error, so ties go to the lower level and NaN maps to -3.
+    int best = -3;
+    float best_error = INFINITY;
+    for (int level = -3; level <= 3; level += 2) {
+      const float error = fabsf(normalized - static_cast<float>(level));
+      if (error < best_error) {
+        best = level;
+        best_error = error;
+      }
+    }
+    return best;
+  } else if constexpr (Format == GFXI_W3G128) {
     return max(-4, min(3, q));
   } else {
     return max(-8, min(7, q));
@@ -109,13 +122,13 @@ __device__ __forceinline__ int encode_level(float value, float scale) {
 }
 
 inline bool valid_weight_format(int32_t format) {
-  return format == GFXI_W3G128 || format == GFXI_W4G128;
+  return format == GFXI_W2G128 || format == GFXI_W3G128 || format == GFXI_W4G128;
 }
 
 // ---------------------------------------------------------------------------
 // gfx950 tile layout of a group-128 packed matrix [N, K] (N % 16 == 0).
 //
-// codes : [N/16 row tiles][K/128 groups][64 lanes][L bytes]  L = 12 (W3), 16 (W4)
+// codes : [N/16 row tiles][K/128 groups][64 lanes][L bytes]  L = 8 (W2), 12 (W3), 16 (W4)
 // scales: [N/16 row tiles][K/128 groups][16 rows] fp16
 //
 // Lane l of a (tile, group) chunk holds row m = l % 16 of the tile and the 32
@@ -138,8 +151,12 @@ inline bool valid_weight_format(int32_t format) {
 //       out7 = (S2&0xC0C0C0C0) | ((S1>>2)&0x20202020)
 // ---------------------------------------------------------------------------
 
+// W2: the 8 lane bytes are one dword D_h per K-step h; the code c = (w + 3) / 2 of
+//     operand slot (h, reg, byte) sits at bits 8*byte + 2*reg of D_h, so that
+//       out_reg = ((D_h << (6 - 2*reg)) & 0xC0C0C0C0) ^ 0xA0A0A0A0
+//     puts 64*c - 96 = 32*w (w = 2c - 3 in {-3, -1, 1, 3}) in every byte.
 __host__ __device__ constexpr unsigned lane_bytes(int32_t format) {
-  return format == GFXI_W3G128 ? 12u : 16u;
+  return format == GFXI_W2G128 ? 8u : (format == GFXI_W3G128 ? 12u : 16u);
 }
 
 // Column (0..31 within the lane's 32) of operand slot (h, reg, byte).
@@ -159,6 +176,19 @@ __host__ __device__ inline void column_slot(unsigned c, unsigned& h, unsigned& r
 // Packs 32 signed weights (column order) of one lane chunk.
 __host__ __device__ inline void pack_lane_chunk(int32_t format, const int8_t* w32,
                                                 uint8_t* out) {
+  if (format == GFXI_W2G128) {
+    uint32_t d[2] = {0, 0};
+    for (unsigned c = 0; c < 32; ++c) {
+      unsigned h, reg, byte;
+      column_slot(c, h, reg, byte);
+      const uint32_t code = static_cast<uint32_t>((w32[c] + 3) / 2) & 3u;
+      d[h] |= code << (8u * byte + 2u * reg);
+    }
+    for (unsigned h = 0; h < 2; ++h) {
+      for (unsigned i = 0; i < 4; ++i) out[4 * h + i] = static_cast<uint8_t>(d[h] >> (8 * i));
+    }
+    return;
+  }
   if (format == GFXI_W4G128) {
     for (unsigned i = 0; i < 16; ++i) {
       out[i] = static_cast<uint8_t>((static_cast<unsigned>(w32[2 * i]) & 0xfu) |
@@ -198,6 +228,12 @@ __host__ __device__ inline void pack_lane_chunk(int32_t format, const int8_t* w3
 // Signed weight at lane-chunk column c (0..31).
 __host__ __device__ inline int unpack_lane_code(int32_t format, const uint8_t* chunk,
                                                 unsigned c) {
+  if (format == GFXI_W2G128) {
+    unsigned h, reg, byte;
+    column_slot(c, h, reg, byte);
+    const unsigned code = (chunk[4 * h + byte] >> (2u * reg)) & 3u;
+    return 2 * static_cast<int>(code) - 3;
+  }
   if (format == GFXI_W4G128) {
     const unsigned v = (chunk[c / 2] >> ((c & 1u) * 4u)) & 0xfu;
     return v >= 8u ? static_cast<int>(v) - 16 : static_cast<int>(v);

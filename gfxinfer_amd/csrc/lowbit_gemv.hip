@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void quantize_group128_kernel(
   // choose_scale, quantization.cpp:67-92
   float scale = 1.0F;
   if (maximum != 0.0F) {
-    scale = maximum / (Format == GFXI_W3G128 ? 4.0F : 8.0F);
+    scale = maximum / (Format == GFXI_W2G128 ? 3.0F : (Format == GFXI_W3G128 ? 4.0F : 8.0F));
     for (int iteration = 0; iteration < 4; ++iteration) {
       double numerator = 0.0;
       double denominator = 0.0;
@@ -156,6 +156,18 @@ __device__ __forceinline__ void expand_w3(unsigned s0, unsigned s1, unsigned s2,
   h1[1] = static_cast<int>((s2 << 2) & E);
   h1[2] = static_cast<int>((s0 & 0xC0C0C0C0u) | ((s1 >> 1) & 0x20202020u));
   h1[3] = static_cast<int>((s2 & 0xC0C0C0C0u) | ((s1 >> 2) & 0x20202020u));
+}
+
+// One W2 dword (16 columns) -> four operand registers (value 32*w): the code of
+// register reg sits at bits 2*reg of each byte; 64*c - 96 = ((c << 6) ^ 0xA0) per byte.
+__device__ __forceinline__ i32x4 expand_w2(unsigned d) {
+  constexpr unsigned M = 0xC0C0C0C0u, X = 0xA0A0A0A0u;
+  i32x4 r;
+  r[0] = static_cast<int>(((d << 6) & M) ^ X);
+  r[1] = static_cast<int>(((d << 4) & M) ^ X);
+  r[2] = static_cast<int>(((d << 2) & M) ^ X);
+  r[3] = static_cast<int>((d & M) ^ X);
+  return r;
 }
 
 // Sixteen int8 activations in column order -> operand registers in slot order.
@@ -335,8 +347,8 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   constexpr unsigned CHG = CH * GP;      // groups per chunk
   constexpr unsigned AGB = ABits == 4 ? 64u : 128u;  // activation bytes per token per group
   constexpr float kInvF =
-      1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
-  constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
+      1.0F / static_cast<float>((Format == GFXI_W4G128 ? 16 : 32) * (ABits == 4 ? 16 : 1));
+  constexpr int kShift = (Format == GFXI_W4G128 ? 4 : 5) + (ABits == 4 ? 4 : 0);
   constexpr bool kDma = ABits == 4;  // A4 pieces go straight from memory to LDS
 
   extern __shared__ __align__(16) uint8_t lds_all[];
@@ -473,7 +485,11 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       for (unsigned j = 0; j < GP; ++j) {
         // groups past the range's end load its last group again (never used)
         const unsigned g_offset = min(g0 + ci * GP + j, span.end - 1u) * 64u * LB;
-        if constexpr (Format == GFXI_W3G128) {
+        if constexpr (Format == GFXI_W2G128) {
+          const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(weights, w_voffset, g_offset, kStreaming);
+          wreg[ci][j][0] = w[0];
+          wreg[ci][j][1] = w[1];
+        } else if constexpr (Format == GFXI_W3G128) {
           const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
           wreg[ci][j][0] = w[0];
           wreg[ci][j][1] = w[1];
@@ -540,7 +556,10 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
       for (unsigned j = 0; j < GP; ++j) {
         if (pg + j >= span.end) break;  // wave-uniform: partial last pack of the range
         i32x4 a0, a1;
-        if constexpr (Format == GFXI_W3G128) {
+        if constexpr (Format == GFXI_W2G128) {
+          a0 = expand_w2(wreg[ci][j][0]);
+          a1 = expand_w2(wreg[ci][j][1]);
+        } else if constexpr (Format == GFXI_W3G128) {
           expand_w3(wreg[ci][j][0], wreg[ci][j][1], wreg[ci][j][2], a0, a1);
         } else {
           a0 = expand_nibbles(wreg[ci][j][0], wreg[ci][j][1]);
@@ -713,8 +732,8 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
   constexpr unsigned AGB = ABits == 4 ? 64u : 128u;   // activation bytes per token per group
   constexpr unsigned AD = ABits == 4 ? 4u : 8u;       // activation dwords per lane per group
   constexpr float kInvF =
-      1.0F / static_cast<float>((Format == GFXI_W3G128 ? 32 : 16) * (ABits == 4 ? 16 : 1));
-  constexpr int kShift = (Format == GFXI_W3G128 ? 5 : 4) + (ABits == 4 ? 4 : 0);
+      1.0F / static_cast<float>((Format == GFXI_W4G128 ? 16 : 32) * (ABits == 4 ? 16 : 1));
+  constexpr int kShift = (Format == GFXI_W4G128 ? 4 : 5) + (ABits == 4 ? 4 : 0);
   constexpr unsigned kOut = 0x80000000u;              // voffset that reads zeros
 
   extern __shared__ __align__(16) uint8_t lds_all[];
@@ -859,7 +878,11 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
 #pragma unroll
         for (unsigned j = 0; j < GP; ++j) {
           const unsigned g_offset = r * tile_bytes + min(pg + j, span.end - 1u) * 64u * LB;
-          if constexpr (Format == GFXI_W3G128) {
+          if constexpr (Format == GFXI_W2G128) {
+            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(weights, w_voffset, g_offset, kStreaming);
+            wreg[r][ci * GP + j][0] = w[0];
+            wreg[r][ci * GP + j][1] = w[1];
+          } else if constexpr (Format == GFXI_W3G128) {
             const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(weights, w_voffset, g_offset, kStreaming);
             wreg[r][ci * GP + j][0] = w[0];
             wreg[r][ci * GP + j][1] = w[1];
@@ -947,7 +970,10 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
           if (pg + j >= span.end) break;  // wave-uniform: partial last pack of the range
           i32x4 a0, a1;
           const unsigned* w = wreg[r][ci * GP + j];
-          if constexpr (Format == GFXI_W3G128) {
+          if constexpr (Format == GFXI_W2G128) {
+            a0 = expand_w2(w[0]);
+            a1 = expand_w2(w[1]);
+          } else if constexpr (Format == GFXI_W3G128) {
             expand_w3(w[0], w[1], w[2], a0, a1);
           } else {
             a0 = expand_nibbles(w[0], w[1]);
@@ -1314,7 +1340,9 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
 
 template <int ABits, bool HalfOut, bool Partials>
 void dispatch_gemm(int32_t format, const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
-  if (format == GFXI_W3G128) {
+  if (format == GFXI_W2G128) {
+    launch_gemm_kernel<GFXI_W2G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+  } else if (format == GFXI_W3G128) {
     launch_gemm_kernel<GFXI_W3G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
   } else {
     launch_gemm_kernel<GFXI_W4G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
@@ -1337,7 +1365,7 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
                    unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0,
                    uint32_t splits = 1) {
   if (!valid_weight_format(format)) {
-    return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W3G128 and W4G128");
+    return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W2G128, W3G128 and W4G128");
   }
   if (count == 0 || count > 4 || activations == nullptr ||
       (partials == nullptr && activation_scales == nullptr) || columns == 0 ||
@@ -1442,7 +1470,7 @@ int32_t row_gather_entry(int32_t format, const uint8_t* weights, const uint16_t*
                          uint16_t* output, std::size_t row, const uint32_t* indirect,
                          std::size_t rows, std::size_t columns, hipStream_t stream) {
   if (!valid_weight_format(format)) {
-    return fail(GFXI_UNSUPPORTED, "tiled row gather supports W3G128 and W4G128");
+    return fail(GFXI_UNSUPPORTED, "tiled row gather supports W2G128, W3G128 and W4G128");
   }
   if (weights == nullptr || scales == nullptr || output == nullptr || rows == 0 ||
       rows % 16 != 0 || columns == 0 || columns % kGroup != 0 ||
@@ -1453,7 +1481,10 @@ int32_t row_gather_entry(int32_t format, const uint8_t* weights, const uint16_t*
   const dim3 grid(static_cast<unsigned>((columns + threads - 1) / threads));
   const auto* ws = reinterpret_cast<const __half*>(scales);
   auto* out = reinterpret_cast<__half*>(output);
-  if (format == GFXI_W3G128) {
+  if (format == GFXI_W2G128) {
+    hipLaunchKernelGGL(row_gather_kernel<GFXI_W2G128>, grid, dim3(threads), 0, stream, weights, ws,
+                       out, row, indirect, rows, columns);
+  } else if (format == GFXI_W3G128) {
     hipLaunchKernelGGL(row_gather_kernel<GFXI_W3G128>, grid, dim3(threads), 0, stream, weights, ws,
                        out, row, indirect, rows, columns);
   } else {
@@ -1475,7 +1506,7 @@ extern "C" int32_t gfxinfer_launch_quantize_group128_gfx950(int32_t format, cons
                                                             int32_t* non_finite_flag,
                                                             void* stream) {
   if (!valid_weight_format(format)) {
-    return fail(GFXI_UNSUPPORTED, "device quantizer supports W3G128 and W4G128");
+    return fail(GFXI_UNSUPPORTED, "device quantizer supports W2G128, W3G128 and W4G128");
   }
   if (weights == nullptr || tiled_codes == nullptr || tiled_scales_f16 == nullptr || rows == 0 ||
       rows % 16 != 0 || columns == 0 || columns % kGroup != 0) {
@@ -1490,7 +1521,10 @@ extern "C" int32_t gfxinfer_launch_quantize_group128_gfx950(int32_t format, cons
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   auto s = static_cast<hipStream_t>(stream);
   auto* scales = reinterpret_cast<__half*>(tiled_scales_f16);
-  if (format == GFXI_W3G128) {
+  if (format == GFXI_W2G128) {
+    hipLaunchKernelGGL(quantize_group128_kernel<GFXI_W2G128>, grid, dim3(256), 0, s, weights, rows,
+                       columns, groups, tiled_codes, scales, non_finite_flag);
+  } else if (format == GFXI_W3G128) {
     hipLaunchKernelGGL(quantize_group128_kernel<GFXI_W3G128>, grid, dim3(256), 0, s, weights, rows,
                        columns, groups, tiled_codes, scales, non_finite_flag);
   } else {

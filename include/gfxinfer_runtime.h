@@ -141,9 +141,10 @@ const void* gfxinfer_artifact_bytes(const gfxinfer_artifact* artifact, uint64_t 
 uint64_t gfxinfer_crc64_ecma(uint64_t state, const void* bytes, size_t count);
 
 /* No reference counterpart: converts codes in the reference's gfx12 tile order
- * (quantization.cpp:253-318, the "gfx1200" recipe) to the gfx950 tile layout (W3
+ * (quantization.cpp:253-318, the "gfx1200" recipe) to the gfx950 tile layout (W2 and W3
  * fragments re-packed, W4 copied); the loader's conversion, on the host.  `bytes` is a
- * multiple of the 32-column fragment (12 B W3, 16 B W4); scales need no conversion. */
+ * multiple of the 32-column fragment (8 B W2, 12 B W3, 16 B W4); scales need no
+ * conversion. */
 int32_t gfxinfer_retile_gfx12_for_gfx950(int32_t format, const uint8_t* gfx12_codes, size_t bytes,
                                          uint8_t* gfx950_codes);
 

@@ -12,11 +12,11 @@ from __future__ import annotations
 
 import numpy as np
 
-W3, W4 = 2, 3
+W2, W3, W4 = 1, 2, 3
 
 
 def lane_bytes(fmt: int) -> int:
-    return 12 if fmt == W3 else 16
+    return {W2: 8, W3: 12}.get(fmt, 16)
 
 
 def i8(x: np.ndarray) -> np.ndarray:
@@ -28,6 +28,12 @@ def expand_nibbles(x0, x1):
     """expand_nibbles(): four operand registers (value 16*x)."""
     M = np.uint32(0xF0F0F0F0)
     return [(x0 << np.uint32(4)) & M, x0 & M, (x1 << np.uint32(4)) & M, x1 & M]
+
+
+def expand_w2(d):
+    """expand_w2(): four operand registers (value 32*w, w = 2c - 3)."""
+    M, X = np.uint32(0xC0C0C0C0), np.uint32(0xA0A0A0A0)
+    return [((d << np.uint32(s)) & M) ^ X for s in (6, 4, 2, 0)]
 
 
 def expand_w3(s0, s1, s2):
@@ -67,10 +73,8 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
     pack and the token slot n % TPAD (+16 t) is below the batch."""
     G = columns // 128
     LB = lane_bytes(fmt)
-    F = (32 if fmt == W3 else 16) * (16 if abits == 4 else 1)
-    if batch <= 4:
-        GP, NTB = 4, 1
-    elif batch <= 8:
+    F = (16 if fmt == W4 else 32) * (16 if abits == 4 else 1)
+    if batch <= 8:
         GP, NTB = 2, 1
     elif batch <= 16:
         GP, NTB = 1, 1
@@ -93,7 +97,9 @@ def simulate_partials(fmt: int, tiled: np.ndarray, abits: int, acts: np.ndarray,
                 if g >= G:
                     break
                 d = chunks[tile, g].copy().view(np.uint32).reshape(64, LB // 4)
-                if fmt == W3:
+                if fmt == W2:
+                    h0, h1 = expand_w2(d[:, 0]), expand_w2(d[:, 1])
+                elif fmt == W3:
                     h0, h1 = expand_w3(d[:, 0], d[:, 1], d[:, 2])
                 else:
                     h0, h1 = expand_nibbles(d[:, 0], d[:, 1]), expand_nibbles(d[:, 2], d[:, 3])

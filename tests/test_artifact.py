@@ -83,6 +83,27 @@ def test_gfx12_tiles_convert_to_gfx950_tiles(orc, gx, name, fmt, rows, cols):
     assert np.array_equal(scales, want_scales)
 
 
+@pytest.mark.parametrize("rows,cols", [(16, 128), (32, 640)])
+def test_gfx12_w2_tiles_convert_to_gfx950_tiles(orc, gx, rows, cols):
+    """W2 (no fixture holds it): the reference quantizer and gfx12 tiler compiled in place
+    make the gfx1200-recipe codes; re-tiling them gives the library's own gfx950 tiling
+    of the same packed codes, and the codes decode to the reference's levels."""
+    if orc.ref_lib() is None:
+        pytest.skip("oracle/_ref (the reference quantizer and gfx12 tiler) is not built")
+    from gfxinfer_amd.runtime import retile_gfx12_for_gfx950
+    w = (np.random.default_rng(rows + cols).standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    status, codes, scales = orc.ref_quantize_group128(w, 1)
+    assert status == 0
+    gfx12, gscales = orc.ref_tile_gfx12(codes, scales, rows, cols, 1)
+    want, want_scales = gx.tile_group128(1, codes, scales, rows, cols)
+    got = retile_gfx12_for_gfx950(1, gfx12)
+    assert np.array_equal(got, want)
+    assert np.array_equal(orc.f32_to_f16_bits(gscales).reshape(-1), want_scales)
+    wq, _ = gx.untile_group128(1, got, want_scales, rows, cols)
+    assert np.array_equal(wq, orc.unpack_weights(codes, rows, cols, 1))
+    assert set(np.unique(wq)) <= {-3, -1, 1, 3}
+
+
 def _corrupt(tmp_path, edit):
     path = tmp_path / "c.gfxi"
     shutil.copy(FIXTURE, path)

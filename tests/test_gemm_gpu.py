@@ -77,7 +77,7 @@ def _pad16(w):
     return out
 
 
-@pytest.mark.parametrize("fmt,name", [(2, "w3"), (3, "w4")])
+@pytest.mark.parametrize("fmt,name", [(1, "w2"), (2, "w3"), (3, "w4")])
 def test_device_quantizer_matches_reference_golden(device, gx, orc, fmt, name):
     from conftest import golden
     g = golden(f"quant_{name}.npz")
@@ -155,6 +155,9 @@ CASES = [
     (2, 4, 5120, 17408, 32), (3, 4, 5120, 17408, 16), (2, 8, 5120, 17408, 32),
     # 9-32 tokens (LDS-ring kernel): workgroups of 4 or 8 tiles with a short last one
     (2, 4, 48, 256, 13), (3, 4, 112, 384, 32), (3, 4, 16480, 5120, 32), (2, 4, 34816, 5120, 24),
+    # W2 (reference formats W2/W3/W4; no BASELINE config uses it)
+    (1, 4, 64, 640, 1), (1, 4, 64, 640, 5), (1, 4, 64, 640, 17), (1, 4, 64, 640, 32),
+    (1, 8, 64, 640, 3), (1, 8, 64, 640, 16), (1, 4, 17408, 5120, 5), (1, 4, 5120, 17408, 32),
 ]
 
 
@@ -184,7 +187,7 @@ def test_gemm_partials_bit_exact_and_output(device, gx, orc, fmt, abits, rows, c
 @pytest.mark.parametrize("fmt,rows,cols,batch,splits", [
     (2, 5120, 17408, 5, 4), (2, 5120, 17408, 32, 4), (3, 5120, 17408, 5, 8), (3, 5120, 6144, 5, 4),
     (3, 5120, 6144, 16, 3), (2, 5120, 5120, 9, 5), (2, 64, 640, 1, 5), (3, 64, 640, 32, 2),
-    (2, 48, 1024, 7, 8),
+    (2, 48, 1024, 7, 8), (1, 5120, 17408, 5, 4), (1, 64, 640, 32, 2),
 ])
 def test_gemm_split_planes_sum_to_product(device, gx, orc, fmt, rows, cols, batch, splits):
     """Split-K planes: plane s = the epilogue over the s-th of `splits` equal pack ranges
@@ -307,7 +310,7 @@ def test_quantize_then_gemm_matches_float_reference(device, gx, orc):
     assert np.abs(got - out).max() <= 1e-4 * np.abs(out).max()
 
 
-@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("fmt", [1, 2, 3])
 def test_row_gather(device, gx, orc, fmt):
     rows, cols = 64, 5120
     p = _problem(orc, gx, fmt, 4, rows, cols, 1, seed=55)

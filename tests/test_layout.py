@@ -25,7 +25,7 @@ def test_packed_row_bytes_matches_reference(gx, orc):
             assert gx.packed_row_bytes(fmt, k) == orc.packed_row_bytes(fmt, k)
 
 
-@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("fmt", [1, 2, 3])
 @pytest.mark.parametrize("shape", [(16, 128), (32, 256), (48, 640)])
 def test_tile_untile_round_trip(gx, orc, fmt, shape):
     rows, cols = shape
@@ -33,19 +33,23 @@ def test_tile_untile_round_trip(gx, orc, fmt, shape):
     w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
     _, codes, scales = orc.quantize_group128(w, fmt)
     tiled, tscales = gx.tile_group128(fmt, codes, scales, rows, cols)
-    assert tiled.nbytes == rows * cols * (3 if fmt == 2 else 4) // 8
+    assert tiled.nbytes == rows * cols * {1: 2, 2: 3, 3: 4}[fmt] // 8
     wq, s16 = gx.untile_group128(fmt, tiled, tscales, rows, cols)
     assert np.array_equal(wq, orc.unpack_weights(codes, rows, cols, fmt))
     assert np.array_equal(s16, orc.f32_to_f16_bits(scales))
 
 
-@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("fmt", [1, 2, 3])
 def test_operand_expansion_bit_tricks(gx, orc, fmt):
-    """Every lane chunk expands to 16*w (W4) / 32*w (W3) in the documented slot order."""
+    """Every lane chunk expands to 16*w (W4) / 32*w (W2, W3) in the documented slot order."""
     rows, cols = 32, 256
     rng = np.random.default_rng(9)
-    lo, hi = (-4, 4) if fmt == 2 else (-8, 8)
-    wint = rng.integers(lo, hi, size=(rows, cols)).astype(np.int8)
+    if fmt == 1:
+        wint = rng.choice(np.array([-3, -1, 1, 3], np.int8), size=(rows, cols))
+        hi = 4
+    else:
+        lo, hi = (-4, 4) if fmt == 2 else (-8, 8)
+        wint = rng.integers(lo, hi, size=(rows, cols)).astype(np.int8)
     # build reference-packed codes from integers via the oracle's storage order
     scales = np.ones((rows, cols // 128), np.float32)
     w = wint.astype(np.float32)
@@ -55,11 +59,13 @@ def test_operand_expansion_bit_tricks(gx, orc, fmt):
     tiled, ts = gx.tile_group128(fmt, codes, sc, rows, cols)
     LB = KM.lane_bytes(fmt)
     chunks = tiled.reshape(rows // 16, cols // 128, 64, LB)
-    factor = 32 if fmt == 2 else 16
+    factor = 16 if fmt == 3 else 32
     for t in range(rows // 16):
         for g in range(cols // 128):
             d = chunks[t, g].copy().view(np.uint32).reshape(64, LB // 4)
-            if fmt == 2:
+            if fmt == 1:
+                h0, h1 = KM.expand_w2(d[:, 0]), KM.expand_w2(d[:, 1])
+            elif fmt == 2:
                 h0, h1 = KM.expand_w3(d[:, 0], d[:, 1], d[:, 2])
             else:
                 h0, h1 = KM.expand_nibbles(d[:, 0], d[:, 1]), KM.expand_nibbles(d[:, 2], d[:, 3])
@@ -73,7 +79,8 @@ def test_operand_expansion_bit_tricks(gx, orc, fmt):
                         assert b[lane, j] == factor * int(wq[t * 16 + m, col])
 
 
-@pytest.mark.parametrize("fmt,abits,batch", [(2, 4, 1), (2, 4, 5), (3, 4, 8), (2, 8, 3), (3, 8, 12), (2, 4, 20)])
+@pytest.mark.parametrize("fmt,abits,batch", [(2, 4, 1), (2, 4, 5), (3, 4, 8), (2, 8, 3), (3, 8, 12), (2, 4, 20),
+                                              (1, 4, 5), (1, 8, 3), (1, 4, 17)])
 def test_kernel_lane_mapping_model(gx, orc, fmt, abits, batch):
     """The kernel's packing of groups/tokens into MFMA columns reproduces the exact
     per-group integer dot products (oracle) under the symmetric-operand MFMA model."""
@@ -101,8 +108,8 @@ def test_launchers_validate_before_launching(gx):
     L = gx.lib()
     st = L.gfxinfer_launch_gfx950_i4_gemm(2, None, None, None, None, None, 16, 128, 1, 1, None)
     assert st == gx.INVALID_ARGUMENT and "batch" in gx.last_error()
-    st = L.gfxinfer_launch_gfx950_i4_gemm(1, None, None, None, None, None, 16, 128, 1, 1, None)
-    assert st == gx.UNSUPPORTED
+    st = L.gfxinfer_launch_gfx950_i4_gemm(4, None, None, None, None, None, 16, 128, 1, 1, None)
+    assert st == gx.UNSUPPORTED  # W8G128: declared, not implemented (as in the reference)
     fake = 1 << 20  # aligned non-null addresses; validation fails before any use
     st = L.gfxinfer_launch_gfx950_i4_gemm(2, fake, fake, fake, fake, fake, 17, 128, 1, 1, None)
     assert st == gx.INVALID_ARGUMENT
@@ -120,7 +127,7 @@ def test_launchers_validate_before_launching(gx):
     assert st == gx.INVALID_ARGUMENT
     st = L.gfxinfer_launch_lowbit_row_gather_tiled(2, fake, fake, fake, 16, 16, 128, None)
     assert st == gx.INVALID_ARGUMENT  # row >= rows
-    st = L.gfxinfer_launch_quantize_group128_gfx950(1, fake, 16, 128, fake, fake, None, None)
+    st = L.gfxinfer_launch_quantize_group128_gfx950(4, fake, 16, 128, fake, fake, None, None)
     assert st == gx.UNSUPPORTED
     with pytest.raises(gx.GfxinferError) as err:
         gx.check(gx.INVALID_ARGUMENT)
