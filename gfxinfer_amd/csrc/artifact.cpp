@@ -180,130 +180,132 @@ extern "C" uint64_t gfxinfer_crc64_ecma(uint64_t state, const void* bytes, size_
 // spirit (a file that fails one is rejected before any payload is used).
 extern "C" int32_t gfxinfer_artifact_open(const char* path, int32_t verify_checksums,
                                           gfxinfer_artifact** out) {
-  if (path == nullptr || out == nullptr) {
-    return fail(GFXI_INVALID_ARGUMENT, "artifact open needs a path and an output handle");
-  }
-  *out = nullptr;
-  auto a = std::make_unique<gfxinfer_artifact>();
-  a->fd = ::open(path, O_RDONLY | O_CLOEXEC);
-  if (a->fd < 0) return fail(GFXI_IO_ERROR, std::string("cannot open ") + path + ": " + std::strerror(errno));
-  struct stat st {};
-  if (::fstat(a->fd, &st) != 0) {
-    return fail(GFXI_IO_ERROR, std::string("cannot stat ") + path + ": " + std::strerror(errno));
-  }
-  if (st.st_size < static_cast<off_t>(sizeof(DiskHeader))) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "artifact is smaller than its header");
-  }
-  a->bytes = static_cast<std::size_t>(st.st_size);
-  void* m = ::mmap(nullptr, a->bytes, PROT_READ, MAP_PRIVATE, a->fd, 0);
-  if (m == MAP_FAILED) {
-    return fail(GFXI_IO_ERROR, std::string("cannot map ") + path + ": " + std::strerror(errno));
-  }
-  a->map = static_cast<const uint8_t*>(m);
+  return guarded([&]() -> int32_t {
+    if (path == nullptr || out == nullptr) {
+      return fail(GFXI_INVALID_ARGUMENT, "artifact open needs a path and an output handle");
+    }
+    *out = nullptr;
+    auto a = std::make_unique<gfxinfer_artifact>();
+    a->fd = ::open(path, O_RDONLY | O_CLOEXEC);
+    if (a->fd < 0) return fail(GFXI_IO_ERROR, std::string("cannot open ") + path + ": " + std::strerror(errno));
+    struct stat st {};
+    if (::fstat(a->fd, &st) != 0) {
+      return fail(GFXI_IO_ERROR, std::string("cannot stat ") + path + ": " + std::strerror(errno));
+    }
+    if (st.st_size < static_cast<off_t>(sizeof(DiskHeader))) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "artifact is smaller than its header");
+    }
+    a->bytes = static_cast<std::size_t>(st.st_size);
+    void* m = ::mmap(nullptr, a->bytes, PROT_READ, MAP_PRIVATE, a->fd, 0);
+    if (m == MAP_FAILED) {
+      return fail(GFXI_IO_ERROR, std::string("cannot map ") + path + ": " + std::strerror(errno));
+    }
+    a->map = static_cast<const uint8_t*>(m);
 
-  DiskHeader h;
-  std::memcpy(&h, a->map, sizeof h);
-  if (std::memcmp(h.magic, kMagic, sizeof kMagic) != 0) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "invalid .gfxi magic");
-  }
-  if (h.version != kFormatVersion || h.header_bytes != sizeof(DiskHeader)) {
-    return fail(GFXI_UNSUPPORTED, "unsupported .gfxi artifact version");
-  }
-  if (h.endian_tag != kEndianTag) return fail(GFXI_UNSUPPORTED, "artifact byte order is unsupported");
-  if (h.directory_entry_bytes != sizeof(DiskEntry)) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "unexpected directory entry size");
-  }
-  if (h.file_bytes != a->bytes) return fail(GFXI_CORRUPT_ARTIFACT, "artifact length does not match header");
-  const uint64_t directory_bytes = static_cast<uint64_t>(h.tensor_count) * sizeof(DiskEntry);
-  if (!in_file(h.directory_offset, directory_bytes, h.file_bytes) ||
-      !in_file(h.strings_offset, h.strings_bytes, h.file_bytes) ||
-      !in_file(h.data_offset, h.data_bytes, h.file_bytes) ||
-      h.strings_offset != h.directory_offset + directory_bytes ||
-      h.data_offset < h.strings_offset + h.strings_bytes) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "artifact section bounds are invalid");
-  }
-  if (verify_checksums != 0 &&
-      crc64_update(0, a->map + h.directory_offset, directory_bytes + h.strings_bytes) !=
-          h.manifest_crc64) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "artifact manifest checksum mismatch");
-  }
-  const std::string arch = fixed(h.target_arch), model = fixed(h.model_id),
-                    weights = fixed(h.weights_id), recipe = fixed(h.recipe_id);
-  if (arch.empty() || model.empty() || weights.empty() || recipe.empty()) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "artifact identity is incomplete");
-  }
-  std::memcpy(a->identity.target_arch, h.target_arch, sizeof h.target_arch);
-  std::memcpy(a->identity.model_id, h.model_id, sizeof h.model_id);
-  std::memcpy(a->identity.weights_id, h.weights_id, sizeof h.weights_id);
-  std::memcpy(a->identity.recipe_id, h.recipe_id, sizeof h.recipe_id);
+    DiskHeader h;
+    std::memcpy(&h, a->map, sizeof h);
+    if (std::memcmp(h.magic, kMagic, sizeof kMagic) != 0) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "invalid .gfxi magic");
+    }
+    if (h.version != kFormatVersion || h.header_bytes != sizeof(DiskHeader)) {
+      return fail(GFXI_UNSUPPORTED, "unsupported .gfxi artifact version");
+    }
+    if (h.endian_tag != kEndianTag) return fail(GFXI_UNSUPPORTED, "artifact byte order is unsupported");
+    if (h.directory_entry_bytes != sizeof(DiskEntry)) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "unexpected directory entry size");
+    }
+    if (h.file_bytes != a->bytes) return fail(GFXI_CORRUPT_ARTIFACT, "artifact length does not match header");
+    const uint64_t directory_bytes = static_cast<uint64_t>(h.tensor_count) * sizeof(DiskEntry);
+    if (!in_file(h.directory_offset, directory_bytes, h.file_bytes) ||
+        !in_file(h.strings_offset, h.strings_bytes, h.file_bytes) ||
+        !in_file(h.data_offset, h.data_bytes, h.file_bytes) ||
+        h.strings_offset != h.directory_offset + directory_bytes ||
+        h.data_offset < h.strings_offset + h.strings_bytes) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "artifact section bounds are invalid");
+    }
+    if (verify_checksums != 0 &&
+        crc64_update(0, a->map + h.directory_offset, directory_bytes + h.strings_bytes) !=
+            h.manifest_crc64) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "artifact manifest checksum mismatch");
+    }
+    const std::string arch = fixed(h.target_arch), model = fixed(h.model_id),
+                      weights = fixed(h.weights_id), recipe = fixed(h.recipe_id);
+    if (arch.empty() || model.empty() || weights.empty() || recipe.empty()) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "artifact identity is incomplete");
+    }
+    std::memcpy(a->identity.target_arch, h.target_arch, sizeof h.target_arch);
+    std::memcpy(a->identity.model_id, h.model_id, sizeof h.model_id);
+    std::memcpy(a->identity.weights_id, h.weights_id, sizeof h.weights_id);
+    std::memcpy(a->identity.recipe_id, h.recipe_id, sizeof h.recipe_id);
 
-  const char* strings = reinterpret_cast<const char*>(a->map + h.strings_offset);
-  std::vector<std::pair<uint64_t, uint64_t>> ranges;
-  a->names.reserve(h.tensor_count);
-  a->tensors.reserve(h.tensor_count);
-  for (uint32_t i = 0; i < h.tensor_count; ++i) {
-    DiskEntry e;
-    std::memcpy(&e, a->map + h.directory_offset + static_cast<uint64_t>(i) * sizeof(DiskEntry), sizeof e);
-    if (e.rank > 4 || e.dtype < kDtypeU8 || e.dtype > kDtypeF32 || e.quantization > 5 ||
-        e.name_bytes == 0 || !in_file(e.name_offset, e.name_bytes, h.strings_bytes)) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor directory entry");
+    const char* strings = reinterpret_cast<const char*>(a->map + h.strings_offset);
+    std::vector<std::pair<uint64_t, uint64_t>> ranges;
+    a->names.reserve(h.tensor_count);
+    a->tensors.reserve(h.tensor_count);
+    for (uint32_t i = 0; i < h.tensor_count; ++i) {
+      DiskEntry e;
+      std::memcpy(&e, a->map + h.directory_offset + static_cast<uint64_t>(i) * sizeof(DiskEntry), sizeof e);
+      if (e.rank > 4 || e.dtype < kDtypeU8 || e.dtype > kDtypeF32 || e.quantization > 5 ||
+          e.name_bytes == 0 || !in_file(e.name_offset, e.name_bytes, h.strings_bytes)) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor directory entry");
+      }
+      std::string name(strings + e.name_offset, e.name_bytes);
+      if (!valid_name(name) || a->index.count(name) != 0) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "invalid or duplicate tensor name: " + name);
+      }
+      if (e.alignment < kFileAlignment || (e.alignment & (e.alignment - 1)) != 0 ||
+          e.data_offset % e.alignment != 0 || !in_file(e.data_offset, e.data_bytes, h.file_bytes) ||
+          e.data_offset < h.data_offset) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor payload bounds: " + name);
+      }
+      if (e.aux_bytes != 0 && (e.aux_offset % e.alignment != 0 ||
+                               !in_file(e.aux_offset, e.aux_bytes, h.file_bytes) ||
+                               e.aux_offset < h.data_offset)) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor auxiliary bounds: " + name);
+      }
+      gfxinfer_artifact_tensor t{};
+      t.dtype = e.dtype;
+      t.quantization = e.quantization;
+      t.rank = e.rank;
+      t.flags = e.flags;
+      t.alignment = e.alignment;
+      std::memcpy(t.dimensions, e.dimensions, sizeof t.dimensions);
+      t.data_offset = e.data_offset;
+      t.data_bytes = e.data_bytes;
+      t.aux_offset = e.aux_offset;
+      t.aux_bytes = e.aux_bytes;
+      t.data_crc64 = e.data_crc64;
+      a->index.emplace(name, a->tensors.size());
+      a->names.push_back(std::move(name));
+      a->tensors.push_back(t);
+      ranges.emplace_back(e.data_offset, e.data_offset + e.data_bytes);
+      if (e.aux_bytes != 0) ranges.emplace_back(e.aux_offset, e.aux_offset + e.aux_bytes);
     }
-    std::string name(strings + e.name_offset, e.name_bytes);
-    if (!valid_name(name) || a->index.count(name) != 0) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "invalid or duplicate tensor name: " + name);
-    }
-    if (e.alignment < kFileAlignment || (e.alignment & (e.alignment - 1)) != 0 ||
-        e.data_offset % e.alignment != 0 || !in_file(e.data_offset, e.data_bytes, h.file_bytes) ||
-        e.data_offset < h.data_offset) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor payload bounds: " + name);
-    }
-    if (e.aux_bytes != 0 && (e.aux_offset % e.alignment != 0 ||
-                             !in_file(e.aux_offset, e.aux_bytes, h.file_bytes) ||
-                             e.aux_offset < h.data_offset)) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor auxiliary bounds: " + name);
-    }
-    gfxinfer_artifact_tensor t{};
-    t.dtype = e.dtype;
-    t.quantization = e.quantization;
-    t.rank = e.rank;
-    t.flags = e.flags;
-    t.alignment = e.alignment;
-    std::memcpy(t.dimensions, e.dimensions, sizeof t.dimensions);
-    t.data_offset = e.data_offset;
-    t.data_bytes = e.data_bytes;
-    t.aux_offset = e.aux_offset;
-    t.aux_bytes = e.aux_bytes;
-    t.data_crc64 = e.data_crc64;
-    a->index.emplace(name, a->tensors.size());
-    a->names.push_back(std::move(name));
-    a->tensors.push_back(t);
-    ranges.emplace_back(e.data_offset, e.data_offset + e.data_bytes);
-    if (e.aux_bytes != 0) ranges.emplace_back(e.aux_offset, e.aux_offset + e.aux_bytes);
-  }
-  if (verify_checksums != 0) {
-    // Tensors are independent: check them in parallel (one core reads ~2 GB/s).
-    int bad = -1;
-#pragma omp parallel for schedule(dynamic, 1)
-    for (long long i = 0; i < static_cast<long long>(a->tensors.size()); ++i) {
-      const auto& t = a->tensors[static_cast<std::size_t>(i)];
-      if (crc64_update(0, a->map + t.data_offset, t.data_bytes) != t.data_crc64) {
-#pragma omp critical
-        bad = static_cast<int>(i);
+    if (verify_checksums != 0) {
+      // Tensors are independent: check them in parallel (one core reads ~2 GB/s).
+      int bad = -1;
+  #pragma omp parallel for schedule(dynamic, 1)
+      for (long long i = 0; i < static_cast<long long>(a->tensors.size()); ++i) {
+        const auto& t = a->tensors[static_cast<std::size_t>(i)];
+        if (crc64_update(0, a->map + t.data_offset, t.data_bytes) != t.data_crc64) {
+  #pragma omp critical
+          bad = static_cast<int>(i);
+        }
+      }
+      if (bad >= 0) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "tensor checksum mismatch: " + a->names[static_cast<std::size_t>(bad)]);
       }
     }
-    if (bad >= 0) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "tensor checksum mismatch: " + a->names[static_cast<std::size_t>(bad)]);
+    std::sort(ranges.begin(), ranges.end());
+    for (std::size_t i = 1; i < ranges.size(); ++i) {
+      if (ranges[i].first < ranges[i - 1].second) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "tensor payload regions overlap");
+      }
     }
-  }
-  std::sort(ranges.begin(), ranges.end());
-  for (std::size_t i = 1; i < ranges.size(); ++i) {
-    if (ranges[i].first < ranges[i - 1].second) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "tensor payload regions overlap");
-    }
-  }
-  for (std::size_t i = 0; i < a->tensors.size(); ++i) a->tensors[i].name = a->names[i].c_str();
-  *out = a.release();
-  return ok();
+    for (std::size_t i = 0; i < a->tensors.size(); ++i) a->tensors[i].name = a->names[i].c_str();
+    *out = a.release();
+    return ok();
+  });
 }
 
 extern "C" void gfxinfer_artifact_close(gfxinfer_artifact* artifact) { delete artifact; }
@@ -465,95 +467,97 @@ extern "C" int32_t gfxinfer_retile_gfx12_for_gfx950(int32_t format, const uint8_
 extern "C" int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec* spec,
                                                        const char* path, int32_t verify_checksums,
                                                        int32_t device, gfxinfer_model** out) {
-  if (spec == nullptr || path == nullptr || out == nullptr) {
-    return fail(GFXI_INVALID_ARGUMENT, "model loading needs a spec, a path and an output handle");
-  }
-  *out = nullptr;
-  gfxinfer_artifact* raw = nullptr;
-  if (const int32_t s = gfxinfer_artifact_open(path, verify_checksums, &raw); s != GFXI_OK) return s;
-  std::unique_ptr<gfxinfer_artifact> a(raw);
-  const std::string arch(a->identity.target_arch, strnlen(a->identity.target_arch, 16));
-  const bool gfx12 = arch == "gfx1200";
-  if (!gfx12 && arch != "gfx950") {
-    return fail(GFXI_UNSUPPORTED, "artifact target is " + arch + "; expected gfx950 or gfx1200");
-  }
-  std::vector<Tensor> tensors = model_tensors(*spec);
-  gfxinfer_artifact_tensor head{}, ids{};
-  const bool draft = a->index.count("mtp.draft_head.weight") != 0;
-  if (draft) {
-    (void)gfxinfer_artifact_find(a.get(), "mtp.draft_head.weight", &head);
-    if (a->index.count("mtp.draft_head_token_ids") == 0) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "artifact has a draft head without token ids");
+  return guarded([&]() -> int32_t {
+    if (spec == nullptr || path == nullptr || out == nullptr) {
+      return fail(GFXI_INVALID_ARGUMENT, "model loading needs a spec, a path and an output handle");
     }
-    (void)gfxinfer_artifact_find(a.get(), "mtp.draft_head_token_ids", &ids);
-    Tensor h;
-    h.name = "mtp.draft_head.weight";
-    h.format = GFXI_W4G128;  // replaced by the artifact's quantization below
-    h.rows = head.dimensions[0];
-    h.columns = head.dimensions[1];
-    tensors.push_back(h);
-    Tensor i;
-    i.name = "mtp.draft_head_token_ids";
-    i.format = kI32;
-    i.rows = 1;
-    i.columns = ids.dimensions[0];
-    tensors.push_back(i);
-  }
-  // Bind and check every tensor before allocating device memory.
-  std::vector<const gfxinfer_artifact_tensor*> source(tensors.size());
-  for (std::size_t k = 0; k < tensors.size(); ++k) {
-    Tensor& t = tensors[k];
-    const auto it = a->index.find(t.name);
-    if (it == a->index.end()) return fail(GFXI_CORRUPT_ARTIFACT, "artifact is missing tensor: " + t.name);
-    const auto& e = a->tensors[it->second];
-    source[k] = &e;
-    const uint64_t count = t.rows * t.columns;
-    if (t.format == kBf16) {
-      if (e.quantization != 0 || e.dtype != kDtypeBf16 || element_count(e) != count ||
-          e.data_bytes != count * 2) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " is not the expected bf16 shape");
+    *out = nullptr;
+    gfxinfer_artifact* raw = nullptr;
+    if (const int32_t s = gfxinfer_artifact_open(path, verify_checksums, &raw); s != GFXI_OK) return s;
+    std::unique_ptr<gfxinfer_artifact> a(raw);
+    const std::string arch(a->identity.target_arch, strnlen(a->identity.target_arch, 16));
+    const bool gfx12 = arch == "gfx1200";
+    if (!gfx12 && arch != "gfx950") {
+      return fail(GFXI_UNSUPPORTED, "artifact target is " + arch + "; expected gfx950 or gfx1200");
+    }
+    std::vector<Tensor> tensors = model_tensors(*spec);
+    gfxinfer_artifact_tensor head{}, ids{};
+    const bool draft = a->index.count("mtp.draft_head.weight") != 0;
+    if (draft) {
+      (void)gfxinfer_artifact_find(a.get(), "mtp.draft_head.weight", &head);
+      if (a->index.count("mtp.draft_head_token_ids") == 0) {
+        return fail(GFXI_CORRUPT_ARTIFACT, "artifact has a draft head without token ids");
       }
-    } else if (t.format == kI32) {
-      if (e.dtype != kDtypeI32 || e.rank != 1 || e.data_bytes != count * 4) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " is not an int32 vector");
-      }
-    } else {
-      if (!valid_weight_format(e.quantization)) {
-        return fail(GFXI_UNSUPPORTED, "tensor " + t.name + " uses a quantization the gfx950 GEMM "
-                                      "does not run (W2G128, W3G128 and W4G128 only)");
-      }
-      t.format = e.quantization;  // the artifact's recipe decides W2, W3 or W4
-      const uint64_t bits = code_bits(t.format);
-      if (e.dtype != kDtypeU8 || e.rank != 2 || e.dimensions[0] != t.rows ||
-          e.dimensions[1] != t.columns || e.data_bytes != count * bits / 8 ||
-          e.aux_bytes != t.rows * (t.columns / kGroup) * 2) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " does not match the model spec");
+      (void)gfxinfer_artifact_find(a.get(), "mtp.draft_head_token_ids", &ids);
+      Tensor h;
+      h.name = "mtp.draft_head.weight";
+      h.format = GFXI_W4G128;  // replaced by the artifact's quantization below
+      h.rows = head.dimensions[0];
+      h.columns = head.dimensions[1];
+      tensors.push_back(h);
+      Tensor i;
+      i.name = "mtp.draft_head_token_ids";
+      i.format = kI32;
+      i.rows = 1;
+      i.columns = ids.dimensions[0];
+      tensors.push_back(i);
+    }
+    // Bind and check every tensor before allocating device memory.
+    std::vector<const gfxinfer_artifact_tensor*> source(tensors.size());
+    for (std::size_t k = 0; k < tensors.size(); ++k) {
+      Tensor& t = tensors[k];
+      const auto it = a->index.find(t.name);
+      if (it == a->index.end()) return fail(GFXI_CORRUPT_ARTIFACT, "artifact is missing tensor: " + t.name);
+      const auto& e = a->tensors[it->second];
+      source[k] = &e;
+      const uint64_t count = t.rows * t.columns;
+      if (t.format == kBf16) {
+        if (e.quantization != 0 || e.dtype != kDtypeBf16 || element_count(e) != count ||
+            e.data_bytes != count * 2) {
+          return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " is not the expected bf16 shape");
+        }
+      } else if (t.format == kI32) {
+        if (e.dtype != kDtypeI32 || e.rank != 1 || e.data_bytes != count * 4) {
+          return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " is not an int32 vector");
+        }
+      } else {
+        if (!valid_weight_format(e.quantization)) {
+          return fail(GFXI_UNSUPPORTED, "tensor " + t.name + " uses a quantization the gfx950 GEMM "
+                                        "does not run (W2G128, W3G128 and W4G128 only)");
+        }
+        t.format = e.quantization;  // the artifact's recipe decides W2, W3 or W4
+        const uint64_t bits = code_bits(t.format);
+        if (e.dtype != kDtypeU8 || e.rank != 2 || e.dimensions[0] != t.rows ||
+            e.dimensions[1] != t.columns || e.data_bytes != count * bits / 8 ||
+            e.aux_bytes != t.rows * (t.columns / kGroup) * 2) {
+          return fail(GFXI_CORRUPT_ARTIFACT, "tensor " + t.name + " does not match the model spec");
+        }
       }
     }
-  }
-  if (draft && (head.dimensions[0] != spec->mtp_draft_vocabulary || head.dimensions[1] != spec->hidden_size ||
-                ids.dimensions[0] != head.dimensions[0])) {
-    return fail(GFXI_CORRUPT_ARTIFACT, "draft head shape does not match the spec's MTP vocabulary");
-  }
-  gfxinfer_model* m = nullptr;
-  if (const int32_t s = allocate_model(*spec, device, std::move(tensors), &m); s != GFXI_OK) return s;
-  Staging staging;
-  int32_t status = ok();
-  for (std::size_t k = 0; k < m->tensors.size() && status == GFXI_OK; ++k) {
-    const Tensor& t = m->tensors[k];
-    const auto& e = *source[k];
-    const int32_t repack = gfx12 && (t.format == GFXI_W2G128 || t.format == GFXI_W3G128) ? t.format : 0;
-    status = upload(*m, m->data(&t), a->map + e.data_offset, e.data_bytes, repack, staging);
-    if (status == GFXI_OK && t.auxiliary_bytes != 0) {
-      status = upload(*m, m->auxiliary(&t), a->map + e.aux_offset, e.aux_bytes, 0, staging);
+    if (draft && (head.dimensions[0] != spec->mtp_draft_vocabulary || head.dimensions[1] != spec->hidden_size ||
+                  ids.dimensions[0] != head.dimensions[0])) {
+      return fail(GFXI_CORRUPT_ARTIFACT, "draft head shape does not match the spec's MTP vocabulary");
     }
-  }
-  if (status != GFXI_OK) {
-    gfxinfer_model_destroy(m);
-    return status;
-  }
-  *out = m;
-  return ok();
+    gfxinfer_model* m = nullptr;
+    if (const int32_t s = allocate_model(*spec, device, std::move(tensors), &m); s != GFXI_OK) return s;
+    Staging staging;
+    int32_t status = ok();
+    for (std::size_t k = 0; k < m->tensors.size() && status == GFXI_OK; ++k) {
+      const Tensor& t = m->tensors[k];
+      const auto& e = *source[k];
+      const int32_t repack = gfx12 && (t.format == GFXI_W2G128 || t.format == GFXI_W3G128) ? t.format : 0;
+      status = upload(*m, m->data(&t), a->map + e.data_offset, e.data_bytes, repack, staging);
+      if (status == GFXI_OK && t.auxiliary_bytes != 0) {
+        status = upload(*m, m->auxiliary(&t), a->map + e.aux_offset, e.aux_bytes, 0, staging);
+      }
+    }
+    if (status != GFXI_OK) {
+      gfxinfer_model_destroy(m);
+      return status;
+    }
+    *out = m;
+    return ok();
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -610,144 +614,146 @@ bool write_zeros(int fd, uint64_t n) {
 extern "C" int32_t gfxinfer_model_write_artifact(const gfxinfer_model* model, const char* path,
                                                  const char* weights_id, const uint32_t* draft_rows,
                                                  size_t draft_count) {
-  if (model == nullptr || path == nullptr || weights_id == nullptr ||
-      (draft_count != 0 && (draft_rows == nullptr || draft_count % 16 != 0))) {
-    return fail(GFXI_INVALID_ARGUMENT, "artifact writing needs a model, a path, a weights id and "
-                                       "a multiple of 16 draft rows (or none)");
-  }
-  if (draft_count != 0 && model->find("mtp.draft_head.weight") != nullptr) {
-    return fail(GFXI_INVALID_ARGUMENT, "the model already has a draft head");
-  }
-  DiskHeader h{};
-  std::memcpy(h.magic, kMagic, sizeof kMagic);
-  h.version = kFormatVersion;
-  h.header_bytes = sizeof(DiskHeader);
-  h.endian_tag = kEndianTag;
-  h.directory_offset = sizeof(DiskHeader);
-  h.directory_entry_bytes = sizeof(DiskEntry);
-  if (!put_fixed(h.target_arch, "gfx950") || !put_fixed(h.model_id, "qwen3.8-27b") ||
-      !put_fixed(h.weights_id, weights_id) || !put_fixed(h.recipe_id, "gfx950-tile16x128-w3w4-bf16")) {
-    return fail(GFXI_INVALID_ARGUMENT, "weights id must be 1..31 characters");
-  }
-  if (auto e = hipSetDevice(model->device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
-  // Host copy of the whole arena in one transfer.
-  std::vector<uint8_t> arena(model->arena_bytes);
-  if (auto e = hipMemcpy(arena.data(), model->arena, model->arena_bytes, hipMemcpyDeviceToHost);
-      e != hipSuccess) {
-    return hip_fail(e, "weight download failed");
-  }
-  struct Payload {
-    Tensor tensor;
-    const uint8_t* data;
-    const uint8_t* aux;
-  };
-  std::vector<Payload> payloads;
-  for (const Tensor& t : model->tensors) {
-    payloads.push_back({t, arena.data() + t.data_offset,
-                        t.auxiliary_bytes != 0 ? arena.data() + t.auxiliary_offset : nullptr});
-  }
-  // Draft head (converter.cpp:252-302): LM-head rows draft_rows[i] re-tiled as rows i.
-  std::vector<uint8_t> head_codes, head_scales;
-  std::vector<uint32_t> head_ids(draft_rows, draft_rows + draft_count);
-  if (draft_count != 0) {
-    const Tensor* lm = model->find("lm_head.weight");
-    if (lm == nullptr) return fail(GFXI_INVALID_ARGUMENT, "model has no LM head");
-    const std::size_t groups = lm->columns / kGroup, lb = lane_bytes(lm->format);
-    Tensor hd;
-    hd.name = "mtp.draft_head.weight";
-    hd.format = lm->format;
-    hd.rows = draft_count;
-    hd.columns = lm->columns;
-    hd.data_bytes = draft_count * lm->columns * code_bits(lm->format) / 8;
-    hd.auxiliary_bytes = draft_count * groups * 2;
-    head_codes.resize(hd.data_bytes);
-    head_scales.resize(hd.auxiliary_bytes);
-    const uint8_t* codes = arena.data() + lm->data_offset;
-    const uint8_t* scales = arena.data() + lm->auxiliary_offset;
-    for (std::size_t i = 0; i < draft_count; ++i) {
-      const std::size_t r = draft_rows[i];
-      if (r >= lm->rows) return fail(GFXI_INVALID_ARGUMENT, "draft row outside the LM head");
-      for (std::size_t g = 0; g < groups; ++g) {
-        for (std::size_t kb = 0; kb < 4; ++kb) {
-          std::memcpy(head_codes.data() + chunk_offset(lm->format, i, g * kGroup + kb * 32, groups),
-                      codes + chunk_offset(lm->format, r, g * kGroup + kb * 32, groups), lb);
+  return guarded([&]() -> int32_t {
+    if (model == nullptr || path == nullptr || weights_id == nullptr ||
+        (draft_count != 0 && (draft_rows == nullptr || draft_count % 16 != 0))) {
+      return fail(GFXI_INVALID_ARGUMENT, "artifact writing needs a model, a path, a weights id and "
+                                         "a multiple of 16 draft rows (or none)");
+    }
+    if (draft_count != 0 && model->find("mtp.draft_head.weight") != nullptr) {
+      return fail(GFXI_INVALID_ARGUMENT, "the model already has a draft head");
+    }
+    DiskHeader h{};
+    std::memcpy(h.magic, kMagic, sizeof kMagic);
+    h.version = kFormatVersion;
+    h.header_bytes = sizeof(DiskHeader);
+    h.endian_tag = kEndianTag;
+    h.directory_offset = sizeof(DiskHeader);
+    h.directory_entry_bytes = sizeof(DiskEntry);
+    if (!put_fixed(h.target_arch, "gfx950") || !put_fixed(h.model_id, "qwen3.8-27b") ||
+        !put_fixed(h.weights_id, weights_id) || !put_fixed(h.recipe_id, "gfx950-tile16x128-w3w4-bf16")) {
+      return fail(GFXI_INVALID_ARGUMENT, "weights id must be 1..31 characters");
+    }
+    if (auto e = hipSetDevice(model->device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
+    // Host copy of the whole arena in one transfer.
+    std::vector<uint8_t> arena(model->arena_bytes);
+    if (auto e = hipMemcpy(arena.data(), model->arena, model->arena_bytes, hipMemcpyDeviceToHost);
+        e != hipSuccess) {
+      return hip_fail(e, "weight download failed");
+    }
+    struct Payload {
+      Tensor tensor;
+      const uint8_t* data;
+      const uint8_t* aux;
+    };
+    std::vector<Payload> payloads;
+    for (const Tensor& t : model->tensors) {
+      payloads.push_back({t, arena.data() + t.data_offset,
+                          t.auxiliary_bytes != 0 ? arena.data() + t.auxiliary_offset : nullptr});
+    }
+    // Draft head (converter.cpp:252-302): LM-head rows draft_rows[i] re-tiled as rows i.
+    std::vector<uint8_t> head_codes, head_scales;
+    std::vector<uint32_t> head_ids(draft_rows, draft_rows + draft_count);
+    if (draft_count != 0) {
+      const Tensor* lm = model->find("lm_head.weight");
+      if (lm == nullptr) return fail(GFXI_INVALID_ARGUMENT, "model has no LM head");
+      const std::size_t groups = lm->columns / kGroup, lb = lane_bytes(lm->format);
+      Tensor hd;
+      hd.name = "mtp.draft_head.weight";
+      hd.format = lm->format;
+      hd.rows = draft_count;
+      hd.columns = lm->columns;
+      hd.data_bytes = draft_count * lm->columns * code_bits(lm->format) / 8;
+      hd.auxiliary_bytes = draft_count * groups * 2;
+      head_codes.resize(hd.data_bytes);
+      head_scales.resize(hd.auxiliary_bytes);
+      const uint8_t* codes = arena.data() + lm->data_offset;
+      const uint8_t* scales = arena.data() + lm->auxiliary_offset;
+      for (std::size_t i = 0; i < draft_count; ++i) {
+        const std::size_t r = draft_rows[i];
+        if (r >= lm->rows) return fail(GFXI_INVALID_ARGUMENT, "draft row outside the LM head");
+        for (std::size_t g = 0; g < groups; ++g) {
+          for (std::size_t kb = 0; kb < 4; ++kb) {
+            std::memcpy(head_codes.data() + chunk_offset(lm->format, i, g * kGroup + kb * 32, groups),
+                        codes + chunk_offset(lm->format, r, g * kGroup + kb * 32, groups), lb);
+          }
+          std::memcpy(head_scales.data() + 2 * scale_offset(i, g, groups),
+                      scales + 2 * scale_offset(r, g, groups), 2);
         }
-        std::memcpy(head_scales.data() + 2 * scale_offset(i, g, groups),
-                    scales + 2 * scale_offset(r, g, groups), 2);
+      }
+      payloads.push_back({hd, head_codes.data(), head_scales.data()});
+      Tensor ids;
+      ids.name = "mtp.draft_head_token_ids";
+      ids.format = kI32;
+      ids.rows = 1;
+      ids.columns = draft_count;
+      ids.data_bytes = draft_count * 4;
+      payloads.push_back({ids, reinterpret_cast<const uint8_t*>(head_ids.data()), nullptr});
+    }
+    h.tensor_count = static_cast<uint32_t>(payloads.size());
+    std::vector<DiskEntry> entries(payloads.size());
+    std::string strings;
+    for (std::size_t k = 0; k < payloads.size(); ++k) {
+      const Tensor& t = payloads[k].tensor;
+      DiskEntry& e = entries[k];
+      e = {};
+      e.name_offset = strings.size();
+      e.name_bytes = static_cast<uint32_t>(t.name.size());
+      strings += t.name;
+      e.dtype = t.format == kBf16 ? kDtypeBf16 : t.format == kI32 ? kDtypeI32 : kDtypeU8;
+      e.quantization = t.format > 0 ? static_cast<uint16_t>(t.format) : 0;
+      e.alignment = static_cast<uint32_t>(kFileAlignment);
+      artifact_shape(t, e);
+      e.data_bytes = t.data_bytes;
+      e.aux_bytes = t.auxiliary_bytes;
+      e.data_crc64 = crc64_update(0, payloads[k].data, t.data_bytes);
+    }
+    const uint64_t directory_bytes = entries.size() * sizeof(DiskEntry);
+    h.strings_offset = h.directory_offset + directory_bytes;
+    h.strings_bytes = strings.size();
+    h.data_offset = align_up(h.strings_offset + h.strings_bytes, kFileAlignment);
+    uint64_t cursor = h.data_offset;
+    for (DiskEntry& e : entries) {
+      cursor = align_up(cursor, e.alignment);
+      e.data_offset = cursor;
+      cursor += e.data_bytes;
+      if (e.aux_bytes != 0) {
+        cursor = align_up(cursor, e.alignment);
+        e.aux_offset = cursor;
+        cursor += e.aux_bytes;
       }
     }
-    payloads.push_back({hd, head_codes.data(), head_scales.data()});
-    Tensor ids;
-    ids.name = "mtp.draft_head_token_ids";
-    ids.format = kI32;
-    ids.rows = 1;
-    ids.columns = draft_count;
-    ids.data_bytes = draft_count * 4;
-    payloads.push_back({ids, reinterpret_cast<const uint8_t*>(head_ids.data()), nullptr});
-  }
-  h.tensor_count = static_cast<uint32_t>(payloads.size());
-  std::vector<DiskEntry> entries(payloads.size());
-  std::string strings;
-  for (std::size_t k = 0; k < payloads.size(); ++k) {
-    const Tensor& t = payloads[k].tensor;
-    DiskEntry& e = entries[k];
-    e = {};
-    e.name_offset = strings.size();
-    e.name_bytes = static_cast<uint32_t>(t.name.size());
-    strings += t.name;
-    e.dtype = t.format == kBf16 ? kDtypeBf16 : t.format == kI32 ? kDtypeI32 : kDtypeU8;
-    e.quantization = t.format > 0 ? static_cast<uint16_t>(t.format) : 0;
-    e.alignment = static_cast<uint32_t>(kFileAlignment);
-    artifact_shape(t, e);
-    e.data_bytes = t.data_bytes;
-    e.aux_bytes = t.auxiliary_bytes;
-    e.data_crc64 = crc64_update(0, payloads[k].data, t.data_bytes);
-  }
-  const uint64_t directory_bytes = entries.size() * sizeof(DiskEntry);
-  h.strings_offset = h.directory_offset + directory_bytes;
-  h.strings_bytes = strings.size();
-  h.data_offset = align_up(h.strings_offset + h.strings_bytes, kFileAlignment);
-  uint64_t cursor = h.data_offset;
-  for (DiskEntry& e : entries) {
-    cursor = align_up(cursor, e.alignment);
-    e.data_offset = cursor;
-    cursor += e.data_bytes;
-    if (e.aux_bytes != 0) {
-      cursor = align_up(cursor, e.alignment);
-      e.aux_offset = cursor;
-      cursor += e.aux_bytes;
-    }
-  }
-  h.file_bytes = cursor;
-  h.data_bytes = cursor - h.data_offset;
-  std::vector<uint8_t> manifest(directory_bytes + strings.size());
-  std::memcpy(manifest.data(), entries.data(), directory_bytes);
-  std::memcpy(manifest.data() + directory_bytes, strings.data(), strings.size());
-  h.manifest_crc64 = crc64_update(0, manifest.data(), manifest.size());
+    h.file_bytes = cursor;
+    h.data_bytes = cursor - h.data_offset;
+    std::vector<uint8_t> manifest(directory_bytes + strings.size());
+    std::memcpy(manifest.data(), entries.data(), directory_bytes);
+    std::memcpy(manifest.data() + directory_bytes, strings.data(), strings.size());
+    h.manifest_crc64 = crc64_update(0, manifest.data(), manifest.size());
 
-  // Written to a temporary name, synced, then renamed into place.
-  const std::string temporary = std::string(path) + ".tmp." + std::to_string(::getpid());
-  const int fd = ::open(temporary.c_str(), O_WRONLY | O_CREAT | O_EXCL | O_CLOEXEC, 0644);
-  if (fd < 0) return fail(GFXI_IO_ERROR, "cannot create " + temporary + ": " + std::strerror(errno));
-  bool good = write_all(fd, &h, sizeof h) && write_all(fd, manifest.data(), manifest.size()) &&
-              write_zeros(fd, h.data_offset - (h.strings_offset + h.strings_bytes));
-  cursor = h.data_offset;
-  for (std::size_t k = 0; good && k < entries.size(); ++k) {
-    const DiskEntry& e = entries[k];
-    good = write_zeros(fd, e.data_offset - cursor) && write_all(fd, payloads[k].data, e.data_bytes);
-    cursor = e.data_offset + e.data_bytes;
-    if (good && e.aux_bytes != 0) {
-      good = write_zeros(fd, e.aux_offset - cursor) && write_all(fd, payloads[k].aux, e.aux_bytes);
-      cursor = e.aux_offset + e.aux_bytes;
+    // Written to a temporary name, synced, then renamed into place.
+    const std::string temporary = std::string(path) + ".tmp." + std::to_string(::getpid());
+    const int fd = ::open(temporary.c_str(), O_WRONLY | O_CREAT | O_EXCL | O_CLOEXEC, 0644);
+    if (fd < 0) return fail(GFXI_IO_ERROR, "cannot create " + temporary + ": " + std::strerror(errno));
+    bool good = write_all(fd, &h, sizeof h) && write_all(fd, manifest.data(), manifest.size()) &&
+                write_zeros(fd, h.data_offset - (h.strings_offset + h.strings_bytes));
+    cursor = h.data_offset;
+    for (std::size_t k = 0; good && k < entries.size(); ++k) {
+      const DiskEntry& e = entries[k];
+      good = write_zeros(fd, e.data_offset - cursor) && write_all(fd, payloads[k].data, e.data_bytes);
+      cursor = e.data_offset + e.data_bytes;
+      if (good && e.aux_bytes != 0) {
+        good = write_zeros(fd, e.aux_offset - cursor) && write_all(fd, payloads[k].aux, e.aux_bytes);
+        cursor = e.aux_offset + e.aux_bytes;
+      }
     }
-  }
-  good = good && ::fsync(fd) == 0;
-  const int saved = errno;
-  ::close(fd);
-  if (!good || ::rename(temporary.c_str(), path) != 0) {
-    const std::string why = std::strerror(good ? errno : saved);
-    ::unlink(temporary.c_str());
-    return fail(GFXI_IO_ERROR, std::string("cannot write artifact ") + path + ": " + why);
-  }
-  return ok();
+    good = good && ::fsync(fd) == 0;
+    const int saved = errno;
+    ::close(fd);
+    if (!good || ::rename(temporary.c_str(), path) != 0) {
+      const std::string why = std::strerror(good ? errno : saved);
+      ::unlink(temporary.c_str());
+      return fail(GFXI_IO_ERROR, std::string("cannot write artifact ") + path + ": " + why);
+    }
+    return ok();
+  });
 }

@@ -7,6 +7,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <exception>
+#include <new>
 #include <string>
 
 #include "gfxinfer_amd.h"
@@ -18,6 +20,19 @@ constexpr unsigned kWave = 64;       // CDNA wavefront
 
 // Records the message for gfxinfer_last_error() and returns the code.
 int32_t fail(int32_t code, const std::string& message);
+
+// Runs a C-ABI entry point's body so that a host allocation failure (or any other
+// exception) becomes a status instead of crossing the C boundary.
+template <typename Body>
+int32_t guarded(Body&& body) noexcept {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    return fail(GFXI_OUT_OF_MEMORY, "host allocation failed");
+  } catch (const std::exception& error) {
+    return fail(GFXI_INTERNAL, error.what());
+  }
+}
 int32_t ok();
 // Maps a HIP error to GFXI_HIP_ERROR with context (reference device.cpp:24-35).
 int32_t hip_fail(hipError_t error, const char* context);

@@ -6,6 +6,7 @@
 // rate, with a periodic re-measurement of the other candidates in turn so that a depth
 // whose rate improved (acceptance drifts with the text) is noticed.
 #include <algorithm>
+#include <new>
 
 #include "common.hpp"
 #include "runtime.hpp"
@@ -70,7 +71,11 @@ extern "C" int32_t gfxinfer_depth_policy_create(uint32_t maximum_depth, gfxinfer
   if (out == nullptr || maximum_depth == 0 || maximum_depth > 31) {
     return gfx950::fail(GFXI_INVALID_ARGUMENT, "depth policy needs a maximum depth in [1, 31]");
   }
-  *out = new gfxinfer_depth_policy(maximum_depth);
+  try {
+    *out = new gfxinfer_depth_policy(maximum_depth);
+  } catch (const std::bad_alloc&) {
+    return gfx950::fail(GFXI_OUT_OF_MEMORY, "depth policy allocation failed");
+  }
   return gfx950::ok();
 }
 

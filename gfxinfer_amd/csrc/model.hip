@@ -355,21 +355,23 @@ int32_t allocate_model(const gfxinfer_model_spec& spec, int32_t device, std::vec
 
 extern "C" int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* spec, uint64_t seed,
                                                    int32_t device, gfxinfer_model** out) {
-  if (spec == nullptr || out == nullptr) {
-    return fail(GFXI_INVALID_ARGUMENT, "model creation needs a spec and an output handle");
-  }
-  *out = nullptr;
-  gfxinfer_model* m = nullptr;
-  if (const int32_t status = allocate_model(*spec, device, model_tensors(*spec), &m);
-      status != GFXI_OK) {
-    return status;
-  }
-  if (const int32_t status = generate(*m, seed); status != GFXI_OK) {
-    gfxinfer_model_destroy(m);
-    return status;
-  }
-  *out = m;
-  return ok();
+  return guarded([&]() -> int32_t {
+    if (spec == nullptr || out == nullptr) {
+      return fail(GFXI_INVALID_ARGUMENT, "model creation needs a spec and an output handle");
+    }
+    *out = nullptr;
+    gfxinfer_model* m = nullptr;
+    if (const int32_t status = allocate_model(*spec, device, model_tensors(*spec), &m);
+        status != GFXI_OK) {
+      return status;
+    }
+    if (const int32_t status = generate(*m, seed); status != GFXI_OK) {
+      gfxinfer_model_destroy(m);
+      return status;
+    }
+    *out = m;
+    return ok();
+  });
 }
 
 extern "C" void gfxinfer_model_destroy(gfxinfer_model* model) {

@@ -769,195 +769,197 @@ void bind_mlp(const gfxinfer_model& m, const std::string& p, Layer& L, bool& mis
 extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
                                            const gfxinfer_session_config* config,
                                            gfxinfer_session** out) {
-  if (model == nullptr || config == nullptr || out == nullptr ||
-      config->maximum_context_tokens == 0 ||
-      (config->graph_verifier_batch != 0 &&
-       (config->graph_verifier_batch < 2 || config->graph_verifier_batch > kMaxBlock))) {
-    return fail(GFXI_INVALID_ARGUMENT, "invalid decode session configuration");
-  }
-  *out = nullptr;
-  if (auto e = hipSetDevice(model->device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
-  auto s = new gfxinfer_session();
-  s->model = model;
-  s->spec = model->spec;
-  s->config = *config;
-  s->stream = model->stream;
-  const auto& sp = s->spec;
-  s->H = sp.hidden_size;
-  s->I = sp.intermediate_size;
-  s->attn_width = static_cast<std::size_t>(sp.attention_head_count) * sp.attention_head_size;
-  s->q_rows = 2 * s->attn_width;
-  s->kv_rows = static_cast<std::size_t>(sp.kv_head_count) * sp.attention_head_size;
-  s->gdn_key = static_cast<std::size_t>(sp.gdn_key_head_count) * sp.gdn_head_size;
-  s->gdn_value = static_cast<std::size_t>(sp.gdn_value_head_count) * sp.gdn_head_size;
-  s->channels = 2 * s->gdn_key + s->gdn_value;
-  s->V = sp.vocabulary_size;
+  return guarded([&]() -> int32_t {
+    if (model == nullptr || config == nullptr || out == nullptr ||
+        config->maximum_context_tokens == 0 ||
+        (config->graph_verifier_batch != 0 &&
+         (config->graph_verifier_batch < 2 || config->graph_verifier_batch > kMaxBlock))) {
+      return fail(GFXI_INVALID_ARGUMENT, "invalid decode session configuration");
+    }
+    *out = nullptr;
+    if (auto e = hipSetDevice(model->device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
+    auto s = new gfxinfer_session();
+    s->model = model;
+    s->spec = model->spec;
+    s->config = *config;
+    s->stream = model->stream;
+    const auto& sp = s->spec;
+    s->H = sp.hidden_size;
+    s->I = sp.intermediate_size;
+    s->attn_width = static_cast<std::size_t>(sp.attention_head_count) * sp.attention_head_size;
+    s->q_rows = 2 * s->attn_width;
+    s->kv_rows = static_cast<std::size_t>(sp.kv_head_count) * sp.attention_head_size;
+    s->gdn_key = static_cast<std::size_t>(sp.gdn_key_head_count) * sp.gdn_head_size;
+    s->gdn_value = static_cast<std::size_t>(sp.gdn_value_head_count) * sp.gdn_head_size;
+    s->channels = 2 * s->gdn_key + s->gdn_value;
+    s->V = sp.vocabulary_size;
 
-  // Bindings (qwen_runtime.cpp:1011-1095).
-  bool missing = false;
-  s->embedding = bind_matrix(*model, "model.language_model.embed_tokens.weight", missing);
-  s->lm_head = bind_matrix(*model, "lm_head.weight", missing);
-  s->final_norm = bind_vector(*model, "model.language_model.norm.weight", missing);
-  s->layers.resize(sp.layer_count);
-  for (uint32_t i = 0; i < sp.layer_count; ++i) {
-    Layer& L = s->layers[i];
-    const std::string p = "model.language_model.layers." + std::to_string(i) + ".";
-    L.attention = is_attention_layer(sp, i);
-    L.state_index = L.attention ? s->attn_layers++ : s->gdn_layers++;
-    bind_mlp(*model, p, L, missing);
-    if (L.attention) {
-      bind_attention(*model, p, L, missing);
-    } else {
-      L.qkv = bind_matrix(*model, p + "linear_attn.in_proj_qkv.weight", missing);
-      L.z = bind_matrix(*model, p + "linear_attn.in_proj_z.weight", missing);
-      L.a = bind_matrix(*model, p + "linear_attn.in_proj_a.weight", missing);
-      L.b = bind_matrix(*model, p + "linear_attn.in_proj_b.weight", missing);
-      L.out = bind_matrix(*model, p + "linear_attn.out_proj.weight", missing);
-      L.conv = bind_vector(*model, p + "linear_attn.conv1d.weight", missing);
-      L.a_log = bind_vector(*model, p + "linear_attn.A_log", missing);
-      L.dt_bias = bind_vector(*model, p + "linear_attn.dt_bias", missing);
-      L.gdn_norm = bind_vector(*model, p + "linear_attn.norm.weight", missing);
-    }
-  }
-  s->mtp_fc = bind_matrix(*model, "mtp.fc.weight", missing);
-  s->mtp_pre_embedding_norm = bind_vector(*model, "mtp.pre_fc_norm_embedding.weight", missing);
-  s->mtp_pre_hidden_norm = bind_vector(*model, "mtp.pre_fc_norm_hidden.weight", missing);
-  s->mtp_final_norm = bind_vector(*model, "mtp.norm.weight", missing);
-  s->mtp.attention = true;
-  bind_mlp(*model, "mtp.layers.0.", s->mtp, missing);
-  bind_attention(*model, "mtp.layers.0.", s->mtp, missing);
-  if (missing) {
-    delete s;
-    return fail(GFXI_CORRUPT_ARTIFACT, "model lacks a tensor the decode session needs");
-  }
-  // The MTP draft head (qwen_runtime.cpp:994-1008): the converter's ranked rows
-  // "mtp.draft_head.weight" with their token ids when the model has them, else the LM
-  // head's first rows (in the tile layout a row prefix is a byte prefix of codes and
-  // scales) with the identity map.
-  if (const Tensor* ids = model->find("mtp.draft_head_token_ids"); ids != nullptr) {
-    bool absent = false;
-    s->draft_head = bind_matrix(*model, "mtp.draft_head.weight", absent);
-    if (absent || ids->format != kI32 || ids->columns != s->draft_head.rows ||
-        s->draft_head.rows != sp.mtp_draft_vocabulary) {
-      delete s;
-      return fail(GFXI_CORRUPT_ARTIFACT, "MTP draft head and token ids do not match the spec");
-    }
-    s->draft_token_ids = static_cast<const uint32_t*>(model->data(ids));
-  } else {
-    s->draft_head = s->lm_head;
-    s->draft_head.rows = sp.mtp_draft_vocabulary;
-  }
-
-  // Arena (qwen_runtime.cpp:1117-1184).
-  const std::size_t B = kMaxBlock, ctx = config->maximum_context_tokens;
-  const std::size_t max_k = std::max({s->I, 2 * s->H, s->attn_width, s->gdn_value});
-  s->attention_workspace_bytes =
-      gfxinfer_attention_workspace_bytes(kMaxBlock, sp.attention_head_count, ctx);
-  s->argmax_keys_bytes = gfxinfer_gemm_argmax_workspace_bytes(s->V, kMaxBlock);
-  const std::size_t conv_bytes = s->gdn_layers * s->conv_state_elements() * 2;
-  const std::size_t gdn_bytes = s->gdn_layers * s->gdn_state_elements() * 4;
-  const std::size_t kv_bytes = s->attn_layers * ctx * s->kv_rows * 2;
-  const std::size_t mtp_kv_bytes = ctx * s->kv_rows * 2;
-  s->buffers = {
-      {"hidden", reinterpret_cast<void**>(&s->hidden_a), B * s->H * 2},
-      {"hidden_b", reinterpret_cast<void**>(&s->hidden_b), B * s->H * 2},
-      {"post_attention", reinterpret_cast<void**>(&s->post_attention), B * s->H * 2},
-      {"mtp_hidden", reinterpret_cast<void**>(&s->mtp_hidden), s->H * 2},
-      {"target_hidden_snapshot", reinterpret_cast<void**>(&s->target_hidden_snapshot), s->H * 2},
-      {"mtp_concat", reinterpret_cast<void**>(&s->mtp_concat), B * 2 * s->H * 2},
-      {"mtp_input", reinterpret_cast<void**>(&s->mtp_input), B * s->H * 2},
-      {"mtp_conditioning", reinterpret_cast<void**>(&s->mtp_conditioning), B * s->H * 2},
-      {"convolved", reinterpret_cast<void**>(&s->convolved), B * s->channels * 2},
-      {"query", reinterpret_cast<void**>(&s->query), B * s->attn_width * 2},
-      {"key", reinterpret_cast<void**>(&s->key), B * s->kv_rows * 2},
-      {"attention_output", reinterpret_cast<void**>(&s->attention_output), B * s->attn_width * 2},
-      {"act_codes", reinterpret_cast<void**>(&s->act_codes), B * max_k / 2},
-      {"act_scales", reinterpret_cast<void**>(&s->act_scales), B * (max_k / 128) * 2},
-      {"projected_main", reinterpret_cast<void**>(&s->projected_main),
-       B * std::max(s->q_rows, s->channels) * 4},
-      {"projected_z", reinterpret_cast<void**>(&s->projected_z), B * s->gdn_value * 4},
-      {"projected_a", reinterpret_cast<void**>(&s->projected_a), B * sp.gdn_value_head_count * 4},
-      {"projected_b", reinterpret_cast<void**>(&s->projected_b), B * sp.gdn_value_head_count * 4},
-      {"projected_k", reinterpret_cast<void**>(&s->projected_k), B * s->kv_rows * 4},
-      {"projected_v", reinterpret_cast<void**>(&s->projected_v), B * s->kv_rows * 4},
-      {"gdn_mixed", reinterpret_cast<void**>(&s->gdn_mixed), B * s->gdn_value * 4},
-      {"mixer_update", reinterpret_cast<void**>(&s->mixer_update), kMaxPlanes * B * s->H * 4},
-      {"gate_output", reinterpret_cast<void**>(&s->gate_output), B * s->I * 4},
-      {"up_output", reinterpret_cast<void**>(&s->up_output), B * s->I * 4},
-      {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), kMaxPlanes * B * s->H * 4},
-      {"logits", reinterpret_cast<void**>(&s->logits), B * s->V * 4},
-      {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
-      {"attention_workspace", reinterpret_cast<void**>(&s->attention_workspace),
-       s->attention_workspace_bytes},
-      {"selected", reinterpret_cast<void**>(&s->selected), B * 4},
-      {"drafts", reinterpret_cast<void**>(&s->draft_tokens), B * 4},
-      {"verify_drafts", reinterpret_cast<void**>(&s->verify_drafts), B * 4},
-      {"result", reinterpret_cast<void**>(&s->result), kResultWords * 4},
-      {"graph_seed", reinterpret_cast<void**>(&s->graph_seed), 4},
-      {"graph_forced", reinterpret_cast<void**>(&s->graph_forced), 4},
-      {"graph_base_position", reinterpret_cast<void**>(&s->graph_base_position), 8},
-      {"graph_mtp_positions", reinterpret_cast<void**>(&s->graph_mtp_positions), B * 8},
-      {"conv_states", reinterpret_cast<void**>(&s->conv_states), conv_bytes},
-      {"conv_snapshot", reinterpret_cast<void**>(&s->conv_snapshot), conv_bytes},
-      {"gdn_states", reinterpret_cast<void**>(&s->gdn_states), gdn_bytes},
-      {"gdn_snapshot", reinterpret_cast<void**>(&s->gdn_snapshot), gdn_bytes},
-      {"conv_log", reinterpret_cast<void**>(&s->conv_log), s->gdn_layers * B * s->channels * 2},
-      {"key_log", reinterpret_cast<void**>(&s->key_log), s->gdn_layers * B * s->gdn_key * 4},
-      {"delta_log", reinterpret_cast<void**>(&s->delta_log), s->gdn_layers * B * s->gdn_value * 4},
-      {"decay_log", reinterpret_cast<void**>(&s->decay_log),
-       s->gdn_layers * B * sp.gdn_value_head_count * 4},
-      {"key_caches", reinterpret_cast<void**>(&s->key_caches), kv_bytes},
-      {"value_caches", reinterpret_cast<void**>(&s->value_caches), kv_bytes},
-      {"mtp_key_cache", reinterpret_cast<void**>(&s->mtp_key_cache), mtp_kv_bytes},
-      {"mtp_value_cache", reinterpret_cast<void**>(&s->mtp_value_cache), mtp_kv_bytes},
-  };
-  std::size_t cursor = 0;
-  std::vector<std::size_t> offsets;
-  for (const auto& b : s->buffers) {
-    cursor = align256(cursor);
-    offsets.push_back(cursor);
-    cursor += b.bytes;
-  }
-  s->arena_bytes = align256(cursor);
-  std::size_t free_bytes = 0, total_bytes = 0;
-  int32_t status = ok();
-  if (auto e = hipMemGetInfo(&free_bytes, &total_bytes); e != hipSuccess) {
-    status = hip_fail(e, "hipMemGetInfo before session allocation failed");
-  } else if (s->arena_bytes > free_bytes) {
-    status = fail(GFXI_OUT_OF_MEMORY, "decode session arena exceeds currently free GPU memory");
-  } else if (auto e2 = hipMalloc(reinterpret_cast<void**>(&s->arena), s->arena_bytes);
-             e2 != hipSuccess) {
-    s->arena = nullptr;
-    status = hip_fail(e2, "decode session arena allocation failed");
-  } else if (auto e3 = hipHostMalloc(reinterpret_cast<void**>(&s->host_result), 256,
-                                     hipHostMallocDefault);
-             e3 != hipSuccess) {
-    s->host_result = nullptr;
-    status = hip_fail(e3, "pinned result buffer allocation failed");
-  }
-  if (status == GFXI_OK) {
-    for (std::size_t i = 0; i < s->buffers.size(); ++i) {
-      *s->buffers[i].slot = s->arena + offsets[i];
-    }
-    // qwen_runtime.cpp:1246-1256: zero recurrent state; also the scalars.
-    for (auto* p : {static_cast<void*>(s->conv_states), static_cast<void*>(s->gdn_states)}) {
-      const std::size_t bytes = p == s->conv_states ? conv_bytes : gdn_bytes;
-      if (auto e = hipMemsetAsync(p, 0, bytes, s->stream); e != hipSuccess) {
-        status = hip_fail(e, "recurrent state initialization failed");
+    // Bindings (qwen_runtime.cpp:1011-1095).
+    bool missing = false;
+    s->embedding = bind_matrix(*model, "model.language_model.embed_tokens.weight", missing);
+    s->lm_head = bind_matrix(*model, "lm_head.weight", missing);
+    s->final_norm = bind_vector(*model, "model.language_model.norm.weight", missing);
+    s->layers.resize(sp.layer_count);
+    for (uint32_t i = 0; i < sp.layer_count; ++i) {
+      Layer& L = s->layers[i];
+      const std::string p = "model.language_model.layers." + std::to_string(i) + ".";
+      L.attention = is_attention_layer(sp, i);
+      L.state_index = L.attention ? s->attn_layers++ : s->gdn_layers++;
+      bind_mlp(*model, p, L, missing);
+      if (L.attention) {
+        bind_attention(*model, p, L, missing);
+      } else {
+        L.qkv = bind_matrix(*model, p + "linear_attn.in_proj_qkv.weight", missing);
+        L.z = bind_matrix(*model, p + "linear_attn.in_proj_z.weight", missing);
+        L.a = bind_matrix(*model, p + "linear_attn.in_proj_a.weight", missing);
+        L.b = bind_matrix(*model, p + "linear_attn.in_proj_b.weight", missing);
+        L.out = bind_matrix(*model, p + "linear_attn.out_proj.weight", missing);
+        L.conv = bind_vector(*model, p + "linear_attn.conv1d.weight", missing);
+        L.a_log = bind_vector(*model, p + "linear_attn.A_log", missing);
+        L.dt_bias = bind_vector(*model, p + "linear_attn.dt_bias", missing);
+        L.gdn_norm = bind_vector(*model, p + "linear_attn.norm.weight", missing);
       }
     }
-    if (status == GFXI_OK) status = s->write_round_scalars(0, -1, 0, 0, 1);
-    if (status == GFXI_OK) status = s->sync("decode session initialization failed");
-    if (status == GFXI_OK) status = s->prepare_graphs();
-    if (status == GFXI_OK) status = s->sync("speculative graph preparation failed");
-  }
-  if (status != GFXI_OK) {
-    delete s;
-    return status;
-  }
-  s->summary = {s->arena_bytes, ctx, conv_bytes + gdn_bytes, kv_bytes * 2, mtp_kv_bytes * 2};
-  *out = s;
-  return ok();
+    s->mtp_fc = bind_matrix(*model, "mtp.fc.weight", missing);
+    s->mtp_pre_embedding_norm = bind_vector(*model, "mtp.pre_fc_norm_embedding.weight", missing);
+    s->mtp_pre_hidden_norm = bind_vector(*model, "mtp.pre_fc_norm_hidden.weight", missing);
+    s->mtp_final_norm = bind_vector(*model, "mtp.norm.weight", missing);
+    s->mtp.attention = true;
+    bind_mlp(*model, "mtp.layers.0.", s->mtp, missing);
+    bind_attention(*model, "mtp.layers.0.", s->mtp, missing);
+    if (missing) {
+      delete s;
+      return fail(GFXI_CORRUPT_ARTIFACT, "model lacks a tensor the decode session needs");
+    }
+    // The MTP draft head (qwen_runtime.cpp:994-1008): the converter's ranked rows
+    // "mtp.draft_head.weight" with their token ids when the model has them, else the LM
+    // head's first rows (in the tile layout a row prefix is a byte prefix of codes and
+    // scales) with the identity map.
+    if (const Tensor* ids = model->find("mtp.draft_head_token_ids"); ids != nullptr) {
+      bool absent = false;
+      s->draft_head = bind_matrix(*model, "mtp.draft_head.weight", absent);
+      if (absent || ids->format != kI32 || ids->columns != s->draft_head.rows ||
+          s->draft_head.rows != sp.mtp_draft_vocabulary) {
+        delete s;
+        return fail(GFXI_CORRUPT_ARTIFACT, "MTP draft head and token ids do not match the spec");
+      }
+      s->draft_token_ids = static_cast<const uint32_t*>(model->data(ids));
+    } else {
+      s->draft_head = s->lm_head;
+      s->draft_head.rows = sp.mtp_draft_vocabulary;
+    }
+
+    // Arena (qwen_runtime.cpp:1117-1184).
+    const std::size_t B = kMaxBlock, ctx = config->maximum_context_tokens;
+    const std::size_t max_k = std::max({s->I, 2 * s->H, s->attn_width, s->gdn_value});
+    s->attention_workspace_bytes =
+        gfxinfer_attention_workspace_bytes(kMaxBlock, sp.attention_head_count, ctx);
+    s->argmax_keys_bytes = gfxinfer_gemm_argmax_workspace_bytes(s->V, kMaxBlock);
+    const std::size_t conv_bytes = s->gdn_layers * s->conv_state_elements() * 2;
+    const std::size_t gdn_bytes = s->gdn_layers * s->gdn_state_elements() * 4;
+    const std::size_t kv_bytes = s->attn_layers * ctx * s->kv_rows * 2;
+    const std::size_t mtp_kv_bytes = ctx * s->kv_rows * 2;
+    s->buffers = {
+        {"hidden", reinterpret_cast<void**>(&s->hidden_a), B * s->H * 2},
+        {"hidden_b", reinterpret_cast<void**>(&s->hidden_b), B * s->H * 2},
+        {"post_attention", reinterpret_cast<void**>(&s->post_attention), B * s->H * 2},
+        {"mtp_hidden", reinterpret_cast<void**>(&s->mtp_hidden), s->H * 2},
+        {"target_hidden_snapshot", reinterpret_cast<void**>(&s->target_hidden_snapshot), s->H * 2},
+        {"mtp_concat", reinterpret_cast<void**>(&s->mtp_concat), B * 2 * s->H * 2},
+        {"mtp_input", reinterpret_cast<void**>(&s->mtp_input), B * s->H * 2},
+        {"mtp_conditioning", reinterpret_cast<void**>(&s->mtp_conditioning), B * s->H * 2},
+        {"convolved", reinterpret_cast<void**>(&s->convolved), B * s->channels * 2},
+        {"query", reinterpret_cast<void**>(&s->query), B * s->attn_width * 2},
+        {"key", reinterpret_cast<void**>(&s->key), B * s->kv_rows * 2},
+        {"attention_output", reinterpret_cast<void**>(&s->attention_output), B * s->attn_width * 2},
+        {"act_codes", reinterpret_cast<void**>(&s->act_codes), B * max_k / 2},
+        {"act_scales", reinterpret_cast<void**>(&s->act_scales), B * (max_k / 128) * 2},
+        {"projected_main", reinterpret_cast<void**>(&s->projected_main),
+         B * std::max(s->q_rows, s->channels) * 4},
+        {"projected_z", reinterpret_cast<void**>(&s->projected_z), B * s->gdn_value * 4},
+        {"projected_a", reinterpret_cast<void**>(&s->projected_a), B * sp.gdn_value_head_count * 4},
+        {"projected_b", reinterpret_cast<void**>(&s->projected_b), B * sp.gdn_value_head_count * 4},
+        {"projected_k", reinterpret_cast<void**>(&s->projected_k), B * s->kv_rows * 4},
+        {"projected_v", reinterpret_cast<void**>(&s->projected_v), B * s->kv_rows * 4},
+        {"gdn_mixed", reinterpret_cast<void**>(&s->gdn_mixed), B * s->gdn_value * 4},
+        {"mixer_update", reinterpret_cast<void**>(&s->mixer_update), kMaxPlanes * B * s->H * 4},
+        {"gate_output", reinterpret_cast<void**>(&s->gate_output), B * s->I * 4},
+        {"up_output", reinterpret_cast<void**>(&s->up_output), B * s->I * 4},
+        {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), kMaxPlanes * B * s->H * 4},
+        {"logits", reinterpret_cast<void**>(&s->logits), B * s->V * 4},
+        {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
+        {"attention_workspace", reinterpret_cast<void**>(&s->attention_workspace),
+         s->attention_workspace_bytes},
+        {"selected", reinterpret_cast<void**>(&s->selected), B * 4},
+        {"drafts", reinterpret_cast<void**>(&s->draft_tokens), B * 4},
+        {"verify_drafts", reinterpret_cast<void**>(&s->verify_drafts), B * 4},
+        {"result", reinterpret_cast<void**>(&s->result), kResultWords * 4},
+        {"graph_seed", reinterpret_cast<void**>(&s->graph_seed), 4},
+        {"graph_forced", reinterpret_cast<void**>(&s->graph_forced), 4},
+        {"graph_base_position", reinterpret_cast<void**>(&s->graph_base_position), 8},
+        {"graph_mtp_positions", reinterpret_cast<void**>(&s->graph_mtp_positions), B * 8},
+        {"conv_states", reinterpret_cast<void**>(&s->conv_states), conv_bytes},
+        {"conv_snapshot", reinterpret_cast<void**>(&s->conv_snapshot), conv_bytes},
+        {"gdn_states", reinterpret_cast<void**>(&s->gdn_states), gdn_bytes},
+        {"gdn_snapshot", reinterpret_cast<void**>(&s->gdn_snapshot), gdn_bytes},
+        {"conv_log", reinterpret_cast<void**>(&s->conv_log), s->gdn_layers * B * s->channels * 2},
+        {"key_log", reinterpret_cast<void**>(&s->key_log), s->gdn_layers * B * s->gdn_key * 4},
+        {"delta_log", reinterpret_cast<void**>(&s->delta_log), s->gdn_layers * B * s->gdn_value * 4},
+        {"decay_log", reinterpret_cast<void**>(&s->decay_log),
+         s->gdn_layers * B * sp.gdn_value_head_count * 4},
+        {"key_caches", reinterpret_cast<void**>(&s->key_caches), kv_bytes},
+        {"value_caches", reinterpret_cast<void**>(&s->value_caches), kv_bytes},
+        {"mtp_key_cache", reinterpret_cast<void**>(&s->mtp_key_cache), mtp_kv_bytes},
+        {"mtp_value_cache", reinterpret_cast<void**>(&s->mtp_value_cache), mtp_kv_bytes},
+    };
+    std::size_t cursor = 0;
+    std::vector<std::size_t> offsets;
+    for (const auto& b : s->buffers) {
+      cursor = align256(cursor);
+      offsets.push_back(cursor);
+      cursor += b.bytes;
+    }
+    s->arena_bytes = align256(cursor);
+    std::size_t free_bytes = 0, total_bytes = 0;
+    int32_t status = ok();
+    if (auto e = hipMemGetInfo(&free_bytes, &total_bytes); e != hipSuccess) {
+      status = hip_fail(e, "hipMemGetInfo before session allocation failed");
+    } else if (s->arena_bytes > free_bytes) {
+      status = fail(GFXI_OUT_OF_MEMORY, "decode session arena exceeds currently free GPU memory");
+    } else if (auto e2 = hipMalloc(reinterpret_cast<void**>(&s->arena), s->arena_bytes);
+               e2 != hipSuccess) {
+      s->arena = nullptr;
+      status = hip_fail(e2, "decode session arena allocation failed");
+    } else if (auto e3 = hipHostMalloc(reinterpret_cast<void**>(&s->host_result), 256,
+                                       hipHostMallocDefault);
+               e3 != hipSuccess) {
+      s->host_result = nullptr;
+      status = hip_fail(e3, "pinned result buffer allocation failed");
+    }
+    if (status == GFXI_OK) {
+      for (std::size_t i = 0; i < s->buffers.size(); ++i) {
+        *s->buffers[i].slot = s->arena + offsets[i];
+      }
+      // qwen_runtime.cpp:1246-1256: zero recurrent state; also the scalars.
+      for (auto* p : {static_cast<void*>(s->conv_states), static_cast<void*>(s->gdn_states)}) {
+        const std::size_t bytes = p == s->conv_states ? conv_bytes : gdn_bytes;
+        if (auto e = hipMemsetAsync(p, 0, bytes, s->stream); e != hipSuccess) {
+          status = hip_fail(e, "recurrent state initialization failed");
+        }
+      }
+      if (status == GFXI_OK) status = s->write_round_scalars(0, -1, 0, 0, 1);
+      if (status == GFXI_OK) status = s->sync("decode session initialization failed");
+      if (status == GFXI_OK) status = s->prepare_graphs();
+      if (status == GFXI_OK) status = s->sync("speculative graph preparation failed");
+    }
+    if (status != GFXI_OK) {
+      delete s;
+      return status;
+    }
+    s->summary = {s->arena_bytes, ctx, conv_bytes + gdn_bytes, kv_bytes * 2, mtp_kv_bytes * 2};
+    *out = s;
+    return ok();
+  });
 }
 
 extern "C" void gfxinfer_session_destroy(gfxinfer_session* session) { delete session; }
@@ -979,17 +981,21 @@ extern "C" int32_t gfxinfer_session_block_step(gfxinfer_session* session,
 
 extern "C" int32_t gfxinfer_session_prefill(gfxinfer_session* session, const uint32_t* tokens,
                                             size_t count, int32_t sync_mtp, uint32_t* next_token) {
-  GFXI_TRY(enter(session));
-  return session->prefill(tokens, count, sync_mtp != 0, next_token);
+  return guarded([&]() -> int32_t {
+    GFXI_TRY(enter(session));
+    return session->prefill(tokens, count, sync_mtp != 0, next_token);
+  });
 }
 
 extern "C" int32_t gfxinfer_session_generate(gfxinfer_session* session, const uint32_t* prompt,
                                              size_t prompt_count, const gfxinfer_generate_config* config,
                                              uint32_t* output, size_t* output_count,
                                              gfxinfer_generate_stats* stats) {
-  GFXI_TRY(enter(session));
-  if (config == nullptr) return fail(GFXI_INVALID_ARGUMENT, "generate needs a configuration");
-  return session->generate(prompt, prompt_count, *config, output, output_count, stats);
+  return guarded([&]() -> int32_t {
+    GFXI_TRY(enter(session));
+    if (config == nullptr) return fail(GFXI_INVALID_ARGUMENT, "generate needs a configuration");
+    return session->generate(prompt, prompt_count, *config, output, output_count, stats);
+  });
 }
 
 extern "C" int32_t gfxinfer_session_greedy_step(gfxinfer_session* session, uint32_t input_token,
