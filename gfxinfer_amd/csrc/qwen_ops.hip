@@ -211,26 +211,66 @@ __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
 // 128 elements (the MTP conditioning norms): sixteen waves, lane pairs in 128-element
 // slots as in rms_norm_rows_kernel, every load issued before the first use.  Same
 // per-element arithmetic as dual_rms_norm_kernel; the sum of squares runs in the slot
-// order of rms_norm_rows_kernel.
-template <unsigned Slots>
-__global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(
-    const __half* __restrict__ left, const uint16_t* __restrict__ left_weight,
-    const __half* __restrict__ right, const uint16_t* __restrict__ right_weight,
-    __half* __restrict__ output, uint32_t elements, float epsilon, bool unit_offset) {
+// order of rms_norm_rows_kernel.  Two optional fusions for the MTP input: with
+// EmbedFormat != 0 the left row is the embedding row of a token dequantized from its
+// tiled matrix exactly as row_gather_kernel writes it (zeros for a token past the
+// table), and with Quantize each 128-slot of the concatenated fp16 row is quantized to
+// A4G128 by the wave that holds it, as quantize_activation_i4 does.
+struct DualNormArgs {
+  const __half* left;           // [rows][elements] fp16 (EmbedFormat == 0)
+  const uint16_t* left_weight;  // bf16 [elements]
+  const __half* right;          // [rows][elements] fp16
+  const uint16_t* right_weight;
+  __half* output;               // [rows][2 * elements] fp16, or null
+  uint8_t* codes;               // A4 [rows][elements] bytes (Quantize)
+  __half* scales;               // [rows][2 * elements / 128] (Quantize)
+  const uint8_t* embed_codes;   // tiled [embed_rows][elements] (EmbedFormat != 0)
+  const __half* embed_scales;
+  uint32_t embed_rows, token;
+  const uint32_t* indirect_token;  // if set, the token id is read here
+  uint32_t elements;
+  float epsilon;
+  bool unit_offset;
+};
+
+template <unsigned Slots, int EmbedFormat, bool Quantize>
+__global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a) {
   __shared__ float scratch[16];
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const uint32_t elements = a.elements;
   const std::size_t row = blockIdx.y;
   const bool second = blockIdx.x != 0;
-  const __half* input = (second ? right : left) + row * elements;
-  const uint16_t* weight = second ? right_weight : left_weight;
-  output += row * 2u * elements + (second ? elements : 0);
+  const uint16_t* weight = second ? a.right_weight : a.left_weight;
+  const uint32_t half_offset = second ? elements : 0u;
   uint32_t hin[Slots], wpair[Slots];
+  if (EmbedFormat != 0 && !second) {
+    // the token's embedding row, dequantized per column pair
+    const uint32_t token = a.indirect_token != nullptr ? *a.indirect_token : a.token;
+    const std::size_t groups = elements / kGroup;
 #pragma unroll
-  for (unsigned j = 0; j < Slots; ++j) {
-    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
-    const uint32_t at = i < elements ? i : 0u;
-    hin[j] = *reinterpret_cast<const uint32_t*>(input + at);
-    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+    for (unsigned j = 0; j < Slots; ++j) {
+      const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+      const uint32_t at = i < elements ? i : 0u;
+      wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+      hin[j] = 0u;
+      if (i < elements && token < a.embed_rows) {
+        const uint8_t* chunk = a.embed_codes + chunk_offset(EmbedFormat, token, i, groups);
+        const int w0 = unpack_lane_code(EmbedFormat, chunk, i % 32u);
+        const int w1 = unpack_lane_code(EmbedFormat, chunk, (i + 1u) % 32u);
+        const float scale = __half2float(a.embed_scales[scale_offset(token, i / kGroup, groups)]);
+        hin[j] = static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w0) * scale))) |
+                 (static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w1) * scale))) << 16);
+      }
+    }
+  } else {
+    const __half* input = (second ? a.right : a.left) + row * elements;
+#pragma unroll
+    for (unsigned j = 0; j < Slots; ++j) {
+      const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+      const uint32_t at = i < elements ? i : 0u;
+      hin[j] = *reinterpret_cast<const uint32_t*>(input + at);
+      wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+    }
   }
   float x[Slots][2];
   float square = 0.0F;
@@ -244,16 +284,26 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(
       square = fmaf(x[j][1], x[j][1], square);
     }
   }
-  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + epsilon);
+  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + a.epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
-    const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+    const uint32_t g = wave + j * waves;
+    const uint32_t i = g * 128u + 2u * lane;
+    if (g * 128u >= elements) break;  // wave-uniform
+    __half n0 = __float2half(0.0F), n1 = n0;
     if (i < elements) {
       const float w0 = bf16_to_float(static_cast<uint16_t>(wpair[j] & 0xffffu));
       const float w1 = bf16_to_float(static_cast<uint16_t>(wpair[j] >> 16));
-      const __half n0 = to_half(x[j][0] * inverse * (unit_offset ? w0 + 1.0F : w0));
-      const __half n1 = to_half(x[j][1] * inverse * (unit_offset ? w1 + 1.0F : w1));
-      *reinterpret_cast<__half2*>(output + i) = __halves2half2(n0, n1);
+      n0 = to_half(x[j][0] * inverse * (a.unit_offset ? w0 + 1.0F : w0));
+      n1 = to_half(x[j][1] * inverse * (a.unit_offset ? w1 + 1.0F : w1));
+      if (a.output != nullptr) {
+        *reinterpret_cast<__half2*>(a.output + row * 2u * elements + half_offset + i) = __halves2half2(n0, n1);
+      }
+    }
+    if constexpr (Quantize) {
+      const std::size_t groups2 = 2u * elements / kGroup;
+      quantize_group_a4(n0, n1, a.codes + row * elements + (half_offset + g * 128u) / 2u,
+                        a.scales + row * groups2 + half_offset / kGroup + g, lane);
     }
   }
 }
@@ -1146,9 +1196,16 @@ void launch_dual_norm(const uint16_t* left, const uint16_t* lw, const uint16_t* 
   const bool rows = elements % 2 == 0 && elements <= 3u * 16u * 128u && aligned4(left) && aligned4(right) &&
                     aligned4(lw) && aligned4(rw) && aligned4(out);
   if (rows) {
-    hipLaunchKernelGGL(dual_rms_norm_rows_kernel<3>, dim3(2, batch), dim3(1024), 0, stream,
-                       reinterpret_cast<const __half*>(left), lw, reinterpret_cast<const __half*>(right), rw,
-                       reinterpret_cast<__half*>(out), static_cast<uint32_t>(elements), epsilon, unit);
+    DualNormArgs a{};
+    a.left = reinterpret_cast<const __half*>(left);
+    a.left_weight = lw;
+    a.right = reinterpret_cast<const __half*>(right);
+    a.right_weight = rw;
+    a.output = reinterpret_cast<__half*>(out);
+    a.elements = static_cast<uint32_t>(elements);
+    a.epsilon = epsilon;
+    a.unit_offset = unit;
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, 0, false>), dim3(2, batch), dim3(1024), 0, stream, a);
   } else {
     hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), 0, stream,
                        reinterpret_cast<const __half*>(left), lw, reinterpret_cast<const __half*>(right), rw,
@@ -1183,6 +1240,50 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat_batch(
   launch_dual_norm(left, left_bf16_weight, right, right_bf16_weight, concatenated_output, elements, batch,
                    epsilon, add_unit_offset != 0, static_cast<hipStream_t>(stream));
   return launch_status("batched dual RMSNorm/concat launch failed");
+}
+
+extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
+    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+    size_t embedding_rows, uint32_t token, const uint32_t* indirect_token,
+    const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
+    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream) {
+  if (!valid_weight_format(embedding_format)) {
+    return fail(GFXI_UNSUPPORTED, "MTP input: embedding format must be W2G128, W3G128 or W4G128");
+  }
+  if (embedding_codes == nullptr || embedding_scales == nullptr || embedding_rows == 0 ||
+      embedding_rows % 16 != 0 || embedding_rows > (1u << 31) || embedding_bf16_norm == nullptr ||
+      conditioning == nullptr || conditioning_bf16_norm == nullptr || packed_output == nullptr ||
+      scales == nullptr || elements == 0 || elements % kGroup != 0 || elements > 3u * 16u * 128u ||
+      !valid_epsilon(epsilon) || !aligned4(embedding_bf16_norm) || !aligned4(conditioning) ||
+      !aligned4(conditioning_bf16_norm) || !aligned4(concatenated_output)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid MTP input arguments (K divisible by 128 up to 6144, "
+                                       "4-byte aligned rows)");
+  }
+  DualNormArgs a{};
+  a.left_weight = embedding_bf16_norm;
+  a.right = reinterpret_cast<const __half*>(conditioning);
+  a.right_weight = conditioning_bf16_norm;
+  a.output = reinterpret_cast<__half*>(concatenated_output);
+  a.codes = packed_output;
+  a.scales = reinterpret_cast<__half*>(scales);
+  a.embed_codes = embedding_codes;
+  a.embed_scales = reinterpret_cast<const __half*>(embedding_scales);
+  a.embed_rows = static_cast<uint32_t>(embedding_rows);
+  a.token = token;
+  a.indirect_token = indirect_token;
+  a.elements = static_cast<uint32_t>(elements);
+  a.epsilon = epsilon;
+  a.unit_offset = add_unit_offset != 0;
+  const auto s = static_cast<hipStream_t>(stream);
+  if (embedding_format == GFXI_W2G128) {
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W2G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+  } else if (embedding_format == GFXI_W3G128) {
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W3G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W4G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+  }
+  return launch_status("MTP input (embedding + dual RMSNorm + A4) launch failed");
 }
 
 // ---- SwiGLU -----------------------------------------------------------------

@@ -377,12 +377,11 @@ struct gfxinfer_session {
   int32_t mtp_proposal(uint32_t token, const uint32_t* device_token, const uint16_t* conditioning,
                        std::size_t position, uint32_t* output_token,
                        const uint64_t* device_position) {
-    GFXI_TRY(gather(hidden_b, token, device_token));
-    GFXI_TRY(gfxinfer_launch_dual_rms_norm_concat(hidden_b, mtp_pre_embedding_norm, conditioning,
-                                                  mtp_pre_hidden_norm, mtp_concat, H,
-                                                  spec.rms_norm_epsilon, 1, stream));
-    GFXI_TRY(gfxinfer_launch_quantize_activation_i4(mtp_concat, act_codes, act_scales, 2 * H, 1,
-                                                    stream));
+    // embedding gather + dual norm/concat + A4 quantizer in one launch
+    GFXI_TRY(gfxinfer_launch_mtp_input_quantize_i4(
+        embedding.format, embedding.weights, embedding.scales, embedding.rows, token, device_token,
+        mtp_pre_embedding_norm, conditioning, mtp_pre_hidden_norm, nullptr, act_codes, act_scales, H,
+        spec.rms_norm_epsilon, 1, stream));
     GFXI_TRY(gfxinfer_launch_gfx950_i4_gemm_half(mtp_fc.format, mtp_fc.weights, mtp_fc.scales,
                                                  act_codes, act_scales, mtp_input, mtp_fc.rows,
                                                  mtp_fc.columns, 1, 0, stream));

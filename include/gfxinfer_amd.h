@@ -270,6 +270,22 @@ int32_t gfxinfer_launch_dual_rms_norm_concat_batch(const uint16_t* left,
                                                    uint32_t batch, float epsilon,
                                                    int32_t add_unit_offset, void* stream);
 
+/* The MTP input in one launch: the token's embedding row dequantized from its tiled
+ * matrix (as gfxinfer_launch_lowbit_row_gather_tiled writes it; zeros for a token
+ * >= embedding_rows; indirect_token, if set, holds the token id), the dual RMSNorm/concat
+ * with the conditioning row (gfxinfer_launch_dual_rms_norm_concat), and the A4G128
+ * quantizer of the concatenated row (gfxinfer_launch_quantize_activation_i4): codes
+ * [2 * elements / 2], scales [2 * elements / 128] bit for bit; concatenated_output
+ * (fp16 [2 * elements]) may be null.  elements % 128 == 0, <= 6144.  No reference
+ * counterpart (the reference launches the three: qwen_runtime.cpp:728-758 and the
+ * quantizer of the fc projection's matrix() call, :779). */
+int32_t gfxinfer_launch_mtp_input_quantize_i4(
+    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+    size_t embedding_rows, uint32_t token, const uint32_t* indirect_token,
+    const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
+    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream);
+
 /* qwen_ops.h:44-49 launch_silu_multiply: fp16(silu(g) * u); elements % 128 == 0. */
 int32_t gfxinfer_launch_silu_multiply(const float* gate, const float* up, uint16_t* output,
                                       size_t elements, void* stream);

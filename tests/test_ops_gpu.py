@@ -170,6 +170,49 @@ def test_dual_rms_norm_concat(device, gx, orc, n):
     assert _close16(host(out, np.uint16), want)
 
 
+@pytest.mark.parametrize("fmt", [1, 2, 3])
+def test_mtp_input_equals_gather_dual_norm_quantizer(device, gx, orc, fmt):
+    """Embedding gather + dual RMSNorm/concat + A4 quantizer in one launch == the three
+    launches: codes, scales and the fp16 concat bit for bit, for a direct and a device
+    token id, and zeros for a token past the table."""
+    n, rows = 5120, 64
+    rng = np.random.default_rng(60 + fmt)
+    w = (rng.standard_normal((rows, n)) * 0.05).astype(np.float32)
+    _, codes, sc = orc.quantize_group128(w, fmt)
+    tcodes, tscales = gx.tile_group128(fmt, codes, sc, rows, n)
+    cond = _half(rng.standard_normal(n) * 3)
+    ew, cw = _bf16(rng.standard_normal(n) * 0.05), _bf16(rng.standard_normal(n) * 0.05)
+    dtc, dts, dcond, dew, dcw = D_(tcodes), D_(tscales), D_(cond), D_(ew), D_(cw)
+    L = gx.lib()
+    for token, indirect in ((37, False), (5, True), (rows + 3, False)):
+        gathered = empty((n,), np.uint16)
+        concat = empty((2 * n,), np.uint16)
+        a4, s4 = empty((n,), np.uint8), empty((2 * n // 128,), np.uint16)
+        say("mtp input pair", fmt, token)
+        if token < rows:
+            gx.check(L.gfxinfer_launch_lowbit_row_gather_tiled(fmt, dtc, dts, gathered.data_ptr(), token, rows, n, None))
+        else:
+            gathered.zero_()
+        gx.check(L.gfxinfer_launch_dual_rms_norm_concat(gathered.data_ptr(), dew, dcond, dcw, concat.data_ptr(), n,
+                                                        EPS, 1, None))
+        gx.check(L.gfxinfer_launch_quantize_activation_i4(concat.data_ptr(), a4.data_ptr(), s4.data_ptr(), 2 * n, 1,
+                                                          None))
+        want = [host(concat, np.uint16), host(a4), host(s4, np.uint16)]
+        concat2 = empty((2 * n,), np.uint16)
+        a42, s42 = empty((n,), np.uint8), empty((2 * n // 128,), np.uint16)
+        ind = dev(np.array([token], np.uint32)) if indirect else None
+        say("mtp input fused", fmt, token, indirect)
+        gx.check(L.gfxinfer_launch_mtp_input_quantize_i4(
+            fmt, dtc, dts, rows, 0 if indirect else token, ind.data_ptr() if indirect else None, dew, dcond, dcw,
+            concat2.data_ptr(), a42.data_ptr(), s42.data_ptr(), n, EPS, 1, None))
+        assert np.array_equal(host(concat2, np.uint16), want[0])
+        assert np.array_equal(host(a42), want[1])
+        assert np.array_equal(host(s42, np.uint16), want[2])
+    assert L.gfxinfer_launch_mtp_input_quantize_i4(fmt, dtc, dts, rows, 1, None, dew, dcond, dcw, None,
+                                                   a42.data_ptr(), s42.data_ptr(), 130, EPS, 1,
+                                                   None) == gx.INVALID_ARGUMENT
+
+
 @pytest.mark.parametrize("batch", [1, 7, 32])
 def test_dual_rms_norm_concat_batch_rows_equal_single(device, gx, orc, batch):
     """Each row of the batched launcher is bit-identical to the single-row launcher on
