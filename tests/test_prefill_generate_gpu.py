@@ -1,4 +1,4 @@
-"""Chunked prefill and the generate loop (§8(f) rows 2-3) against the reference's own
+"""Chunked prefill and the generate loop against the reference's own
 serial loops (cli/main.cpp:1055-1069 prefill, 1072-1110 generation), run through the
 same session API on the same synthetic model."""
 from __future__ import annotations
