@@ -201,6 +201,142 @@ def verify_gemm_bench(batches=(5, 16, 32), copies=4, reps=20):
     return out
 
 
+def _graph_time(stream, fn, n, reps):
+    """Average microseconds of fn(i) for i in 0..n-1, captured once and replayed reps times."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for i in range(n):
+            fn(i)
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(n):
+                fn(i)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+
+def gemv_table_bench(reps=40, budget=600e6):
+    """W3A4 and W4A4 GEMV on [17408, 5120] (up/gate) and
+    [5120, 17408] (down) at batch 1 and 5, the plain product over rotating weight copies
+    (about 600 MB, beyond the 256 MB Infinity Cache), plus the down shape as the
+    verifier launches it (split-K planes).  One JSON line per case; bit-exact int32
+    partials of the same kernels are checked by tests/test_gemm_gpu.py."""
+    import torch
+    import gfxinfer_amd as gx
+
+    torch.manual_seed(0x6E7)
+    stream = torch.cuda.Stream()
+    out = []
+    for fmt, wbits in ((gx.W3G128, 3), (gx.W4G128, 4)):
+        for rows, cols in ((17408, 5120), (5120, 17408)):
+            w = torch.randn(rows, cols, device="cuda") * 0.02
+            c0 = torch.empty(gx.tile_bytes(fmt, rows, cols), dtype=torch.uint8, device="cuda")
+            s0 = torch.empty(rows * cols // 128, dtype=torch.int16, device="cuda")
+            gx.launch_quantize_group128(fmt, w, rows, cols, c0, s0)
+            del w
+            n = max(2, int(budget // c0.numel()))
+            weights = [(c0, s0)] + [(c0.clone(), s0.clone()) for _ in range(n - 1)]
+            for batch in (1, 5):
+                x = torch.randn(batch, cols, device="cuda").half()
+                a = torch.empty(batch, cols // 2, dtype=torch.uint8, device="cuda")
+                sa = torch.empty(batch, cols // 128, dtype=torch.int16, device="cuda")
+                gx.launch_quantize_activation_i4(x, a, sa, cols, batch)
+                splits = gx.gemm_split_count(rows, cols, batch)
+                y = torch.empty(splits, batch, rows, device="cuda")
+                cases = [("plain", 1)] + ([("split", splits)] if splits > 1 else [])
+                for mode, sp in cases:
+                    if sp == 1:
+                        def fn(i):
+                            gx.launch_i4_gemm(fmt, weights[i][0], weights[i][1], a, sa, y, rows, cols, batch,
+                                              stream=stream)
+                    else:
+                        def fn(i):
+                            gx.launch_i4_gemm_split(fmt, weights[i][0], weights[i][1], a, sa, y, rows, cols, batch,
+                                                    sp, stream=stream)
+                    us = _graph_time(stream, fn, n, reps)
+                    nbytes = algorithmic_bytes(rows, cols, batch, wbits=wbits) + (sp - 1) * batch * rows * 4
+                    line = {"gemv": f"W{wbits}A4", "rows": rows, "columns": cols, "batch": batch, "mode": mode,
+                            "splits": sp, "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / us / 1e3, 1),
+                            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                    out.append(line)
+                    print(json.dumps(line), flush=True)
+            del weights
+    return out
+
+
+def gdn_window_bench(tokens=32, layers=48, reps=20, seed=2026):
+    """the GDN verify window at 27B shapes (32 value heads x 128 x 128
+    fp32 state, 16 key heads x 128) over `tokens` tokens with every per-token log the
+    rollback needs (conv inputs, normalized keys, deltas, decays), for `layers` layers'
+    own buffers, then the prefix restore of all layers to a seeded accepted length drawn
+    uniformly from [0, tokens].  Inputs follow the config: projected q/k/v ~ N(0, 1),
+    a, b ~ N(0, 1) (decay = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)).
+    Correctness of both launches: tests/test_ops_gpu.py, tests/test_runtime_gpu.py."""
+    import numpy as np
+    import torch
+    import gfxinfer_amd as gx
+
+    HK, HV, D, T = 16, 32, 128, tokens
+    C = 2 * HK * D + HV * D
+    L = gx.lib()
+    torch.manual_seed(seed)
+    accepted = int(np.random.default_rng(seed).integers(0, T + 1))
+    f32 = dict(device="cuda", dtype=torch.float32)
+    proj = [torch.randn(T, C, **f32) for _ in range(layers)]
+    conv_w = (torch.randn(C, 4, **f32) * 0.5).to(torch.bfloat16)
+    a = torch.randn(T, HV, **f32)
+    b = torch.randn(T, HV, **f32)
+    a_log = (torch.randn(HV, **f32) * 0.5).to(torch.bfloat16)
+    dt_bias = (torch.randn(HV, **f32) * 0.5).to(torch.bfloat16)
+    conv_states = torch.randn(layers, C, 4, **f32).half()
+    conv_final = torch.empty_like(conv_states)
+    states = torch.randn(layers, HV, D, D, **f32) * 0.1
+    states_final = torch.empty_like(states)
+    mixed = torch.empty(T, HV * D, **f32)
+    conv_log = torch.empty(layers, T, C, device="cuda", dtype=torch.float16)
+    key_log = torch.empty(layers, T, HK * D, **f32)
+    delta_log = torch.empty(layers, T, HV * D, **f32)
+    decay_log = torch.empty(layers, T, HV, **f32)
+    stream = torch.cuda.Stream()
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def window(i):
+        gx.check(L.gfxinfer_launch_gdn_conv_window(
+            p(proj[i]), p(conv_w), p(conv_states[i]), p(conv_final[i]), p(conv_log[i]), p(a), p(b), p(a_log),
+            p(dt_bias), p(states[i]), p(states_final[i]), p(mixed), p(key_log[i]), p(delta_log[i]),
+            p(decay_log[i]), T, HK, HV, D, stream.cuda_stream))
+
+    def restore(_):
+        gx.check(L.gfxinfer_launch_gdn_restore_prefix_all(
+            p(conv_states), p(states), p(conv_log), p(key_log), p(delta_log), p(decay_log), C, layers, T,
+            accepted, HK, HV, D, stream.cuda_stream))
+
+    window_us = _graph_time(stream, window, layers, reps)
+    restore_us = _graph_time(stream, restore, 1, reps)
+    state = HV * D * D * 4
+    window_bytes = (2 * state + T * C * 4 + T * HV * 8 + T * HV * D * 4 + C * 4 * 2 * 2
+                    + T * (C * 2 + HK * D * 4 + HV * D * 4 + HV * 4))
+    restore_bytes = layers * (2 * state + C * 4 * 2 * 2 + accepted * (C * 2 + HK * D * 4 + HV * D * 4 + HV * 4))
+    lines = [{"gdn": "conv_window", "tokens": T, "us_per_layer": round(window_us, 3), "bytes": window_bytes,
+              "gbs": round(window_bytes / window_us / 1e3, 1)},
+             {"gdn": "restore_prefix_all", "layers": layers, "accepted": accepted, "us": round(restore_us, 3),
+              "bytes": restore_bytes, "gbs": round(restore_bytes / restore_us / 1e3, 1),
+              "frac_hbm": round(restore_bytes / restore_us / 1e3 / HBM_PEAK_GBS, 4)}]
+    for line in lines:
+        print(json.dumps(line), flush=True)
+    return lines
+
+
 def _forced_acceptance(rng, depth):
     """Seeded Bernoulli(0.85) per draft; accepted = index of the first failure."""
     trials = rng.random(depth) < 0.85
@@ -402,6 +538,10 @@ def main():
     ap.add_argument("--probe-batch", type=int, default=5, help="--pmc-probe GEMM tokens")
     ap.add_argument("--verify-gemms", action="store_true",
                     help="time BASELINE config 3 (one block's projections + LM head argmax at 5/16/32 rows)")
+    ap.add_argument("--gemv-table", action="store_true",
+                    help="time BASELINE config 2 (W3A4/W4A4 GEMV, up and down shapes, batch 1 and 5)")
+    ap.add_argument("--gdn-window", action="store_true",
+                    help="time BASELINE config 4 (32-token GDN window with logs + restore to a seeded length)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -414,6 +554,12 @@ def main():
         return
     if args.verify_gemms:
         verify_gemm_bench()
+        return
+    if args.gemv_table:
+        gemv_table_bench()
+        return
+    if args.gdn_window:
+        gdn_window_bench()
         return
 
     r = gemv_bench(args.steps, args.warmup)

@@ -859,12 +859,13 @@ __global__ __launch_bounds__(256) void gdn_restore_conv_kernel(
   const std::size_t layer = i / channels, c = i - layer * channels;
   __half* s = states + i * 4;
   const __half* log = logs + layer * max_logged * channels;
-  __half w[4] = {s[0], s[1], s[2], s[3]};
-  for (uint32_t t = 0; t < accepted; ++t) {
-    w[0] = w[1];
-    w[1] = w[2];
-    w[2] = w[3];
-    w[3] = log[static_cast<std::size_t>(t) * channels + c];
+  // After `accepted` shifts the state is the last four of [state, log_0 .. log_{A-1}]:
+  // word j is element A + j of that sequence (no chain of dependent loads).
+  __half w[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t n = accepted + j;
+    w[j] = n < 4 ? s[n] : log[static_cast<std::size_t>(n - 4) * channels + c];
   }
   s[0] = w[0];
   s[1] = w[1];
@@ -873,38 +874,58 @@ __global__ __launch_bounds__(256) void gdn_restore_conv_kernel(
 }
 
 // Thread per four consecutive state columns of one row.
-__global__ __launch_bounds__(256) void gdn_restore_recurrent_kernel(
+// One workgroup per (layer, value head): the head's logged keys, deltas and decays of
+// the accepted tokens are staged in LDS once, then each thread replays them onto 16
+// four-column pieces of the 128 x 128 state (per element the same operations in token
+// order as the recurrence), so the logs cross the memory hierarchy once per head
+// instead of once per state piece.
+constexpr unsigned kRestoreThreads = 256;
+
+__global__ __launch_bounds__(kRestoreThreads) void gdn_restore_recurrent_kernel(
     float* __restrict__ states, const float* __restrict__ key_logs, const float* __restrict__ delta_logs,
-    const float* __restrict__ decay_logs, uint32_t layers, uint32_t max_logged, uint32_t accepted,
-    uint32_t key_heads, uint32_t value_heads) {
+    const float* __restrict__ decay_logs, uint32_t max_logged, uint32_t accepted, uint32_t key_heads,
+    uint32_t value_heads) {
   constexpr unsigned D = kGdnD;
-  const std::size_t per_layer = static_cast<std::size_t>(value_heads) * D * (D / 4);
-  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= per_layer * layers) return;
-  const std::size_t layer = i / per_layer;
-  const std::size_t rem = i - layer * per_layer;
-  const unsigned h = static_cast<unsigned>(rem / (D * (D / 4)));
-  const unsigned k = static_cast<unsigned>((rem / (D / 4)) % D);
-  const unsigned v4 = static_cast<unsigned>(rem % (D / 4));
+  constexpr unsigned kPieces = D * D / 4 / kRestoreThreads;  // 16 f32x4 per thread
+  __shared__ float keys[kGdnMaxTokens][D];
+  __shared__ float deltas[kGdnMaxTokens][D];
+  __shared__ float decays[kGdnMaxTokens];
+  const unsigned layer = blockIdx.x / value_heads, h = blockIdx.x - layer * value_heads;
   const unsigned kh = h / (value_heads / key_heads);
+  const unsigned tid = threadIdx.x;
   const std::size_t key_elements = static_cast<std::size_t>(key_heads) * D;
   const std::size_t value_elements = static_cast<std::size_t>(value_heads) * D;
-  f32x4* s = reinterpret_cast<f32x4*>(states) + i;
-  f32x4 S = *s;
-  const float* key_log = key_logs + layer * max_logged * key_elements + static_cast<std::size_t>(kh) * D + k;
-  const float* delta_log = delta_logs + layer * max_logged * value_elements + static_cast<std::size_t>(h) * D + v4 * 4;
-  const float* decay_log = decay_logs + layer * max_logged * value_heads + h;
-  for (uint32_t t = 0; t < accepted; ++t) {
-    const float decay = decay_log[static_cast<std::size_t>(t) * value_heads];
-    const float key = key_log[static_cast<std::size_t>(t) * key_elements];
-    const f32x4 delta = *reinterpret_cast<const f32x4*>(delta_log + static_cast<std::size_t>(t) * value_elements);
+  f32x4* state = reinterpret_cast<f32x4*>(states + (static_cast<std::size_t>(layer) * value_heads + h) * D * D);
+  f32x4 S[kPieces];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      S[j] = S[j] * decay;
-      S[j] = fmaf(key, delta[j], S[j]);
-    }
+  for (unsigned j = 0; j < kPieces; ++j) S[j] = state[tid + j * kRestoreThreads];
+  const float* key_log = key_logs + static_cast<std::size_t>(layer) * max_logged * key_elements + kh * D;
+  const float* delta_log = delta_logs + static_cast<std::size_t>(layer) * max_logged * value_elements + h * D;
+  for (unsigned e = tid; e < accepted * D; e += kRestoreThreads) {
+    const unsigned t = e / D, c = e - t * D;
+    keys[t][c] = key_log[static_cast<std::size_t>(t) * key_elements + c];
+    deltas[t][c] = delta_log[static_cast<std::size_t>(t) * value_elements + c];
   }
-  *s = S;
+  if (tid < accepted) {
+    decays[tid] = decay_logs[(static_cast<std::size_t>(layer) * max_logged + tid) * value_heads + h];
+  }
+  __syncthreads();
+#pragma unroll
+  for (unsigned j = 0; j < kPieces; ++j) {
+    const unsigned piece = tid + j * kRestoreThreads;
+    const unsigned k = piece / (D / 4), v = (piece % (D / 4)) * 4;
+    f32x4 x = S[j];
+    for (uint32_t t = 0; t < accepted; ++t) {
+      const float decay = decays[t], key = keys[t][k];
+      const f32x4 delta = *reinterpret_cast<const f32x4*>(&deltas[t][v]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[q] = x[q] * decay;
+        x[q] = fmaf(key, delta[q], x[q]);
+      }
+    }
+    state[piece] = x;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1486,9 +1507,11 @@ extern "C" int32_t gfxinfer_launch_gdn_restore_prefix_all(
   if (conv_states == nullptr || recurrent_states == nullptr || appended_logs == nullptr ||
       key_logs == nullptr || delta_logs == nullptr || decay_logs == nullptr || channels == 0 ||
       layer_count == 0 || maximum_logged_tokens == 0 || accepted_tokens == 0 ||
-      accepted_tokens > maximum_logged_tokens || channels > (1u << 24) || key_heads == 0 ||
-      value_heads == 0 || value_heads % key_heads != 0 || head_size != kGdnD) {
-    return fail(GFXI_INVALID_ARGUMENT, "invalid all-layer GDN prefix restore arguments");
+      accepted_tokens > maximum_logged_tokens || accepted_tokens > kGdnMaxTokens ||
+      channels > (1u << 24) || key_heads == 0 || value_heads == 0 || value_heads % key_heads != 0 ||
+      head_size != kGdnD || static_cast<uint64_t>(layer_count) * value_heads > (1u << 30)) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid all-layer GDN prefix restore arguments (at most 32 "
+                                       "accepted tokens)");
   }
   auto st = static_cast<hipStream_t>(stream);
   const std::size_t conv_threads = static_cast<std::size_t>(layer_count) * channels;
@@ -1499,10 +1522,9 @@ extern "C" int32_t gfxinfer_launch_gdn_restore_prefix_all(
   if (const int32_t s = launch_status("all-layer GDN convolution prefix restore launch failed"); s != GFXI_OK) {
     return s;
   }
-  const std::size_t threads = static_cast<std::size_t>(layer_count) * value_heads * kGdnD * (kGdnD / 4);
-  hipLaunchKernelGGL(gdn_restore_recurrent_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                     dim3(256), 0, st, recurrent_states, key_logs, delta_logs, decay_logs, layer_count,
-                     maximum_logged_tokens, accepted_tokens, key_heads, value_heads);
+  hipLaunchKernelGGL(gdn_restore_recurrent_kernel, dim3(layer_count * value_heads), dim3(kRestoreThreads), 0,
+                     st, recurrent_states, key_logs, delta_logs, decay_logs, maximum_logged_tokens,
+                     accepted_tokens, key_heads, value_heads);
   return launch_status("all-layer GDN recurrent prefix restore launch failed");
 }
 

@@ -389,6 +389,7 @@ def test_gdn_restore_rejects_bad_accept(gx):
     L = gx.lib()
     assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
     assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 64, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("T,in_place", [(32, False), (5, True), (1, True)])
