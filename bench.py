@@ -530,7 +530,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--verify-rounds", type=int, default=60)
-    ap.add_argument("--verify-depths", default="4,31",
+    ap.add_argument("--verify-depths", default="4,8,16,31",
                     help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the rocprofv3 --pmc workload (calibration copy + plain GEMM launches)")
