@@ -406,6 +406,50 @@ def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026):
             **results}
 
 
+def prefill_bench(prompt_tokens=512, serial_tokens=64, seed=2026, context=4096):
+    """Chunked prefill against the reference's serial prefill loop on the synthetic
+    27B-shaped model: time to the first generated token for a `prompt_tokens` prompt
+    with the MTP cache kept in step (gfxinfer_session_prefill, 32-token verifier blocks
+    + batched MTP cache update), and the per-token rate of the loop the reference CLI
+    runs (greedy_step + mtp_draft per prompt token, cli/main.cpp:1055-1069), timed over
+    `serial_tokens` tokens.  Both leave the same state (tests/test_prefill_generate_gpu.py)."""
+    import numpy as np
+    import torch
+    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, qwen38_27b_spec
+
+    spec = qwen38_27b_spec()
+    model = SyntheticModel(spec, seed)
+    prompt = np.random.default_rng(seed).integers(0, spec.tokenizer_vocabulary_size, prompt_tokens)
+    prompt = [int(t) for t in prompt]
+    try:
+        chunked = QwenDecodeSession(model, context, 0)
+        chunked.prefill(prompt[:64])  # warm-up of the block kernels
+        chunked.close()
+        chunked = QwenDecodeSession(model, context, 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        chunked.prefill(prompt)
+        chunked_s = time.perf_counter() - t0
+        chunked.close()
+        serial = QwenDecodeSession(model, context, 0)
+        serial.greedy_step(prompt[0])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in prompt[1:1 + serial_tokens]:
+            serial.mtp_draft(t)
+            serial.greedy_step(t)
+        serial_s = time.perf_counter() - t0
+        serial.close()
+    finally:
+        model.close()
+    line = {"prefill": "chunked", "prompt_tokens": prompt_tokens, "seconds": round(chunked_s, 4),
+            "tok_s": round(prompt_tokens / chunked_s, 1),
+            "serial_tok_s": round(serial_tokens / serial_s, 1),
+            "speedup": round((prompt_tokens / chunked_s) / (serial_tokens / serial_s), 2)}
+    print(json.dumps(line), flush=True)
+    return line
+
+
 def _tensor_names(spec):
     """Matrix and vector names of the synthetic checkpoint (converter naming)."""
     names = ["lm_head.weight", "model.language_model.norm.weight"]
@@ -540,6 +584,8 @@ def main():
                     help="time BASELINE config 3 (one block's projections + LM head argmax at 5/16/32 rows)")
     ap.add_argument("--gemv-table", action="store_true",
                     help="time BASELINE config 2 (W3A4/W4A4 GEMV, up and down shapes, batch 1 and 5)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time chunked prefill against the reference's serial prefill loop (27B shapes)")
     ap.add_argument("--gdn-window", action="store_true",
                     help="time BASELINE config 4 (32-token GDN window with logs + restore to a seeded length)")
     args = ap.parse_args()
@@ -560,6 +606,9 @@ def main():
         return
     if args.gdn_window:
         gdn_window_bench()
+        return
+    if args.prefill:
+        prefill_bench()
         return
 
     r = gemv_bench(args.steps, args.warmup)
