@@ -274,6 +274,41 @@ def gemv_table_bench(reps=40, budget=600e6):
     return out
 
 
+def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
+    """Yardstick for the GEMV roofline: one launch of a plain streaming read
+    (gfxinfer_debug_stream_read) of the headline GEMV's algorithmic bytes, half and
+    twice that, and the LM head's size, rotating over copies (about 640 MB, beyond the
+    256 MB Infinity Cache) and over launch widths.  One JSON line per case and one per
+    size with the fastest width."""
+    import math
+    import torch
+    import gfxinfer_amd as gx
+
+    stream = torch.cuda.Stream()
+    data = torch.randint(0, 2**31 - 1, (total // 4,), dtype=torch.int32, device="cuda")
+    widths = (1024, 2048, 4096, 8192)
+    sink = torch.zeros(max(widths) * 256, dtype=torch.int32, device="cuda")
+    headline = algorithmic_bytes(17408, 5120, 5)
+    out = []
+    for nbytes in (headline // 2, headline, 2 * headline, 423624704):
+        nbytes -= nbytes % 16
+        slot = (nbytes + 255) // 256 * 256
+        copies = max(1, min(total // slot, math.ceil(budget / slot)))
+        best = None
+        for width in widths:
+            def fn(i, width=width):
+                gx.debug_stream_read(data.data_ptr() + (i % copies) * slot, nbytes, sink, width, stream=stream)
+            us = _graph_time(stream, fn, max(copies, 16) // copies * copies, reps)
+            line = {"read_floor": nbytes, "workgroups": width, "copies": copies, "us": round(us, 3),
+                    "gbs": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            print(json.dumps(line), flush=True)
+            if best is None or us < best["us"]:
+                best = line
+        out.append(dict(best, best=True))
+        print(json.dumps(out[-1]), flush=True)
+    return out
+
+
 def gdn_window_bench(tokens=32, layers=48, reps=20, seed=2026):
     """the GDN verify window at 27B shapes (32 value heads x 128 x 128
     fp32 state, 16 key heads x 128) over `tokens` tokens with every per-token log the
@@ -586,6 +621,8 @@ def main():
                     help="time BASELINE config 2 (W3A4/W4A4 GEMV, up and down shapes, batch 1 and 5)")
     ap.add_argument("--prefill", action="store_true",
                     help="time chunked prefill against the reference's serial prefill loop (27B shapes)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="time a plain streaming read of the GEMV's bytes (what one launch can reach)")
     ap.add_argument("--gdn-window", action="store_true",
                     help="time BASELINE config 4 (32-token GDN window with logs + restore to a seeded length)")
     args = ap.parse_args()
@@ -606,6 +643,9 @@ def main():
         return
     if args.gdn_window:
         gdn_window_bench()
+        return
+    if args.read_floor:
+        read_floor_bench()
         return
     if args.prefill:
         prefill_bench()

@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_gemm_argmax_workspace_bytes": (SZ, [SZ, U32]),
     "gfxinfer_launch_gfx950_i4_gemm_argmax": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, SZ, P, P]),
     "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
+    "gfxinfer_debug_stream_read": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled_indirect": (I32, [I32, P, P, P, P, SZ, SZ, P]),
     "gfxinfer_launch_rms_norm": (I32, [P, P, P, SZ, F32, I32, P]),
@@ -249,6 +250,10 @@ def launch_i8_gemm(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
 
 def debug_gemm_partials(fmt, w, abits, a, rows, columns, batch, partials, stream=None):
     check(lib().gfxinfer_debug_gemm_partials(fmt, _p(w), abits, _p(a), rows, columns, batch, _p(partials), _stream(stream)))
+
+
+def debug_stream_read(data, nbytes, sink, workgroups, stream=None):
+    check(lib().gfxinfer_debug_stream_read(_p(data), nbytes, _p(sink), workgroups, _stream(stream)))
 
 
 def launch_row_gather_tiled(fmt, w, ws, out, row, rows, columns, stream=None):

@@ -1705,3 +1705,41 @@ extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled_indirect(
   return row_gather_entry(format, tiled_weights, tiled_scales, output, 0, row, rows, columns,
                           static_cast<hipStream_t>(stream));
 }
+
+// HBM read floor: a plain streaming read of `bytes` (16-byte loads, grid-stride, two
+// loads in flight per lane), the yardstick for what one launch of a weight-streaming
+// kernel can reach at a given size on this device.  Each lane folds what it read into
+// an XOR; the one store is taken only when the fold equals a fixed odd constant, so
+// the reads stay live and the sink is written (by whichever lanes hit it) at most once.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ data,
+                                                          size_t count, uint32_t* sink) {
+  const size_t lane = static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x;
+  const size_t stride = static_cast<size_t>(gridDim.x) * 256u;
+  uint32_t fold = 0;
+  size_t i = lane;
+  for (; i + stride < count; i += 2 * stride) {
+    const uint4 a = data[i];
+    const uint4 b = data[i + stride];
+    fold ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+  }
+  if (i < count) {
+    const uint4 a = data[i];
+    fold ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  if (fold == 0x9E3779B9u) sink[lane] = fold;
+}
+
+extern "C" int32_t gfxinfer_debug_stream_read(const void* data, size_t bytes, uint32_t* sink,
+                                              uint32_t workgroups, void* stream) {
+  if (data == nullptr || sink == nullptr) return fail(GFXI_INVALID_ARGUMENT, "null buffer");
+  if (bytes == 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(data) % 16 != 0) {
+    return fail(GFXI_INVALID_ARGUMENT, "stream read needs a 16-byte aligned, nonzero multiple of 16 bytes");
+  }
+  if (workgroups == 0 || workgroups > 65536) {
+    return fail(GFXI_INVALID_ARGUMENT, "workgroups must be in [1, 65536]");
+  }
+  hipLaunchKernelGGL(stream_read_kernel, dim3(workgroups), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint4*>(data), bytes / 16,
+                     sink);
+  return launch_status("stream read");
+}

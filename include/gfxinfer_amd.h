@@ -188,6 +188,14 @@ int32_t gfxinfer_debug_gemm_partials(int32_t format, const uint8_t* tiled_weight
                                      size_t rows, size_t columns, uint32_t batch,
                                      int32_t* partials, void* stream);
 
+/* Calibration: a plain streaming read of `bytes` from `data` (16-byte aligned,
+ * a nonzero multiple of 16) by `workgroups` x 256 lanes, so that a weight-streaming
+ * kernel's time can be set beside what one launch reading the same bytes takes on the
+ * same device.  `sink` must hold workgroups x 256 uint32; it is written only in the
+ * unlikely case a lane's XOR of its data equals 0x9E3779B9.  No reference counterpart. */
+int32_t gfxinfer_debug_stream_read(const void* data, size_t bytes, uint32_t* sink,
+                                   uint32_t workgroups, void* stream);
+
 /* lowbit_gemv.h:46-54 (launch_lowbit_row_gather_tiled): fp16 row
  * out[c] = fp16(w(row, c) * ws(row, c/128)).  W3G128 and W4G128. */
 int32_t gfxinfer_launch_lowbit_row_gather_tiled(int32_t format, const uint8_t* tiled_weights,

@@ -380,3 +380,19 @@ def test_gemm_argmax_ties_limit_and_mapping(device, gx, orc):
     ids = (np.arange(rows, dtype=np.uint32) * 7 + 3) % 100000
     tokens, _ = _gemm_argmax(gx, fmt, q, rows, cols, batch, 100, ids=ids)
     assert (tokens == ids[0]).all()
+
+
+def test_stream_read_floor_entry(gx, device):
+    """The calibration read runs over in-bounds sizes (a tail shorter than one stride
+    included), leaves the sink untouched for data whose XOR is not the marker, and
+    rejects misaligned or empty requests."""
+    import torch
+    data = torch.zeros(3 * 256 * 16 + 7 * 16, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4 * 256, dtype=torch.int32, device="cuda")
+    for width in (1, 3, 4):
+        gx.debug_stream_read(data, data.numel(), sink, width)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    for nbytes, width in ((0, 1), (24, 1), (16, 0)):
+        with pytest.raises(gx.GfxinferError):
+            gx.debug_stream_read(data, nbytes, sink, width)
