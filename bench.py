@@ -21,6 +21,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -36,7 +37,10 @@ def algorithmic_bytes(rows, cols, batch, wbits=3, abits=4):
             + batch * (cols // 128) * 2 + batch * rows * 4)
 
 
-def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16):
+def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16, windows=5):
+    """The headline step, timed exactly: `warmup` untimed steps, then `windows` timing
+    windows of exactly `steps` steps each (HIP events on the launch stream around graph
+    replays); the median window is reported.  Step i uses weight copy i % copies."""
     import numpy as np
     import torch
     import gfxinfer_amd as gx
@@ -66,40 +70,59 @@ def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16):
     def gemm_only(i, s):
         gx.launch_i4_gemm(fmt, codes[i % copies], scales[i % copies], acodes, ascales, y, rows, cols, batch, stream=s)
 
-    def capture(fn):
+    def capture(fn, n):
+        """Graph of steps 0 .. n-1 (n a multiple of `copies` keeps the rotation aligned)."""
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
-            for i in range(copies):  # warm the kernels outside capture
+            for i in range(min(n, copies)):  # warm the kernels outside capture
                 fn(i, stream)
             stream.synchronize()
             with torch.cuda.graph(g, stream=stream):
-                for i in range(copies):
+                for i in range(n):
                     fn(i, stream)
         return g
 
-    g_step = capture(step)
-    g_gemm = capture(gemm_only)
-    reps = max(1, steps // copies)
-    wreps = max(1, warmup // copies)
+    # `steps` = full * chunk + rest: `full` replays of a chunk graph plus one remainder graph.
+    chunk = min(steps, 32 * copies) // copies * copies or steps
+    full, rest = divmod(steps, chunk)
 
-    def timed(graph):
+    def runner(fn):
+        main = capture(fn, chunk)
+        tail = capture(fn, rest) if rest else None
+
+        def run_steps(n_full, with_tail):
+            for _ in range(n_full):
+                main.replay()
+            if with_tail and tail is not None:
+                tail.replay()
+        return run_steps
+
+    def timed(fn):
+        run_steps = runner(fn)
         with torch.cuda.stream(stream):
-            for _ in range(wreps):
-                graph.replay()
+            wfull, wrest = divmod(warmup, chunk)
+            run_steps(wfull, False)
+            if wrest:  # the warmup's remainder as eager steps
+                for i in range(wrest):
+                    fn(i, stream)
             torch.cuda.synchronize()
-            start = torch.cuda.Event(enable_timing=True)
-            stop = torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            for _ in range(reps):
-                graph.replay()
-            stop.record(stream)
-            stop.synchronize()
+            results = []
+            for _ in range(windows):
+                start = torch.cuda.Event(enable_timing=True)
+                stop = torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                run_steps(full, True)
+                stop.record(stream)
+                stop.synchronize()
+                results.append(start.elapsed_time(stop) / steps)  # ms per step
             torch.cuda.synchronize()
-        return start.elapsed_time(stop) / (reps * copies)  # ms per step
+        return float(np.median(results)), results
 
-    ms_step = timed(g_step)
-    ms_gemm = timed(g_gemm)
-    return dict(ms_step=ms_step, ms_gemm=ms_gemm, steps=reps * copies, warmup=wreps * copies,
+    ms_step, step_windows = timed(step)
+    ms_gemm, gemm_windows = timed(gemm_only)
+    return dict(ms_step=ms_step, ms_gemm=ms_gemm, steps=steps, warmup=warmup, windows=windows,
+                step_windows_ms=[round(v, 6) for v in step_windows],
+                gemm_windows_ms=[round(v, 6) for v in gemm_windows],
                 rows=rows, cols=cols, batch=batch, copies=copies,
                 weight_bytes=sum(c.numel() for c in codes) + 2 * sum(s.numel() for s in scales))
 
@@ -434,11 +457,56 @@ def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026):
                 "weight_gbs": round(round_bytes * n / elapsed / 1e9, 1),
                 "weight_frac_of_hbm_peak": round(round_bytes * n / elapsed / 1e9 / HBM_PEAK_GBS, 4),
             }
+        results.update(reference_bench_rates(model, spec))
     finally:
         model.close()
     return {"model_weight_bytes": verifier_bytes + proposal_bytes, "create_s": round(create_s, 3),
             "verifier_weight_bytes": verifier_bytes, "proposal_weight_bytes": proposal_bytes,
             **results}
+
+
+def reference_bench_rates(model, spec, block_sizes=(5, 32), blocks=12, mtp_steps=40):
+    """The reference's own verifier-only and proposal-only rates, measured the way its CLI
+    measures them on the same session API:
+    - block-bench (cli/main.cpp:846-915): block_step over B tokens, each block's outputs
+      feeding the next, wall clock per call; tokens/s = blocks * B / total time;
+    - mtp-bench (cli/main.cpp:1140-1207): greedy_step and mtp_draft alternating; target
+      and MTP-draft steps/s = calls / time spent in each."""
+    from gfxinfer_amd.runtime import QwenDecodeSession
+    out = {}
+    for batch in block_sizes:
+        session = QwenDecodeSession(model, 4096, 0)
+        try:
+            inputs = [(1 + i) % spec.tokenizer_vocabulary_size for i in range(batch)]
+            inputs = session.block_step(inputs)  # warm-up block (kernels, caches)
+            total = 0.0
+            for _ in range(blocks):
+                t0 = time.perf_counter()
+                inputs = session.block_step(inputs)
+                total += time.perf_counter() - t0
+        finally:
+            session.close()
+        out[f"block_step_{batch}"] = {"blocks": blocks, "ms_per_block": round(total / blocks * 1e3, 4),
+                                      "evaluated_tok_s": round(blocks * batch / total, 2)}
+    session = QwenDecodeSession(model, 4096, 0)
+    try:
+        target_s = draft_s = 0.0
+        token = session.greedy_step(1)
+        candidate = session.mtp_draft(token)
+        for _ in range(mtp_steps):
+            t0 = time.perf_counter()
+            token = session.greedy_step(token)
+            t1 = time.perf_counter()
+            candidate = session.mtp_draft(token)
+            t2 = time.perf_counter()
+            target_s += t1 - t0
+            draft_s += t2 - t1
+    finally:
+        session.close()
+    out["mtp_bench"] = {"steps": mtp_steps, "target_steps_s": round(mtp_steps / target_s, 2),
+                        "mtp_draft_steps_s": round(mtp_steps / draft_s, 2)}
+    del candidate
+    return out
 
 
 def prefill_bench(prompt_tokens=512, serial_tokens=64, seed=2026, context=4096):
@@ -513,9 +581,15 @@ def _tensor_names(spec):
 def cpu_baseline(rows=17408, cols=5120, seconds=10.0):
     """Oracle W3A8 quantize + dequant-dot GEMV on host cores: the
     GEMV repeats for about `seconds` of CPU time and the median run is reported."""
+    import tempfile
     import numpy as np
     from oracle import oracle as O
 
+    build_dir = tempfile.mkdtemp(prefix="gfxi_cpu_baseline_")
+    try:
+        flags = O.use_native_build(build_dir)
+    except (OSError, subprocess.CalledProcessError) as e:  # no compiler: the prebuilt -O2 oracle
+        flags = f"prebuilt oracle/liboracle.so (-O2; native build failed: {e})"
     rng = np.random.default_rng(0x5EED0001)
     w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
     x16 = rng.standard_normal((1, cols)).astype(np.float16).view(np.uint16)
@@ -551,7 +625,7 @@ def cpu_baseline(rows=17408, cols=5120, seconds=10.0):
         "sample": (f"BASELINE config 1: W3G128 [{rows},{cols}] x A8 batch 1 dequant-dot GEMV, median of "
                    f"{repeats} runs = {gemv * 1e3:.1f} ms over {nbytes} algorithmic bytes; "
                    f"quantize_group128 of the same matrix {min(tq):.2f} s; CPU {model}, "
-                   f"nproc {os.cpu_count()}"),
+                   f"nproc {os.cpu_count()}; oracle/oracle.c built with {flags}, OpenMP over rows"),
     }
 
 
@@ -590,22 +664,29 @@ def pmc_probe(launches=8, rows=17408, cols=5120, batch=5):
                       "gemm_algorithmic_bytes": algorithmic_bytes(rows, cols, batch)}))
 
 
-def measured_traffic():
-    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, or None."""
+def committed_profile():
+    """The headline kernel's committed rocprofv3 summary: its file, average dispatch
+    duration (kernel trace) and HBM bytes per launch (FETCH_SIZE + WRITE_SIZE passes,
+    calibrated), or None where the summary lacks them."""
+    out = {"file": os.path.relpath(PROFILE, ROOT), "kernel_us": None, "traffic": None}
     try:
         for line in open(PROFILE):
             if line.startswith("traffic_bytes_per_launch"):
-                return int(line.split("=")[1].split()[0])
+                out["traffic"] = int(line.split("=")[1].split()[0])
+            elif line.startswith("kernel_avg_us"):
+                out["kernel_us"] = float(line.split("=")[1].split()[0])
+            elif line.startswith("tree"):
+                out["tree"] = line.split("=", 1)[1].strip()
     except (OSError, ValueError, IndexError):
         pass
-    return None
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=8000)
-    ap.add_argument("--warmup", type=int, default=800)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--verify-rounds", type=int, default=60)
@@ -652,6 +733,7 @@ def main():
         return
 
     r = gemv_bench(args.steps, args.warmup)
+    profile = committed_profile()
     nbytes = algorithmic_bytes(r["rows"], r["cols"], r["batch"])
     step_gbs = nbytes / (r["ms_step"] * 1e-3) / 1e9
     gemm_gbs = nbytes / (r["ms_gemm"] * 1e-3) / 1e9
@@ -682,13 +764,27 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemm_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "traffic": profile["traffic"],
             "kernel": "lowbit_gemm_kernel<W3,A4,GP=2>",
             "kernel_us": round(r["ms_gemm"] * 1e3, 3),
             "algorithmic_bytes": nbytes,
+            "timing": (f"median of {r['windows']} windows of exactly {r['steps']} launches after "
+                       f"{r['warmup']} warmup launches, HIP events on the launch stream around "
+                       "graph replays (includes the gap between consecutive dispatches)"),
+            "profile": profile,
         },
+        "step_windows_ms": r["step_windows_ms"],
+        "gemm_windows_ms": r["gemm_windows_ms"],
         "reference_packed_gbps": round(codes_only / (r["ms_step"] * 1e-3) / 1e9, 2),
     }
+    if profile["kernel_us"]:
+        agree = abs(profile["kernel_us"] - r["ms_gemm"] * 1e3) / profile["kernel_us"]
+        out["roofline"]["profile"]["frac"] = round(nbytes / profile["kernel_us"] / 1e3 / HBM_PEAK_GBS, 4)
+        out["roofline"]["profile"]["events_vs_profile"] = round(agree, 4)
+        if agree > 0.05:
+            out["roofline"]["profile"]["why_they_differ"] = (
+                "rocprofv3 times each dispatch from its first wave to its end; the events here time "
+                "back-to-back graph launches, so they also hold the dispatch gap between launches")
     if not args.no_verify:
         depths = tuple(int(d) for d in args.verify_depths.split(",") if d)
         out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds)

@@ -103,8 +103,16 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position": (I32, [P, P, P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_gdn_conv_update": (I32, [P, P, P, P, SZ, P]),
+    "gfxinfer_launch_gdn_recurrent_decode": (I32, [P, P, P, P, P, P, P, P, P, U32, U32, U32, P, P]),
+    "gfxinfer_launch_gdn_restore_prefix": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P]),
+    "gfxinfer_launch_kv_append": (I32, [P, P, P, P, SZ, SZ, SZ, P]),
+    "gfxinfer_launch_gated_attention_decode": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_argmax": (I32, [P, P, SZ, P]),
     # include/gfxinfer_runtime.h
     "gfxinfer_model_spec_qwen38_27b": (None, [P]),
+    "gfxinfer_model_spec_tensor_count": (SZ, [P]),
+    "gfxinfer_model_spec_tensor": (I32, [P, SZ, P]),
     "gfxinfer_model_create_synthetic": (I32, [P, ctypes.c_uint64, I32, P]),
     "gfxinfer_model_destroy": (None, [P]),
     "gfxinfer_model_stream": (P, [P]),

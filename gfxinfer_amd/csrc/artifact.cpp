@@ -193,7 +193,7 @@ extern "C" int32_t gfxinfer_artifact_open(const char* path, int32_t verify_check
       return fail(GFXI_IO_ERROR, std::string("cannot stat ") + path + ": " + std::strerror(errno));
     }
     if (st.st_size < static_cast<off_t>(sizeof(DiskHeader))) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "artifact is smaller than its header");
+      return fail(GFXI_CORRUPT_ARTIFACT, "file too short to hold a .gfxi header");
     }
     a->bytes = static_cast<std::size_t>(st.st_size);
     void* m = ::mmap(nullptr, a->bytes, PROT_READ, MAP_PRIVATE, a->fd, 0);
@@ -205,33 +205,33 @@ extern "C" int32_t gfxinfer_artifact_open(const char* path, int32_t verify_check
     DiskHeader h;
     std::memcpy(&h, a->map, sizeof h);
     if (std::memcmp(h.magic, kMagic, sizeof kMagic) != 0) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "invalid .gfxi magic");
+      return fail(GFXI_CORRUPT_ARTIFACT, "not a .gfxi file (first eight bytes differ)");
     }
     if (h.version != kFormatVersion || h.header_bytes != sizeof(DiskHeader)) {
-      return fail(GFXI_UNSUPPORTED, "unsupported .gfxi artifact version");
+      return fail(GFXI_UNSUPPORTED, "format version or header size this reader does not know");
     }
-    if (h.endian_tag != kEndianTag) return fail(GFXI_UNSUPPORTED, "artifact byte order is unsupported");
+    if (h.endian_tag != kEndianTag) return fail(GFXI_UNSUPPORTED, "file written with the other byte order");
     if (h.directory_entry_bytes != sizeof(DiskEntry)) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "unexpected directory entry size");
+      return fail(GFXI_CORRUPT_ARTIFACT, "directory entries are not 128 bytes");
     }
-    if (h.file_bytes != a->bytes) return fail(GFXI_CORRUPT_ARTIFACT, "artifact length does not match header");
+    if (h.file_bytes != a->bytes) return fail(GFXI_CORRUPT_ARTIFACT, "file size differs from the size the header records");
     const uint64_t directory_bytes = static_cast<uint64_t>(h.tensor_count) * sizeof(DiskEntry);
     if (!in_file(h.directory_offset, directory_bytes, h.file_bytes) ||
         !in_file(h.strings_offset, h.strings_bytes, h.file_bytes) ||
         !in_file(h.data_offset, h.data_bytes, h.file_bytes) ||
         h.strings_offset != h.directory_offset + directory_bytes ||
         h.data_offset < h.strings_offset + h.strings_bytes) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "artifact section bounds are invalid");
+      return fail(GFXI_CORRUPT_ARTIFACT, "directory, name table or payload area lies outside the file or out of order");
     }
     if (verify_checksums != 0 &&
         crc64_update(0, a->map + h.directory_offset, directory_bytes + h.strings_bytes) !=
             h.manifest_crc64) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "artifact manifest checksum mismatch");
+      return fail(GFXI_CORRUPT_ARTIFACT, "CRC-64 of directory and names differs from the header");
     }
     const std::string arch = fixed(h.target_arch), model = fixed(h.model_id),
                       weights = fixed(h.weights_id), recipe = fixed(h.recipe_id);
     if (arch.empty() || model.empty() || weights.empty() || recipe.empty()) {
-      return fail(GFXI_CORRUPT_ARTIFACT, "artifact identity is incomplete");
+      return fail(GFXI_CORRUPT_ARTIFACT, "target, model, weights or recipe id is empty");
     }
     std::memcpy(a->identity.target_arch, h.target_arch, sizeof h.target_arch);
     std::memcpy(a->identity.model_id, h.model_id, sizeof h.model_id);
@@ -247,21 +247,21 @@ extern "C" int32_t gfxinfer_artifact_open(const char* path, int32_t verify_check
       std::memcpy(&e, a->map + h.directory_offset + static_cast<uint64_t>(i) * sizeof(DiskEntry), sizeof e);
       if (e.rank > 4 || e.dtype < kDtypeU8 || e.dtype > kDtypeF32 || e.quantization > 5 ||
           e.name_bytes == 0 || !in_file(e.name_offset, e.name_bytes, h.strings_bytes)) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor directory entry");
+        return fail(GFXI_CORRUPT_ARTIFACT, "directory entry has an impossible rank, dtype, quantization or name span");
       }
       std::string name(strings + e.name_offset, e.name_bytes);
       if (!valid_name(name) || a->index.count(name) != 0) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "invalid or duplicate tensor name: " + name);
+        return fail(GFXI_CORRUPT_ARTIFACT, "tensor name empty, malformed or repeated: " + name);
       }
       if (e.alignment < kFileAlignment || (e.alignment & (e.alignment - 1)) != 0 ||
           e.data_offset % e.alignment != 0 || !in_file(e.data_offset, e.data_bytes, h.file_bytes) ||
           e.data_offset < h.data_offset) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor payload bounds: " + name);
+        return fail(GFXI_CORRUPT_ARTIFACT, "data payload misaligned or outside the file: " + name);
       }
       if (e.aux_bytes != 0 && (e.aux_offset % e.alignment != 0 ||
                                !in_file(e.aux_offset, e.aux_bytes, h.file_bytes) ||
                                e.aux_offset < h.data_offset)) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "invalid tensor auxiliary bounds: " + name);
+        return fail(GFXI_CORRUPT_ARTIFACT, "scale payload misaligned or outside the file: " + name);
       }
       gfxinfer_artifact_tensor t{};
       t.dtype = e.dtype;
@@ -293,13 +293,13 @@ extern "C" int32_t gfxinfer_artifact_open(const char* path, int32_t verify_check
         }
       }
       if (bad >= 0) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "tensor checksum mismatch: " + a->names[static_cast<std::size_t>(bad)]);
+        return fail(GFXI_CORRUPT_ARTIFACT, "CRC-64 of the payload differs from its entry: " + a->names[static_cast<std::size_t>(bad)]);
       }
     }
     std::sort(ranges.begin(), ranges.end());
     for (std::size_t i = 1; i < ranges.size(); ++i) {
       if (ranges[i].first < ranges[i - 1].second) {
-        return fail(GFXI_CORRUPT_ARTIFACT, "tensor payload regions overlap");
+        return fail(GFXI_CORRUPT_ARTIFACT, "two payloads share bytes");
       }
     }
     for (std::size_t i = 0; i < a->tensors.size(); ++i) a->tensors[i].name = a->names[i].c_str();
@@ -480,6 +480,17 @@ extern "C" int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec
     if (!gfx12 && arch != "gfx950") {
       return fail(GFXI_UNSUPPORTED, "artifact target is " + arch + "; expected gfx950 or gfx1200");
     }
+    // The reference runtime reads gfx1200 codes as gfx12 tiles only when the recipe names
+    // "tiled-v", and W3 codes as sequential 3-bit fragments only when it names "w3seq"
+    // (qwen_runtime.cpp:957-960); the other layouts (row-major codes, bit-plane W3) are not
+    // re-tiled here, so such files are refused rather than loaded as the wrong weights.
+    const std::string recipe(a->identity.recipe_id, strnlen(a->identity.recipe_id, 64));
+    const bool tiled = recipe.find("tiled-v") != std::string::npos;
+    const bool sequential_w3 = recipe.find("w3seq") != std::string::npos;
+    if (gfx12 && !tiled) {
+      return fail(GFXI_UNSUPPORTED, "gfx1200 recipe " + recipe + " stores row-major codes; only the "
+                                    "tiled recipes (\"tiled-v\") load");
+    }
     std::vector<Tensor> tensors = model_tensors(*spec);
     gfxinfer_artifact_tensor head{}, ids{};
     const bool draft = a->index.count("mtp.draft_head.weight") != 0;
@@ -526,6 +537,10 @@ extern "C" int32_t gfxinfer_model_create_from_artifact(const gfxinfer_model_spec
                                         "does not run (W2G128, W3G128 and W4G128 only)");
         }
         t.format = e.quantization;  // the artifact's recipe decides W2, W3 or W4
+        if (gfx12 && t.format == GFXI_W3G128 && !sequential_w3) {
+          return fail(GFXI_UNSUPPORTED, "gfx1200 recipe " + recipe + " stores W3 tensor " + t.name +
+                                        " as bit planes; only sequential W3 (\"w3seq\") loads");
+        }
         const uint64_t bits = code_bits(t.format);
         if (e.dtype != kDtypeU8 || e.rank != 2 || e.dimensions[0] != t.rows ||
             e.dimensions[1] != t.columns || e.data_bytes != count * bits / 8 ||

@@ -374,13 +374,69 @@ extern "C" int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* sp
   });
 }
 
-extern "C" void gfxinfer_model_destroy(gfxinfer_model* model) {
-  if (model == nullptr) return;
+namespace gfx950 {
+namespace {
+void free_model(gfxinfer_model* model) {
   (void)hipSetDevice(model->device);
   if (model->stream != nullptr) (void)hipStreamSynchronize(model->stream);
   if (model->arena != nullptr) (void)hipFree(model->arena);
   if (model->stream != nullptr) (void)hipStreamDestroy(model->stream);
   delete model;
+}
+}  // namespace
+
+void retain_model(gfxinfer_model* model) {
+  const std::lock_guard<std::mutex> hold(model->lifetime);
+  ++model->sessions;
+}
+
+void release_model_reference(gfxinfer_model* model) {
+  bool last = false;
+  {
+    const std::lock_guard<std::mutex> hold(model->lifetime);
+    --model->sessions;
+    last = model->released && model->sessions == 0;
+  }
+  if (last) free_model(model);
+}
+}  // namespace gfx950
+
+extern "C" void gfxinfer_model_destroy(gfxinfer_model* model) {
+  if (model == nullptr) return;
+  bool unused = false;
+  {
+    const std::lock_guard<std::mutex> hold(model->lifetime);
+    model->released = true;
+    unused = model->sessions == 0;
+  }
+  if (unused) gfx950::free_model(model);
+}
+
+extern "C" size_t gfxinfer_model_spec_tensor_count(const gfxinfer_model_spec* spec) {
+  if (spec == nullptr || validate_spec(*spec) != GFXI_OK) return 0;
+  return model_tensors(*spec).size();
+}
+
+extern "C" int32_t gfxinfer_model_spec_tensor(const gfxinfer_model_spec* spec, size_t index,
+                                              gfxinfer_spec_tensor* out) {
+  return guarded([&]() -> int32_t {
+    if (spec == nullptr || out == nullptr) {
+      return fail(GFXI_INVALID_ARGUMENT, "tensor enumeration needs a spec and an output");
+    }
+    if (const int32_t status = validate_spec(*spec); status != GFXI_OK) return status;
+    const std::vector<Tensor> tensors = model_tensors(*spec);
+    if (index >= tensors.size()) return fail(GFXI_INVALID_ARGUMENT, "tensor index past the table");
+    const Tensor& t = tensors[index];
+    if (t.name.size() >= sizeof out->name) return fail(GFXI_INTERNAL, "tensor name too long");
+    *out = {};
+    std::memcpy(out->name, t.name.c_str(), t.name.size() + 1);
+    out->format = t.format;
+    out->rows = t.rows;
+    out->columns = t.columns;
+    out->mean = t.mean;
+    out->sigma = t.sigma;
+    return ok();
+  });
 }
 
 extern "C" void* gfxinfer_model_stream(const gfxinfer_model* model) {

@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -47,6 +48,13 @@ int32_t validate_spec(const gfxinfer_model_spec& spec);
 int32_t allocate_model(const gfxinfer_model_spec& spec, int32_t device, std::vector<Tensor> tensors,
                        gfxinfer_model** out);
 
+// Session references to a model.  A session borrows its model's compute stream and
+// arena, so gfxinfer_model_destroy with sessions still open only marks the model
+// released, and the last session to end frees it (a session ending after its model
+// would otherwise synchronize a destroyed stream).
+void retain_model(gfxinfer_model* model);
+void release_model_reference(gfxinfer_model* model);
+
 // FNV-1a of a tensor name: the per-tensor key of the synthetic generator.
 inline uint64_t name_hash(const std::string& name) {
   uint64_t h = 1469598103934665603ull;
@@ -67,6 +75,10 @@ struct gfxinfer_model {
   std::size_t arena_bytes{0};
   std::vector<gfx950::Tensor> tensors;
   std::unordered_map<std::string, std::size_t> index;
+  // Lifetime: open sessions and whether gfxinfer_model_destroy has been called.
+  std::mutex lifetime;
+  uint32_t sessions{0};
+  bool released{false};
 
   const gfx950::Tensor* find(const std::string& name) const {
     const auto it = index.find(name);

@@ -190,6 +190,7 @@ struct gfxinfer_session {
     }
     if (host_result != nullptr) (void)hipHostFree(host_result);
     if (arena != nullptr) (void)hipFree(arena);
+    if (model != nullptr) release_model_reference(model);
   }
 
   // ---- sizes of the per-layer state -----------------------------------------
@@ -778,6 +779,7 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
     *out = nullptr;
     if (auto e = hipSetDevice(model->device); e != hipSuccess) return hip_fail(e, "hipSetDevice failed");
     auto s = new gfxinfer_session();
+    retain_model(model);
     s->model = model;
     s->spec = model->spec;
     s->config = *config;

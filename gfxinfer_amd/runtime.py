@@ -70,6 +70,33 @@ def tiny_spec(**overrides) -> ModelSpec:
     return spec
 
 
+class SpecTensor(ctypes.Structure):
+    """gfxinfer_spec_tensor: one entry of a spec's tensor table (converter naming)."""
+    _fields_ = [("name", ctypes.c_char * 96), ("format", ctypes.c_int32), ("rows", ctypes.c_uint64),
+                ("columns", ctypes.c_uint64), ("mean", ctypes.c_float), ("sigma", ctypes.c_float)]
+
+
+def spec_tensors(spec: ModelSpec) -> list[dict]:
+    """The tensors a model of `spec` binds (host only): name, format, rows, columns and
+    the synthetic value law."""
+    out = []
+    for i in range(int(lib().gfxinfer_model_spec_tensor_count(ctypes.byref(spec)))):
+        t = SpecTensor()
+        check(lib().gfxinfer_model_spec_tensor(ctypes.byref(spec), i, ctypes.byref(t)))
+        out.append(dict(name=t.name.decode(), format=int(t.format), rows=int(t.rows), columns=int(t.columns),
+                        mean=float(t.mean), sigma=float(t.sigma)))
+    return out
+
+
+def artifact_tiny_spec() -> ModelSpec:
+    """The smallest spec the kernels accept (one GDN and one attention layer, hidden 128),
+    used for the committed gfx1200 artifact fixture."""
+    return tiny_spec(hidden_size=128, intermediate_size=128, layer_count=2, full_attention_interval=2,
+                     attention_head_count=1, kv_head_count=1, gdn_key_head_count=1, gdn_value_head_count=16,
+                     vocabulary_size=256, tokenizer_vocabulary_size=250, mtp_draft_vocabulary=128,
+                     w3_mlp_layers=1)
+
+
 class TensorView(ctypes.Structure):
     """gfxinfer_tensor_view (engine.h:47-60 DeviceTensorView)."""
     _fields_ = [("format", ctypes.c_int32), ("rows", ctypes.c_uint64), ("columns", ctypes.c_uint64),

@@ -469,6 +469,52 @@ int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_positi
     uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
     size_t workspace_bytes, void* stream);
 
+/* ---- single-token launchers: the one-token calls of greedy_step and the MTP proposal ---
+ * Each is its block launcher at batch 1 (same kernels, bit-identical results). */
+
+/* qwen_ops.h:83-88 launch_gdn_conv_update (called at qwen_runtime.cpp:389): conv state
+ * [channels][4] fp16 advanced in place by one token; convolved_qkv fp16 [channels].  The
+ * reference fixes channels at its model's 10240. */
+int32_t gfxinfer_launch_gdn_conv_update(const float* projected_qkv, const uint16_t* bf16_conv_weight,
+                                        uint16_t* conv_state, uint16_t* convolved_qkv, size_t channels,
+                                        void* stream);
+
+/* qwen_ops.h:101-111 launch_gdn_recurrent_decode (called at qwen_runtime.cpp:394): one token
+ * of the gated delta rule, recurrent state fp32 [value_heads][128][128] updated in place, no
+ * logs.  mixed_workspace: fp32 [value_heads * 128] (as for the block form). */
+int32_t gfxinfer_launch_gdn_recurrent_decode(
+    const uint16_t* convolved_qkv, const float* projected_z, const float* projected_a,
+    const float* projected_b, const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias,
+    const uint16_t* bf16_norm_weight, float* recurrent_state, uint16_t* output, uint32_t key_heads,
+    uint32_t value_heads, uint32_t head_size, float* mixed_workspace, void* stream);
+
+/* qwen_ops.h:130-139 launch_gdn_restore_prefix: one layer's conv and recurrent states replayed
+ * over the first accepted_tokens (>= 1) tokens of that layer's logs ([tokens][...]). */
+int32_t gfxinfer_launch_gdn_restore_prefix(uint16_t* conv_state, float* recurrent_state,
+                                           const uint16_t* appended_log, const float* key_log,
+                                           const float* delta_log, const float* decay_log,
+                                           size_t channels, uint32_t accepted_tokens, uint32_t key_heads,
+                                           uint32_t value_heads, uint32_t head_size, void* stream);
+
+/* qwen_ops.h:217-224 launch_kv_append (called at qwen_runtime.cpp:372 and :818): one token's
+ * K (fp16) and V (fp32 -> fp16) rows of kv_elements at position < capacity. */
+int32_t gfxinfer_launch_kv_append(const uint16_t* key, const float* value, uint16_t* key_cache,
+                                  uint16_t* value_cache, size_t position, size_t capacity,
+                                  size_t kv_elements, void* stream);
+
+/* qwen_ops.h:246-254 launch_gated_attention_decode (called at qwen_runtime.cpp:375 and :831):
+ * one token attending to the first token_count (1..capacity) cached positions; layouts and
+ * workspace as gfxinfer_launch_gated_attention_decode_block with batch 1. */
+int32_t gfxinfer_launch_gated_attention_decode(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, size_t token_count, size_t capacity, uint32_t q_heads, uint32_t kv_heads,
+    uint32_t head_size, float* workspace, size_t workspace_bytes, void* stream);
+
+/* qwen_ops.h:278-282 launch_argmax (called at qwen_runtime.cpp:866 and :1305): the index of
+ * the largest of vocabulary_size logits; ties go to the lowest index. */
+int32_t gfxinfer_launch_argmax(const float* logits, uint32_t* token, size_t vocabulary_size,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

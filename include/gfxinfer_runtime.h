@@ -61,6 +61,10 @@ typedef struct gfxinfer_model gfxinfer_model;
  * 16-bit uniforms), so a CPU restatement reproduces every value bit for bit. */
 int32_t gfxinfer_model_create_synthetic(const gfxinfer_model_spec* spec, uint64_t seed,
                                         int32_t device, gfxinfer_model** out);
+/* Releases the model.  Sessions created on it keep it alive: with sessions still open the
+ * weights and stream are freed when the last of them is destroyed (a session borrows the
+ * model's stream and arena).  No reference counterpart: the reference's session holds an
+ * Engine& that must outlive it. */
 void gfxinfer_model_destroy(gfxinfer_model* model);
 /* Engine::compute_stream (engine.h:89): the hipStream_t every session call runs on. */
 void* gfxinfer_model_stream(const gfxinfer_model* model);
@@ -78,6 +82,22 @@ typedef struct gfxinfer_tensor_view {
   size_t data_bytes;
   size_t auxiliary_bytes;
 } gfxinfer_tensor_view;
+
+/* One entry of the tensor table a spec implies, in converter naming (converter.cpp:78-119):
+ * format as in gfxinfer_tensor_view, shape, and the synthetic value law mean + sigma * N(0, 1).
+ * Host only (no device access).  No reference counterpart: it lets a host tool (a converter
+ * or a fixture writer) enumerate what gfxinfer_model_create_from_artifact binds. */
+typedef struct gfxinfer_spec_tensor {
+  char name[96];
+  int32_t format;
+  uint64_t rows;
+  uint64_t columns;
+  float mean;
+  float sigma;
+} gfxinfer_spec_tensor;
+size_t gfxinfer_model_spec_tensor_count(const gfxinfer_model_spec* spec);
+int32_t gfxinfer_model_spec_tensor(const gfxinfer_model_spec* spec, size_t index,
+                                   gfxinfer_spec_tensor* out);
 
 /* Engine::find_device_tensor (engine.h:87-88). */
 int32_t gfxinfer_model_find_tensor(const gfxinfer_model* model, const char* name,

@@ -32,30 +32,53 @@ def _laws(name: str):
 
 
 class Matrix:
-    def __init__(self, seed, name, fmt, rows, cols):
-        w = O.synthetic_values(seed, name, rows * cols, 0.02, 0.0).reshape(rows, cols)
+    """A W3/W4 projection.  `splits` selects the order of the fp32 epilogue over K: None is
+    the reference's sequential epilogue (lowbit_gemv.hip:540-551); an integer S is the
+    canonical order of the gfx950 library (S split-K planes, each cut into ranges of about
+    ten groups, orc_gemm_epilogue_ranges), with the planes added in plane order as the
+    library's residual norm adds them.  The epilogue order is the one place where the
+    library's GEMMs differ from the reference's, within the fp32 tolerance."""
+
+    def __init__(self, seed, name, fmt, rows, cols, splits=None):
+        w = O.synthetic_values_c(seed, name, rows * cols, 0.02, 0.0).reshape(rows, cols)
         status, codes, scales = O.quantize_group128(w, fmt)
         assert status == 0
+        del w
         self.w = O.unpack_weights(codes, rows, cols, fmt)
         self.ws16 = O.f32_to_f16_bits(scales)
         self.rows, self.cols = rows, cols
+        self.splits = splits
 
     def __call__(self, x16: np.ndarray) -> np.ndarray:
         """fp16 [B, K] -> fp32 [B, N] through A4 activations (lowbit_gemv.hip:373-553)."""
         packed, as16 = O.quantize_activation_i4(x16)
         a = O.unpack_a4(packed, self.cols)
-        return O.gemm_epilogue(O.gemm_partials(self.w, a), self.ws16, as16)
+        partials = O.gemm_partials(self.w, a)
+        if self.splits is None:
+            return O.gemm_epilogue(partials, self.ws16, as16)
+        planes = O.gemm_epilogue_ranges(partials, self.ws16, as16, self.splits)
+        out = planes[0].copy()
+        for plane in planes[1:]:
+            out = (out + plane).astype(np.float32)
+        return out
 
     def head(self, rows: int) -> "Matrix":
         m = Matrix.__new__(Matrix)
-        m.w, m.ws16, m.rows, m.cols = self.w[:rows], self.ws16[:rows], rows, self.cols
+        m.w, m.ws16, m.rows, m.cols, m.splits = self.w[:rows], self.ws16[:rows], rows, self.cols, self.splits
         return m
 
 
 class OracleModel:
-    def __init__(self, spec: dict, seed: int):
+    """The synthetic checkpoint on the CPU.  k_order: None for the reference's GEMM
+    epilogue everywhere; or a function (rows, columns) -> split count, to add the group
+    partials in the gfx950 library's canonical order (the residual-feeding [hidden, K]
+    projections as that many split-K planes, every other projection as one).  The MTP
+    weights are built on first use."""
+
+    def __init__(self, spec: dict, seed: int, k_order=None):
         self.s = s = dict(spec)
         self.seed = seed
+        self.k_order = k_order
         H, I, hd = s["hidden_size"], s["intermediate_size"], s["attention_head_size"]
         self.hd = hd
         self.q_rows = 2 * s["attention_head_count"] * hd
@@ -64,12 +87,7 @@ class OracleModel:
         self.gv = s["gdn_value_head_count"] * s["gdn_head_size"]
         self.C = 2 * self.gk + self.gv
 
-        def mat(name, fmt, rows, cols):
-            return Matrix(seed, name, fmt, rows, cols)
-
-        def vec(name, n):
-            mean, sigma = _laws(name)
-            return O.f32_to_bf16_bits(O.synthetic_values(seed, name, n, sigma, mean))
+        mat, vec = self._mat, self._vec
 
         V = s["vocabulary_size"]
         self.embed = mat("model.language_model.embed_tokens.weight", O.W4, V, H)
@@ -84,7 +102,7 @@ class OracleModel:
                      post_norm=vec(p + "post_attention_layernorm.weight", H),
                      gate=mat(p + "mlp.gate_proj.weight", fmt, I, H),
                      up=mat(p + "mlp.up_proj.weight", fmt, I, H),
-                     down=mat(p + "mlp.down_proj.weight", fmt, H, I))
+                     down=mat(p + "mlp.down_proj.weight", fmt, H, I, planes=True))
             if L["attention"]:
                 self._attention(L, p)
             else:
@@ -96,28 +114,49 @@ class OracleModel:
                          a_log=vec(p + "linear_attn.A_log", s["gdn_value_head_count"]),
                          dt_bias=vec(p + "linear_attn.dt_bias", s["gdn_value_head_count"]),
                          gdn_norm=vec(p + "linear_attn.norm.weight", s["gdn_head_size"]),
-                         out=mat(p + "linear_attn.out_proj.weight", O.W4, H, self.gv))
+                         out=mat(p + "linear_attn.out_proj.weight", O.W4, H, self.gv, planes=True))
             self.layers.append(L)
-        self.mtp_fc = mat("mtp.fc.weight", O.W4, H, 2 * H)
-        self.mtp_pre_embedding_norm = vec("mtp.pre_fc_norm_embedding.weight", H)
-        self.mtp_pre_hidden_norm = vec("mtp.pre_fc_norm_hidden.weight", H)
-        self.mtp_final_norm = vec("mtp.norm.weight", H)
-        self.mtp = dict(attention=True, input_norm=vec("mtp.layers.0.input_layernorm.weight", H),
-                        post_norm=vec("mtp.layers.0.post_attention_layernorm.weight", H),
-                        gate=mat("mtp.layers.0.mlp.gate_proj.weight", O.W4, I, H),
-                        up=mat("mtp.layers.0.mlp.up_proj.weight", O.W4, I, H),
-                        down=mat("mtp.layers.0.mlp.down_proj.weight", O.W4, H, I))
-        self._attention(self.mtp, "mtp.layers.0.")
-        self.draft_head = self.lm_head.head(s["mtp_draft_vocabulary"])
+        self._mtp = None
+
+    def _mat(self, name, fmt, rows, cols, planes=False):
+        splits = None
+        if self.k_order is not None:
+            splits = self.k_order(rows, cols) if planes else 1
+        return Matrix(self.seed, name, fmt, rows, cols, splits)
+
+    def _vec(self, name, n):
+        mean, sigma = _laws(name)
+        return O.f32_to_bf16_bits(O.synthetic_values(self.seed, name, n, sigma, mean))
+
+    @property
+    def mtp(self):
+        """The MTP block's weights (qwen_runtime.cpp:972-1008), built on first use."""
+        if self._mtp is None:
+            s, mat, vec = self.s, self._mat, self._vec
+            H, I = s["hidden_size"], s["intermediate_size"]
+            self.mtp_fc = mat("mtp.fc.weight", O.W4, H, 2 * H)
+            self.mtp_pre_embedding_norm = vec("mtp.pre_fc_norm_embedding.weight", H)
+            self.mtp_pre_hidden_norm = vec("mtp.pre_fc_norm_hidden.weight", H)
+            self.mtp_final_norm = vec("mtp.norm.weight", H)
+            mtp = dict(attention=True, input_norm=vec("mtp.layers.0.input_layernorm.weight", H),
+                       post_norm=vec("mtp.layers.0.post_attention_layernorm.weight", H),
+                       gate=mat("mtp.layers.0.mlp.gate_proj.weight", O.W4, I, H),
+                       up=mat("mtp.layers.0.mlp.up_proj.weight", O.W4, I, H),
+                       down=mat("mtp.layers.0.mlp.down_proj.weight", O.W4, H, I, planes=True))
+            self._attention(mtp, "mtp.layers.0.")
+            self.draft_head = self.lm_head.head(s["mtp_draft_vocabulary"])
+            self._mtp = mtp
+        return self._mtp
 
     def _attention(self, L, p):
         s, H, hd = self.s, self.s["hidden_size"], self.hd
-        L.update(q=Matrix(self.seed, p + "self_attn.q_proj.weight", O.W4, self.q_rows, H),
-                 k=Matrix(self.seed, p + "self_attn.k_proj.weight", O.W4, self.kv_rows, H),
-                 v=Matrix(self.seed, p + "self_attn.v_proj.weight", O.W4, self.kv_rows, H),
+        mat = self._mat
+        L.update(q=mat(p + "self_attn.q_proj.weight", O.W4, self.q_rows, H),
+                 k=mat(p + "self_attn.k_proj.weight", O.W4, self.kv_rows, H),
+                 v=mat(p + "self_attn.v_proj.weight", O.W4, self.kv_rows, H),
                  q_norm=O.f32_to_bf16_bits(O.synthetic_values(self.seed, p + "self_attn.q_norm.weight", hd, 0.02, 0.0)),
                  k_norm=O.f32_to_bf16_bits(O.synthetic_values(self.seed, p + "self_attn.k_norm.weight", hd, 0.02, 0.0)),
-                 o=Matrix(self.seed, p + "self_attn.o_proj.weight", O.W4, H, s["attention_head_count"] * hd))
+                 o=mat(p + "self_attn.o_proj.weight", O.W4, H, s["attention_head_count"] * hd, planes=True))
 
 
 def _p(a):
@@ -238,6 +277,7 @@ class OracleSession:
     def mtp_proposal(self, token, conditioning16, position):
         m, s = self.m, self.m.s
         H = s["hidden_size"]
+        m.mtp  # builds the MTP weights on first use
         emb = self._gather(token)[None, :]
         concat = np.empty((1, 2 * H), np.uint16)
         O.lib().orc_dual_rms_norm_concat(O.ptr(emb), _p(m.mtp_pre_embedding_norm), _p(conditioning16),

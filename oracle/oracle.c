@@ -790,3 +790,33 @@ size_t orc_accept(const uint32_t* drafts, const uint32_t* targets, size_t draft_
   while (accepted < draft_count && drafts[accepted] == targets[accepted]) ++accepted;
   return accepted;
 }
+
+/* Synthetic checkpoint values (the generator of gfxinfer_model_create_synthetic, restated
+ * in oracle.py's synthetic_values): element i of a tensor with generator key `key` is
+ * mean + n_i * (sigma * 2^-16) in fp32, n_i = the twelve 16-bit fields of
+ * splitmix64(key + 3 i + j), j = 0..2, summed, plus 6 - 6 * 65536. */
+static uint64_t orc_splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+void orc_synthetic_values(uint64_t seed_xor_name_hash, size_t first, size_t count, float sigma,
+                          float mean, float* out) {
+  const uint64_t key = orc_splitmix64(seed_xor_name_hash);
+  const float scale = sigma * 0x1p-16f;
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < (long long)count; ++i) {
+    const uint64_t index = (uint64_t)first + (uint64_t)i;
+    int64_t total = 0;
+    for (uint64_t j = 0; j < 3; ++j) {
+      const uint64_t h = orc_splitmix64(key + 3u * index + j);
+      total += (int64_t)(h & 0xFFFF) + (int64_t)((h >> 16) & 0xFFFF) + (int64_t)((h >> 32) & 0xFFFF) +
+               (int64_t)(h >> 48);
+    }
+    const float n = (float)(total + 6 - 6 * 65536);
+    const float spread = n * scale;
+    out[i] = mean + spread;
+  }
+}

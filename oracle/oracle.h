@@ -125,6 +125,11 @@ void orc_argmax(const float* logits, size_t vocabulary, size_t stride, unsigned 
                 const uint32_t* token_ids, uint32_t* out);
 /* Acceptance (qwen_runtime.cpp:1497-1501): first i < D with drafts[i] != targets[i]. */
 size_t orc_accept(const uint32_t* drafts, const uint32_t* targets, size_t draft_count);
+/* Synthetic checkpoint values, elements first .. first+count-1 (not a reference algorithm:
+ * the generator of gfxinfer_model_create_synthetic; oracle.py's synthetic_values is the
+ * same function in numpy). */
+void orc_synthetic_values(uint64_t seed_xor_name_hash, size_t first, size_t count, float sigma,
+                          float mean, float* out);
 
 #ifdef __cplusplus
 }

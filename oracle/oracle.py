@@ -37,6 +37,23 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+NATIVE_FLAGS = ["-O3", "-march=native", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off"]
+
+
+def use_native_build(directory: str) -> str:
+    """Compile oracle.c for this host's CPU (gcc with NATIVE_FLAGS) into `directory` and
+    route every later call through that build; returns the compile command.  The CPU
+    baseline uses it on the machine it runs on, so -march=native matches that CPU."""
+    global _lib
+    path = os.path.join(directory, "liboracle_native.so")
+    cmd = ["gcc"] + NATIVE_FLAGS + ["-shared", os.path.join(HERE, "oracle.c"), "-o", path, "-lm"]
+    subprocess.run(cmd, check=True)
+    native = ctypes.CDLL(path)
+    _declare(native)
+    _lib = native
+    return " ".join(["gcc"] + NATIVE_FLAGS)
+
+
 def ref_lib() -> ctypes.CDLL | None:
     """The reference's own quantizer, or None when _ref/ was not built."""
     global _ref
@@ -140,6 +157,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_dual_rms_norm_concat": (None, [P, P, P, P, P, SZ, F, I]),
         "orc_silu_multiply_quantize_i4": (I, [P, P, P, P, SZ, U]),
         "orc_silu_multiply": (None, [P, P, P, SZ]),
+        "orc_synthetic_values": (None, [ctypes.c_uint64, SZ, SZ, F, F, P]),
         "orc_gdn_conv_update": (None, [P, P, P, P, P, P, SZ, U]),
         "orc_gdn_recurrent": (None, [P, P, P, P, P, P, P, P, P, P, P, P, P, U, U, U, U]),
         "orc_gdn_restore_conv": (None, [P, P, SZ, U]),
@@ -317,6 +335,17 @@ def name_hash(name: str) -> int:
         h ^= c
         h = (h * 1099511628211) & 0xFFFFFFFFFFFFFFFF
     return h
+
+
+def synthetic_values_c(seed: int, name: str, count: int, sigma: float, mean: float,
+                       first: int = 0) -> np.ndarray:
+    """synthetic_values computed by liboracle.so (OpenMP): the same values, for the
+    full-width model tensors where the numpy form is slow."""
+    out = np.empty(count, dtype=np.float32)
+    key = (np.uint64(seed) ^ np.uint64(name_hash(name)))
+    lib().orc_synthetic_values(ctypes.c_uint64(int(key)), first, count, ctypes.c_float(sigma),
+                               ctypes.c_float(mean), ptr(out))
+    return out
 
 
 def synthetic_values(seed: int, name: str, count: int, sigma: float, mean: float,

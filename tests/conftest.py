@@ -16,24 +16,6 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
-def pytest_sessionfinish(session, exitstatus):
-    session.config._gfxi_exit_status = int(exitstatus)
-
-
-def pytest_unconfigure(config):
-    """After a GPU test run has been reported, leave without the interpreter's final
-    teardown: device buffers that a failed test's traceback still holds would be freed
-    after the HIP runtime has finalized, which aborts the process and hides pytest's
-    exit status."""
-    torch = sys.modules.get("torch")
-    if torch is None or not torch.cuda.is_initialized():
-        return
-    status = getattr(config, "_gfxi_exit_status", 0)
-    sys.stdout.flush()
-    sys.stderr.flush()
-    os._exit(status)
-
-
 @pytest.fixture(scope="session")
 def orc():
     from oracle import oracle as O

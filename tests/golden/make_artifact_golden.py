@@ -5,9 +5,17 @@ The reference's src/quantization.cpp and src/artifact.cpp are compiled where the
 matrices with the reference quantizer, tiles them with the reference's gfx12 tiler
 (quantization.cpp:253-318) and writes them, with bf16 and int32 vectors, through the
 reference ArtifactWriter (artifact.cpp:427-545) as a "gfx1200" artifact — the layout the
-reference converter emits (converter.cpp:345-393).  The inputs (packed codes, float
+reference converter emits (converter.cpp:345-393), under the recipe id the converter
+gives a W3-sequential tiled checkpoint (converter.cpp:540-541): the reference runtime
+reads codes as tiled only when the recipe names "tiled-v" and W3 as sequential only
+when it names "w3seq" (qwen_runtime.cpp:957-960).  The inputs (packed codes, float
 scales) are stored next to it so the tests can build the expected gfx950 tiles with the
-library's own tiler.  Only data is committed; re-running reproduces both files.
+library's own tiler.
+
+A second file holds a whole synthetic model (the smallest spec the kernels take, seed
+77) in the same recipe, every matrix quantized by the reference quantizer and tiled by
+the reference tiler, for the GPU test that loads it into the library's arena.  Only
+data is committed; re-running reproduces the files.
 
     python tests/golden/make_artifact_golden.py
 """
@@ -24,7 +32,9 @@ sys.path.insert(0, ROOT)
 
 from oracle import oracle as O  # noqa: E402
 
-IDENTITY = ("gfx1200", "qwen3.8-27b", "golden-small", "gfx12-w3-w4-fixture")
+RECIPE = "qwen38-code-w3seq-w4-wmma-tiled-v9"
+IDENTITY = ("gfx1200", "qwen3.8-27b", "golden-small", RECIPE)
+MODEL_SEED = 77
 MATRICES = [("layers.0.mlp.gate_proj.weight", 2, 32, 256),   # W3
             ("layers.0.self_attn.q_proj.weight", 3, 48, 384),  # W4
             ("layers.1.mlp.down_proj.weight", 2, 16, 640)]     # W3, five groups
@@ -63,6 +73,33 @@ def main() -> None:
     if rc != 0:
         raise SystemExit(f"reference writer failed: {rc}")
     np.savez(os.path.join(HERE, "artifact_gfx1200_small.npz"), **arrays)
+    print("wrote", path, os.path.getsize(path), "bytes")
+    write_tiny_model()
+
+
+def write_tiny_model() -> None:
+    """The synthetic model of artifact_tiny_spec() as the reference converter would write it."""
+    from gfxinfer_amd.runtime import artifact_tiny_spec, spec_tensors
+    tensors = []
+    for t in spec_tensors(artifact_tiny_spec()):
+        name, fmt, rows, cols = t["name"], t["format"], t["rows"], t["columns"]
+        values = O.synthetic_values(MODEL_SEED, name, rows * cols, t["sigma"], t["mean"])
+        if fmt == 0:
+            dims = (rows, 1, cols) if name.endswith("conv1d.weight") else ((cols,) if rows == 1 else (rows, cols))
+            tensors.append(dict(name=name, dtype=4, quantization=0, dims=dims,
+                                data=O.f32_to_bf16_bits(values).tobytes(), aux=None))
+            continue
+        status, codes, scales = O.ref_quantize_group128(values.reshape(rows, cols), fmt)
+        assert status == 0, name
+        tiled, tscales = O.ref_tile_gfx12(codes, scales, rows, cols, fmt)
+        tensors.append(dict(name=name, dtype=1, quantization=fmt, dims=(rows, cols), data=tiled.tobytes(),
+                            aux=O.f32_to_f16_bits(tscales).tobytes()))
+    path = os.path.join(HERE, "artifact_gfx1200_tiny_model.gfxi")
+    if os.path.exists(path):
+        os.remove(path)
+    rc = O.ref_write_artifact(path, ("gfx1200", "qwen3.8-27b", f"synthetic-{MODEL_SEED}", RECIPE), tensors)
+    if rc != 0:
+        raise SystemExit(f"reference writer failed: {rc}")
     print("wrote", path, os.path.getsize(path), "bytes")
 
 

@@ -47,7 +47,8 @@ def test_reads_reference_written_artifact():
     g = golden("artifact_gfx1200_small.npz")
     with Artifact(FIXTURE) as a:
         assert a.identity() == {"target_arch": "gfx1200", "model_id": "qwen3.8-27b",
-                                "weights_id": "golden-small", "recipe_id": "gfx12-w3-w4-fixture"}
+                                "weights_id": "golden-small",
+                                "recipe_id": "qwen38-code-w3seq-w4-wmma-tiled-v9"}
         tensors = {t.name.decode(): t for t in a.tensors()}
         assert list(tensors) == ["layers.0.mlp.gate_proj.weight", "layers.0.self_attn.q_proj.weight",
                                  "layers.1.mlp.down_proj.weight", "layers.0.input_layernorm.weight",
@@ -152,3 +153,49 @@ def test_rejects_damaged_artifacts(orc, tmp_path, case, want, want_unverified):
 
 def test_missing_file_is_io_error(tmp_path):
     assert _open_rc(tmp_path / "absent.gfxi") == IO
+
+
+TINY_MODEL = os.path.join(HERE, "golden", "artifact_gfx1200_tiny_model.gfxi")
+RECIPE_OFFSET = 168  # header: magic .. manifest CRC (88 bytes), target 16, model 32, weights 32
+
+
+@pytest.mark.parametrize("recipe", [
+    "qwen38-code-w3seq-w4-rowmajor-v9",  # row-major codes (no "tiled-v")
+    "qwen38-code-w4-wmma-tiled-v7",      # W3 tensors without "w3seq": bit-plane W3
+])
+def test_loader_refuses_gfx1200_layouts_it_does_not_retile(tmp_path, recipe):
+    """qwen_runtime.cpp:957-960: the reference reads gfx1200 codes as tiles only under a
+    "tiled-v" recipe and W3 as sequential fragments only under "w3seq".  The loader
+    refuses the other layouts with GFXI_UNSUPPORTED before any device work (the recipe id
+    is outside the checksummed manifest, so the patched file still opens)."""
+    import ctypes
+    from gfxinfer_amd import lib
+    from gfxinfer_amd.runtime import Artifact, artifact_tiny_spec
+    path = tmp_path / "patched.gfxi"
+    data = bytearray(open(TINY_MODEL, "rb").read())
+    assert bytes(data[RECIPE_OFFSET:RECIPE_OFFSET + 34]) == b"qwen38-code-w3seq-w4-wmma-tiled-v9"
+    data[RECIPE_OFFSET:RECIPE_OFFSET + 64] = recipe.encode().ljust(64, b"\0")
+    path.write_bytes(bytes(data))
+    with Artifact(path) as a:
+        assert a.identity()["recipe_id"] == recipe
+    spec = artifact_tiny_spec()
+    handle = ctypes.c_void_p()
+    rc = lib().gfxinfer_model_create_from_artifact(ctypes.byref(spec), str(path).encode(), 1, 0,
+                                                   ctypes.byref(handle))
+    assert rc == UNSUPPORTED, lib().gfxinfer_last_error()
+    assert not handle.value
+
+
+def test_tiny_model_fixture_covers_the_spec():
+    """The committed gfx1200 model fixture holds every tensor the tiny spec binds, in the
+    converter's shapes, with the quantization the spec gives it."""
+    from gfxinfer_amd.runtime import Artifact, artifact_tiny_spec, spec_tensors
+    with Artifact(TINY_MODEL) as a:
+        assert a.identity()["weights_id"] == "synthetic-77"
+        found = {t.name.decode(): t for t in a.tensors()}
+    want = spec_tensors(artifact_tiny_spec())
+    assert sorted(found) == sorted(t["name"] for t in want)
+    for t in want:
+        e = found[t["name"]]
+        assert e.quantization == max(t["format"], 0)
+        assert int(np.prod(e.shape)) == t["rows"] * t["columns"]

@@ -3,9 +3,10 @@
 - gfx950 recipe: a synthetic model written by the library and loaded back is the same
   model byte for byte and gives the same tokens and logits; the reference reader
   (oracle/_ref, where built) accepts the file.
-- gfx1200 recipe: the same synthetic weights quantized, gfx12-tiled and written by the
-  reference's own code (quantizer, tile_group128_for_gfx12, ArtifactWriter) load into
-  the identical gfx950 arena.
+- gfx1200 recipe: synthetic weights quantized, gfx12-tiled and written by the
+  reference's own code (quantizer, tile_group128_for_gfx12, ArtifactWriter) in the CPU
+  container (a committed fixture; no reference code runs on the GPU box) load into the
+  identical gfx950 arena.
 - The converter's MTP draft head (ranked LM-head rows + token ids) drives the MTP
   proposal through the token-id map.
 """
@@ -92,36 +93,24 @@ def test_gfx950_artifact_round_trip(model, orc, tmp_path):
     assert np.array_equal(got[1], want[1]) and np.array_equal(got[2], want[2])
 
 
-def test_gfx1200_artifact_from_reference_writer(model, orc, tmp_path):
-    if orc.ref_lib() is None:
-        pytest.skip("oracle/_ref (the reference quantizer, tiler and writer) is not built")
-    from gfxinfer_amd.runtime import SyntheticModel
-    ours = tmp_path / "tiny_gfx950.gfxi"
-    model.write_artifact(ours, "synthetic-77")
-    tensors = []
-    for name, quant, shape in _names(ours):
-        if quant == 0:
-            dtype = 4
-            data, aux = model.tensor_bytes(name).tobytes(), None
-        else:
-            dtype = 1
-            rows, cols = shape
-            w = orc.synthetic_values(SEED, name, rows * cols, 0.02, 0.0).reshape(rows, cols)
-            status, codes, scales = orc.ref_quantize_group128(w, quant)
-            assert status == 0
-            tiled, tscales = orc.ref_tile_gfx12(codes, scales, rows, cols, quant)
-            data, aux = tiled.tobytes(), orc.f32_to_f16_bits(tscales).tobytes()
-        tensors.append(dict(name=name, dtype=dtype, quantization=quant, dims=shape, data=data, aux=aux))
-    path = tmp_path / "tiny_gfx1200.gfxi"
-    say("reference writer: gfx1200 artifact of", len(tensors), "tensors")
-    assert orc.ref_write_artifact(path, ("gfx1200", "qwen3.8-27b", "synthetic-77", "reference-gfx12"),
-                                  tensors) == 0
-    say("load gfx1200 artifact")
-    loaded = SyntheticModel.from_artifact(_spec(), path)
+def test_gfx1200_artifact_from_reference_writer(device):
+    """tests/golden/artifact_gfx1200_tiny_model.gfxi holds the synthetic model of
+    artifact_tiny_spec() (seed 77) as the reference's own quantizer, gfx12 tiler and
+    ArtifactWriter wrote it in this repository's CPU container: loading it re-tiles every
+    matrix into exactly the arena the device generator fills."""
+    import os
+    from gfxinfer_amd.runtime import SyntheticModel, artifact_tiny_spec, spec_tensors
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "artifact_gfx1200_tiny_model.gfxi")
+    spec = artifact_tiny_spec()
+    say("load the reference-written gfx1200 artifact")
+    loaded = SyntheticModel.from_artifact(spec, path)
+    generated = SyntheticModel(spec, SEED)
     try:
-        _same_arena(model, loaded, _names(ours))
+        names = [(t["name"], max(t["format"], 0), None) for t in spec_tensors(spec)]
+        _same_arena(generated, loaded, names)
     finally:
         loaded.close()
+        generated.close()
 
 
 def test_draft_head_artifact_uses_token_ids(model, tmp_path):

@@ -151,6 +151,9 @@ CASES = [
     (3, 8, 64, 640, 3), (3, 8, 64, 640, 16),
     (2, 4, 17408, 5120, 5), (2, 4, 5120, 17408, 5), (3, 4, 17408, 5120, 5),
     (2, 4, 17408, 5120, 1), (2, 4, 17408, 5120, 32), (2, 8, 17408, 5120, 1),
+    # the remaining timed GEMV shapes: W4A4 up at batch 1, plain
+    # W3A4 / W4A4 down at batch 1 and 5
+    (3, 4, 17408, 5120, 1), (2, 4, 5120, 17408, 1), (3, 4, 5120, 17408, 1), (3, 4, 5120, 17408, 5),
     # down projection at verify batches: K = 17408 needs the LDS wave cap at 32 tokens
     (2, 4, 5120, 17408, 32), (3, 4, 5120, 17408, 16), (2, 8, 5120, 17408, 32),
     # 9-32 tokens (LDS-ring kernel): workgroups of 4 or 8 tiles with a short last one
@@ -348,7 +351,7 @@ def _gemm_argmax(gx, fmt, p, rows, cols, batch, argmax_rows, ids=None, logits=Tr
 
 @pytest.mark.parametrize("fmt,rows,cols,batch,limit", [
     (3, 1024, 256, 1, 1024), (3, 1024, 256, 5, 1000), (3, 4096, 640, 32, 4000), (2, 2048, 512, 17, 2048),
-    (3, 151936, 5120, 5, 151936),
+    (3, 151936, 5120, 5, 151936), (3, 151936, 5120, 16, 151936), (3, 151936, 5120, 32, 151936),
     # 17000 tiles: more keys per row than one pass of the reduction's loads holds
     (3, 272000, 128, 2, 271990)])
 def test_gemm_argmax_matches_logits_argmax(device, gx, orc, fmt, rows, cols, batch, limit):
@@ -359,9 +362,11 @@ def test_gemm_argmax_matches_logits_argmax(device, gx, orc, fmt, rows, cols, bat
     want = np.empty(batch, np.uint32)
     orc.lib().orc_argmax(orc.ptr(np.ascontiguousarray(y)), limit, rows, batch, None, orc.ptr(want))
     assert np.array_equal(tokens, want)
-    if rows * cols <= 4096 * 640:
-        want_y = orc.gemm_epilogue(orc.gemm_partials(p["wint"], p["aint"]), p["ws16"], p["as16"])
-        assert np.abs(y - want_y).max() <= 2e-5 * max(1e-30, float(np.abs(want_y).max()))
+    P = orc.gemm_partials(p["wint"], p["aint"])
+    assert np.array_equal(y, orc.gemm_epilogue_ranges(P, p["ws16"], p["as16"])[0])
+    want_y = orc.gemm_epilogue(P, p["ws16"], p["as16"])
+    del P
+    assert np.abs(y - want_y).max() <= 2e-5 * max(1e-30, float(np.abs(want_y).max()))
     tokens_only, _ = _gemm_argmax(gx, fmt, p, rows, cols, batch, limit, logits=False)
     assert np.array_equal(tokens_only, tokens)
 

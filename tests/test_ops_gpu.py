@@ -658,3 +658,108 @@ def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T):
     # the conv state cannot be updated in place
     assert L.gfxinfer_launch_gdn_conv_window(dp, dw, dc0, dc0, None, da, db, dal, ddt, ds0, ds0, ds0, None, None,
                                              None, T, HK, HV, D, None) == gx.INVALID_ARGUMENT
+
+
+# ---- single-token launchers (qwen_ops.h:83,101,130,217,246,278) ------------------------
+
+def test_single_token_launchers_equal_block_forms(device, gx, orc):
+    """The one-token entry points of greedy_step / the MTP proposal give what their block
+    launchers give at batch 1, bit for bit, with the states updated in place; the conv
+    and recurrent steps also agree with the oracle."""
+    L = gx.lib()
+    rng = np.random.default_rng(77)
+    # conv update, in place
+    proj = rng.standard_normal((1, C)).astype(np.float32)
+    w = _bf16(rng.standard_normal((C, 4)) * 0.5)
+    s0 = _half(rng.standard_normal((C, 4)))
+    block_fin, block_out = empty((C, 4), np.uint16), empty((1, C), np.uint16)
+    say("single conv update vs block")
+    gx.check(L.gfxinfer_launch_gdn_conv_update_block(D_(proj), D_(w), D_(s0), block_fin.data_ptr(),
+                                                     block_out.data_ptr(), None, C, 1, None))
+    state, out = dev(s0), empty((1, C), np.uint16)
+    gx.check(L.gfxinfer_launch_gdn_conv_update(D_(proj), D_(w), state.data_ptr(), out.data_ptr(), C, None))
+    assert np.array_equal(host(state, np.uint16), host(block_fin, np.uint16))
+    assert np.array_equal(host(out, np.uint16), host(block_out, np.uint16))
+    want_f, want_o = np.empty_like(s0), np.empty((1, C), np.uint16)
+    orc.lib().orc_gdn_conv_update(orc.ptr(proj), orc.ptr(w), orc.ptr(s0), orc.ptr(want_f), orc.ptr(want_o),
+                                  None, C, 1)
+    assert np.array_equal(host(state, np.uint16), want_f)
+    # recurrent decode, in place
+    qkv, z, a, b, a_log, dt, nw, r0 = _gdn_inputs(78, 1)
+    d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
+    say("single recurrent decode vs block")
+    fin, block_o, *_ = _gpu_window(gx, d, 1, dev(r0), logs=False)
+    rs, o, work = dev(r0), empty((1, HV * D), np.uint16), empty((1, HV * D), np.float32)
+    gx.check(L.gfxinfer_launch_gdn_recurrent_decode(
+        d["qkv"].data_ptr(), d["z"].data_ptr(), d["a"].data_ptr(), d["b"].data_ptr(), d["a_log"].data_ptr(),
+        d["dt"].data_ptr(), d["nw"].data_ptr(), rs.data_ptr(), o.data_ptr(), HK, HV, D, work.data_ptr(), None))
+    assert np.array_equal(host(rs), host(fin))
+    assert np.array_equal(host(o, np.uint16), host(block_o, np.uint16))
+    want_s = np.empty_like(r0)
+    orc.lib().orc_gdn_recurrent(orc.ptr(qkv), orc.ptr(z), orc.ptr(a), orc.ptr(b), orc.ptr(a_log), orc.ptr(dt),
+                                orc.ptr(nw), orc.ptr(r0), orc.ptr(want_s), orc.ptr(np.empty((1, HV * D), np.uint16)),
+                                None, None, None, 1, HK, HV, D)
+    assert np.abs(host(rs) - want_s).max() <= 1e-5 * max(1.0, np.abs(want_s).max())
+    # restore of one layer == restore_prefix_all over one layer
+    T, accepted = 8, 5
+    qkv, z, a, b, a_log, dt, nw, r0 = _gdn_inputs(79, T)
+    d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
+    _, _, kl, dl, yl = _gpu_window(gx, d, T, dev(r0))
+    clog = _half(rng.standard_normal((T, C)))
+    cs0 = _half(rng.standard_normal((C, 4)))
+    st_all, cs_all, st_one, cs_one = dev(r0), dev(cs0), dev(r0), dev(cs0)
+    say("single restore vs all-layer restore")
+    gx.check(L.gfxinfer_launch_gdn_restore_prefix_all(cs_all.data_ptr(), st_all.data_ptr(), D_(clog), kl.data_ptr(),
+                                                      dl.data_ptr(), yl.data_ptr(), C, 1, T, accepted, HK, HV, D,
+                                                      None))
+    gx.check(L.gfxinfer_launch_gdn_restore_prefix(cs_one.data_ptr(), st_one.data_ptr(), D_(clog), kl.data_ptr(),
+                                                  dl.data_ptr(), yl.data_ptr(), C, accepted, HK, HV, D, None))
+    assert np.array_equal(host(st_one), host(st_all))
+    assert np.array_equal(host(cs_one, np.uint16), host(cs_all, np.uint16))
+    assert L.gfxinfer_launch_gdn_restore_prefix(cs_one.data_ptr(), st_one.data_ptr(), D_(clog), kl.data_ptr(),
+                                                dl.data_ptr(), yl.data_ptr(), C, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    # K/V append at one position
+    capacity, pos, row = 64, 17, HKV * AD
+    key = _half(rng.standard_normal((1, row)))
+    value = rng.standard_normal((1, row)).astype(np.float32)
+    kc1, vc1 = empty((capacity, row), np.uint16), empty((capacity, row), np.uint16)
+    kc2, vc2 = empty((capacity, row), np.uint16), empty((capacity, row), np.uint16)
+    say("single kv append vs block")
+    gx.check(L.gfxinfer_launch_kv_append_block(D_(key), D_(value), kc1.data_ptr(), vc1.data_ptr(), pos, capacity, 1,
+                                               row, None))
+    gx.check(L.gfxinfer_launch_kv_append(D_(key), D_(value), kc2.data_ptr(), vc2.data_ptr(), pos, capacity, row, None))
+    assert np.array_equal(host(kc1, np.uint16), host(kc2, np.uint16))
+    assert np.array_equal(host(vc1, np.uint16), host(vc2, np.uint16))
+    assert np.array_equal(host(kc2, np.uint16)[pos], key[0])
+    assert L.gfxinfer_launch_kv_append(D_(key), D_(value), kc2.data_ptr(), vc2.data_ptr(), capacity, capacity, row,
+                                       None) == gx.INVALID_ARGUMENT
+    # attention of one token over token_count positions
+    capacity, count = 4096 + 32, 1000
+    q = _half(rng.standard_normal((1, HQ, AD)))
+    gate = rng.standard_normal((1, HQ, 2 * AD)).astype(np.float32)
+    kc = np.zeros((capacity, HKV, AD), np.uint16)
+    vc = np.zeros((capacity, HKV, AD), np.uint16)
+    kc[:count] = _half(rng.standard_normal((count, HKV, AD)))
+    vc[:count] = _half(rng.standard_normal((count, HKV, AD)))
+    wb = L.gfxinfer_attention_workspace_bytes(1, HQ, capacity)
+    work = empty((wb // 4,), np.float32)
+    o1, o2 = empty((1, HQ, AD), np.uint16), empty((1, HQ, AD), np.uint16)
+    say("single attention vs block")
+    args = (D_(q), D_(gate), D_(kc), D_(vc))
+    gx.check(L.gfxinfer_launch_gated_attention_decode_block(*args, o1.data_ptr(), count, capacity, 1, HQ, HKV, AD,
+                                                            work.data_ptr(), wb, None))
+    gx.check(L.gfxinfer_launch_gated_attention_decode(*args, o2.data_ptr(), count, capacity, HQ, HKV, AD,
+                                                      work.data_ptr(), wb, None))
+    assert np.array_equal(host(o1, np.uint16), host(o2, np.uint16))
+    want = np.empty((1, HQ, AD), np.uint16)
+    orc.lib().orc_gated_attention(orc.ptr(q), orc.ptr(gate), orc.ptr(kc), orc.ptr(vc), orc.ptr(want), count, 1, HQ,
+                                  HKV, AD, np.float32(1 / np.sqrt(AD)))
+    assert np.abs(_f(host(o2, np.uint16)) - _f(want)).max() <= 1e-2 * max(1.0, np.abs(_f(want)).max())
+    # argmax of one row, ties to the lowest index
+    V = 151936
+    logits = rng.standard_normal(V).astype(np.float32)
+    logits[[9000, 120000]] = 50.0
+    token = empty((1,), np.uint32)
+    say("single argmax")
+    gx.check(L.gfxinfer_launch_argmax(D_(logits), token.data_ptr(), V, None))
+    assert int(host(token, np.uint32)[0]) == 9000

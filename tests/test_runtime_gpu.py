@@ -198,6 +198,23 @@ def test_session_rejects_misaligned_steps(tiny, gx):
         s.speculative_step_forced(1, 4, 5)
 
 
+def test_session_outlives_its_model(device):
+    """Destroying a model while a session on it is open defers the release to the end of
+    the last session: the session keeps stepping on the model's stream and weights, and
+    closing it frees both (a session destroyed after its model once synchronized a
+    destroyed stream)."""
+    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel
+    model = SyntheticModel(_spec(), SEED)
+    reference = _session(model)
+    want = [reference.greedy_step(t) for t in (5, 6, 7)]
+    reference.close()
+    session = QwenDecodeSession(model, 256, 0)
+    say("destroy the model under an open session")
+    model.close()
+    assert [session.greedy_step(t) for t in (5, 6, 7)] == want
+    session.close()
+
+
 def test_full_size_model_speculative_rounds(device):
     """The 27B-shaped synthetic model: generation, a graph session at depth 4 and 31,
     forced 85 % acceptance rounds and block == serial on the first tokens."""
