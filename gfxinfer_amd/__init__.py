@@ -143,6 +143,8 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_session_get_summary": (I32, [P, P]),
     "gfxinfer_session_copy_buffer": (I32, [P, ctypes.c_char_p, SZ, P, SZ]),
     "gfxinfer_session_buffer_bytes": (SZ, [P, ctypes.c_char_p]),
+    "gfxinfer_session_set_layer_trace": (I32, [P, P, SZ]),
+    "gfxinfer_session_layer_trace_bytes": (SZ, [P]),
     "gfxinfer_session_prefill": (I32, [P, P, SZ, I32, P]),
     "gfxinfer_session_generate": (I32, [P, P, SZ, P, P, P, P]),
     "gfxinfer_depth_policy_create": (I32, [U32, P]),

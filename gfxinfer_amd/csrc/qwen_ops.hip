@@ -24,18 +24,44 @@ __device__ __forceinline__ float bf16_to_float(uint16_t value) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
 
-// Block-wide sum for blockDim.x <= 1024 (all threads receive the result).
-__device__ float block_sum(float value, float* scratch) {
-  value = wave_sum(value);
-  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+
+// Sum of squares of an fp16 row staged in LDS, in the order of the reference's rms_norm
+// (qwen_ops.hip:31-63: 256 threads of wave32): partial t (t < 256) is the fmaf chain over
+// elements t, t + 256, ... in index order; each 32 partials are reduced by the shfl_down
+// tree (lane l adds lane l + d, d = 16, 8, 4, 2, 1), here on the two 32-lane halves of
+// each wave64; the eight group sums by the same tree (lanes 8..31 hold zeros, which add
+// exactly).  Summing in the reference's order makes the normalized fp16 rows, and so the
+// A4 codes of the next projection, independent of this build's launch shape: a code that
+// flips between two summation orders changes a projection by a whole quantization step.
+// Needs blockDim.x >= 256; all threads return the total.  The caller synchronizes the
+// workgroup between writing `row` and this call.
+__device__ float reference_square_sum(const __half* row, uint32_t elements, float* scratch) {
+  const unsigned t = threadIdx.x;
+  float s = 0.0F;
+  if (t < 256u) {
+    for (uint32_t i = t; i < elements; i += 256u) {
+      const float f = __half2float(row[i]);
+      s = fmaf(f, f, s);
+    }
+  }
+  s += __shfl_down(s, 16, 32);
+  s += __shfl_down(s, 8, 32);
+  s += __shfl_down(s, 4, 32);
+  s += __shfl_down(s, 2, 32);
+  s += __shfl_down(s, 1, 32);
+  if (t < 256u && (t & 31u) == 0u) scratch[t >> 5] = s;
   __syncthreads();
-  if (lane == 0) scratch[wave] = value;
-  __syncthreads();
-  float total = 0.0F;
-  for (unsigned w = 0; w < waves; ++w) total += scratch[w];
-  return total;
+  const float a0 = scratch[0] + scratch[4], a1 = scratch[1] + scratch[5];
+  const float a2 = scratch[2] + scratch[6], a3 = scratch[3] + scratch[7];
+  return (a0 + a2) + (a1 + a3);
 }
 
+// Inverse RMS from the reference-ordered sum: the correctly rounded 1 / sqrt (the build
+// rounds fp32 division and square root correctly), where the reference calls rsqrtf, the
+// hardware approximation within 1 ulp; a CPU restatement reproduces this value exactly.
+__device__ __forceinline__ float inverse_rms(float total, uint32_t elements, float epsilon) {
+  return 1.0F / sqrtf(total / static_cast<float>(elements) + epsilon);
+}
 
 // ---------------------------------------------------------------------------
 // RMSNorm family (qwen_ops.hip:31-106, 176-217).  One workgroup per row.
@@ -58,7 +84,6 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   __half* row = reinterpret_cast<__half*>(smem);           // [elements] staged values
   float* scratch = reinterpret_cast<float*>(smem + ((elements * 2 + 15) & ~15u));
   const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
-  float square = 0.0F;
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
     __half v = input[base + i];
     if constexpr (Residual) {
@@ -68,11 +93,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
       residual_out[base + i] = v;
     }
     row[i] = v;
-    const float f = __half2float(v);
-    square = fmaf(f, f, square);
   }
-  const float total = block_sum(square, scratch);
-  const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
+  __syncthreads();
+  const float inverse = inverse_rms(reference_square_sum(row, elements, scratch), elements, epsilon);
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
     const __half n = to_half(__half2float(row[i]) * inverse * norm_scale(weight, i, unit_offset));
     row[i] = n;
@@ -102,6 +125,8 @@ constexpr unsigned kNormSlots = 10;
 constexpr unsigned kNormPlaneSlots = 3;  // split-update variant: rows up to 6144
 constexpr unsigned kNormMaxPlanes = 8;
 constexpr uint32_t kNormFastMax = kNormSlots * 16u * 128u;
+// Rows longer than this do not fit the LDS row the reference-ordered sum reads (64 KB).
+constexpr std::size_t kNormMaxElements = 32768;
 
 template <bool Residual, bool Quantize, unsigned Slots, unsigned MaxPlanes>
 __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
@@ -110,6 +135,7 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
     uint32_t elements, float epsilon, bool unit_offset, uint32_t planes, uint64_t plane_stride) {
   __shared__ float scratch[16];
+  __shared__ __half staged[Slots * 16u * 128u];  // the row, for the reference-ordered sum
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
   // 1) Loads.  Dead slots read element 0 (always valid) and are ignored.
@@ -131,9 +157,8 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
       }
     }
   }
-  // 2) Residual add (fp16 rounding of the sum), squares.
+  // 2) Residual add (fp16 rounding of the sum), staged for the sum of squares.
   float x[Slots][2];
-  float square = 0.0F;
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     x[j][0] = 0.0F;
@@ -157,12 +182,11 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
       }
       x[j][0] = __half2float(a);
       x[j][1] = __half2float(b);
-      square = fmaf(x[j][0], x[j][0], square);
-      square = fmaf(x[j][1], x[j][1], square);
+      *reinterpret_cast<__half2*>(staged + i) = __halves2half2(a, b);
     }
   }
-  const float total = block_sum(square, scratch);
-  const float inverse = rsqrtf(total / static_cast<float>(elements) + epsilon);
+  __syncthreads();
+  const float inverse = inverse_rms(reference_square_sum(staged, elements, scratch), elements, epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t g = wave + j * waves;
@@ -196,14 +220,13 @@ __global__ __launch_bounds__(256) void dual_rms_norm_kernel(
   const __half* input = (second ? right : left) + row * elements;
   const uint16_t* weight = second ? right_weight : left_weight;
   output += row * 2u * elements + (second ? elements : 0);
-  float square = 0.0F;
+  extern __shared__ __align__(16) uint8_t dual_smem[];
+  __half* staged = reinterpret_cast<__half*>(dual_smem);  // [elements]
+  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) staged[i] = input[i];
+  __syncthreads();
+  const float inverse = inverse_rms(reference_square_sum(staged, elements, scratch), elements, epsilon);
   for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
-    const float f = __half2float(input[i]);
-    square = fmaf(f, f, square);
-  }
-  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + epsilon);
-  for (uint32_t i = threadIdx.x; i < elements; i += blockDim.x) {
-    output[i] = to_half(__half2float(input[i]) * inverse * norm_scale(weight, i, unit_offset));
+    output[i] = to_half(__half2float(staged[i]) * inverse * norm_scale(weight, i, unit_offset));
   }
 }
 
@@ -236,6 +259,7 @@ struct DualNormArgs {
 template <unsigned Slots, int EmbedFormat, bool Quantize>
 __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a) {
   __shared__ float scratch[16];
+  __shared__ __half staged[Slots * 16u * 128u];  // the half row, for the reference-ordered sum
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const uint32_t elements = a.elements;
   const std::size_t row = blockIdx.y;
@@ -273,18 +297,15 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
     }
   }
   float x[Slots][2];
-  float square = 0.0F;
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
     x[j][0] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] & 0xffffu)));
     x[j][1] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] >> 16)));
-    if (i < elements) {
-      square = fmaf(x[j][0], x[j][0], square);
-      square = fmaf(x[j][1], x[j][1], square);
-    }
+    if (i < elements) *reinterpret_cast<uint32_t*>(staged + i) = hin[j];
   }
-  const float inverse = rsqrtf(block_sum(square, scratch) / static_cast<float>(elements) + a.epsilon);
+  __syncthreads();
+  const float inverse = inverse_rms(reference_square_sum(staged, elements, scratch), elements, a.epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t g = wave + j * waves;
@@ -1101,7 +1122,7 @@ int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_
                    uint32_t batch, float epsilon, bool unit, hipStream_t stream,
                    uint32_t planes = 1) {
   if (input == nullptr || weight == nullptr || elements == 0 || batch == 0 ||
-      !valid_epsilon(epsilon) || elements > (1u << 20) ||
+      !valid_epsilon(epsilon) || elements > kNormMaxElements ||
       (residual && (update == nullptr || residual_out == nullptr)) ||
       (!quantize && output == nullptr) ||
       (quantize && (codes == nullptr || scales == nullptr || elements % 128 != 0)) ||
@@ -1121,7 +1142,9 @@ int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_
                     aligned(residual_out, 4) && aligned(output, 4) && aligned(update, 8) &&
                     aligned(weight, 4);
   const unsigned slots = (e + 127u) / 128u;
-  const unsigned waves = std::min(16u, slots);  // slots <= 16 * kNormSlots on the fast path
+  // slots <= 16 * kNormSlots on the fast path; at least four waves for the 256 partial
+  // sums of the reference-ordered sum of squares
+  const unsigned waves = std::max(4u, std::min(16u, slots));
   const unsigned per_wave = (slots + waves - 1) / waves;
   const dim3 block(64u * waves);
   const uint64_t stride = static_cast<uint64_t>(batch) * e;
@@ -1228,7 +1251,7 @@ void launch_dual_norm(const uint16_t* left, const uint16_t* lw, const uint16_t* 
     a.unit_offset = unit;
     hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, 0, false>), dim3(2, batch), dim3(1024), 0, stream, a);
   } else {
-    hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), 0, stream,
+    hipLaunchKernelGGL(dual_rms_norm_kernel, dim3(2, batch), dim3(256), (elements * 2 + 15) & ~std::size_t{15}, stream,
                        reinterpret_cast<const __half*>(left), lw, reinterpret_cast<const __half*>(right), rw,
                        reinterpret_cast<__half*>(out), static_cast<uint32_t>(elements), epsilon, unit);
   }
@@ -1241,7 +1264,7 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat(
     float epsilon, int32_t add_unit_offset, void* stream) {
   if (left == nullptr || left_bf16_weight == nullptr || right == nullptr ||
       right_bf16_weight == nullptr || concatenated_output == nullptr || elements == 0 ||
-      elements > (1u << 30) || !valid_epsilon(epsilon)) {
+      elements > kNormMaxElements || !valid_epsilon(epsilon)) {
     return fail(GFXI_INVALID_ARGUMENT, "invalid dual RMSNorm/concat arguments");
   }
   launch_dual_norm(left, left_bf16_weight, right, right_bf16_weight, concatenated_output, elements, 1,
@@ -1255,7 +1278,7 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat_batch(
     float epsilon, int32_t add_unit_offset, void* stream) {
   if (left == nullptr || left_bf16_weight == nullptr || right == nullptr ||
       right_bf16_weight == nullptr || concatenated_output == nullptr || elements == 0 ||
-      elements > (1u << 30) || batch == 0 || batch > 65535 || !valid_epsilon(epsilon)) {
+      elements > kNormMaxElements || batch == 0 || batch > 65535 || !valid_epsilon(epsilon)) {
     return fail(GFXI_INVALID_ARGUMENT, "invalid batched dual RMSNorm/concat arguments");
   }
   launch_dual_norm(left, left_bf16_weight, right, right_bf16_weight, concatenated_output, elements, batch,

@@ -138,6 +138,9 @@ struct gfxinfer_session {
   bool mtp_chain_active{false};
   bool record_rollback{false};
   bool parity{false};
+  // Test hook: when set, eager verifier passes copy each layer's stage boundaries into
+  // this device buffer (layout: trace_layout()).
+  uint8_t* layer_trace{nullptr};
   const uint16_t* last_hidden{nullptr};
 
   std::vector<Layer> layers;
@@ -289,6 +292,7 @@ struct gfxinfer_session {
           spec.kv_head_count, spec.attention_head_size, attention_workspace,
           attention_workspace_bytes, stream));
     }
+    GFXI_TRY(trace_codes(L, true, attn_width, batch));
     return gemm_planes(L.o, mixer_update, batch, mixer_planes);
   }
 
@@ -299,9 +303,11 @@ struct gfxinfer_session {
     GFXI_TRY(gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
         input, mixer_update, mixer_planes, post_attention, L.post_norm, nullptr, act_codes,
         act_scales, H, batch, spec.rms_norm_epsilon, 1, stream));
+    GFXI_TRY(trace_post(L, batch));
     GFXI_TRY(gemm_fused({{&L.gate, gate_output}, {&L.up, up_output}}, batch));
     GFXI_TRY(gfxinfer_launch_silu_multiply_quantize_i4(gate_output, up_output, act_codes,
                                                        act_scales, I, batch, stream));
+    GFXI_TRY(trace_codes(L, false, I, batch));
     GFXI_TRY(gemm_planes(L.down, mlp_update, batch, mlp_planes));
     return gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
         post_attention, mlp_update, mlp_planes, output, next_norm, nullptr, act_codes, act_scales,
@@ -342,6 +348,7 @@ struct gfxinfer_session {
                                                       act_codes, act_scales, batch,
                                                       spec.gdn_value_head_count,
                                                       spec.gdn_head_size, stream));
+      GFXI_TRY(trace_codes(L, true, gdn_value, batch));
       GFXI_TRY(gemm_planes(L.out, mixer_update, batch, mixer_planes));
     }
     return mlp_tail(L, input, output, next_norm, batch);
@@ -349,15 +356,72 @@ struct gfxinfer_session {
 
   // Layers + final norm + LM head + argmax over hidden_a[0..batch) (the body shared
   // by block_step and the verifier, qwen_runtime.cpp:615-640 / 1341-1376).
+  // Layer trace sections (byte offsets), each sized for kMaxBlock tokens:
+  //   residual [layers + 1][32][H] fp16: rows entering layer 0, then leaving each layer;
+  //   post [layers][32][H] fp16: rows after the mixer's residual add;
+  //   mixer codes [layers][32 * W / 2] + scales [layers][32 * W / 128] fp16: the A4 input
+  //     of the o / out projection (W = the wider of the attention and GDN widths);
+  //   mlp codes [layers][32 * I / 2] + scales [layers][32 * I / 128] fp16: the SwiGLU
+  //     output's A4 codes, the down projection's input.
+  // A layer's codes and scales are stored packed as [batch][width / 2] / [batch][width / 128].
+  struct TraceLayout {
+    std::size_t residual, post, mixer_codes, mixer_scales, mlp_codes, mlp_scales, total;
+  };
+  TraceLayout trace_layout() const {
+    const std::size_t L = layers.size(), W = std::max(attn_width, gdn_value), B = kMaxBlock;
+    TraceLayout t{};
+    t.residual = 0;
+    t.post = t.residual + (L + 1) * B * H * 2;
+    t.mixer_codes = t.post + L * B * H * 2;
+    t.mixer_scales = t.mixer_codes + L * B * W / 2;
+    t.mlp_codes = t.mixer_scales + L * B * (W / 128) * 2;
+    t.mlp_scales = t.mlp_codes + L * B * I / 2;
+    t.total = t.mlp_scales + L * B * (I / 128) * 2;
+    return t;
+  }
+  int32_t trace_copy(std::size_t offset, const void* source, std::size_t bytes) {
+    if (auto e = hipMemcpyAsync(layer_trace + offset, source, bytes, hipMemcpyDeviceToDevice, stream);
+        e != hipSuccess) {
+      return hip_fail(e, "layer trace copy failed");
+    }
+    return ok();
+  }
+  int32_t trace_rows(std::size_t slot, const uint16_t* rows, unsigned batch) {
+    if (layer_trace == nullptr) return ok();
+    return trace_copy(trace_layout().residual + slot * kMaxBlock * H * 2, rows, batch * H * 2);
+  }
+  // Index of a decoder layer, or -1 for the MTP block (never traced).
+  long layer_index(const Layer& L) const {
+    return (&L >= layers.data() && &L < layers.data() + layers.size()) ? &L - layers.data() : -1;
+  }
+  // The A4 codes and scales in act_codes / act_scales of `width` columns.
+  int32_t trace_codes(const Layer& L, bool mixer, std::size_t width, unsigned batch) {
+    const long i = layer_index(L);
+    if (layer_trace == nullptr || i < 0) return ok();
+    const TraceLayout t = trace_layout();
+    const std::size_t W = mixer ? std::max(attn_width, gdn_value) : I;
+    const std::size_t codes = (mixer ? t.mixer_codes : t.mlp_codes) + i * kMaxBlock * W / 2;
+    const std::size_t scales = (mixer ? t.mixer_scales : t.mlp_scales) + i * kMaxBlock * (W / 128) * 2;
+    GFXI_TRY(trace_copy(codes, act_codes, batch * width / 2));
+    return trace_copy(scales, act_scales, batch * (width / 128) * 2);
+  }
+  int32_t trace_post(const Layer& L, unsigned batch) {
+    const long i = layer_index(L);
+    if (layer_trace == nullptr || i < 0) return ok();
+    return trace_copy(trace_layout().post + i * kMaxBlock * H * 2, post_attention, batch * H * 2);
+  }
+
   int32_t decoder_stack(unsigned batch, const uint64_t* device_position) {
     GFXI_TRY(gfxinfer_launch_rms_norm_quantize_i4(hidden_a, layers.front().input_norm, nullptr,
                                                   act_codes, act_scales, H, batch,
                                                   spec.rms_norm_epsilon, 1, stream));
     uint16_t* current = hidden_a;
     uint16_t* next = hidden_b;
+    GFXI_TRY(trace_rows(0, current, batch));
     for (std::size_t i = 0; i < layers.size(); ++i) {
       const uint16_t* next_norm = i + 1 < layers.size() ? layers[i + 1].input_norm : final_norm;
       GFXI_TRY(layer_block(layers[i], current, next, batch, next_norm, device_position));
+      GFXI_TRY(trace_rows(i + 1, next, batch));
       std::swap(current, next);
     }
     return gemm_argmax(lm_head, batch, spec.tokenizer_vocabulary_size, selected);
@@ -1096,6 +1160,20 @@ const gfxinfer_session::Buffer* find_buffer(const gfxinfer_session* s, const cha
   return nullptr;
 }
 }  // namespace
+
+extern "C" size_t gfxinfer_session_layer_trace_bytes(const gfxinfer_session* session) {
+  return session == nullptr ? 0 : session->trace_layout().total;
+}
+
+extern "C" int32_t gfxinfer_session_set_layer_trace(gfxinfer_session* session, void* device_trace,
+                                                    size_t bytes) {
+  GFXI_TRY(enter(session));
+  if (device_trace != nullptr && bytes < session->trace_layout().total) {
+    return fail(GFXI_INVALID_ARGUMENT, "layer trace buffer is smaller than gfxinfer_session_layer_trace_bytes");
+  }
+  session->layer_trace = static_cast<uint8_t*>(device_trace);
+  return ok();
+}
 
 extern "C" size_t gfxinfer_session_buffer_bytes(const gfxinfer_session* session, const char* name) {
   const auto* b = find_buffer(session, name);

@@ -419,6 +419,13 @@ class QwenDecodeSession:
         check(lib().gfxinfer_session_get_summary(self._handle, ctypes.byref(s)))
         return s
 
+    def layer_trace_bytes(self) -> int:
+        return int(lib().gfxinfer_session_layer_trace_bytes(self._handle))
+
+    def set_layer_trace(self, device_pointer, nbytes: int) -> None:
+        """Per-layer stage boundaries into a device buffer (test hook; 0 turns it off)."""
+        check(lib().gfxinfer_session_set_layer_trace(self._handle, device_pointer or None, nbytes))
+
     def buffer(self, name: str, dtype=np.uint8, count: int | None = None, offset: int = 0) -> np.ndarray:
         """Copy of a named session buffer (test accessor)."""
         total = int(lib().gfxinfer_session_buffer_bytes(self._handle, name.encode()))

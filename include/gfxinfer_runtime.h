@@ -262,6 +262,22 @@ int32_t gfxinfer_session_copy_buffer(const gfxinfer_session* session, const char
                                      size_t offset, void* host, size_t bytes);
 /* Byte size of a named session buffer (0 if unknown). */
 size_t gfxinfer_session_buffer_bytes(const gfxinfer_session* session, const char* name);
+/* Test hook, no reference counterpart: with device_trace set (NULL turns it off), every
+ * eager verifier pass (block_step, greedy_step, prefill, planted rounds) copies each
+ * decoder layer's stage boundaries into device_trace (at least
+ * gfxinfer_session_layer_trace_bytes bytes), for stage-by-stage comparison against a CPU
+ * model.  Sections, in order, each sized for 32 tokens (W = max(attention width, GDN
+ * value width), I = MLP width):
+ *   residual [layers + 1][32][hidden] fp16 -- rows entering layer 0, then leaving each layer;
+ *   post [layers][32][hidden] fp16 -- rows after the mixer's residual add;
+ *   mixer codes [layers][32 * W / 2] and scales [layers][32 * W / 128] fp16 -- the A4 input
+ *     of the o / out projection, stored as [tokens][width / 2] and [tokens][width / 128];
+ *   MLP codes [layers][32 * I / 2] and scales [layers][32 * I / 128] fp16 -- the A4 SwiGLU
+ *     output (the down projection's input), stored the same way.
+ * Captured graphs are not affected. */
+size_t gfxinfer_session_layer_trace_bytes(const gfxinfer_session* session);
+int32_t gfxinfer_session_set_layer_trace(gfxinfer_session* session, void* device_trace,
+                                         size_t bytes);
 
 /* Chunked prefill.  The reference prefills a prompt with one greedy_step per token and,
  * when MTP is on, an mtp_draft per token from the second on (cli/main.cpp:1055-1069);

@@ -52,7 +52,11 @@ class Matrix:
     def __call__(self, x16: np.ndarray) -> np.ndarray:
         """fp16 [B, K] -> fp32 [B, N] through A4 activations (lowbit_gemv.hip:373-553)."""
         packed, as16 = O.quantize_activation_i4(x16)
-        a = O.unpack_a4(packed, self.cols)
+        return self.apply(packed, as16)
+
+    def apply(self, packed: np.ndarray, as16: np.ndarray) -> np.ndarray:
+        """A4 codes [B, K/2] + fp16 scales [B, K/128] -> fp32 [B, N]."""
+        a = O.unpack_a4(np.ascontiguousarray(packed), self.cols)
         partials = O.gemm_partials(self.w, a)
         if self.splits is None:
             return O.gemm_epilogue(partials, self.ws16, as16)
@@ -195,7 +199,7 @@ class OracleSession:
                                           res16.shape[0], EPS, 1)
         return r, n
 
-    def _attention_mixer(self, L, normed, kcache, vcache, position, stop_after_append=False):
+    def _attention_mixer(self, L, normed, kcache, vcache, position, stop_after_append=False, raw=False):
         m, s = self.m, self.m.s
         T, hd = normed.shape[0], m.hd
         q = L["q"](normed)
@@ -215,9 +219,11 @@ class OracleSession:
         O.lib().orc_gated_attention(O.ptr(qn), _p(q), O.ptr(kcache), O.ptr(vcache), O.ptr(out), position + 1, T,
                                     s["attention_head_count"], s["kv_head_count"], hd,
                                     ctypes.c_float(np.float32(1.0 / np.sqrt(hd))))
+        if raw:
+            return out.reshape(T, -1)
         return L["o"](out.reshape(T, -1))
 
-    def _gdn_mixer(self, L, normed, index):
+    def _gdn_mixer(self, L, normed, index, raw=False):
         m, s = self.m, self.m.s
         T = normed.shape[0]
         proj = L["qkv"](normed)
@@ -234,6 +240,8 @@ class OracleSession:
                                   None, None, T, s["gdn_key_head_count"], s["gdn_value_head_count"],
                                   s["gdn_head_size"])
         self.state[index] = state
+        if raw:
+            return out
         return L["out"](out)
 
     def _mlp(self, L, residual, mixer_update, next_norm):
@@ -242,6 +250,64 @@ class OracleSession:
         act = np.empty(gate.shape, np.uint16)
         O.lib().orc_silu_multiply(_p(gate), _p(up), O.ptr(act), gate.size)
         return self._residual_norm(post, L["down"](act), next_norm)
+
+    # ---- one layer, teacher-forced (qwen_runtime.cpp:421-544) ----------------------
+    def layer_forward(self, i: int, residual16: np.ndarray, position: int) -> np.ndarray:
+        """Layer i of a block whose residual rows entering the layer are `residual16`
+        (fp16 [T, H], e.g. another implementation's), from this session's state of that
+        layer (which it advances); returns the residual rows leaving the layer."""
+        m = self.m
+        L = m.layers[i]
+        normed = self._norm(residual16, L["input_norm"])
+        index = sum(1 for M in m.layers[:i] if M["attention"] == L["attention"])
+        if L["attention"]:
+            update = self._attention_mixer(L, normed, self.kcache[index], self.vcache[index], position)
+        else:
+            update = self._gdn_mixer(L, normed, index)
+        hidden, _ = self._mlp(L, residual16, update, L["input_norm"])
+        return hidden
+
+    # ---- one layer, stage by stage, each stage from given inputs -------------------
+    def _index(self, i):
+        L = self.m.layers[i]
+        return L, sum(1 for M in self.m.layers[:i] if M["attention"] == L["attention"])
+
+    def mixer_stage(self, i, residual16, position):
+        """Input norm + mixer of layer i up to its fp16 output, as A4 codes and scales (the
+        o / out projection's input); advances this session's state of the layer."""
+        L, index = self._index(i)
+        normed = self._norm(residual16, L["input_norm"])
+        if L["attention"]:
+            out = self._attention_mixer(L, normed, self.kcache[index], self.vcache[index], position, raw=True)
+        else:
+            out = self._gdn_mixer(L, normed, index, raw=True)
+        return O.quantize_activation_i4(out)
+
+    def post_stage(self, i, residual16, mixer_codes, mixer_scales):
+        """o / out projection of given A4 codes + residual add: the rows after the mixer."""
+        L, _ = self._index(i)
+        update = (L["o"] if L["attention"] else L["out"]).apply(mixer_codes, mixer_scales)
+        post, _ = self._residual_norm(residual16, update, L["post_norm"])
+        return post
+
+    def mlp_codes_stage(self, i, post16):
+        """Post norm, gate/up, SwiGLU: the down projection's A4 codes and scales."""
+        L, _ = self._index(i)
+        normed = self._norm(post16, L["post_norm"])
+        gate, up = L["gate"](normed), L["up"](normed)
+        act = np.empty(gate.shape, np.uint16)
+        O.lib().orc_silu_multiply(_p(gate), _p(up), O.ptr(act), gate.size)
+        return O.quantize_activation_i4(act)
+
+    def out_stage(self, i, post16, mlp_codes, mlp_scales):
+        """Down projection of given A4 codes + residual add: the rows leaving the layer."""
+        L, _ = self._index(i)
+        hidden, _ = self._residual_norm(post16, L["down"].apply(mlp_codes, mlp_scales), L["post_norm"])
+        return hidden
+
+    def final_logits(self, residual16: np.ndarray) -> np.ndarray:
+        """Final norm + LM head of residual rows leaving the last layer (qwen_runtime.cpp:635)."""
+        return self.m.lm_head(self._norm(residual16, self.m.final_norm))
 
     # ---- QwenDecodeSession::block_step (qwen_runtime.cpp:1320-1392) --------------
     def block_step(self, tokens):

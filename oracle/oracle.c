@@ -477,12 +477,35 @@ static float norm_scale(uint16_t w, int unit_offset) {
 }
 
 /* qwen_ops.hip:31-63 */
+/* Sum of squares of an fp16 row in the order of the reference's rms_norm kernel
+ * (qwen_ops.hip:31-63, 256 threads of wave32): partial t = fmaf chain over elements
+ * t, t + 256, ... in index order; each group of 32 partials reduced by the shfl_down
+ * tree (lane l += lane l + d for d = 16, 8, 4, 2, 1); the eight group sums by the same
+ * tree over lanes 0..7 (lanes 8..31 hold zeros).  The inverse RMS is then the correctly
+ * rounded 1 / sqrtf; the reference's rsqrtf is the hardware approximation, within 1 ulp. */
+static float reference_square_sum(const uint16_t* x, size_t n) {
+  float partial[256];
+  for (size_t t = 0; t < 256; ++t) {
+    float s = 0.0f;
+    for (size_t i = t; i < n; i += 256) s = fmaf(h2f(x[i]), h2f(x[i]), s);
+    partial[t] = s;
+  }
+  float group[8];
+  for (size_t g = 0; g < 8; ++g) {
+    float* p = partial + 32 * g;
+    for (size_t d = 16; d >= 1; d /= 2) {
+      for (size_t l = 0; l < d; ++l) p[l] = p[l] + p[l + d];
+    }
+    group[g] = p[0];
+  }
+  return ((group[0] + group[4]) + (group[2] + group[6])) + ((group[1] + group[5]) + (group[3] + group[7]));
+}
+
 void orc_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, size_t n, unsigned batch,
                   float epsilon, int unit_offset) {
   for (unsigned b = 0; b < batch; ++b) {
     const uint16_t* x = in + (size_t)b * n;
-    float sum = 0.0f;
-    for (size_t i = 0; i < n; ++i) sum = fmaf(h2f(x[i]), h2f(x[i]), sum);
+    const float sum = reference_square_sum(x, n);
     const float inverse = 1.0f / sqrtf(sum / (float)n + epsilon);
     for (size_t i = 0; i < n; ++i) {
       out[(size_t)b * n + i] = f2h(h2f(x[i]) * inverse * norm_scale(w[i], unit_offset));
@@ -496,12 +519,8 @@ void orc_residual_add_rms_norm(const uint16_t* residual, const float* update, ui
                                float epsilon, int unit_offset) {
   for (unsigned b = 0; b < batch; ++b) {
     const size_t base = (size_t)b * n;
-    float sum = 0.0f;
-    for (size_t i = 0; i < n; ++i) {
-      const uint16_t rounded = f2h(h2f(residual[base + i]) + update[base + i]);
-      residual_out[base + i] = rounded;
-      sum = fmaf(h2f(rounded), h2f(rounded), sum);
-    }
+    for (size_t i = 0; i < n; ++i) residual_out[base + i] = f2h(h2f(residual[base + i]) + update[base + i]);
+    const float sum = reference_square_sum(residual_out + base, n);
     const float inverse = 1.0f / sqrtf(sum / (float)n + epsilon);
     for (size_t i = 0; i < n; ++i) {
       normalized[base + i] = f2h(h2f(residual_out[base + i]) * inverse * norm_scale(w[i], unit_offset));

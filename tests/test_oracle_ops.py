@@ -63,6 +63,56 @@ def test_rms_norm_is_textbook(orc, unit):
     assert _ulps16(out, want).max() <= 1.0
 
 
+def _reference_kernel_norm(x16, w16, eps, unit, sequential=False):
+    """The reference's rms_norm kernel (qwen_ops.hip:31-63) simulated thread by thread:
+    256 threads with per-thread fmaf chains, wave32 __shfl_down trees (a lane whose
+    source is past its 32-lane segment keeps its own value), wave 0's tree over the eight
+    wave sums, then 1/sqrt correctly rounded and fp16(x * inverse * (1 + w)).  fmaf is
+    emulated in float64, exact for the magnitudes the caller uses (squares and partial
+    sums within 2^29 of each other), then rounded once to float32."""
+    x = x16.view(np.float16).astype(np.float32)
+    n = x.size
+    lanes = np.zeros(256, np.float32)
+    for t in range(256):
+        s = np.float32(0.0)
+        for i in range(t, n, 256):
+            s = np.float32(np.float64(x[i]) * np.float64(x[i]) + np.float64(s))
+        lanes[t] = s
+
+    def shfl_tree(v):  # v: 32 lanes; returns lane 0 after += shfl_down 16, 8, 4, 2, 1
+        v = v.copy()
+        for d in (16, 8, 4, 2, 1):
+            src = np.array([v[l + d] if l + d < 32 else v[l] for l in range(32)], np.float32)
+            v = (v + src).astype(np.float32)
+        return v[0]
+
+    waves = np.array([shfl_tree(lanes[32 * g:32 * g + 32]) for g in range(8)], np.float32)
+    total = shfl_tree(np.concatenate([waves, np.zeros(24, np.float32)]))
+    if sequential:  # a planted mistake: one fmaf chain over the whole row
+        total = np.float32(0.0)
+        for v in x:
+            total = np.float32(np.float64(v) * np.float64(v) + np.float64(total))
+    inverse = np.float32(1.0) / np.float32(np.sqrt(np.float32(total / np.float32(n) + np.float32(eps))))
+    scale = (w16.astype(np.uint32) << 16).view(np.float32) + np.float32(1.0 if unit else 0.0)
+    return ((x * inverse).astype(np.float32) * scale).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("n", [5120, 300, 7, 256])
+def test_rms_norm_sums_in_the_reference_kernel_order(orc, n):
+    """orc_rms_norm == the thread-level simulation of the reference kernel, bit for bit;
+    a row whose sequential fmaf sum differs from the kernel's tree sum proves the
+    comparison sees the order."""
+    rng = np.random.default_rng(n)
+    mags = rng.uniform(0.25, 4.0, n) * rng.choice([-1.0, 1.0], n)
+    x = _h(mags)
+    w = _bf(rng.standard_normal(n) * 0.05)
+    out = np.empty(n, np.uint16)
+    orc.lib().orc_rms_norm(orc.ptr(x), orc.ptr(w), orc.ptr(out), n, 1, ctypes.c_float(1e-6), 1)
+    assert np.array_equal(out, _reference_kernel_norm(x, w, 1e-6, True))
+    if n == 5120:  # the comparison distinguishes the summation orders
+        assert not np.array_equal(out, _reference_kernel_norm(x, w, 1e-6, True, sequential=True))
+
+
 def test_residual_add_norm_normalizes_the_rounded_sum(orc):
     rng = np.random.default_rng(2)
     n, b = 384, 2
