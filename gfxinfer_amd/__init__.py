@@ -68,6 +68,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gfx950_i8_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, P]),
     "gfxinfer_gemm_argmax_workspace_bytes": (SZ, [SZ, U32]),
     "gfxinfer_launch_gfx950_i4_gemm_argmax": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, SZ, P, P]),
+    "gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, P]),
     "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
     "gfxinfer_debug_stream_read": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),

@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -1659,6 +1660,62 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(
   hipLaunchKernelGGL(argmax_keys_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, keys,
                      static_cast<uint32_t>(rows / 16), token_ids, tokens);
   return launch_status("fused GEMM argmax reduction launch failed");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused head.  The per-(token, tile) argmax keys of
+// gfxinfer_launch_gfx950_i4_gemm_argmax live in this file-scope device array instead of
+// a caller workspace: 4 MiB, i.e. batch * ceil(rows / 16) <= 524288 keys (every LM head
+// up to 262144 rows at 32 tokens).  Each GPU holds its own copy until the process ends;
+// host code reaches it only through the address hipGetSymbolAddress returns on that
+// device (the array's name is a host-side stand-in, not a device address).  Every key
+// the reduction reads is written by the GEMM of the same call, so nothing needs to be
+// cleared between calls; calls that overlap on one GPU (concurrent streams) race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned long long scratch[1u << 19];
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_address[kScratchDevices] = {};
+
+// The calling thread's current device's copy of `scratch`, looked up on the first call
+// on that device (with it current) and kept.
+int32_t scratch_address(void** out) {
+  int device = 0;
+  if (auto e = hipGetDevice(&device); e != hipSuccess) return hip_fail(e, "hipGetDevice failed");
+  if (device < 0 || device >= kScratchDevices) {
+    return fail(GFXI_UNSUPPORTED, "device index beyond the allocation-free entry's table");
+  }
+  const std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (g_scratch_address[device] == nullptr) {
+    void* address = nullptr;
+    if (auto e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)); e != hipSuccess) {
+      return hip_fail(e, "address of the argmax key scratch array");
+    }
+    g_scratch_address[device] = address;
+  }
+  *out = g_scratch_address[device];
+  return ok();
+}
+
+}  // namespace
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc(
+    int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_weight_scales,
+    const uint8_t* packed_activations, const uint16_t* activation_scales, float* logits,
+    size_t rows, size_t columns, uint32_t batch, size_t argmax_rows, const uint32_t* token_ids,
+    uint32_t* tokens, void* stream) {
+  if (gfxinfer_gemm_argmax_workspace_bytes(rows, batch) > sizeof(scratch)) {
+    return fail(GFXI_INVALID_ARGUMENT, "allocation-free fused GEMM argmax holds at most 524288 keys "
+                                       "(batch * ceil(rows / 16)); use the workspace entry point");
+  }
+  void* keys = nullptr;
+  if (const int32_t status = scratch_address(&keys); status != GFXI_OK) return status;
+  return gfxinfer_launch_gfx950_i4_gemm_argmax(format, tiled_weights, tiled_weight_scales,
+                                               packed_activations, activation_scales, logits, rows,
+                                               columns, batch, argmax_rows, token_ids, keys,
+                                               sizeof(scratch), tokens, stream);
 }
 
 extern "C" int32_t gfxinfer_launch_gfx950_i8_gemm(int32_t format, const uint8_t* tiled_weights,

@@ -169,6 +169,18 @@ int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(int32_t format, const uint8_t* til
                                               void* workspace, size_t workspace_bytes,
                                               uint32_t* tokens, void* stream);
 
+/* No reference counterpart: gfxinfer_launch_gfx950_i4_gemm_argmax with no workspace
+ * argument, for callers that cannot allocate (code under hipGraph capture, serving loops
+ * or harnesses that forbid hipMalloc).  The argmax keys live in a library-owned 4 MiB
+ * device array per GPU, so batch * ceil(rows / 16) must not exceed 524288 (larger shapes
+ * return GFXI_INVALID_ARGUMENT); the entry allocates nothing.  Every call on a GPU shares
+ * that array: calls that overlap on one GPU (concurrent streams) race. */
+int32_t gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc(
+    int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_weight_scales,
+    const uint8_t* packed_activations, const uint16_t* activation_scales, float* logits,
+    size_t rows, size_t columns, uint32_t batch, size_t argmax_rows, const uint32_t* token_ids,
+    uint32_t* tokens, void* stream);
+
 /* lowbit_gemv.h:147-157 (launch_gfx12_i8_gemm): W{3,4}G128 x A8G128 -> fp32.
  * The reference accepts W2/W4 only; W3 x A8 is added here. */
 int32_t gfxinfer_launch_gfx950_i8_gemm(int32_t format, const uint8_t* tiled_weights,
