@@ -218,7 +218,77 @@ struct GemmArgs {
   // b / splits and writes fp32 plane `split` ([splits][batch][rows] per matrix); the
   // consumer sums the planes in plane order.  1 = one plane, the plain product.
   uint32_t splits;
+  // SwiGLU tail (matrix 0 = gate, matrix 1 = up, equal rows, one split): the workgroup
+  // that completes the last of the 16 tiles (8 gate + 8 up) of a 128-row group writes
+  // the A4 codes of fp16(silu(gate) * up) over that group, as silu_multiply_quantize_i4
+  // does.  group_counters[rows / 128] are zero at launch and left zero.
+  unsigned* group_counters;
+  uint8_t* swiglu_codes;   // [batch][rows / 2]
+  __half* swiglu_scales;   // [batch][rows / 128]
 };
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
+
+// Device-coherent (agent-scope relaxed atomic) stores and loads: on gfx950 they are
+// global stores / loads with the sc1 bit, written through to and read from the device's
+// coherence point instead of a per-XCD L2, so a workgroup on another XCD sees them
+// without an L2 write-back or invalidation (which a device-scope fence would do, for
+// the whole L2, in every workgroup).
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The SwiGLU + A4 step of one 128-row group (qwen_ops.hip:120-163, the arithmetic of
+// silu_multiply_kernel<true>): wave w of the finishing workgroup takes tokens w,
+// w + waves, ...; lane i the columns 2i, 2i + 1.  Every load of a pass of up to eight
+// tokens is issued before the first use.
+__device__ void swiglu_group(const GemmArgs& args, unsigned group, unsigned wave, unsigned waves,
+                             unsigned lane) {
+  constexpr unsigned kPass = 8;
+  const uint32_t rows = args.matrix[0].tiles * 16u;
+  const float* gate = static_cast<const float*>(args.matrix[0].output);
+  const float* up = static_cast<const float*>(args.matrix[1].output);
+  for (unsigned first = wave; first < args.batch; first += kPass * waves) {
+    float2 g[kPass], u[kPass];
+#pragma unroll
+    for (unsigned k = 0; k < kPass; ++k) {
+      const unsigned t = first + k * waves;
+      const std::size_t at = static_cast<std::size_t>(t < args.batch ? t : 0u) * rows + group * 128u + 2u * lane;
+      g[k].x = coherent_load(gate + at);
+      g[k].y = coherent_load(gate + at + 1);
+      u[k].x = coherent_load(up + at);
+      u[k].y = coherent_load(up + at + 1);
+    }
+#pragma unroll
+    for (unsigned k = 0; k < kPass; ++k) {
+      const unsigned t = first + k * waves;
+      if (t >= args.batch) break;  // wave-uniform
+      const __half p0 = to_half(silu(g[k].x) * u[k].x);
+      const __half p1 = to_half(silu(g[k].y) * u[k].y);
+      quantize_group_a4(p0, p1, args.swiglu_codes + static_cast<std::size_t>(t) * (rows / 2) + group * 64u,
+                        args.swiglu_scales + static_cast<std::size_t>(t) * (rows / 128) + group, lane);
+    }
+  }
+}
+
+// Arrival of the wave that stored `tiles_done` finished tiles of one 128-row group with
+// coherent stores: once those stores have completed, a device-scope counter counts the
+// group's tiles, and the wave that brings it to 16 reads the group with coherent loads
+// and runs its SwiGLU tail.  No wave waits for another workgroup; the workgroup's other
+// waves have already left.
+__device__ void swiglu_arrival(const GemmArgs& args, unsigned tile, unsigned tiles_done, unsigned lane) {
+  const unsigned group = tile / 8u;
+  __builtin_amdgcn_s_waitcnt(0);  // the coherent stores have completed
+  unsigned prev = 0u;
+  if (lane == 0) prev = atomicAdd(args.group_counters + group, tiles_done);
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  if (prev + tiles_done != 16u) return;
+  swiglu_group(args, group, 0u, 1u, lane);
+  if (lane == 0) atomicExch(args.group_counters + group, 0u);
+}
 
 // Canonical summation over K.  Every GEMM variant adds the int32 group partials the
 // same way, so an output depends only on (row, token, K, splits): not on the batch,
@@ -335,6 +405,76 @@ __host__ __device__ inline GemmLds gemm_lds_layout(uint32_t chunk_groups, uint32
   if (region < reduce) region = reduce;
   l.region = (region + 15u) & ~15u;
   return l;
+}
+
+// The LDS kernel's final step for one tile: the split's value from the range values in
+// LDS (several ranges) or registers, the fused argmax keys and the output rows.
+template <int GP, int NTB, bool HalfOut>
+__device__ __forceinline__ void gemm_store_tile(const GemmArgs& args, const GemmMatrix& matrix,
+                                                float (&total)[NTB][4], unsigned ranges, unsigned lane,
+                                                uint32_t results_offset, unsigned tile, unsigned split,
+                                                uint32_t rows) {
+  extern __shared__ __align__(16) uint8_t lds_all[];
+  constexpr unsigned TPAD = 16 / GP;
+  const unsigned n = lane & 15u, kb = lane >> 4;
+  const unsigned slot = n % TPAD, window = n / TPAD;
+  const uint32_t batch = args.batch;
+  if (ranges > 1) {
+    const float* results = reinterpret_cast<const float*>(lds_all + results_offset);
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total[t][r] = results[(t * 4 + r) * 64 + lane];
+    }
+    for (unsigned rg = 1; rg < ranges; ++rg) {
+#pragma unroll
+      for (int t = 0; t < NTB; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) total[t][r] += results[(rg * NTB * 4u + t * 4 + r) * 64 + lane];
+      }
+    }
+  }
+  if (args.argmax_keys != nullptr) {
+    // Fused greedy argmax: the best of the tile's 16 rows per token (rows 4kb+r of
+    // lanes n, n+16, n+32, n+48), one key per (token, tile).
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned long long key = argmax_key(total[t][r], tile * 16u + 4u * kb + r, args.argmax_rows);
+        best = key > best ? key : best;
+      }
+      unsigned long long other = __shfl_xor(best, 16);
+      best = other > best ? other : best;
+      other = __shfl_xor(best, 32);
+      best = other > best ? other : best;
+      const unsigned token = t * 16u + slot;
+      if (kb == 0 && window == 0 && token < batch) {
+        args.argmax_keys[static_cast<std::size_t>(token) * matrix.tiles + tile] = best;
+      }
+    }
+  }
+  if (window != 0 || matrix.output == nullptr) return;
+  const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
+#pragma unroll
+  for (int t = 0; t < NTB; ++t) {
+    if (t * 16u + slot >= batch) continue;
+    const std::size_t out =
+        plane + static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
+    if constexpr (HalfOut) {
+      __half* o = reinterpret_cast<__half*>(matrix.output) + out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = to_half(total[t][r]);
+    } else if (args.group_counters != nullptr) {  // read by another workgroup's SwiGLU tail
+      float* o = reinterpret_cast<float*>(matrix.output) + out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) coherent_store(o + r, total[t][r]);
+    } else {
+      float4 value = {total[t][0], total[t][1], total[t][2], total[t][3]};
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
+    }
+  }
 }
 
 // Workgroups of up to 16 waves (large K) for the 16-token variants; the
@@ -639,60 +779,13 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   if constexpr (Partials) return;
 
   if (ranges > 1) {
-    // The split's value: range values added in range order.
+    // The split's value: range values added in range order, by wave 0.
     __syncthreads();
     if (wave != 0) return;
-    const float* results = reinterpret_cast<const float*>(lds_all + layout.results_offset);
-#pragma unroll
-    for (int t = 0; t < NTB; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) total[t][r] = results[(t * 4 + r) * 64 + lane];
-    }
-    for (unsigned rg = 1; rg < ranges; ++rg) {
-#pragma unroll
-      for (int t = 0; t < NTB; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) total[t][r] += results[(rg * NTB * 4u + t * 4 + r) * 64 + lane];
-      }
-    }
   }
-  if (args.argmax_keys != nullptr) {
-    // Fused greedy argmax: the best of the tile's 16 rows per token (rows 4kb+r of
-    // lanes n, n+16, n+32, n+48), one key per (token, tile).
-#pragma unroll
-    for (int t = 0; t < NTB; ++t) {
-      unsigned long long best = 0ull;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const unsigned long long key = argmax_key(total[t][r], tile * 16u + 4u * kb + r, args.argmax_rows);
-        best = key > best ? key : best;
-      }
-      unsigned long long other = __shfl_xor(best, 16);
-      best = other > best ? other : best;
-      other = __shfl_xor(best, 32);
-      best = other > best ? other : best;
-      const unsigned token = t * 16u + slot;
-      if (kb == 0 && window == 0 && token < batch) {
-        args.argmax_keys[static_cast<std::size_t>(token) * matrix.tiles + tile] = best;
-      }
-    }
-  }
-  if (window != 0 || matrix.output == nullptr) return;
-  const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
-#pragma unroll
-  for (int t = 0; t < NTB; ++t) {
-    if (t * 16u + slot >= batch) continue;
-    const std::size_t out =
-        plane + static_cast<std::size_t>(t * 16u + slot) * rows + tile * 16u + 4u * kb;
-    if constexpr (HalfOut) {
-      __half* o = reinterpret_cast<__half*>(matrix.output) + out;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = to_half(total[t][r]);
-    } else {
-      float4 value = {total[t][0], total[t][1], total[t][2], total[t][3]};
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
-    }
-  }
+  gemm_store_tile<GP, NTB, HalfOut>(args, matrix, total, ranges, lane, layout.results_offset, tile, split,
+                                    rows);
+  if (args.group_counters != nullptr) swiglu_arrival(args, tile, 1u, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1039,25 +1132,27 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
   }  // ranges
   if constexpr (Partials) return;
   if (ranges > 1) {
-    // The split's value: range values added in range order.
+    // The split's value: range values added in range order, by wave 0.
     __syncthreads();
     if (wave != 0) return;
-    const float* results = reinterpret_cast<const float*>(lds_all);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < NTB; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) total[r][t][i] = results[((r * NTB + t) * 4 + i) * 64 + lane];
-    for (unsigned rg = 1; rg < ranges; ++rg) {
+    {
+      const float* results = reinterpret_cast<const float*>(lds_all);
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < NTB; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            total[r][t][i] += results[(((rg * R + r) * NTB + t) * 4 + i) * 64 + lane];
-          }
+          for (int i = 0; i < 4; ++i) total[r][t][i] = results[((r * NTB + t) * 4 + i) * 64 + lane];
+      for (unsigned rg = 1; rg < ranges; ++rg) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int t = 0; t < NTB; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              total[r][t][i] += results[(((rg * R + r) * NTB + t) * 4 + i) * 64 + lane];
+            }
+      }
     }
   }
   const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
@@ -1094,12 +1189,17 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
         __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = to_half(total[r][t][i]);
+      } else if (args.group_counters != nullptr) {  // read by another workgroup's SwiGLU tail
+        float* o = reinterpret_cast<float*>(matrix.output) + out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) coherent_store(o + i, total[r][t][i]);
       } else {
         float4 value = {total[r][t][0], total[r][t][1], total[r][t][2], total[r][t][3]};
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
       }
     }
   }
+  if (args.group_counters != nullptr) swiglu_arrival(args, tile0, valid, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1364,7 +1464,8 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
                    const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
                    uint32_t batch, bool half_out, hipStream_t stream,
                    unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0,
-                   uint32_t splits = 1) {
+                   uint32_t splits = 1, unsigned* group_counters = nullptr,
+                   uint8_t* swiglu_codes = nullptr, uint16_t* swiglu_scales = nullptr) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W2G128, W3G128 and W4G128");
   }
@@ -1422,6 +1523,9 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   args.groups = static_cast<uint32_t>(columns / kGroup);
   args.batch = batch;
   args.splits = splits;
+  args.group_counters = group_counters;
+  args.swiglu_codes = swiglu_codes;
+  args.swiglu_scales = reinterpret_cast<__half*>(swiglu_scales);
   if (tiles * splits > std::numeric_limits<uint32_t>::max() / 2) {
     return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " grid is too large");
   }
@@ -1632,6 +1736,24 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
   return gemm_entry("gfx950 fused INT4 GEMM", format, bindings, matrix_count, 4,
                     packed_activations, activation_scales, nullptr, columns, batch, false,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4(
+    int32_t format, const uint8_t* gate_weights, const uint16_t* gate_scales, const uint8_t* up_weights,
+    const uint16_t* up_scales, const uint8_t* packed_activations, const uint16_t* activation_scales,
+    float* gate_output, float* up_output, uint8_t* packed_output, uint16_t* output_scales, size_t rows,
+    size_t columns, uint32_t batch, uint32_t* group_counters, void* stream) {
+  if (gate_output == nullptr || up_output == nullptr || packed_output == nullptr ||
+      output_scales == nullptr || group_counters == nullptr || rows == 0 || rows % kGroup != 0 ||
+      !aligned(gate_output, 16) || !aligned(up_output, 16) || !aligned(group_counters, 4)) {
+    return fail(GFXI_INVALID_ARGUMENT, "fused gate/up GEMM + SwiGLU needs gate/up outputs, A4 outputs, "
+                                       "rows divisible by 128 and a counter per 128 rows");
+  }
+  const MatrixBinding bindings[2] = {{gate_weights, gate_scales, gate_output, rows},
+                                     {up_weights, up_scales, up_output, rows}};
+  return gemm_entry("fused gate/up GEMM + SwiGLU", format, bindings, 2, 4, packed_activations,
+                    activation_scales, nullptr, columns, batch, false, static_cast<hipStream_t>(stream),
+                    nullptr, 0, 1, group_counters, packed_output, output_scales);
 }
 
 extern "C" size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch) {

@@ -175,6 +175,9 @@ struct gfxinfer_session {
   std::size_t argmax_keys_bytes{0};
   std::size_t attention_workspace_bytes{0};
   uint32_t *selected{}, *draft_tokens{}, *verify_drafts{}, *result{}, *graph_seed{};
+  // A4 input of the down projection (SwiGLU output), apart from act_codes
+  uint8_t* mlp_codes{};
+  uint16_t* mlp_scales{};
   int32_t* graph_forced{};
   uint64_t *graph_base_position{}, *graph_mtp_positions{};
   uint16_t *conv_states{}, *conv_snapshot{}, *conv_log{};
@@ -212,11 +215,13 @@ struct gfxinfer_session {
   }
   // [hidden, K] projections that feed a residual RMSNorm: split-K planes when the
   // plain grid would leave the GPU underfilled; the norm sums them.
-  int32_t gemm_planes(const Matrix& m, float* out, unsigned batch, uint32_t& planes) {
+  int32_t gemm_planes(const Matrix& m, float* out, unsigned batch, uint32_t& planes,
+                      const uint8_t* codes = nullptr, const uint16_t* scales = nullptr) {
     planes = gfxinfer_gemm_split_count(m.rows, m.columns, batch);
-    return gfxinfer_launch_gfx950_i4_gemm_split(m.format, m.weights, m.scales, act_codes,
-                                                act_scales, out, m.rows, m.columns, batch, planes,
-                                                stream);
+    return gfxinfer_launch_gfx950_i4_gemm_split(m.format, m.weights, m.scales,
+                                                codes != nullptr ? codes : act_codes,
+                                                scales != nullptr ? scales : act_scales, out, m.rows,
+                                                m.columns, batch, planes, stream);
   }
   int32_t gemm_fused(std::initializer_list<std::pair<const Matrix*, float*>> list,
                      unsigned batch) {
@@ -304,11 +309,14 @@ struct gfxinfer_session {
         input, mixer_update, mixer_planes, post_attention, L.post_norm, nullptr, act_codes,
         act_scales, H, batch, spec.rms_norm_epsilon, 1, stream));
     GFXI_TRY(trace_post(L, batch));
+    // The gate/up grid and SwiGLU -> A4 stay two launches: the one-launch form
+    // (gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4, same codes) measured slower on
+    // MI355X, its cross-workgroup completion costing more than the second launch.
     GFXI_TRY(gemm_fused({{&L.gate, gate_output}, {&L.up, up_output}}, batch));
-    GFXI_TRY(gfxinfer_launch_silu_multiply_quantize_i4(gate_output, up_output, act_codes,
-                                                       act_scales, I, batch, stream));
-    GFXI_TRY(trace_codes(L, false, I, batch));
-    GFXI_TRY(gemm_planes(L.down, mlp_update, batch, mlp_planes));
+    GFXI_TRY(gfxinfer_launch_silu_multiply_quantize_i4(gate_output, up_output, mlp_codes,
+                                                       mlp_scales, I, batch, stream));
+    GFXI_TRY(trace_codes(L, false, I, batch, mlp_codes, mlp_scales));
+    GFXI_TRY(gemm_planes(L.down, mlp_update, batch, mlp_planes, mlp_codes, mlp_scales));
     return gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
         post_attention, mlp_update, mlp_planes, output, next_norm, nullptr, act_codes, act_scales,
         H, batch, spec.rms_norm_epsilon, 1, stream);
@@ -395,15 +403,16 @@ struct gfxinfer_session {
     return (&L >= layers.data() && &L < layers.data() + layers.size()) ? &L - layers.data() : -1;
   }
   // The A4 codes and scales in act_codes / act_scales of `width` columns.
-  int32_t trace_codes(const Layer& L, bool mixer, std::size_t width, unsigned batch) {
+  int32_t trace_codes(const Layer& L, bool mixer, std::size_t width, unsigned batch,
+                      const uint8_t* codes_from = nullptr, const uint16_t* scales_from = nullptr) {
     const long i = layer_index(L);
     if (layer_trace == nullptr || i < 0) return ok();
     const TraceLayout t = trace_layout();
     const std::size_t W = mixer ? std::max(attn_width, gdn_value) : I;
     const std::size_t codes = (mixer ? t.mixer_codes : t.mlp_codes) + i * kMaxBlock * W / 2;
     const std::size_t scales = (mixer ? t.mixer_scales : t.mlp_scales) + i * kMaxBlock * (W / 128) * 2;
-    GFXI_TRY(trace_copy(codes, act_codes, batch * width / 2));
-    return trace_copy(scales, act_scales, batch * (width / 128) * 2);
+    GFXI_TRY(trace_copy(codes, codes_from != nullptr ? codes_from : act_codes, batch * width / 2));
+    return trace_copy(scales, scales_from != nullptr ? scales_from : act_scales, batch * (width / 128) * 2);
   }
   int32_t trace_post(const Layer& L, unsigned batch) {
     const long i = layer_index(L);
@@ -950,6 +959,8 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
         {"mixer_update", reinterpret_cast<void**>(&s->mixer_update), kMaxPlanes * B * s->H * 4},
         {"gate_output", reinterpret_cast<void**>(&s->gate_output), B * s->I * 4},
         {"up_output", reinterpret_cast<void**>(&s->up_output), B * s->I * 4},
+        {"mlp_codes", reinterpret_cast<void**>(&s->mlp_codes), B * s->I / 2},
+        {"mlp_scales", reinterpret_cast<void**>(&s->mlp_scales), B * (s->I / 128) * 2},
         {"mlp_update", reinterpret_cast<void**>(&s->mlp_update), kMaxPlanes * B * s->H * 4},
         {"logits", reinterpret_cast<void**>(&s->logits), B * s->V * 4},
         {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
