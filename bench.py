@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import subprocess
 import sys
@@ -127,14 +128,15 @@ def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16, windows
                 weight_bytes=sum(c.numel() for c in codes) + 2 * sum(s.numel() for s in scales))
 
 
-def verify_gemm_bench(batches=(5, 16, 32), copies=4, reps=20):
+def verify_gemm_bench(batches=(5, 16, 32), budget=640e6, reps=20):
     """one dense decoder block's projection set in W3A4 (q/k/v from
     hidden 5120 with 40 Q / 8 KV heads x 128, o, SwiGLU MLP 5120 -> 17408 -> 5120) at
     k + 1 = 5, 16, 32 rows, launched the way the verifier launches them (q/k/v and
     gate/up fused into one grid each, o and down as split-K planes), and the W4 LM head
     [151936, 5120] with the fused greedy argmax.  Each launch is timed alone under graph
-    replay over rotating weight copies (the block's weights x copies exceed the 256 MB
-    Infinity Cache); one JSON line per (projection, rows)."""
+    replay over rotating weight copies: every projection gets enough copies that one
+    pass over them reads about `budget` bytes, beyond the 256 MB Infinity Cache, as the
+    verifier's pass over the whole model does.  One JSON line per (projection, rows)."""
     import ctypes
     import torch
     import gfxinfer_amd as gx
@@ -153,7 +155,13 @@ def verify_gemm_bench(batches=(5, 16, 32), copies=4, reps=20):
     torch.manual_seed(0x5EED)
     mats = {"q": (w3, H, H), "k": (w3, 1024, H), "v": (w3, 1024, H), "o": (w3, H, H),
             "gate": (w3, I, H), "up": (w3, I, H), "down": (w3, H, I)}
-    weights = {name: matrix(f, r, c, copies) for name, (f, r, c) in mats.items()}
+    groups = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
+    copies = {}
+    for label, names in groups.items():
+        case_bytes = sum(algorithmic_bytes(mats[m][1], mats[m][2], 1) for m in names)
+        for m in names:
+            copies[m] = max(4, math.ceil(budget / case_bytes))
+    weights = {name: matrix(f, r, c, copies[name]) for name, (f, r, c) in mats.items()}
     head = matrix(w4, V, H, 1)[0]
     out = []
     stream = torch.cuda.Stream()
@@ -193,7 +201,7 @@ def verify_gemm_bench(batches=(5, 16, 32), copies=4, reps=20):
                  ("down", ("down",), lambda i, s: split("down", i, s)),
                  ("lm_head_argmax", None, lm_head)]
         for label, names, fn in cases:
-            n = copies if names is not None else 1
+            n = copies[names[0]] if names is not None else 1
             g = torch.cuda.CUDAGraph()
             with torch.cuda.stream(stream):
                 for i in range(n):

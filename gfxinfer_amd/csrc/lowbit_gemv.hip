@@ -813,9 +813,41 @@ __device__ __forceinline__ i32x4 expand_nibbles_masked(unsigned x0, unsigned x1,
   return r;
 }
 
+// Lane `source` of each 16-lane row, broadcast over its row (DPP row_newbcast); source
+// is a compile-time constant wherever the callers' loops are unrolled.
+template <int Source>
+__device__ __forceinline__ unsigned row_broadcast_lane(unsigned v) {
+  return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x150 + Source, 0xF, 0xF, false));
+}
+__device__ __forceinline__ unsigned row_broadcast(unsigned v, unsigned source) {
+  switch (source) {
+    case 0: return row_broadcast_lane<0>(v);
+    case 1: return row_broadcast_lane<1>(v);
+    case 2: return row_broadcast_lane<2>(v);
+    case 3: return row_broadcast_lane<3>(v);
+    case 4: return row_broadcast_lane<4>(v);
+    case 5: return row_broadcast_lane<5>(v);
+    case 6: return row_broadcast_lane<6>(v);
+    case 7: return row_broadcast_lane<7>(v);
+    case 8: return row_broadcast_lane<8>(v);
+    case 9: return row_broadcast_lane<9>(v);
+    case 10: return row_broadcast_lane<10>(v);
+    case 11: return row_broadcast_lane<11>(v);
+    case 12: return row_broadcast_lane<12>(v);
+    case 13: return row_broadcast_lane<13>(v);
+    case 14: return row_broadcast_lane<14>(v);
+    default: return row_broadcast_lane<15>(v);
+  }
+}
+
 // Waves per workgroup of the direct kernel: the stream sets of the canonical
 // summation need up to ~190 VGPRs at 32 tokens, so a workgroup stops at eight waves.
 constexpr unsigned kDirectMaxWaves = 8;
+
+template <int GP, int NTB, int R, bool HalfOut>
+__device__ __forceinline__ void direct_finish(const GemmArgs& args, const GemmMatrix& matrix,
+                                              float (&total)[R][NTB][4], unsigned ranges, unsigned lane,
+                                              unsigned tile0, unsigned valid, unsigned split);
 
 template <int Format, int ABits, int GP, int NTB, int CH, int R, bool HalfOut, bool Partials>
 __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kernel(GemmArgs args) {
@@ -865,7 +897,7 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
   const unsigned kb = lane >> 4;
   const unsigned slot = n % TPAD;
   const unsigned window = n / TPAD;
-  const unsigned w_voffset = lane * LB;
+  const unsigned w_lane = lane * LB;
   const unsigned ws_voffset = (window * 16u + 4u * kb) * 2u;
   // With one window (GP == 1) the activation loads run in quad-coalesced order
   // (lanes 4m..4m+3 read the 64 contiguous bytes of token m) and ds_bpermute routes
@@ -902,6 +934,20 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     unsigned short asreg[CH][NTB];
     unsigned wreg[R][CHG][WD];
     u32x2 wsreg[R][CH];
+    // GP == 1: the weight scales of the chunk's CH groups in one load per tile: lane
+    // 16 kb + n holds rows 4 kb .. 4 kb + 3 of group g0 + n, and group g0 + ci reaches
+    // every lane of row kb by a DPP row broadcast of lane ci (no lane loads a scale that
+    // another lane of its row also loads).
+    u32x2 wsrow[R];
+    if constexpr (GP == 1 && !Partials) {
+      static_assert(CHG <= 16, "one scale per lane of a 16-lane row");
+      const unsigned wsv = n < CHG && g0 + n < span.end ? n * 32u + kb * 8u : kOut;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        wsrow[r] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, static_cast<unsigned>(r) < valid ? wsv : kOut,
+                                                        r * groups * 32u + g0 * 32u, 0);
+      }
+    }
     // GP == 1: the activation scales of the chunk's CH groups, one load per token block
     // (a token's scales are contiguous over groups but may start at an odd half, so
     // the aligned dwords around them are loaded and shifted into place; entries past
@@ -969,6 +1015,8 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
       const unsigned pg = min(g0 + ci * GP, span.end - 1u);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
+        // a tile past the matrix (short last block) reads zeros and is never stored
+        const unsigned w_voffset = static_cast<unsigned>(r) < valid ? w_lane : kOut;
 #pragma unroll
         for (unsigned j = 0; j < GP; ++j) {
           const unsigned g_offset = r * tile_bytes + min(pg + j, span.end - 1u) * 64u * LB;
@@ -989,9 +1037,9 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
             wreg[r][ci * GP + j][3] = w[3];
           }
         }
-        if constexpr (!Partials) {
-          wsreg[r][ci] = __builtin_amdgcn_raw_buffer_load_b64(weight_scales, ws_voffset,
-                                                              r * groups * 32u + pg * 32u, 0);
+        if constexpr (!Partials && GP > 1) {
+          wsreg[r][ci] = __builtin_amdgcn_raw_buffer_load_b64(
+              weight_scales, static_cast<unsigned>(r) < valid ? ws_voffset : kOut, r * groups * 32u + pg * 32u, 0);
         }
       }
     }
@@ -1093,7 +1141,13 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
           }
         } else {
           // Dead tokens and a missing last group hold exact zeros (and zero scales).
-          const u32x2 pw = wsreg[r][ci];
+          u32x2 pw;
+          if constexpr (GP == 1) {
+            pw[0] = row_broadcast(wsrow[r][0], ci);
+            pw[1] = row_broadcast(wsrow[r][1], ci);
+          } else {
+            pw = wsreg[r][ci];
+          }
           float ws[4];
           ws[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] & 0xffffu)));
           ws[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(pw[0] >> 16)));
@@ -1135,24 +1189,40 @@ __global__ __launch_bounds__(kDirectMaxWaves * 64) void lowbit_gemm_direct_kerne
     // The split's value: range values added in range order, by wave 0.
     __syncthreads();
     if (wave != 0) return;
-    {
-      const float* results = reinterpret_cast<const float*>(lds_all);
+  }
+  direct_finish<GP, NTB, R, HalfOut>(args, matrix, total, ranges, lane, tile0, valid, split);
+}
+
+// The direct kernels' final step for R tiles (in the wave that holds the split's value
+// in `total`, or after the range values were written to LDS): the ordered sum of the
+// range values, the fused argmax keys, the output rows and the SwiGLU arrival.
+template <int GP, int NTB, int R, bool HalfOut>
+__device__ __forceinline__ void direct_finish(const GemmArgs& args, const GemmMatrix& matrix,
+                                              float (&total)[R][NTB][4], unsigned ranges, unsigned lane,
+                                              unsigned tile0, unsigned valid, unsigned split) {
+  extern __shared__ __align__(16) uint8_t lds_all[];
+  constexpr unsigned TPAD = 16 / GP;
+  const unsigned n = lane & 15u, kb = lane >> 4;
+  const unsigned slot = n % TPAD, window = n / TPAD;
+  const uint32_t batch = args.batch;
+  const uint32_t rows = matrix.tiles * 16u;
+  if (ranges > 1) {
+    const float* results = reinterpret_cast<const float*>(lds_all);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < NTB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) total[r][t][i] = results[((r * NTB + t) * 4 + i) * 64 + lane];
+    for (unsigned rg = 1; rg < ranges; ++rg) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < NTB; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) total[r][t][i] = results[((r * NTB + t) * 4 + i) * 64 + lane];
-      for (unsigned rg = 1; rg < ranges; ++rg) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int t = 0; t < NTB; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              total[r][t][i] += results[(((rg * R + r) * NTB + t) * 4 + i) * 64 + lane];
-            }
-      }
+          for (int i = 0; i < 4; ++i) {
+            total[r][t][i] += results[(((rg * R + r) * NTB + t) * 4 + i) * 64 + lane];
+          }
     }
   }
   const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
@@ -1375,21 +1445,35 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
          min_range_count(args.groups, args.splits), kDirectMaxWaves});
     hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), lds, stream, args);
   };
-  (void)total_tiles;
+  // Two row tiles per workgroup halve the activation reads per weight byte, but only
+  // pay off while the grid still has about two waves per SIMD (q/k/v and the split o
+  // projection at 16-32 tokens measured faster with one).
   const int forced = rowtiles_override();
+  bool pair = forced == 2;
+  if (forced == 0) {
+    uint64_t blocks = 0;
+    for (unsigned i = 0; i < 4; ++i) {
+      const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
+      if (used) blocks += (base_args.matrix[i].tiles + 1u) / 2u;
+    }
+    const unsigned waves = std::min({choose_waves(base_args.groups / base_args.splits, 1),
+                                     min_range_count(base_args.groups, base_args.splits), kDirectMaxWaves});
+    pair = blocks * base_args.splits * waves >= 2048u;
+  }
+  (void)total_tiles;
   if (batch <= 4) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 4, 1, 3, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 8) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 2, 1, 6, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 16) {
-    if (forced == 1) {
+    if (!pair) {
       go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 1, HalfOut, Partials>, 1, 1);
     } else {
       go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 5, 2, HalfOut, Partials>, 2, 1);
     }
   } else if constexpr (ABits == 8) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
-  } else if (forced == 1) {
+  } else if (!pair) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
   } else {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 5, 2, HalfOut, Partials>, 2, 2);
