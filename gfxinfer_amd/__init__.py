@@ -18,7 +18,9 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-LIBRARY = os.path.join(HERE, "libgfxinfer_amd.so")
+# GFXINFER_AMD_LIBRARY selects another build of the same library (the host-sanitizer
+# build of `make -C gfxinfer_amd sanitize`); the default is the in-tree build.
+LIBRARY = os.environ.get("GFXINFER_AMD_LIBRARY") or os.path.join(HERE, "libgfxinfer_amd.so")
 HEADERS = [os.path.join(ROOT, "include", "gfxinfer_amd.h"),
            os.path.join(ROOT, "include", "gfxinfer_runtime.h")]
 

@@ -237,14 +237,23 @@ int orc_quantize_group128(const float* weights, size_t rows, size_t columns, int
     uint8_t* destination = codes + row * row_bytes;
     for (size_t group = 0; group < groups; ++group) {
       float maximum = 0.0f;
+      int group_non_finite = 0;
       for (size_t offset = 0; offset < GROUP; ++offset) {
         const float value = source[group * GROUP + offset];
         if (!isfinite(value)) {
-          non_finite = 1;
+          group_non_finite = 1;
           continue;
         }
         const float magnitude = fabsf(value);
         if (magnitude > maximum) maximum = magnitude;
+      }
+      if (group_non_finite) {
+        /* The whole matrix is rejected below, so this group's codes and scale are never
+           read; the reference still converts the NaN quotients to int, which is undefined
+           behaviour in C, so the oracle leaves the group at zero codes and scale 1. */
+        non_finite = 1;
+        scales[row * groups + group] = 1.0f;
+        continue;
       }
       const float scale = choose_scale(source + group * GROUP, maximum, format);
       scales[row * groups + group] = scale;

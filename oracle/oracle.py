@@ -27,9 +27,11 @@ def build(reference: bool = False) -> None:
 
 
 def lib() -> ctypes.CDLL:
+    """liboracle.so, or the build GFXINFER_ORACLE_LIBRARY names (the sanitizer build of
+    `make -C oracle sanitize`)."""
     global _lib
     if _lib is None:
-        path = os.path.join(HERE, "liboracle.so")
+        path = os.environ.get("GFXINFER_ORACLE_LIBRARY") or os.path.join(HERE, "liboracle.so")
         if not os.path.exists(path):
             build()
         _lib = ctypes.CDLL(path)
