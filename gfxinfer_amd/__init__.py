@@ -131,6 +131,13 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_artifact_find": (I32, [P, ctypes.c_char_p, P]),
     "gfxinfer_artifact_bytes": (P, [P, ctypes.c_uint64, ctypes.c_uint64]),
     "gfxinfer_crc64_ecma": (ctypes.c_uint64, [ctypes.c_uint64, P, SZ]),
+    "gfxinfer_artifact_resource": (I32, [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(ctypes.c_uint64)]),
+    "gfxinfer_tokenizer_create": (I32, [P, SZ, ctypes.POINTER(P)]),
+    "gfxinfer_tokenizer_destroy": (None, [P]),
+    "gfxinfer_tokenizer_vocabulary_size": (SZ, [P]),
+    "gfxinfer_tokenizer_encode": (I32, [P, ctypes.c_char_p, SZ, P, SZ, ctypes.POINTER(SZ)]),
+    "gfxinfer_tokenizer_decode": (I32, [P, P, SZ, P, SZ, ctypes.POINTER(SZ)]),
+    "gfxinfer_render_chat_prompt": (I32, [ctypes.c_char_p, SZ, P, SZ, ctypes.POINTER(SZ)]),
     "gfxinfer_retile_gfx12_for_gfx950": (I32, [I32, P, SZ, P]),
     "gfxinfer_model_create_from_artifact": (I32, [P, ctypes.c_char_p, I32, I32, P]),
     "gfxinfer_model_write_artifact": (I32, [P, ctypes.c_char_p, ctypes.c_char_p, P, SZ]),

@@ -28,6 +28,7 @@
 #include <memory>
 #include <set>
 #include <string>
+#include <string_view>
 #include <unordered_map>
 #include <vector>
 
@@ -345,6 +346,27 @@ extern "C" const void* gfxinfer_artifact_bytes(const gfxinfer_artifact* artifact
                                                uint64_t bytes) {
   if (artifact == nullptr || !in_file(offset, bytes, artifact->bytes)) return nullptr;
   return artifact->map + offset;
+}
+
+extern "C" int32_t gfxinfer_artifact_resource(const gfxinfer_artifact* artifact, const char* name,
+                                              const void** data, uint64_t* bytes) {
+  if (artifact == nullptr || name == nullptr || data == nullptr || bytes == nullptr) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid artifact resource query");
+  }
+  *data = nullptr;
+  *bytes = 0;
+  // Resources are unquantized u8 tensors named "resources/..." (engine.cpp:32-34, 229-236).
+  const auto it = artifact->index.find(name);
+  if (std::string_view(name).rfind("resources/", 0) != 0 || it == artifact->index.end()) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string("no resource ") + name);
+  }
+  const gfxinfer_artifact_tensor& t = artifact->tensors[it->second];
+  if (t.quantization != 0 || t.dtype != 1) {
+    return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " is not an unquantized u8 resource");
+  }
+  *data = gfxinfer_artifact_bytes(artifact, t.data_offset, t.data_bytes);
+  *bytes = t.data_bytes;
+  return *data != nullptr || t.data_bytes == 0 ? ok() : fail(GFXI_CORRUPT_ARTIFACT, "resource lies outside the file");
 }
 
 // ---------------------------------------------------------------------------

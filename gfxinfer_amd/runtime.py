@@ -234,12 +234,88 @@ class Artifact:
         check(lib().gfxinfer_artifact_find(self._handle, name.encode(), ctypes.byref(t)))
         return t
 
+    def resource(self, name: str) -> bytes:
+        """Engine::resource (engine.cpp:229-236): an unquantized u8 "resources/..." tensor."""
+        data = ctypes.c_void_p()
+        n = ctypes.c_uint64()
+        check(lib().gfxinfer_artifact_resource(self._handle, name.encode(), ctypes.byref(data), ctypes.byref(n)))
+        return ctypes.string_at(data.value, n.value) if n.value else b""
+
     def payload(self, t: ArtifactTensor, auxiliary: bool = False) -> np.ndarray:
         offset, n = (t.aux_offset, t.aux_bytes) if auxiliary else (t.data_offset, t.data_bytes)
         ptr = lib().gfxinfer_artifact_bytes(self._handle, offset, n)
         if ptr is None:
             raise GfxinferError(1, "payload outside the artifact")
         return np.frombuffer((ctypes.c_uint8 * n).from_address(ptr), np.uint8).copy()
+
+
+class Tokenizer:
+    """Byte-level BPE of a tokenizer.json document (QwenTokenizer, tokenizer.h:17-32):
+    from_json / encode / decode / vocabulary_size, run by libgfxinfer_amd.so."""
+
+    def __init__(self, tokenizer_json: bytes):
+        data = bytes(tokenizer_json)
+        handle = ctypes.c_void_p()
+        buf = ctypes.create_string_buffer(data, len(data)) if data else None
+        check(lib().gfxinfer_tokenizer_create(buf, len(data), ctypes.byref(handle)))
+        self._handle = handle
+        _LIVE_OTHERS.add(self)
+
+    @classmethod
+    def from_file(cls, path: str) -> "Tokenizer":
+        with open(path, "rb") as f:
+            return cls(f.read())
+
+    def close(self):
+        if getattr(self, "_handle", None) is not None:
+            lib().gfxinfer_tokenizer_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def vocabulary_size(self) -> int:
+        return int(lib().gfxinfer_tokenizer_vocabulary_size(self._handle))
+
+    def encode(self, text: str) -> list[int]:
+        raw = text.encode("utf-8")
+        count = ctypes.c_size_t()
+        capacity = len(raw) + 16  # at most one id per byte, plus added tokens
+        ids = np.empty(capacity, np.uint32)
+        check(lib().gfxinfer_tokenizer_encode(self._handle, raw, len(raw), ids.ctypes.data, capacity,
+                                              ctypes.byref(count)))
+        if count.value > capacity:
+            ids = np.empty(count.value, np.uint32)
+            check(lib().gfxinfer_tokenizer_encode(self._handle, raw, len(raw), ids.ctypes.data, count.value,
+                                                  ctypes.byref(count)))
+        return [int(i) for i in ids[:count.value]]
+
+    def decode_bytes(self, ids) -> bytes:
+        arr = np.ascontiguousarray(np.asarray(list(ids), dtype=np.int64).astype(np.uint32))
+        length = ctypes.c_size_t()
+        check(lib().gfxinfer_tokenizer_decode(self._handle, arr.ctypes.data if arr.size else None, arr.size,
+                                              None, 0, ctypes.byref(length)))
+        out = ctypes.create_string_buffer(max(length.value, 1))
+        check(lib().gfxinfer_tokenizer_decode(self._handle, arr.ctypes.data if arr.size else None, arr.size,
+                                              out, length.value, ctypes.byref(length)))
+        return out.raw[:length.value]
+
+    def decode(self, ids) -> str:
+        return self.decode_bytes(ids).decode("utf-8", errors="replace")
+
+
+def render_chat_prompt(prompt: str) -> str:
+    """The generate command's chat rendering (cli/main.cpp:1037-1039)."""
+    raw = prompt.encode("utf-8")
+    length = ctypes.c_size_t()
+    check(lib().gfxinfer_render_chat_prompt(raw, len(raw), None, 0, ctypes.byref(length)))
+    out = ctypes.create_string_buffer(length.value)
+    check(lib().gfxinfer_render_chat_prompt(raw, len(raw), out, length.value, ctypes.byref(length)))
+    return out.raw[:length.value].decode("utf-8")
 
 
 def crc64_ecma(data: bytes, state: int = 0) -> int:

@@ -157,6 +157,11 @@ int32_t gfxinfer_artifact_find(const gfxinfer_artifact* artifact, const char* na
 /* ArtifactView::data / auxiliary (artifact.cpp:419-425): `bytes` bytes of the mapped
  * file at `offset`, or NULL outside the file. */
 const void* gfxinfer_artifact_bytes(const gfxinfer_artifact* artifact, uint64_t offset, uint64_t bytes);
+/* Engine::resource (engine.h:90-91, engine.cpp:229-236): the bytes of an unquantized u8
+ * tensor named "resources/..." (for example "resources/tokenizer.json"), valid until the
+ * artifact is closed.  GFXI_INVALID_ARGUMENT when there is no such resource. */
+int32_t gfxinfer_artifact_resource(const gfxinfer_artifact* artifact, const char* name, const void** data,
+                                   uint64_t* bytes);
 /* crc64_ecma_update (artifact.cpp:191-213). */
 uint64_t gfxinfer_crc64_ecma(uint64_t state, const void* bytes, size_t count);
 
@@ -335,6 +340,34 @@ int32_t gfxinfer_session_generate(gfxinfer_session* session, const uint32_t* pro
                                   size_t prompt_count, const gfxinfer_generate_config* config,
                                   uint32_t* output, size_t* output_count,
                                   gfxinfer_generate_stats* stats);
+
+/* ---- Tokenizer and chat prompt (tokenizer.h, tokenizer.cpp; cli/main.cpp) ----------
+ * Byte-level BPE over a tokenizer.json document: NFC normalization, the Qwen pre-token
+ * pattern, the GPT-2 byte alphabet and ranked merges, with added tokens matched in the raw
+ * text.  Sizes are in bytes of UTF-8 (text) or in ids; an output buffer that is too small
+ * receives a prefix and the full size is still returned, so a caller can retry. */
+typedef struct gfxinfer_tokenizer gfxinfer_tokenizer;
+
+/* QwenTokenizer::from_json (tokenizer.h:19-20, tokenizer.cpp:174-248).  Ids of the
+ * vocabulary and the added tokens must cover 0 .. N-1; merges are "left right" strings or
+ * [left, right] pairs.  GFXI_CORRUPT_ARTIFACT for a malformed document. */
+int32_t gfxinfer_tokenizer_create(const void* json, size_t bytes, gfxinfer_tokenizer** out);
+void gfxinfer_tokenizer_destroy(gfxinfer_tokenizer* tokenizer);
+/* QwenTokenizer::vocabulary_size (tokenizer.h:25). */
+size_t gfxinfer_tokenizer_vocabulary_size(const gfxinfer_tokenizer* tokenizer);
+/* QwenTokenizer::encode (tokenizer.h:23-24, tokenizer.cpp:277-357): writes
+ * min(count, capacity) ids and sets *count to the number of ids of the text. */
+int32_t gfxinfer_tokenizer_encode(const gfxinfer_tokenizer* tokenizer, const char* text, size_t length,
+                                  uint32_t* ids, size_t capacity, size_t* count);
+/* QwenTokenizer::decode (tokenizer.h:21-22, tokenizer.cpp:250-275): writes
+ * min(length, capacity) bytes (no terminator) and sets *length to the decoded size.
+ * GFXI_INVALID_ARGUMENT for an id outside the vocabulary. */
+int32_t gfxinfer_tokenizer_decode(const gfxinfer_tokenizer* tokenizer, const uint32_t* ids, size_t count,
+                                  char* text, size_t capacity, size_t* length);
+/* The generate command's chat rendering (cli/main.cpp:1037-1039): one user turn and an
+ * opened assistant turn with an empty thinking block. */
+int32_t gfxinfer_render_chat_prompt(const char* prompt, size_t length, char* text, size_t capacity,
+                                    size_t* rendered_length);
 
 #ifdef __cplusplus
 }
