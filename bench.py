@@ -417,7 +417,7 @@ def _matrix_bytes(model, names):
     return total
 
 
-def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026):
+def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates=True):
     """Full synthetic 27B-shaped model: hipGraph-captured MTP chain +
     64-layer verifier of depth D, forced seeded 85 % Bernoulli acceptance, rollback or
     state swap per round.  Emitted tok/s = sum(accepted + 1) / time, verified tok/s =
@@ -465,7 +465,8 @@ def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026):
                 "weight_gbs": round(round_bytes * n / elapsed / 1e9, 1),
                 "weight_frac_of_hbm_peak": round(round_bytes * n / elapsed / 1e9 / HBM_PEAK_GBS, 4),
             }
-        results.update(reference_bench_rates(model, spec))
+        if reference_rates:
+            results.update(reference_bench_rates(model, spec))
     finally:
         model.close()
     return {"model_weight_bytes": verifier_bytes + proposal_bytes, "create_s": round(create_s, 3),
@@ -698,6 +699,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--verify-rounds", type=int, default=60)
+    ap.add_argument("--no-reference-rates", action="store_true",
+                    help="skip the verifier-only block_step and proposal-only rates (a round profile "
+                         "then ends with the last round)")
     ap.add_argument("--verify-depths", default="4,8,16,31",
                     help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -795,7 +799,8 @@ def main():
                 "back-to-back graph launches, so they also hold the dispatch gap between launches")
     if not args.no_verify:
         depths = tuple(int(d) for d in args.verify_depths.split(",") if d)
-        out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds)
+        out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds,
+                                     reference_rates=not args.no_reference_rates)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
