@@ -422,6 +422,65 @@ constexpr unsigned kGdnD = 128;      // head size (both key and value)
 constexpr unsigned kGdnCols = 16;    // state columns per workgroup
 constexpr unsigned kGdnMaxTokens = 32;
 
+// The gated delta rule over a window for one lane (k-slice ks: state rows ks*8 ..
+// ks*8+7 of column `col`, held in S): per token S = S * decay; memory = sum_i S_i k_i
+// (an fmaf chain over the lane's rows, then the 16-lane xor tree); delta = (v - memory)
+// * beta; S = fmaf(k, delta, S); o = the same chain and tree over S_i q_i.  Lane ks == 0
+// writes o (and delta to the log).  Every LDS operand of token t + 1 (its key and query
+// slices, value, decay and beta) is read while token t computes, and the loop body is
+// unrolled by two so the hand-over costs no register moves.  The arithmetic per token
+// does not depend on the window length, so a window equals the same tokens one by one.
+__device__ __forceinline__ void gdn_scan(float (&S)[8], const float (*kn)[kGdnD], const float (*qn)[kGdnD],
+                                         const float (*vv)[kGdnCols], const float* decay_s,
+                                         const float* beta_s, unsigned T, unsigned ks, unsigned col,
+                                         float* mixed, float* delta_log, std::size_t value_elements,
+                                         std::size_t out_column) {
+  struct Operands {
+    float k[8], q[8], value, decay, beta;
+  };
+  auto fetch = [&](Operands& o, unsigned t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o.k[i] = kn[t][ks * 8 + i];
+      o.q[i] = qn[t][ks * 8 + i];
+    }
+    o.value = vv[t][col];
+    o.decay = decay_s[t];
+    o.beta = beta_s[t];
+  };
+  auto step = [&](const Operands& o, unsigned t) __attribute__((always_inline)) {
+    float memory = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = S[i] * o.decay;
+      memory = fmaf(S[i], o.k[i], memory);
+    }
+    memory = row16_sum(memory);
+    const float delta = (o.value - memory) * o.beta;
+    float out = 0.0F;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      S[i] = fmaf(o.k[i], delta, S[i]);
+      out = fmaf(S[i], o.q[i], out);
+    }
+    out = row16_sum(out);
+    if (ks == 0) {
+      mixed[static_cast<std::size_t>(t) * value_elements + out_column] = out;
+      if (delta_log != nullptr) delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
+    }
+  };
+  Operands a, b;
+  fetch(a, 0);
+  unsigned t = 0;
+  for (; t + 1 < T; t += 2) {
+    fetch(b, t + 1);
+    step(a, t);
+    fetch(a, t + 2 < T ? t + 2 : t + 1);
+    step(b, t + 1);
+  }
+  if (t < T) step(a, t);
+}
+
 struct GdnArgs {
   const __half* qkv;        // conv output [T][2*Hk*D + Hv*D]
   const float* a;           // [T][Hv]
@@ -519,37 +578,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs args) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
   const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
-
-  for (unsigned t = 0; t < T; ++t) {
-    const float decay = decay_s[t], beta = beta_s[t];
-    float kv[8], qv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kv[i] = kn[t][ks * 8 + i];
-      qv[i] = qn[t][ks * 8 + i];
-    }
-    float memory = 0.0F;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      S[i] = S[i] * decay;
-      memory = fmaf(S[i], kv[i], memory);
-    }
-    memory = row16_sum(memory);
-    const float delta = (vv[t][col] - memory) * beta;
-    float o = 0.0F;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      S[i] = fmaf(kv[i], delta, S[i]);
-      o = fmaf(S[i], qv[i], o);
-    }
-    o = row16_sum(o);
-    if (ks == 0) {
-      args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
-      if (args.delta_log != nullptr) {
-        args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
-      }
-    }
-  }
+  gdn_scan(S, kn, qn, vv, decay_s, beta_s, T, ks, col, args.mixed, args.delta_log, value_elements, out_column);
 
   // Epilogue: state back through the LDS tile, row-contiguous stores.
   __syncthreads();
@@ -772,8 +801,7 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   }
   __syncthreads();
 
-  // Stage 4: the recurrence (gdn_recurrent_kernel), on waves 0-3; each token's key
-  // and query slices are read from LDS one token ahead.
+  // Stage 4: the recurrence (gdn_scan, as gdn_recurrent_kernel), on waves 0-3.
   const unsigned ks = lane & 15u;
   const unsigned col = wave * 4u + (lane >> 4);
   const bool recurrent = wave < kWindowRecurrenceWaves;
@@ -782,48 +810,8 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
 #pragma unroll
     for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
     const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
-    float kv_next[8], qv_next[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kv_next[i] = kn[0][ks * 8 + i];
-      qv_next[i] = qn[0][ks * 8 + i];
-    }
-    for (unsigned t = 0; t < T; ++t) {
-      const float decay = decay_s[t], beta = beta_s[t];
-      float kv[8], qv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kv[i] = kv_next[i];
-        qv[i] = qv_next[i];
-      }
-      const unsigned tn = t + 1 < T ? t + 1 : t;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kv_next[i] = kn[tn][ks * 8 + i];
-        qv_next[i] = qn[tn][ks * 8 + i];
-      }
-      float memory = 0.0F;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        S[i] = S[i] * decay;
-        memory = fmaf(S[i], kv[i], memory);
-      }
-      memory = row16_sum(memory);
-      const float delta = (vv[t][col] - memory) * beta;
-      float o = 0.0F;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        S[i] = fmaf(kv[i], delta, S[i]);
-        o = fmaf(S[i], qv[i], o);
-      }
-      o = row16_sum(o);
-      if (ks == 0) {
-        args.mixed[static_cast<std::size_t>(t) * value_elements + out_column] = o;
-        if (args.delta_log != nullptr) {
-          args.delta_log[static_cast<std::size_t>(t) * value_elements + out_column] = delta;
-        }
-      }
-    }
+    gdn_scan(S, kn, qn, vv, decay_s, beta_s, T, ks, col, args.mixed, args.delta_log, value_elements,
+             out_column);
   }  // recurrent
   __syncthreads();
   if (recurrent) {
