@@ -76,6 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_debug_stream_read": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled_indirect": (I32, [I32, P, P, P, P, SZ, SZ, P]),
+    "gfxinfer_launch_lowbit_row_gather_tiled_batch": (I32, [I32, P, P, P, P, P, P, U32, SZ, SZ, P]),
     "gfxinfer_launch_rms_norm": (I32, [P, P, P, SZ, F32, I32, P]),
     "gfxinfer_launch_rms_norm_batch": (I32, [P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_residual_add_rms_norm_batch": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
@@ -279,6 +280,16 @@ def debug_stream_read(data, nbytes, sink, workgroups, stream=None):
 
 def launch_row_gather_tiled(fmt, w, ws, out, row, rows, columns, stream=None):
     check(lib().gfxinfer_launch_lowbit_row_gather_tiled(fmt, _p(w), _p(ws), _p(out), row, rows, columns, _stream(stream)))
+
+
+def launch_row_gather_tiled_batch(fmt, w, ws, out, host_rows, first_row, rest_rows, count, rows, columns,
+                                  stream=None):
+    """host_rows: a sequence of ints or None; first_row / rest_rows: device uint32 tensors or None."""
+    array = (ctypes.c_uint32 * count)(*host_rows) if host_rows is not None else None
+    host = ctypes.cast(array, ctypes.c_void_p) if array is not None else None
+    check(lib().gfxinfer_launch_lowbit_row_gather_tiled_batch(fmt, _p(w), _p(ws), _p(out), host, _p(first_row),
+                                                              _p(rest_rows), count, rows, columns,
+                                                              _stream(stream)))
 
 
 def launch_row_gather_tiled_indirect(fmt, w, ws, out, row_ptr, rows, columns, stream=None):

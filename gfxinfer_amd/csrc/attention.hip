@@ -64,32 +64,13 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   const unsigned group = a.q_heads / a.kv_heads;
   const unsigned rows = group * a.tokens;
 
-  // Stage K [pos][d] and V^T [d][pos] for the split's positions (zeros past the
-  // last visible position or the cache capacity).
-  const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
-  for (unsigned i = tid; i < kSplit * (kD / 8); i += blockDim.x) {
-    const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
-    const uint64_t pos = p0 + p;
-    u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-    if (pos < limit) {
-      const std::size_t at = (pos * a.kv_heads + hk) * kD + d8;
-      kv = *reinterpret_cast<const u32x4*>(a.key_cache + at);
-      vv = *reinterpret_cast<const u32x4*>(a.value_cache + at);
-    }
-    *reinterpret_cast<u32x4*>(&ks[p][d8]) = kv;
-    const _Float16* v = reinterpret_cast<const _Float16*>(&vv);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vt[d8 + e][p] = v[e];
-  }
-  __syncthreads();
-
   const unsigned m = lane & 15u, kb = lane >> 4;
   const unsigned row_tiles = (rows + 15) / 16;
-  for (unsigned rt = wave; rt < row_tiles; rt += 4) {
-    // Q operand rows (row = t * group + g -> head hk*group + g of token t).
+  // The Q operand of row tile rt (row = t * group + g -> head hk*group + g of token t),
+  // zeros past the last row.
+  auto load_q = [&](unsigned rt, h8 (&q)[4]) __attribute__((always_inline)) {
     const unsigned qrow = rt * 16 + m;
-    h8 q[4];
-    if (qrow < rows) {
+    if (rt < row_tiles && qrow < rows) {
       const unsigned t = qrow / group, g = qrow - t * group;
       const __half* src = a.query + (static_cast<std::size_t>(t) * a.q_heads + hk * group + g) * kD + 8 * kb;
 #pragma unroll
@@ -98,6 +79,49 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) q[s] = h8{};
     }
+  };
+
+  // Stage K [pos][d] and V^T [d][pos] for the split's positions (zeros past the
+  // last visible position or the cache capacity).  Every K/V load of the split and the
+  // wave's first Q tile are issued before the first LDS write (one memory latency).
+  constexpr unsigned kThreads = 256;
+  constexpr unsigned kStage = kSplit * (kD / 8) / kThreads;  // 16-byte K and V loads per thread
+  const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
+  // Positions past the limit load position p0 (always valid: p0 < limit) and are
+  // zeroed when written, so no load waits on a branch.
+  u32x4 kr[kStage], vr[kStage];
+#pragma unroll
+  for (unsigned u = 0; u < kStage; ++u) {
+    const unsigned i = tid + u * kThreads;
+    const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
+    const uint64_t pos = p0 + p < limit ? p0 + p : p0;
+    const std::size_t at = (pos * a.kv_heads + hk) * kD + d8;
+    kr[u] = *reinterpret_cast<const u32x4*>(a.key_cache + at);
+    vr[u] = *reinterpret_cast<const u32x4*>(a.value_cache + at);
+  }
+  h8 q_next[4];
+  load_q(wave, q_next);
+#pragma unroll
+  for (unsigned u = 0; u < kStage; ++u) {
+    const unsigned i = tid + u * kThreads;
+    const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
+    if (p0 + p >= limit) {
+      kr[u] = u32x4{0, 0, 0, 0};
+      vr[u] = u32x4{0, 0, 0, 0};
+    }
+    *reinterpret_cast<u32x4*>(&ks[p][d8]) = kr[u];
+    const _Float16* v = reinterpret_cast<const _Float16*>(&vr[u]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt[d8 + e][p] = v[e];
+  }
+  __syncthreads();
+
+  for (unsigned rt = wave; rt < row_tiles; rt += 4) {
+    // This tile's Q operand was loaded one tile ahead; the next tile's goes out now.
+    h8 q[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) q[s] = q_next[s];
+    load_q(rt + 4, q_next);
     // S = Q K^T for the split's positions (kTiles tiles of 16).
     f4 sc[kTiles];
 #pragma unroll

@@ -1276,14 +1276,26 @@ __device__ __forceinline__ void direct_finish(const GemmArgs& args, const GemmMa
 // Tiled row gather (lowbit_gemv.hip:191-231): out[c] = fp16(w(row,c) * ws(row,g)).
 // ---------------------------------------------------------------------------
 
+// Rows of a gather: row j is first[0] (device) or host[0] for j == 0, then rest[j - 1]
+// (device) or host[j]; up to kGatherRows rows per launch, one grid row each.
+constexpr unsigned kGatherRows = 32;
+struct GatherRows {
+  uint32_t host[kGatherRows];
+  const uint32_t* first;
+  const uint32_t* rest;
+};
+
 template <int Format>
 __global__ __launch_bounds__(256) void row_gather_kernel(
     const uint8_t* __restrict__ weights, const __half* __restrict__ scales,
-    __half* __restrict__ output, std::size_t row, const uint32_t* __restrict__ indirect_row,
-    std::size_t rows, std::size_t columns) {
+    __half* __restrict__ output, GatherRows ids, std::size_t rows, std::size_t columns) {
   const std::size_t column = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (column >= columns) return;
-  if (indirect_row != nullptr) row = *indirect_row;
+  const unsigned j = blockIdx.y;
+  std::size_t row = ids.host[j];
+  if (j == 0 && ids.first != nullptr) row = *ids.first;
+  if (j != 0 && ids.rest != nullptr) row = ids.rest[j - 1];
+  output += static_cast<std::size_t>(j) * columns;
   if (row >= rows) {
     output[column] = __float2half(0.0F);
     return;
@@ -1656,29 +1668,28 @@ int32_t quantize_activation_entry(int bits, const uint16_t* input, void* output,
 }
 
 int32_t row_gather_entry(int32_t format, const uint8_t* weights, const uint16_t* scales,
-                         uint16_t* output, std::size_t row, const uint32_t* indirect,
-                         std::size_t rows, std::size_t columns, hipStream_t stream) {
+                         uint16_t* output, const GatherRows& ids, unsigned count, std::size_t rows,
+                         std::size_t columns, hipStream_t stream) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, "tiled row gather supports W2G128, W3G128 and W4G128");
   }
   if (weights == nullptr || scales == nullptr || output == nullptr || rows == 0 ||
-      rows % 16 != 0 || columns == 0 || columns % kGroup != 0 ||
-      (indirect == nullptr && row >= rows)) {
+      rows % 16 != 0 || columns == 0 || columns % kGroup != 0 || count == 0 || count > kGatherRows) {
     return fail(GFXI_INVALID_ARGUMENT, "invalid tiled low-bit row gather arguments");
   }
   constexpr unsigned threads = 256;
-  const dim3 grid(static_cast<unsigned>((columns + threads - 1) / threads));
+  const dim3 grid(static_cast<unsigned>((columns + threads - 1) / threads), count);
   const auto* ws = reinterpret_cast<const __half*>(scales);
   auto* out = reinterpret_cast<__half*>(output);
   if (format == GFXI_W2G128) {
     hipLaunchKernelGGL(row_gather_kernel<GFXI_W2G128>, grid, dim3(threads), 0, stream, weights, ws,
-                       out, row, indirect, rows, columns);
+                       out, ids, rows, columns);
   } else if (format == GFXI_W3G128) {
     hipLaunchKernelGGL(row_gather_kernel<GFXI_W3G128>, grid, dim3(threads), 0, stream, weights, ws,
-                       out, row, indirect, rows, columns);
+                       out, ids, rows, columns);
   } else {
     hipLaunchKernelGGL(row_gather_kernel<GFXI_W4G128>, grid, dim3(threads), 0, stream, weights, ws,
-                       out, row, indirect, rows, columns);
+                       out, ids, rows, columns);
   }
   return launch_status("tiled low-bit row gather launch failed");
 }
@@ -1957,7 +1968,10 @@ extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled(int32_t format,
                                                            uint16_t* output, size_t row,
                                                            size_t rows, size_t columns,
                                                            void* stream) {
-  return row_gather_entry(format, tiled_weights, tiled_scales, output, row, nullptr, rows, columns,
+  if (row >= rows) return fail(GFXI_INVALID_ARGUMENT, "invalid tiled low-bit row gather arguments");
+  GatherRows ids{};
+  ids.host[0] = static_cast<uint32_t>(row);
+  return row_gather_entry(format, tiled_weights, tiled_scales, output, ids, 1, rows, columns,
                           static_cast<hipStream_t>(stream));
 }
 
@@ -1965,7 +1979,29 @@ extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled_indirect(
     int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_scales, uint16_t* output,
     const uint32_t* row, size_t rows, size_t columns, void* stream) {
   if (row == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect row pointer is null");
-  return row_gather_entry(format, tiled_weights, tiled_scales, output, 0, row, rows, columns,
+  GatherRows ids{};
+  ids.first = row;
+  return row_gather_entry(format, tiled_weights, tiled_scales, output, ids, 1, rows, columns,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled_batch(
+    int32_t format, const uint8_t* tiled_weights, const uint16_t* tiled_scales, uint16_t* output,
+    const uint32_t* host_rows, const uint32_t* first_row, const uint32_t* rest_rows, uint32_t count,
+    size_t rows, size_t columns, void* stream) {
+  if (count == 0 || count > kGatherRows) {
+    return fail(GFXI_INVALID_ARGUMENT, "a batched row gather takes 1..32 rows");
+  }
+  if (host_rows == nullptr && (first_row == nullptr || (count > 1 && rest_rows == nullptr))) {
+    return fail(GFXI_INVALID_ARGUMENT, "rows without a host or device source");
+  }
+  GatherRows ids{};
+  if (host_rows != nullptr) {
+    for (uint32_t j = 0; j < count; ++j) ids.host[j] = host_rows[j];
+  }
+  ids.first = first_row;
+  ids.rest = rest_rows;
+  return row_gather_entry(format, tiled_weights, tiled_scales, output, ids, count, rows, columns,
                           static_cast<hipStream_t>(stream));
 }
 

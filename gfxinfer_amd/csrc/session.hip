@@ -251,15 +251,13 @@ struct gfxinfer_session {
         argmax_keys, argmax_keys_bytes, tokens, stream);
   }
 
-  int32_t gather(uint16_t* destination, uint32_t token, const uint32_t* indirect) {
-    if (indirect != nullptr) {
-      return gfxinfer_launch_lowbit_row_gather_tiled_indirect(
-          embedding.format, embedding.weights, embedding.scales, destination, indirect,
-          embedding.rows, embedding.columns, stream);
-    }
-    return gfxinfer_launch_lowbit_row_gather_tiled(embedding.format, embedding.weights,
-                                                   embedding.scales, destination, token,
-                                                   embedding.rows, embedding.columns, stream);
+  // Embedding rows of `count` tokens in one launch (row j at destination + j * H): token
+  // 0 from *first (device) or host[0], tokens j >= 1 from rest[j - 1] (device) or host[j].
+  int32_t gather_rows(uint16_t* destination, const uint32_t* host, const uint32_t* first,
+                      const uint32_t* rest, unsigned count) {
+    return gfxinfer_launch_lowbit_row_gather_tiled_batch(embedding.format, embedding.weights,
+                                                         embedding.scales, destination, host, first, rest,
+                                                         count, embedding.rows, embedding.columns, stream);
   }
 
   // Attention mixer of a block (qwen_runtime.cpp:432-474); input A4 codes ready.
@@ -439,10 +437,8 @@ struct gfxinfer_session {
   // qwen_runtime.cpp:546-640 enqueue_verifier_body: seed + D drafts (device ids).
   int32_t verifier(uint32_t seed, const uint32_t* device_seed, const uint32_t* drafts,
                    unsigned draft_count, const uint64_t* device_position) {
-    GFXI_TRY(gather(hidden_a, seed, device_seed));
-    for (unsigned i = 0; i < draft_count; ++i) {
-      GFXI_TRY(gather(hidden_a + (i + 1) * H, 0, drafts + i));
-    }
+    uint32_t host[kMaxBlock] = {seed};
+    GFXI_TRY(gather_rows(hidden_a, host, device_seed, drafts, draft_count + 1));
     return decoder_stack(draft_count + 1, device_position);
   }
 
@@ -473,7 +469,7 @@ struct gfxinfer_session {
   // cache entries at once: entry position + i from tokens[i] and conditioning row i
   // (mtp_conditioning).  Every kernel computes each row as the one-token path does.
   int32_t mtp_sync(const uint32_t* tokens, unsigned count, std::size_t position) {
-    for (unsigned i = 0; i < count; ++i) GFXI_TRY(gather(hidden_b + i * H, tokens[i], nullptr));
+    GFXI_TRY(gather_rows(hidden_b, tokens, nullptr, nullptr, count));
     GFXI_TRY(gfxinfer_launch_dual_rms_norm_concat_batch(hidden_b, mtp_pre_embedding_norm, mtp_conditioning,
                                                         mtp_pre_hidden_norm, mtp_concat, H, count,
                                                         spec.rms_norm_epsilon, 1, stream));
@@ -781,7 +777,7 @@ struct gfxinfer_session {
       }
     }
     const auto batch = static_cast<unsigned>(count);
-    for (unsigned i = 0; i < batch; ++i) GFXI_TRY(gather(hidden_a + i * H, tokens[i], nullptr));
+    GFXI_TRY(gather_rows(hidden_a, tokens, nullptr, nullptr, batch));
     GFXI_TRY(decoder_stack(batch, nullptr));
     // The windows wrote the advanced states into the snapshot buffers: keep them.
     std::swap(conv_states, conv_snapshot);

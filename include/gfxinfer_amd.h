@@ -239,6 +239,17 @@ int32_t gfxinfer_launch_lowbit_row_gather_tiled_indirect(int32_t format,
                                                          size_t rows, size_t columns,
                                                          void* stream);
 
+/* Rows 0..count-1 (count <= 32) of the two launchers above in one launch, row j written
+ * at output + j * columns: row 0 is *first_row when first_row is set, else
+ * host_rows[0]; row j >= 1 is rest_rows[j - 1] when rest_rows is set, else host_rows[j]
+ * (host_rows travel as kernel arguments).  Out-of-range rows yield zeros.  No reference
+ * counterpart: the reference gathers one row per launch (qwen_runtime.cpp:553-615). */
+int32_t gfxinfer_launch_lowbit_row_gather_tiled_batch(int32_t format, const uint8_t* tiled_weights,
+                                                      const uint16_t* tiled_scales, uint16_t* output,
+                                                      const uint32_t* host_rows, const uint32_t* first_row,
+                                                      const uint32_t* rest_rows, uint32_t count,
+                                                      size_t rows, size_t columns, void* stream);
+
 
 /* ---- decoder operators: src/kernels/qwen_ops.hip -------------------------- */
 

@@ -333,6 +333,27 @@ def test_row_gather(device, gx, orc, fmt):
     gx.launch_row_gather_tiled_indirect(fmt, dw, dws, out, idx, rows, cols)
     assert np.all(host(out, np.uint16) == 0)
 
+    # Batched gather: every row equals the one-row launch; host rows, a device first row
+    # with device rest rows (the verifier's seed + drafts), out-of-range rows are zeros.
+    def want_rows(ids):
+        return np.stack([_half(p["wint"][r].astype(np.float32) * np.repeat(ws[r], 128)) if r < rows
+                         else np.zeros(cols, np.uint16) for r in ids])
+    ids = [5, 63, 0, rows + 1, 17, 17, 40, 2]
+    many = empty((len(ids), cols), np.uint16)
+    say("batched row gather", fmt, len(ids))
+    gx.launch_row_gather_tiled_batch(fmt, dw, dws, many, ids, None, None, len(ids), rows, cols)
+    assert np.array_equal(host(many, np.uint16), want_rows(ids))
+    first, rest = dev(np.array([33], np.uint32)), dev(np.array(ids[1:], np.uint32))
+    gx.launch_row_gather_tiled_batch(fmt, dw, dws, many, [0] * len(ids), first, rest, len(ids), rows, cols)
+    assert np.array_equal(host(many, np.uint16), want_rows([33] + ids[1:]))
+    full = empty((32, cols), np.uint16)
+    ids32 = [(7 * j) % rows for j in range(32)]
+    gx.launch_row_gather_tiled_batch(fmt, dw, dws, full, ids32, None, None, 32, rows, cols)
+    assert np.array_equal(host(full, np.uint16), want_rows(ids32))
+    for count in (0, 33):
+        with pytest.raises(gx.GfxinferError):
+            gx.launch_row_gather_tiled_batch(fmt, dw, dws, full, None, first, rest, count, rows, cols)
+
 
 def _gemm_argmax(gx, fmt, p, rows, cols, batch, argmax_rows, ids=None, logits=True):
     ws_bytes = gx.lib().gfxinfer_gemm_argmax_workspace_bytes(rows, batch)
