@@ -39,9 +39,19 @@ __device__ float reference_square_sum(const __half* row, uint32_t elements, floa
   const unsigned t = threadIdx.x;
   float s = 0.0F;
   if (t < 256u) {
-    for (uint32_t i = t; i < elements; i += 256u) {
-      const float f = __half2float(row[i]);
-      s = fmaf(f, f, s);
+    // Eight LDS reads in flight per batch; the fmaf chain keeps index order.
+    constexpr unsigned kBatch = 8;
+    for (uint32_t i0 = t; i0 < elements; i0 += 256u * kBatch) {
+      float f[kBatch];
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) {
+        const uint32_t i = i0 + 256u * k;
+        f[k] = __half2float(row[i < elements ? i : 0u]);  // unconditional read, used if in range
+      }
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) {
+        if (i0 + 256u * k < elements) s = fmaf(f[k], f[k], s);
+      }
     }
   }
   s += __shfl_down(s, 16, 32);
@@ -128,7 +138,7 @@ constexpr uint32_t kNormFastMax = kNormSlots * 16u * 128u;
 // Rows longer than this do not fit the LDS row the reference-ordered sum reads (64 KB).
 constexpr std::size_t kNormMaxElements = 32768;
 
-template <bool Residual, bool Quantize, unsigned Slots, unsigned MaxPlanes>
+template <bool Residual, bool Quantize, unsigned Slots, unsigned MaxPlanes, bool ExactPlanes = false>
 __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     const __half* __restrict__ input, const float* __restrict__ update,
     __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
@@ -151,7 +161,7 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     if constexpr (Residual) {
 #pragma unroll
       for (unsigned p = 0; p < MaxPlanes; ++p) {
-        if (p < planes) {
+        if (ExactPlanes || p < planes) {
           upd[j][p] = *reinterpret_cast<const float2*>(update + p * plane_stride + base + at);
         }
       }
@@ -171,7 +181,7 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
         float2 u = upd[j][0];
 #pragma unroll
         for (unsigned p = 1; p < MaxPlanes; ++p) {
-          if (p < planes) {
+          if (ExactPlanes || p < planes) {
             u.x += upd[j][p].x;
             u.y += upd[j][p].y;
           }
@@ -1085,6 +1095,10 @@ void launch_norm(bool fast, unsigned per_wave_slots, uint32_t planes, dim3 block
       hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, 1>), dim3(batch),
                          block, 0, stream, in, update, ro, weight, out, codes, sc, e, epsilon, unit,
                          planes, plane_stride);
+    } else if (planes == 4) {  // the session's split-K plane count: loads without conditions
+      hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, Residual ? 4 : 1, true>),
+                         dim3(batch), block, 0, stream, in, update, ro, weight, out, codes, sc, e,
+                         epsilon, unit, planes, plane_stride);
     } else {
       hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots,
                                                Residual ? kNormMaxPlanes : 1>),
