@@ -690,11 +690,11 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
                                               channel(q * 4));
     }
   }
-  float a_in = 0.0F, b_in = 0.0F;
-  if (tid < T) {
-    a_in = args.a[static_cast<std::size_t>(tid) * args.value_heads + h];
-    b_in = args.b[static_cast<std::size_t>(tid) * args.value_heads + h];
-  }
+  // Token tid's a/b (token 0's for threads past the window: loaded, never used) and the
+  // head's dt_bias / A_log, unconditionally so that no load waits on a branch.
+  const std::size_t ab = static_cast<std::size_t>(tid < T ? tid : 0u) * args.value_heads + h;
+  const float a_in = args.a[ab], b_in = args.b[ab];
+  const uint16_t dt_bias = args.dt_bias[h], a_log = args.a_log[h];
   uint16_t wv[kChannelLoads][4];
   __half iv[kChannelLoads][4];
 #pragma unroll
@@ -750,9 +750,9 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   }
   // decay and beta per token (qwen_ops.hip:342-349).
   if (tid < T) {
-    const float a_value = a_in + bf16_to_float(args.dt_bias[h]);
+    const float a_value = a_in + bf16_to_float(dt_bias);
     const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
-    const float g = -expf(bf16_to_float(args.a_log[h])) * softplus;
+    const float g = -expf(bf16_to_float(a_log)) * softplus;
     const float decay = expf(g);
     decay_s[tid] = decay;
     beta_s[tid] = 1.0F / (1.0F + expf(-b_in));
@@ -850,11 +850,13 @@ __global__ __launch_bounds__(256) void gdn_output_kernel(
   const unsigned lane = threadIdx.x & 63u;
   const uint32_t t = linear / value_heads, h = linear - t * value_heads;
   const std::size_t row = static_cast<std::size_t>(t) * value_heads * kGdnD + h * kGdnD;
+  // Every load before the first use: the mixed row, the gate row and the norm weights.
   const float2 o = *reinterpret_cast<const float2*>(mixed + row + 2 * lane);
-  const float inverse = rsqrtf(wave_sum(o.x * o.x + o.y * o.y) / static_cast<float>(kGdnD) + 1.0e-6F);
   const float2 g = *reinterpret_cast<const float2*>(z + row + 2 * lane);
-  const __half r0 = to_half(o.x * inverse * bf16_to_float(weight[2 * lane]) * silu(g.x));
-  const __half r1 = to_half(o.y * inverse * bf16_to_float(weight[2 * lane + 1]) * silu(g.y));
+  const uint32_t w2 = *reinterpret_cast<const uint32_t*>(weight + 2 * lane);
+  const float inverse = rsqrtf(wave_sum(o.x * o.x + o.y * o.y) / static_cast<float>(kGdnD) + 1.0e-6F);
+  const __half r0 = to_half(o.x * inverse * bf16_to_float(static_cast<uint16_t>(w2 & 0xffffu)) * silu(g.x));
+  const __half r1 = to_half(o.y * inverse * bf16_to_float(static_cast<uint16_t>(w2 >> 16)) * silu(g.y));
   if (output != nullptr) {
     output[row + 2 * lane] = r0;
     output[row + 2 * lane + 1] = r1;
@@ -986,10 +988,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   __half* out = (is_key ? a.key_output : a.query_output) + (static_cast<std::size_t>(t) * count + head) * D;
   const uint64_t base = a.indirect_position != nullptr ? *a.indirect_position : a.base_position;
   const float position = static_cast<float>(base + t);
+  // Every load before the first use: the head row, its norm weights and (for a key head
+  // with the cache append) the value row.
   const float x0 = in[lane], x1 = in[lane + 64];
+  const uint16_t w0 = w[lane], w1 = w[lane + 64];
+  const bool append = is_key && a.value_input != nullptr;
+  float value0 = 0.0F, value1 = 0.0F;
+  if (append) {
+    const float* value = a.value_input + (static_cast<std::size_t>(t) * count + head) * D;
+    value0 = value[lane];
+    value1 = value[lane + 64];
+  }
   const float inverse = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / static_cast<float>(D) + 1.0e-6F);
-  const float n0 = x0 * (inverse * (1.0F + bf16_to_float(w[lane])));
-  const float n1 = x1 * (inverse * (1.0F + bf16_to_float(w[lane + 64])));
+  const float n0 = x0 * (inverse * (1.0F + bf16_to_float(w0)));
+  const float n1 = x1 * (inverse * (1.0F + bf16_to_float(w1)));
   float v0 = n0;
   const unsigned half = a.rotary / 2;
   // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.
@@ -1005,13 +1017,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   const __half h0 = to_half(v0), h1 = to_half(n1);
   out[lane] = h0;
   out[lane + 64] = h1;
-  if (is_key && a.value_input != nullptr) {
+  if (append) {
     const std::size_t row = (static_cast<std::size_t>(base + t) * count + head) * D;
-    const float* value = a.value_input + (static_cast<std::size_t>(t) * count + head) * D;
     a.key_cache[row + lane] = h0;
     a.key_cache[row + lane + 64] = h1;
-    a.value_cache[row + lane] = to_half(value[lane]);
-    a.value_cache[row + lane + 64] = to_half(value[lane + 64]);
+    a.value_cache[row + lane] = to_half(value0);
+    a.value_cache[row + lane + 64] = to_half(value1);
   }
 }
 
