@@ -215,6 +215,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   if (linear >= a.tokens * a.q_heads) return;
   const unsigned lane = threadIdx.x & 63u;
   const uint32_t t = linear / a.q_heads, qh = linear - t * a.q_heads;
+  // The gate row first: it does not depend on the position.
+  const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
+  const float g_lo = g[2 * lane], g_hi = g[2 * lane + 1];
   const uint64_t count = base_count_of(a) + t;
   const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
   const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
@@ -239,18 +242,20 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
       mls[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
       v[k] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD);
     }
+    // No early exit: the loads above stay ahead of every use (splits past `used` are
+    // loaded again from split s0 and skipped here, in split order as before).
 #pragma unroll
     for (unsigned k = 0; k < kBatch; ++k) {
-      if (s0 + k >= used) break;
-      const float w = expf(mls[k].x - best);
-      total = fmaf(mls[k].y, w, total);
-      o0 = fmaf(v[k].x, w, o0);
-      o1 = fmaf(v[k].y, w, o1);
+      if (s0 + k < used) {
+        const float w = expf(mls[k].x - best);
+        total = fmaf(mls[k].y, w, total);
+        o0 = fmaf(v[k].x, w, o0);
+        o1 = fmaf(v[k].y, w, o1);
+      }
     }
   }
-  const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
-  const float g0 = 1.0F / (1.0F + expf(-g[2 * lane]));
-  const float g1 = 1.0F / (1.0F + expf(-g[2 * lane + 1]));
+  const float g0 = 1.0F / (1.0F + expf(-g_lo));
+  const float g1 = 1.0F / (1.0F + expf(-g_hi));
   __half* out = output + static_cast<std::size_t>(linear) * kD + 2 * lane;
   const __half h0 = to_half(o0 / total * g0), h1 = to_half(o1 / total * g1);
   out[0] = h0;

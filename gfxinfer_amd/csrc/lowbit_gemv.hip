@@ -1325,7 +1325,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_keys_kernel(
 #pragma unroll
     for (unsigned u = 0; u < kArgmaxLoads; ++u) {
       const uint32_t i = base + u * kArgmaxThreads + threadIdx.x;
-      k[u] = i < count ? row[i] : 0ull;
+      const unsigned long long key = row[i < count ? i : 0u];  // unconditional: no load waits on a branch
+      k[u] = i < count ? key : 0ull;
     }
 #pragma unroll
     for (unsigned u = 0; u < kArgmaxLoads; ++u) best = k[u] > best ? k[u] : best;
