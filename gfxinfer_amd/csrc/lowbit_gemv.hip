@@ -1387,12 +1387,13 @@ int kernel_override() {  // 0 default, 1 lds everywhere, 2 direct everywhere
   return value;
 }
 
-// GFXI_GEMM_ROWTILES (1 or 2) overrides the row tiles per workgroup (tuning knob).
+// GFXI_GEMM_ROWTILES (1..5) overrides the direct kernel's row tiles x chunk groups
+// (tuning knob; the summation order does not depend on it).
 int rowtiles_override() {
   static const int value = [] {
     const char* text = std::getenv("GFXI_GEMM_ROWTILES");
     const int v = text != nullptr ? std::atoi(text) : 0;
-    return v == 1 || v == 2 ? v : 0;
+    return v >= 1 && v <= 5 ? v : 0;
   }();
   return value;
 }
@@ -1458,38 +1459,60 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
          min_range_count(args.groups, args.splits), kDirectMaxWaves});
     hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), lds, stream, args);
   };
-  // Two row tiles per workgroup halve the activation reads per weight byte, but only
-  // pay off while the grid still has about two waves per SIMD (q/k/v and the split o
-  // projection at 16-32 tokens measured faster with one).
-  const int forced = rowtiles_override();
-  bool pair = forced == 2;
-  if (forced == 0) {
-    uint64_t blocks = 0;
-    for (unsigned i = 0; i < 4; ++i) {
-      const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
-      if (used) blocks += (base_args.matrix[i].tiles + 1u) / 2u;
-    }
-    const unsigned waves = std::min({choose_waves(base_args.groups / base_args.splits, 1),
-                                     min_range_count(base_args.groups, base_args.splits), kDirectMaxWaves});
-    pair = blocks * base_args.splits * waves >= 2048u;
+  // Row tiles per wave (R) and groups per load chunk (CH), by grid shape (measured on
+  // MI355X over the verifier's projections at 16 and 32 tokens, weights rotated past the
+  // Infinity Cache).  More tiles share each activation load and its expansion; shorter
+  // chunks need fewer registers, so more waves stay resident.  A split of one canonical
+  // range (the o and GDN out projections: 8-10 groups per split) runs one wave per
+  // workgroup and keeps one tile; otherwise, by row tiles x splits:
+  //   >= 2048 (gate/up): 3 tiles, 2-group chunks (32 tokens 25.3 -> 21.4 us);
+  //   1024..2047 (down as four splits): 3 tiles, 3-group chunks (16.0 -> 14.3 us);
+  //   < 1024 (q/k/v, GDN in-projection): 2 tiles, 2-group chunks at 17-32 tokens
+  //   (15.3 -> 12.2 us), 2 tiles of 5-group chunks at 9-16 tokens.
+  // GFXI_GEMM_ROWTILES (1, 2 or 3) forces 1 tile x 4 groups, 2 x 5 or 3 x 2.
+  uint64_t tile_splits = 0;
+  for (unsigned i = 0; i < 4; ++i) {
+    const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
+    if (used) tile_splits += static_cast<uint64_t>(base_args.matrix[i].tiles) * base_args.splits;
   }
+  const bool one_range = min_range_count(base_args.groups, base_args.splits) <= 1;
+  int shape = rowtiles_override();  // 1: 1 x 4, 2: 2 x 5, 3: 3 x 2, 4: 3 x 3, 5: 2 x 2
+  if (shape == 0) {
+    if (one_range) {
+      shape = 1;
+    } else if (tile_splits >= 2048) {
+      shape = 3;
+    } else if (tile_splits >= 1024) {
+      shape = 4;
+    } else {
+      shape = batch > 16 ? 5 : 2;
+    }
+  }
+  // The SwiGLU tail counts finished tiles per 128-row group (8 tiles): a workgroup's
+  // tiles must not straddle two groups, so three-tile shapes fall back to two tiles.
+  if (base_args.group_counters != nullptr && (shape == 3 || shape == 4)) shape = batch > 16 ? 5 : 2;
   (void)total_tiles;
   if (batch <= 4) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 4, 1, 3, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 8) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 2, 1, 6, 1, HalfOut, Partials>, 1, 1);
   } else if (batch <= 16) {
-    if (!pair) {
-      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 1, HalfOut, Partials>, 1, 1);
-    } else {
-      go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 5, 2, HalfOut, Partials>, 2, 1);
+    switch (shape) {
+      case 2: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 5, 2, HalfOut, Partials>, 2, 1); break;
+      case 3: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 2, 3, HalfOut, Partials>, 3, 1); break;
+      case 4: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 3, 3, HalfOut, Partials>, 3, 1); break;
+      default: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 1, 4, 1, HalfOut, Partials>, 1, 1); break;
     }
   } else if constexpr (ABits == 8) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
-  } else if (!pair) {
-    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2);
   } else {
-    go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 5, 2, HalfOut, Partials>, 2, 2);
+    switch (shape) {
+      case 2: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 5, 2, HalfOut, Partials>, 2, 2); break;
+      case 3: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 2, 3, HalfOut, Partials>, 3, 2); break;
+      case 4: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 3, 3, HalfOut, Partials>, 3, 2); break;
+      case 5: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 2, 2, HalfOut, Partials>, 2, 2); break;
+      default: go(lowbit_gemm_direct_kernel<Format, ABits, 1, 2, 4, 1, HalfOut, Partials>, 1, 2); break;
+    }
   }
 }
 

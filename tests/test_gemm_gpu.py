@@ -158,6 +158,9 @@ CASES = [
     (2, 4, 5120, 17408, 32), (3, 4, 5120, 17408, 16), (2, 8, 5120, 17408, 32),
     # 9-32 tokens (LDS-ring kernel): workgroups of 4 or 8 tiles with a short last one
     (2, 4, 48, 256, 13), (3, 4, 112, 384, 32), (3, 4, 16480, 5120, 32), (2, 4, 34816, 5120, 24),
+    # each direct-kernel shape class (row tiles x chunk groups by grid size) at 9-16 and
+    # 17-32 tokens, with a short last workgroup where the tiles do not divide by three
+    (2, 4, 34816, 5120, 16), (2, 4, 17408, 5120, 12), (3, 4, 12288, 5120, 32), (3, 4, 12352, 5120, 9),
     # W2 (reference formats W2/W3/W4; no BASELINE config uses it)
     (1, 4, 64, 640, 1), (1, 4, 64, 640, 5), (1, 4, 64, 640, 17), (1, 4, 64, 640, 32),
     (1, 8, 64, 640, 3), (1, 8, 64, 640, 16), (1, 4, 17408, 5120, 5), (1, 4, 5120, 17408, 32),
