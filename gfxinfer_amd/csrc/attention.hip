@@ -54,7 +54,9 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   __shared__ __align__(16) _Float16 ps[4][16][kRow];
   __shared__ __align__(16) _Float16 ps_lo[4][16][kRow];
 
-  const unsigned split = blockIdx.x, hk = blockIdx.y;
+  // Workgroups in split-major order (KV head fastest): the splits that hold visible
+  // positions come first in dispatch order, ahead of the ones that exit at once.
+  const unsigned split = blockIdx.x / a.kv_heads, hk = blockIdx.x - split * a.kv_heads;
   const uint64_t base = base_count_of(a);
   const uint64_t max_count = base + a.tokens - 1;  // visible positions of the last token
   const uint64_t p0 = static_cast<uint64_t>(split) * kSplit;
@@ -89,15 +91,27 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
   // Positions past the limit load position p0 (always valid: p0 < limit) and are
   // zeroed when written, so no load waits on a branch.
-  u32x4 kr[kStage], vr[kStage];
+  // K rows: thread i holds dims 8 (i % 16) .. + 7 of position i / 16.  V: thread i holds
+  // the same eight dims of positions 2 (i % 32) and 2 (i % 32) + 1 (chunk i / 32), so that
+  // it writes V^T as position pairs, one dword per dim, with the 64 lanes of a wave on
+  // 64 different LDS banks.
+  constexpr unsigned kVItems = (kSplit / 2) * (kD / 8) / kThreads;
+  u32x4 kr[kStage], va[kVItems], vb[kVItems];
 #pragma unroll
   for (unsigned u = 0; u < kStage; ++u) {
     const unsigned i = tid + u * kThreads;
     const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
     const uint64_t pos = p0 + p < limit ? p0 + p : p0;
-    const std::size_t at = (pos * a.kv_heads + hk) * kD + d8;
-    kr[u] = *reinterpret_cast<const u32x4*>(a.key_cache + at);
-    vr[u] = *reinterpret_cast<const u32x4*>(a.value_cache + at);
+    kr[u] = *reinterpret_cast<const u32x4*>(a.key_cache + (pos * a.kv_heads + hk) * kD + d8);
+  }
+#pragma unroll
+  for (unsigned u = 0; u < kVItems; ++u) {
+    const unsigned i = tid + u * kThreads;
+    const unsigned pair = i % (kSplit / 2), d8 = (i / (kSplit / 2)) * 8;
+    const uint64_t pa = p0 + 2 * pair < limit ? p0 + 2 * pair : p0;
+    const uint64_t pb = p0 + 2 * pair + 1 < limit ? p0 + 2 * pair + 1 : p0;
+    va[u] = *reinterpret_cast<const u32x4*>(a.value_cache + (pa * a.kv_heads + hk) * kD + d8);
+    vb[u] = *reinterpret_cast<const u32x4*>(a.value_cache + (pb * a.kv_heads + hk) * kD + d8);
   }
   h8 q_next[4];
   load_q(wave, q_next);
@@ -105,14 +119,21 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   for (unsigned u = 0; u < kStage; ++u) {
     const unsigned i = tid + u * kThreads;
     const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
-    if (p0 + p >= limit) {
-      kr[u] = u32x4{0, 0, 0, 0};
-      vr[u] = u32x4{0, 0, 0, 0};
-    }
+    if (p0 + p >= limit) kr[u] = u32x4{0, 0, 0, 0};
     *reinterpret_cast<u32x4*>(&ks[p][d8]) = kr[u];
-    const _Float16* v = reinterpret_cast<const _Float16*>(&vr[u]);
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vt[d8 + e][p] = v[e];
+  for (unsigned u = 0; u < kVItems; ++u) {
+    const unsigned i = tid + u * kThreads;
+    const unsigned pair = i % (kSplit / 2), d8 = (i / (kSplit / 2)) * 8;
+    if (p0 + 2 * pair >= limit) va[u] = u32x4{0, 0, 0, 0};
+    if (p0 + 2 * pair + 1 >= limit) vb[u] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const unsigned lo = (va[u][e / 2] >> (16 * (e % 2))) & 0xffffu;
+      const unsigned hi = (vb[u][e / 2] >> (16 * (e % 2))) & 0xffffu;
+      *reinterpret_cast<unsigned*>(&vt[d8 + e][2 * pair]) = lo | (hi << 16);
+    }
   }
   __syncthreads();
 
@@ -311,7 +332,7 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
                 reinterpret_cast<const __half*>(value_cache), partial_o, partial_ml, base_count, indirect,
                 batch, q_heads, kv_heads, splits, static_cast<uint32_t>(capacity),
                 1.0F / std::sqrt(static_cast<float>(kD))};
-  hipLaunchKernelGGL(attention_split_kernel, dim3(splits, kv_heads), dim3(256), 0, stream, args);
+  hipLaunchKernelGGL(attention_split_kernel, dim3(splits * kv_heads), dim3(256), 0, stream, args);
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
   const uint32_t total = batch * q_heads;
   hipLaunchKernelGGL(attention_combine_kernel, dim3((total + 3) / 4), dim3(256), 0, stream, args, gate,
