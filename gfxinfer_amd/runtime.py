@@ -318,6 +318,30 @@ def render_chat_prompt(prompt: str) -> str:
     return out.raw[:length.value].decode("utf-8")
 
 
+# The chat special tokens that end a generated answer (cli/main.cpp:1100-1103 stops at
+# the ids of <|im_end|> and <|endoftext|> of the model's own tokenizer).
+STOP_PIECES = ("<|im_end|>", "<|endoftext|>")
+
+
+def generate_text(session: "QwenDecodeSession", tokenizer: Tokenizer, prompt: str, maximum_tokens: int,
+                  draft_count: int = 0, adaptive_depth: bool = False) -> dict:
+    """The generate command's text path (cli/main.cpp:1023-1120) over the session API:
+    render the one-turn chat prompt, encode it, run the generate loop (prefill, then
+    greedy or speculative rounds) until `maximum_tokens` or a stop token, decode the
+    generated ids.  Returns the prompt ids, the generated ids, their decoded bytes and
+    the loop statistics; raises GfxinferError when the prompt and the generation do
+    not fit the session's context, as the command refuses to run."""
+    ids = tokenizer.encode(render_chat_prompt(prompt))
+    stops = []
+    for piece in STOP_PIECES:
+        encoded = tokenizer.encode(piece)
+        if len(encoded) == 1:
+            stops.append(encoded[0])
+    tokens, stats = session.generate(ids, maximum_tokens, draft_count, adaptive_depth, stops)
+    return {"prompt_ids": ids, "tokens": tokens, "text": tokenizer.decode_bytes(tokens), "stats": stats,
+            "stop_ids": stops}
+
+
 def crc64_ecma(data: bytes, state: int = 0) -> int:
     """CRC-64/ECMA-182 (artifact.cpp:187-213)."""
     buf = np.frombuffer(bytes(data), np.uint8)
