@@ -46,13 +46,16 @@ __device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
   return a.indirect_position != nullptr ? *a.indirect_position + 1u : a.base_count;
 }
 
-__global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
+// Waves = 4 or 8 per workgroup: each wave takes every Waves-th 16-row tile of the
+// (token, q head) rows of its KV head; eight waves for blocks of more than four tiles.
+template <unsigned Waves>
+__global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a) {
   __shared__ __align__(16) _Float16 ks[kSplit][kD + kPad];  // K rows of the split
   __shared__ __align__(16) _Float16 vt[kD][kRow];           // V transposed: [d][position]
   // Per-wave P tile as an fp16 pair p = hi + lo (hi = fp16(p), lo = fp16(p - hi)): two
   // f16 MFMAs then carry ~22 significant bits of p, close to the reference's fp32 P.V.
-  __shared__ __align__(16) _Float16 ps[4][16][kRow];
-  __shared__ __align__(16) _Float16 ps_lo[4][16][kRow];
+  __shared__ __align__(16) _Float16 ps[Waves][16][kRow];
+  __shared__ __align__(16) _Float16 ps_lo[Waves][16][kRow];
 
   // Workgroups in split-major order (KV head fastest): the splits that hold visible
   // positions come first in dispatch order, ahead of the ones that exit at once.
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   // Stage K [pos][d] and V^T [d][pos] for the split's positions (zeros past the
   // last visible position or the cache capacity).  Every K/V load of the split and the
   // wave's first Q tile are issued before the first LDS write (one memory latency).
-  constexpr unsigned kThreads = 256;
+  constexpr unsigned kThreads = Waves * 64;
   constexpr unsigned kStage = kSplit * (kD / 8) / kThreads;  // 16-byte K and V loads per thread
   const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
   // Positions past the limit load position p0 (always valid: p0 < limit) and are
@@ -96,6 +99,8 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   // it writes V^T as position pairs, one dword per dim, with the 64 lanes of a wave on
   // 64 different LDS banks.
   constexpr unsigned kVItems = (kSplit / 2) * (kD / 8) / kThreads;
+  static_assert(kStage >= 1 && kVItems >= 1 && kSplit * (kD / 8) % kThreads == 0 &&
+                (kSplit / 2) * (kD / 8) % kThreads == 0, "staging covers the split exactly");
   u32x4 kr[kStage], va[kVItems], vb[kVItems];
 #pragma unroll
   for (unsigned u = 0; u < kStage; ++u) {
@@ -137,12 +142,12 @@ __global__ __launch_bounds__(256) void attention_split_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  for (unsigned rt = wave; rt < row_tiles; rt += 4) {
+  for (unsigned rt = wave; rt < row_tiles; rt += Waves) {
     // This tile's Q operand was loaded one tile ahead; the next tile's goes out now.
     h8 q[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) q[s] = q_next[s];
-    load_q(rt + 4, q_next);
+    load_q(rt + Waves, q_next);
     // S = Q K^T for the split's positions (kTiles tiles of 16).
     f4 sc[kTiles];
 #pragma unroll
@@ -332,7 +337,12 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
                 reinterpret_cast<const __half*>(value_cache), partial_o, partial_ml, base_count, indirect,
                 batch, q_heads, kv_heads, splits, static_cast<uint32_t>(capacity),
                 1.0F / std::sqrt(static_cast<float>(kD))};
-  hipLaunchKernelGGL(attention_split_kernel, dim3(splits * kv_heads), dim3(256), 0, stream, args);
+  const unsigned rows = (q_heads / kv_heads) * batch;
+  if (rows > 4 * 16) {
+    hipLaunchKernelGGL(attention_split_kernel<8>, dim3(splits * kv_heads), dim3(512), 0, stream, args);
+  } else {
+    hipLaunchKernelGGL(attention_split_kernel<4>, dim3(splits * kv_heads), dim3(256), 0, stream, args);
+  }
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
   const uint32_t total = batch * q_heads;
   hipLaunchKernelGGL(attention_combine_kernel, dim3((total + 3) / 4), dim3(256), 0, stream, args, gate,

@@ -281,6 +281,34 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
     // the token's embedding row, dequantized per column pair
     const uint32_t token = a.indirect_token != nullptr ? *a.indirect_token : a.token;
     const std::size_t groups = elements / kGroup;
+    if constexpr (EmbedFormat == GFXI_W4G128) {
+      // W4: one byte holds the lane pair's two codes (even column in the low nibble).
+      // Every slot's loads go out before the first use (row 0 / column 0 stand in for a
+      // dead slot or a token past the table, whose values are zeros).
+      const bool in_table = token < a.embed_rows;
+      const uint32_t table_row = in_table ? token : 0u;
+      uint32_t code[Slots];
+      uint16_t scale_bits[Slots];
+#pragma unroll
+      for (unsigned j = 0; j < Slots; ++j) {
+        const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+        const uint32_t at = i < elements ? i : 0u;
+        wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+        code[j] = a.embed_codes[chunk_offset(EmbedFormat, table_row, at, groups) + (at % 32u) / 2u];
+        scale_bits[j] = __half_as_ushort(a.embed_scales[scale_offset(table_row, at / kGroup, groups)]);
+      }
+#pragma unroll
+      for (unsigned j = 0; j < Slots; ++j) {
+        const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+        const int lo = static_cast<int>(code[j] & 0xfu), hi = static_cast<int>(code[j] >> 4);
+        const int w0 = lo >= 8 ? lo - 16 : lo, w1 = hi >= 8 ? hi - 16 : hi;
+        const float scale = __half2float(__ushort_as_half(scale_bits[j]));
+        const uint32_t value =
+            static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w0) * scale))) |
+            (static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w1) * scale))) << 16);
+        hin[j] = i < elements && in_table ? value : 0u;
+      }
+    } else {
 #pragma unroll
     for (unsigned j = 0; j < Slots; ++j) {
       const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
@@ -295,6 +323,7 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
         hin[j] = static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w0) * scale))) |
                  (static_cast<uint32_t>(__half_as_ushort(to_half(static_cast<float>(w1) * scale))) << 16);
       }
+    }
     }
   } else {
     const __half* input = (second ? a.right : a.left) + row * elements;
