@@ -194,6 +194,8 @@ def test_gemm_partials_bit_exact_and_output(device, gx, orc, fmt, abits, rows, c
     (2, 5120, 17408, 5, 4), (2, 5120, 17408, 32, 4), (3, 5120, 17408, 5, 8), (3, 5120, 6144, 5, 4),
     (3, 5120, 6144, 16, 3), (2, 5120, 5120, 9, 5), (2, 64, 640, 1, 5), (3, 64, 640, 32, 2),
     (2, 48, 1024, 7, 8), (1, 5120, 17408, 5, 4), (1, 64, 640, 32, 2),
+    # split grids in each direct-kernel shape class: 1280 and 2560 row tiles x splits
+    (2, 5120, 17408, 12, 4), (2, 5120, 17408, 32, 8), (3, 5120, 17408, 20, 8),
 ])
 def test_gemm_split_planes_sum_to_product(device, gx, orc, fmt, rows, cols, batch, splits):
     """Split-K planes: plane s = the epilogue over the s-th of `splits` equal pack ranges
