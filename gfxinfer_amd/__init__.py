@@ -103,7 +103,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_kv_append_block_indirect_position": (I32, [P, P, P, P, P, SZ, U32, SZ, P]),
     "gfxinfer_launch_argmax_batch": (I32, [P, P, SZ, SZ, U32, P]),
     "gfxinfer_launch_argmax_mapped": (I32, [P, P, P, SZ, P]),
-    "gfxinfer_attention_workspace_bytes": (SZ, [U32, U32, SZ]),
+    "gfxinfer_attention_workspace_bytes": (SZ, [U32, U32, U32, SZ]),
     "gfxinfer_launch_gated_attention_decode_block": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
@@ -113,9 +113,18 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gdn_restore_prefix": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P]),
     "gfxinfer_launch_kv_append": (I32, [P, P, P, P, SZ, SZ, SZ, P]),
     "gfxinfer_launch_gated_attention_decode": (I32, [P, P, P, P, P, SZ, SZ, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_qwen38_scratch_bytes": (SZ, [U32, SZ]),
+    "gfxinfer_qwen38_bind_scratch": (I32, [P, P, SZ, U32, SZ]),
+    "gfxinfer_qwen38_unbind_scratch": (I32, [P]),
+    "gfxinfer_qwen38_launch_gated_attention_decode": (I32, [P, P, P, P, P, SZ, SZ, P]),
+    "gfxinfer_qwen38_launch_gated_attention_decode_block": (I32, [P, P, P, P, P, SZ, SZ, U32, P]),
+    "gfxinfer_qwen38_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, P]),
+    "gfxinfer_qwen38_launch_gdn_recurrent_decode_block": (I32, [P] * 13 + [U32, P]),
+    "gfxinfer_qwen38_launch_gdn_recurrent_decode": (I32, [P] * 10),
     "gfxinfer_launch_argmax": (I32, [P, P, SZ, P]),
     # include/gfxinfer_runtime.h
     "gfxinfer_model_spec_qwen38_27b": (None, [P]),
+    "gfxinfer_model_spec_qwen38_reference": (None, [P]),
     "gfxinfer_model_spec_tensor_count": (SZ, [P]),
     "gfxinfer_model_spec_tensor": (I32, [P, SZ, P]),
     "gfxinfer_model_create_synthetic": (I32, [P, ctypes.c_uint64, I32, P]),

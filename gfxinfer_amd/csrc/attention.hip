@@ -7,9 +7,11 @@
 // sigmoid(gate) rounded to fp16, the gate being the second half of each head's
 // 2*head_size query-projection row.  The reference runs one 256-thread block per
 // (head, token) that walks the whole context; here one workgroup per (KV head,
-// 64-position split) stages K and V^T in LDS once and serves all
+// split of positions) stages K and V^T in LDS once and serves all
 // (q_heads/kv_heads) x tokens query rows of that KV head with MFMA, writing a
 // split-local (max, sum, unnormalized output); a combine kernel merges splits.
+// Head sizes 128 (64-position splits) and 256 (the reference model's 24/4 x 256,
+// 32-position splits so that K, V^T and the P tiles stay within 64 KB of LDS).
 #include <cmath>
 #include <limits>
 #include <string>
@@ -23,12 +25,19 @@ using h8 = _Float16 __attribute__((ext_vector_type(8)));
 using f4 = float __attribute__((ext_vector_type(4)));
 using u32x4 = unsigned __attribute__((ext_vector_type(4)));
 
-constexpr unsigned kD = 128;       // head size
-constexpr unsigned kSplit = 64;    // positions per workgroup
-constexpr unsigned kTiles = kSplit / 16;  // score tiles of 16 positions
-constexpr unsigned kSteps = kSplit / 32;  // P.V K-steps of 32 positions
-constexpr unsigned kPad = 8;       // LDS row padding (halves)
-constexpr unsigned kRow = kSplit + kPad;
+constexpr unsigned kPad = 8;  // LDS row padding (halves; rows stay 16-byte aligned)
+
+// Positions per workgroup for a head size.
+template <unsigned D>
+constexpr unsigned split_positions() {
+  static_assert(D == 128 || D == 256, "head size 128 or 256");
+  return D == 128 ? 64 : 32;
+}
+
+std::size_t split_count(uint32_t head_size, std::size_t capacity) {
+  const std::size_t split = head_size == 128 ? split_positions<128>() : split_positions<256>();
+  return (capacity + split - 1) / split;
+}
 
 struct AttnArgs {
   const __half* query;        // [T][Hq][D]
@@ -48,8 +57,13 @@ __device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
 
 // Waves = 4 or 8 per workgroup: each wave takes every Waves-th 16-row tile of the
 // (token, q head) rows of its KV head; eight waves for blocks of more than four tiles.
-template <unsigned Waves>
+template <unsigned kD, unsigned Waves>
 __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a) {
+  constexpr unsigned kSplit = split_positions<kD>();
+  constexpr unsigned kTiles = kSplit / 16;  // score tiles of 16 positions
+  constexpr unsigned kSteps = kSplit / 32;  // P.V K-steps of 32 positions
+  constexpr unsigned kRow = kSplit + kPad;
+  constexpr unsigned kQ = kD / 32;          // Q.K^T K-steps of 32 head dims
   __shared__ __align__(16) _Float16 ks[kSplit][kD + kPad];  // K rows of the split
   __shared__ __align__(16) _Float16 vt[kD][kRow];           // V transposed: [d][position]
   // Per-wave P tile as an fp16 pair p = hi + lo (hi = fp16(p), lo = fp16(p - hi)): two
@@ -73,16 +87,16 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   const unsigned row_tiles = (rows + 15) / 16;
   // The Q operand of row tile rt (row = t * group + g -> head hk*group + g of token t),
   // zeros past the last row.
-  auto load_q = [&](unsigned rt, h8 (&q)[4]) __attribute__((always_inline)) {
+  auto load_q = [&](unsigned rt, h8 (&q)[kQ]) __attribute__((always_inline)) {
     const unsigned qrow = rt * 16 + m;
     if (rt < row_tiles && qrow < rows) {
       const unsigned t = qrow / group, g = qrow - t * group;
       const __half* src = a.query + (static_cast<std::size_t>(t) * a.q_heads + hk * group + g) * kD + 8 * kb;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) q[s] = *reinterpret_cast<const h8*>(src + 32 * s);
+      for (unsigned s = 0; s < kQ; ++s) q[s] = *reinterpret_cast<const h8*>(src + 32 * s);
     } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) q[s] = h8{};
+      for (unsigned s = 0; s < kQ; ++s) q[s] = h8{};
     }
   };
 
@@ -94,10 +108,10 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   const uint64_t limit = max_count < a.capacity ? max_count : a.capacity;
   // Positions past the limit load position p0 (always valid: p0 < limit) and are
   // zeroed when written, so no load waits on a branch.
-  // K rows: thread i holds dims 8 (i % 16) .. + 7 of position i / 16.  V: thread i holds
-  // the same eight dims of positions 2 (i % 32) and 2 (i % 32) + 1 (chunk i / 32), so that
-  // it writes V^T as position pairs, one dword per dim, with the 64 lanes of a wave on
-  // 64 different LDS banks.
+  // K rows: thread i holds dims 8 (i % (D/8)) .. + 7 of position i / (D/8).  V: thread i
+  // holds eight dims (chunk i / (split/2)) of positions 2 (i % (split/2)) and the one after,
+  // so that it writes V^T as position pairs, one dword per dim (at head size 128 the 64
+  // lanes of a wave land on 64 different LDS banks).
   constexpr unsigned kVItems = (kSplit / 2) * (kD / 8) / kThreads;
   static_assert(kStage >= 1 && kVItems >= 1 && kSplit * (kD / 8) % kThreads == 0 &&
                 (kSplit / 2) * (kD / 8) % kThreads == 0, "staging covers the split exactly");
@@ -118,7 +132,7 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
     va[u] = *reinterpret_cast<const u32x4*>(a.value_cache + (pa * a.kv_heads + hk) * kD + d8);
     vb[u] = *reinterpret_cast<const u32x4*>(a.value_cache + (pb * a.kv_heads + hk) * kD + d8);
   }
-  h8 q_next[4];
+  h8 q_next[kQ];
   load_q(wave, q_next);
 #pragma unroll
   for (unsigned u = 0; u < kStage; ++u) {
@@ -144,9 +158,9 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
 
   for (unsigned rt = wave; rt < row_tiles; rt += Waves) {
     // This tile's Q operand was loaded one tile ahead; the next tile's goes out now.
-    h8 q[4];
+    h8 q[kQ];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) q[s] = q_next[s];
+    for (unsigned s = 0; s < kQ; ++s) q[s] = q_next[s];
     load_q(rt + Waves, q_next);
     // S = Q K^T for the split's positions (kTiles tiles of 16).
     f4 sc[kTiles];
@@ -154,7 +168,7 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
     for (unsigned j = 0; j < kTiles; ++j) {
       f4 acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      for (unsigned s = 0; s < kQ; ++s) {
         const h8 kk = *reinterpret_cast<const h8*>(&ks[j * 16 + m][32 * s + 8 * kb]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(q[s], kk, acc, 0, 0, 0);
       }
@@ -188,7 +202,7 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
       mx[r] = best;
       sum[r] = total;
     }
-    // O = P V: 8 tiles of 16 head dims, kSteps K-steps of 32 positions.
+    // O = P V: kD / 16 tiles of 16 head dims, kSteps K-steps of 32 positions.
     h8 pa[kSteps], pl[kSteps];
 #pragma unroll
     for (unsigned s = 0; s < kSteps; ++s) {
@@ -196,7 +210,7 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
       pl[s] = *reinterpret_cast<const h8*>(&ps_lo[wave][m][32 * s + 8 * kb]);
     }
 #pragma unroll
-    for (int dj = 0; dj < 8; ++dj) {
+    for (unsigned dj = 0; dj < kD / 16; ++dj) {
       f4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (unsigned s = 0; s < kSteps; ++s) {
@@ -230,20 +244,26 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
 }
 
 // Merge the splits of each (token, q head) and apply the sigmoid gate.  One
-// wave per (token, head); lane owns head dims 2l, 2l+1.  With codes set, the wave
-// also quantizes its head (one 128 group) to A4G128 as quantize_activation_i4 does
-// on the fp16 output row ([T][Hq * 128] -> codes [T][Hq * 64], scales [T][Hq]).
+// wave per (token, head); lane owns head dims 128 j + 2l, 128 j + 2l + 1 of each 128-dim
+// group j of the head.  With codes set, the wave also quantizes each group of its head
+// to A4G128 as quantize_activation_i4 does on the fp16 output row
+// ([T][Hq * D] -> codes [T][Hq * D / 2], scales [T][Hq * D / 128]).
+template <unsigned kD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, const float* __restrict__ gate,
                                                                 __half* __restrict__ output,
                                                                 uint8_t* __restrict__ codes,
                                                                 __half* __restrict__ scales) {
+  constexpr unsigned kSplit = split_positions<kD>();
+  constexpr unsigned kG = kD / 128;  // 128-dim groups per head
   const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (linear >= a.tokens * a.q_heads) return;
   const unsigned lane = threadIdx.x & 63u;
   const uint32_t t = linear / a.q_heads, qh = linear - t * a.q_heads;
   // The gate row first: it does not depend on the position.
   const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
-  const float g_lo = g[2 * lane], g_hi = g[2 * lane + 1];
+  float2 gv[kG];
+#pragma unroll
+  for (unsigned j = 0; j < kG; ++j) gv[j] = *reinterpret_cast<const float2*>(g + 128 * j + 2 * lane);
   const uint64_t count = base_count_of(a) + t;
   const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
   const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
@@ -259,14 +279,19 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
 #pragma unroll
     for (unsigned k = 0; k < kBatch; ++k) best = fmaxf(best, m[k]);
   }
-  float o0 = 0.0F, o1 = 0.0F, total = 0.0F;
+  float o0[kG], o1[kG], total = 0.0F;
+#pragma unroll
+  for (unsigned j = 0; j < kG; ++j) o0[j] = o1[j] = 0.0F;
   for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
-    float2 mls[kBatch], v[kBatch];
+    float2 mls[kBatch], v[kBatch][kG];
 #pragma unroll
     for (unsigned k = 0; k < kBatch; ++k) {
       const unsigned s = s0 + k < used ? s0 + k : s0;
       mls[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
-      v[k] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD);
+#pragma unroll
+      for (unsigned j = 0; j < kG; ++j) {
+        v[k][j] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD + 128 * j);
+      }
     }
     // No early exit: the loads above stay ahead of every use (splits past `used` are
     // loaded again from split s0 and skipped here, in split order as before).
@@ -275,19 +300,26 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
       if (s0 + k < used) {
         const float w = expf(mls[k].x - best);
         total = fmaf(mls[k].y, w, total);
-        o0 = fmaf(v[k].x, w, o0);
-        o1 = fmaf(v[k].y, w, o1);
+#pragma unroll
+        for (unsigned j = 0; j < kG; ++j) {
+          o0[j] = fmaf(v[k][j].x, w, o0[j]);
+          o1[j] = fmaf(v[k][j].y, w, o1[j]);
+        }
       }
     }
   }
-  const float g0 = 1.0F / (1.0F + expf(-g_lo));
-  const float g1 = 1.0F / (1.0F + expf(-g_hi));
-  __half* out = output + static_cast<std::size_t>(linear) * kD + 2 * lane;
-  const __half h0 = to_half(o0 / total * g0), h1 = to_half(o1 / total * g1);
-  out[0] = h0;
-  out[1] = h1;
-  if (codes != nullptr) {
-    quantize_group_a4(h0, h1, codes + static_cast<std::size_t>(linear) * (kD / 2), scales + linear, lane);
+#pragma unroll
+  for (unsigned j = 0; j < kG; ++j) {
+    const float g0 = 1.0F / (1.0F + expf(-gv[j].x));
+    const float g1 = 1.0F / (1.0F + expf(-gv[j].y));
+    __half* out = output + static_cast<std::size_t>(linear) * kD + 128 * j + 2 * lane;
+    const __half h0 = to_half(o0[j] / total * g0), h1 = to_half(o1[j] / total * g1);
+    out[0] = h0;
+    out[1] = h1;
+    if (codes != nullptr) {
+      quantize_group_a4(h0, h1, codes + static_cast<std::size_t>(linear) * (kD / 2) + 64 * j,
+                        scales + static_cast<std::size_t>(linear) * kG + j, lane);
+    }
   }
 }
 
@@ -304,9 +336,10 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
 using namespace gfx950;
 
 extern "C" size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_heads,
-                                                     size_t capacity) {
-  const std::size_t splits = (capacity + kSplit - 1) / kSplit;
-  return static_cast<std::size_t>(batch) * q_heads * splits * (kD + 2) * sizeof(float);
+                                                     uint32_t head_size, size_t capacity) {
+  if (head_size != 128 && head_size != 256) return 0;
+  return static_cast<std::size_t>(batch) * q_heads * split_count(head_size, capacity) * (head_size + 2) *
+         sizeof(float);
 }
 
 namespace gfx950 {
@@ -322,31 +355,45 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
   }
   if (query == nullptr || gate == nullptr || key_cache == nullptr || value_cache == nullptr ||
       output == nullptr || workspace == nullptr || batch == 0 || batch > 32 || q_heads == 0 ||
-      kv_heads == 0 || q_heads % kv_heads != 0 || head_size != kD || capacity == 0 ||
-      capacity > (1u << 24) || (indirect == nullptr && (base_count == 0 || base_count + batch - 1 > capacity))) {
-    return fail(GFXI_INVALID_ARGUMENT, "invalid gated attention decode arguments (head size 128, "
-                                       "1..32 tokens, visible positions within capacity)");
+      kv_heads == 0 || q_heads % kv_heads != 0 || (head_size != 128 && head_size != 256) ||
+      capacity == 0 || capacity > (1u << 24) ||
+      (indirect == nullptr && (base_count == 0 || base_count + batch - 1 > capacity))) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid gated attention decode arguments (head size 128 or "
+                                       "256, 1..32 tokens, visible positions within capacity)");
   }
-  if (workspace_bytes < gfxinfer_attention_workspace_bytes(batch, q_heads, capacity)) {
+  if (workspace_bytes < gfxinfer_attention_workspace_bytes(batch, q_heads, head_size, capacity)) {
     return fail(GFXI_INVALID_ARGUMENT, "attention workspace is too small");
   }
-  const auto splits = static_cast<uint32_t>((capacity + kSplit - 1) / kSplit);
+  const auto splits = static_cast<uint32_t>(split_count(head_size, capacity));
   float* partial_o = workspace;
-  float* partial_ml = workspace + static_cast<std::size_t>(batch) * q_heads * splits * kD;
+  float* partial_ml = workspace + static_cast<std::size_t>(batch) * q_heads * splits * head_size;
   AttnArgs args{reinterpret_cast<const __half*>(query), reinterpret_cast<const __half*>(key_cache),
                 reinterpret_cast<const __half*>(value_cache), partial_o, partial_ml, base_count, indirect,
                 batch, q_heads, kv_heads, splits, static_cast<uint32_t>(capacity),
-                1.0F / std::sqrt(static_cast<float>(kD))};
+                1.0F / std::sqrt(static_cast<float>(head_size))};
   const unsigned rows = (q_heads / kv_heads) * batch;
-  if (rows > 4 * 16) {
-    hipLaunchKernelGGL(attention_split_kernel<8>, dim3(splits * kv_heads), dim3(512), 0, stream, args);
+  const bool wide = rows > 4 * 16;
+  const dim3 grid(splits * kv_heads), block(wide ? 512 : 256);
+  if (head_size == 128 && wide) {
+    hipLaunchKernelGGL((attention_split_kernel<128, 8>), grid, block, 0, stream, args);
+  } else if (head_size == 128) {
+    hipLaunchKernelGGL((attention_split_kernel<128, 4>), grid, block, 0, stream, args);
+  } else if (wide) {
+    hipLaunchKernelGGL((attention_split_kernel<256, 8>), grid, block, 0, stream, args);
   } else {
-    hipLaunchKernelGGL(attention_split_kernel<4>, dim3(splits * kv_heads), dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((attention_split_kernel<256, 4>), grid, block, 0, stream, args);
   }
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
-  const uint32_t total = batch * q_heads;
-  hipLaunchKernelGGL(attention_combine_kernel, dim3((total + 3) / 4), dim3(256), 0, stream, args, gate,
-                     reinterpret_cast<__half*>(output), codes, reinterpret_cast<__half*>(scales));
+  const dim3 combine_grid((batch * q_heads + 3) / 4);
+  __half* out16 = reinterpret_cast<__half*>(output);
+  __half* scales16 = reinterpret_cast<__half*>(scales);
+  if (head_size == 128) {
+    hipLaunchKernelGGL(attention_combine_kernel<128>, combine_grid, dim3(256), 0, stream, args, gate, out16,
+                       codes, scales16);
+  } else {
+    hipLaunchKernelGGL(attention_combine_kernel<256>, combine_grid, dim3(256), 0, stream, args, gate, out16,
+                       codes, scales16);
+  }
   return launch_status("gated attention combine launch failed");
 }
 }  // namespace

@@ -127,7 +127,8 @@ int32_t validate_spec(const gfxinfer_model_spec& s) {
       s.hidden_size != 0 && s.hidden_size % 128 == 0 && s.intermediate_size != 0 &&
       s.intermediate_size % 128 == 0 && s.layer_count != 0 && s.layer_count % 2 == 0 &&
       s.full_attention_interval != 0 && s.attention_head_count != 0 && s.kv_head_count != 0 &&
-      s.attention_head_count % s.kv_head_count == 0 && s.attention_head_size == 128 &&
+      s.attention_head_count % s.kv_head_count == 0 &&
+      (s.attention_head_size == 128 || s.attention_head_size == 256) &&
       s.rotary_size != 0 && s.rotary_size % 2 == 0 && s.rotary_size <= 64 &&
       s.gdn_key_head_count != 0 && s.gdn_value_head_count != 0 &&
       s.gdn_value_head_count % s.gdn_key_head_count == 0 && s.gdn_value_head_count % 16 == 0 &&
@@ -138,9 +139,10 @@ int32_t validate_spec(const gfxinfer_model_spec& s) {
       s.rms_norm_epsilon > 0.0F && s.rope_theta > 0.0F;
   if (!valid) {
     return fail(GFXI_INVALID_ARGUMENT,
-                "model spec needs hidden/intermediate % 128 == 0, an even layer count, head "
-                "size 128, kv heads dividing attention heads, GDN value heads a multiple of 16 "
-                "and of the key heads, rotary <= 64, and vocabulary sizes % 16 == 0 in range");
+                "model spec needs hidden/intermediate % 128 == 0, an even layer count, attention "
+                "head size 128 or 256, kv heads dividing attention heads, GDN head size 128, GDN "
+                "value heads a multiple of 16 and of the key heads, rotary <= 64, and vocabulary "
+                "sizes % 16 == 0 in range");
   }
   return ok();
 }
@@ -243,6 +245,17 @@ extern "C" void gfxinfer_model_spec_qwen38_27b(gfxinfer_model_spec* spec) {
   spec->w3_mlp_layers = 56;
   spec->rms_norm_epsilon = 1.0e-6F;
   spec->rope_theta = 10000000.0F;
+}
+
+extern "C" void gfxinfer_model_spec_qwen38_reference(gfxinfer_model_spec* spec) {
+  if (spec == nullptr) return;
+  gfxinfer_model_spec_qwen38_27b(spec);
+  spec->attention_head_count = 24;
+  spec->kv_head_count = 4;
+  spec->attention_head_size = 256;
+  spec->gdn_value_head_count = 48;
+  spec->vocabulary_size = 248320;
+  spec->tokenizer_vocabulary_size = 248077;
 }
 
 namespace {

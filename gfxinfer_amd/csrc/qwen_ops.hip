@@ -980,7 +980,8 @@ __global__ __launch_bounds__(kRestoreThreads) void gdn_restore_recurrent_kernel(
 
 // ---------------------------------------------------------------------------
 // Per-head RMSNorm(1 + w) + partial rotate-half RoPE for Q and K heads
-// (qwen_ops.hip:599-676).  One wave per (token, head); lane owns dims l, l+64.
+// (qwen_ops.hip:599-676).  One wave per (token, head) of D = 128 or 256 dims; lane owns
+// dims l + 64 j (j < D / 64), so the rotary dims (< 64) all sit in the lane's first value.
 // ---------------------------------------------------------------------------
 
 struct RopeArgs {
@@ -1001,8 +1002,9 @@ struct RopeArgs {
   __half* value_cache;
 };
 
+template <unsigned D>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
-  constexpr unsigned D = 128;
+  constexpr unsigned J = D / 64;  // values per lane
   const uint32_t heads = a.query_heads + a.key_heads;
   const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (linear >= heads * a.tokens) return;
@@ -1019,39 +1021,52 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   const float position = static_cast<float>(base + t);
   // Every load before the first use: the head row, its norm weights and (for a key head
   // with the cache append) the value row.
-  const float x0 = in[lane], x1 = in[lane + 64];
-  const uint16_t w0 = w[lane], w1 = w[lane + 64];
-  const bool append = is_key && a.value_input != nullptr;
-  float value0 = 0.0F, value1 = 0.0F;
-  if (append) {
-    const float* value = a.value_input + (static_cast<std::size_t>(t) * count + head) * D;
-    value0 = value[lane];
-    value1 = value[lane + 64];
+  float x[J], value[J];
+  uint16_t wb[J];
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) {
+    x[j] = in[lane + 64 * j];
+    wb[j] = w[lane + 64 * j];
+    value[j] = 0.0F;
   }
-  const float inverse = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / static_cast<float>(D) + 1.0e-6F);
-  const float n0 = x0 * (inverse * (1.0F + bf16_to_float(w0)));
-  const float n1 = x1 * (inverse * (1.0F + bf16_to_float(w1)));
-  float v0 = n0;
+  const bool append = is_key && a.value_input != nullptr;
+  if (append) {
+    const float* v = a.value_input + (static_cast<std::size_t>(t) * count + head) * D;
+#pragma unroll
+    for (unsigned j = 0; j < J; ++j) value[j] = v[lane + 64 * j];
+  }
+  float square = 0.0F;
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) square += x[j] * x[j];
+  const float inverse = rsqrtf(wave_sum(square) / static_cast<float>(D) + 1.0e-6F);
+  float n[J];
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) n[j] = x[j] * (inverse * (1.0F + bf16_to_float(wb[j])));
+  float v0 = n[0];
   const unsigned half = a.rotary / 2;
   // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.
-  const float partner = __shfl(n0, lane < half ? lane + half : lane - half);
+  const float partner = __shfl(n[0], lane < half ? lane + half : lane - half);
   if (lane < a.rotary) {
     const unsigned fi = lane % half;
     const float exponent = (2.0F * static_cast<float>(fi)) / static_cast<float>(a.rotary);
     const float inverse_frequency = powf(a.theta, -exponent);
     const float angle = position * inverse_frequency;
     const float rotated = lane < half ? -partner : partner;
-    v0 = fmaf(n0, cosf(angle), rotated * sinf(angle));
+    v0 = fmaf(n[0], cosf(angle), rotated * sinf(angle));
   }
-  const __half h0 = to_half(v0), h1 = to_half(n1);
-  out[lane] = h0;
-  out[lane + 64] = h1;
+  __half h[J];
+  h[0] = to_half(v0);
+#pragma unroll
+  for (unsigned j = 1; j < J; ++j) h[j] = to_half(n[j]);
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) out[lane + 64 * j] = h[j];
   if (append) {
     const std::size_t row = (static_cast<std::size_t>(base + t) * count + head) * D;
-    a.key_cache[row + lane] = h0;
-    a.key_cache[row + lane + 64] = h1;
-    a.value_cache[row + lane] = to_half(value0);
-    a.value_cache[row + lane + 64] = to_half(value1);
+#pragma unroll
+    for (unsigned j = 0; j < J; ++j) {
+      a.key_cache[row + lane + 64 * j] = h[j];
+      a.value_cache[row + lane + 64 * j] = to_half(value[j]);
+    }
   }
 }
 
@@ -1610,11 +1625,12 @@ int32_t rope_entry(const float* query_input, const uint16_t* query_weight, uint1
   }
   if (query_input == nullptr || query_weight == nullptr || query_output == nullptr ||
       key_input == nullptr || key_weight == nullptr || key_output == nullptr || query_heads == 0 ||
-      key_heads == 0 || head_size != 128 || rotary == 0 || rotary > 64 || rotary % 2 != 0 ||
+      key_heads == 0 || (head_size != 128 && head_size != 256) || rotary == 0 || rotary > 64 ||
+      rotary % 2 != 0 ||
       query_stride < head_size || key_stride < head_size || batch == 0 || !std::isfinite(theta) ||
       theta <= 0.0F || query_heads > 4096 || key_heads > 4096) {
-    return fail(GFXI_INVALID_ARGUMENT, "invalid Q/K RMSNorm/RoPE arguments (head size 128, even "
-                                       "rotary size <= 64)");
+    return fail(GFXI_INVALID_ARGUMENT, "invalid Q/K RMSNorm/RoPE arguments (head size 128 or 256, "
+                                       "even rotary size <= 64)");
   }
   RopeArgs a{query_input, query_weight, reinterpret_cast<__half*>(query_output), key_input, key_weight,
              reinterpret_cast<__half*>(key_output), static_cast<uint32_t>(query_heads),
@@ -1623,7 +1639,11 @@ int32_t rope_entry(const float* query_input, const uint16_t* query_weight, uint1
              theta, value_input, reinterpret_cast<__half*>(key_cache),
              reinterpret_cast<__half*>(value_cache)};
   const uint32_t waves = static_cast<uint32_t>(query_heads + key_heads) * batch;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, a);
+  if (head_size == 128) {
+    hipLaunchKernelGGL(qk_norm_rope_kernel<128>, dim3((waves + 3) / 4), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(qk_norm_rope_kernel<256>, dim3((waves + 3) / 4), dim3(256), 0, stream, a);
+  }
   return launch_status("Q/K RMSNorm/RoPE launch failed");
 }
 

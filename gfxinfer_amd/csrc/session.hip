@@ -923,7 +923,7 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
     const std::size_t B = kMaxBlock, ctx = config->maximum_context_tokens;
     const std::size_t max_k = std::max({s->I, 2 * s->H, s->attn_width, s->gdn_value});
     s->attention_workspace_bytes =
-        gfxinfer_attention_workspace_bytes(kMaxBlock, sp.attention_head_count, ctx);
+        gfxinfer_attention_workspace_bytes(kMaxBlock, sp.attention_head_count, sp.attention_head_size, ctx);
     s->argmax_keys_bytes = gfxinfer_gemm_argmax_workspace_bytes(s->V, kMaxBlock);
     const std::size_t conv_bytes = s->gdn_layers * s->conv_state_elements() * 2;
     const std::size_t gdn_bytes = s->gdn_layers * s->gdn_state_elements() * 4;

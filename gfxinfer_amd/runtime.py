@@ -57,6 +57,13 @@ def qwen38_27b_spec() -> ModelSpec:
     return spec
 
 
+def qwen38_reference_spec() -> ModelSpec:
+    """The reference's own Qwen3.8 shape (24/4 x 256 attention, 16/48 GDN heads)."""
+    spec = ModelSpec()
+    lib().gfxinfer_model_spec_qwen38_reference(ctypes.byref(spec))
+    return spec
+
+
 def tiny_spec(**overrides) -> ModelSpec:
     """A small model of the same structure for oracle parity (2 GDN + 2 attention layers)."""
     spec = qwen38_27b_spec()
@@ -95,6 +102,23 @@ def artifact_tiny_spec() -> ModelSpec:
                      attention_head_count=1, kv_head_count=1, gdn_key_head_count=1, gdn_value_head_count=16,
                      vocabulary_size=256, tokenizer_vocabulary_size=250, mtp_draft_vocabulary=128,
                      w3_mlp_layers=1)
+
+
+def reference_tiny_spec(**overrides) -> ModelSpec:
+    """A small model of the reference's own head shapes (qwen38_spec.h:22-29): attention
+    heads of 256 dims with six query heads per KV head and rotary 64, GDN 16 key / 48
+    value heads (three value heads per key head, 10240 conv channels)."""
+    values = dict(attention_head_count=6, kv_head_count=1, attention_head_size=256, rotary_size=64,
+                  gdn_key_head_count=16, gdn_value_head_count=48, full_attention_interval=2)
+    values.update(overrides)
+    return tiny_spec(**values)
+
+
+def artifact_reference_tiny_spec() -> ModelSpec:
+    """reference_tiny_spec() at the smallest widths (one GDN and one attention layer,
+    hidden 128), used for the committed gfx1200 artifact of the reference's shape."""
+    return reference_tiny_spec(hidden_size=128, intermediate_size=256, layer_count=2, vocabulary_size=256,
+                               tokenizer_vocabulary_size=250, mtp_draft_vocabulary=128, w3_mlp_layers=1)
 
 
 class TensorView(ctypes.Structure):

@@ -467,16 +467,19 @@ int32_t gfxinfer_launch_argmax_mapped(const float* logits, const uint32_t* token
 
 /* ---- verify attention: src/kernels/qwen_ops.hip:698-766 --------------------- */
 
-/* Bytes of fp32 workspace gfxinfer_launch_gated_attention_decode_block needs. */
-size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, size_t capacity);
+/* Bytes of fp32 workspace gfxinfer_launch_gated_attention_decode_block needs for up to
+ * `batch` tokens of q_heads heads of head_size (128 or 256; 0 for any other) over a cache
+ * of `capacity` positions. */
+size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_size,
+                                          size_t capacity);
 
 /* qwen_ops.h:256-265 launch_gated_attention_decode_block: causal GQA decode attention of a
  * block of batch <= 32 tokens; token t sees the first base_token_count + t cached positions.
- * query fp16 [batch, q_heads, 128]; gate fp32 [batch, q_heads, 256] (second half of each head
- * row); caches fp16 [capacity, kv_heads, 128]; output fp16 [batch, q_heads, 128].  Head counts
- * are parameters (the reference hard-codes 24/4 x 256).  workspace: split-local partial
- * results, gfxinfer_attention_workspace_bytes() bytes (no reference counterpart: the
- * reference walks the context serially inside one block). */
+ * query fp16 [batch, q_heads, hd]; gate fp32 [batch, q_heads, 2 hd] (second half of each head
+ * row); caches fp16 [capacity, kv_heads, hd]; output fp16 [batch, q_heads, hd]; head size hd
+ * 128 or 256.  Head counts and size are parameters (the reference hard-codes 24/4 x 256).
+ * workspace: split-local partial results, gfxinfer_attention_workspace_bytes() bytes (no
+ * reference counterpart: the reference walks the context serially inside one block). */
 int32_t gfxinfer_launch_gated_attention_decode_block(
     const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
     uint16_t* output, size_t base_token_count, size_t capacity, uint32_t batch, uint32_t q_heads,
@@ -490,9 +493,9 @@ int32_t gfxinfer_launch_gated_attention_decode_block_indirect_position(
     size_t workspace_bytes, void* stream);
 
 /* Attention followed by the A4G128 quantizer of its output in the same launch: output as
- * gfxinfer_launch_gated_attention_decode_block writes it, and codes [batch, q_heads * 64] /
- * fp16 scales [batch, q_heads] as gfxinfer_launch_quantize_activation_i4 makes them from
- * that output (each 128-wide head is one group), bit for bit.  No reference counterpart
+ * gfxinfer_launch_gated_attention_decode_block writes it, and codes [batch, q_heads * hd / 2] /
+ * fp16 scales [batch, q_heads * hd / 128] as gfxinfer_launch_quantize_activation_i4 makes them
+ * from that output (a head is hd / 128 groups), bit for bit.  No reference counterpart
  * (the reference quantizes the attention output in a launch of its own inside the o
  * projection's matrix() call, qwen_runtime.cpp:471-481 and :116-120). */
 int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4(
@@ -552,6 +555,56 @@ int32_t gfxinfer_launch_gated_attention_decode(
  * the largest of vocabulary_size logits; ties go to the lowest index. */
 int32_t gfxinfer_launch_argmax(const float* logits, uint32_t* token, size_t vocabulary_size,
                                void* stream);
+
+/* ---- the reference's scratch-free signatures at its own model's shapes ----------------
+ * launch_gdn_recurrent_decode[_block] (qwen_ops.h:101-127) and
+ * launch_gated_attention_decode[_block][_indirect_position] (qwen_ops.h:246-276) take no
+ * workspace and hard-code the reference model (attention 24 Q / 4 KV heads x 256, GDN 16
+ * key / 48 value heads x 128; qwen38_spec.h:22-29).  The entries below take exactly the
+ * reference's arguments (no head counts, no workspace).  Their scratch is a device buffer
+ * of gfxinfer_qwen38_scratch_bytes(max_batch, capacity) bytes that the caller allocates
+ * and binds to the launch stream once, before any graph capture; a launch then only looks
+ * it up on the host and allocates nothing, so it can be captured.  Launches on one stream
+ * share its scratch and run in stream order; launches on two streams bound to one buffer
+ * race.  A launch on a stream with no scratch bound, or with a batch or capacity above
+ * the binding's, returns GFXI_INVALID_ARGUMENT without launching.  No reference
+ * counterpart for the three scratch calls. */
+
+/* Bytes of scratch for up to max_batch (1..32) tokens over caches of `capacity` positions;
+ * 0 for invalid arguments. */
+size_t gfxinfer_qwen38_scratch_bytes(uint32_t max_batch, size_t capacity);
+/* Binds (or rebinds) a 256-byte aligned device buffer of at least
+ * gfxinfer_qwen38_scratch_bytes(max_batch, capacity) bytes to `stream` (may be null: the
+ * null stream).  The buffer stays the caller's; it must outlive the launches. */
+int32_t gfxinfer_qwen38_bind_scratch(void* stream, void* scratch, size_t bytes, uint32_t max_batch,
+                                     size_t capacity);
+/* Forgets the stream's binding (GFXI_INVALID_ARGUMENT if it has none). */
+int32_t gfxinfer_qwen38_unbind_scratch(void* stream);
+
+/* qwen_ops.h:246-254: one token attending to the first token_count cached positions. */
+int32_t gfxinfer_qwen38_launch_gated_attention_decode(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, size_t token_count, size_t capacity, void* stream);
+/* qwen_ops.h:256-265: gfxinfer_launch_gated_attention_decode_block at 24/4 x 256. */
+int32_t gfxinfer_qwen38_launch_gated_attention_decode_block(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, size_t base_token_count, size_t capacity, uint32_t batch, void* stream);
+/* qwen_ops.h:267-276: the same with base_token_count = *device_base_position + 1. */
+int32_t gfxinfer_qwen38_launch_gated_attention_decode_block_indirect_position(
+    const uint16_t* query, const float* gate, const uint16_t* key_cache, const uint16_t* value_cache,
+    uint16_t* output, const uint64_t* device_base_position, size_t capacity, uint32_t batch, void* stream);
+/* qwen_ops.h:113-127: gfxinfer_launch_gdn_recurrent_decode_block at 16 key / 48 value heads
+ * x 128 (10240 conv channels). */
+int32_t gfxinfer_qwen38_launch_gdn_recurrent_decode_block(
+    const uint16_t* convolved_qkv, const float* projected_z, const float* projected_a, const float* projected_b,
+    const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias, const uint16_t* bf16_norm_weight,
+    const float* initial_recurrent_state, float* final_recurrent_state, uint16_t* output, float* key_log,
+    float* delta_log, float* decay_log, uint32_t batch, void* stream);
+/* qwen_ops.h:101-111: one token, recurrent state updated in place, no logs. */
+int32_t gfxinfer_qwen38_launch_gdn_recurrent_decode(
+    const uint16_t* convolved_qkv, const float* projected_z, const float* projected_a, const float* projected_b,
+    const uint16_t* bf16_a_log, const uint16_t* bf16_dt_bias, const uint16_t* bf16_norm_weight,
+    float* recurrent_state, uint16_t* output, void* stream);
 
 #ifdef __cplusplus
 }

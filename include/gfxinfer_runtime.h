@@ -31,7 +31,7 @@ typedef struct gfxinfer_model_spec {
   uint32_t full_attention_interval;   /* :21; layer i is attention iff (i+1) % interval == 0 */
   uint32_t attention_head_count;      /* :22 */
   uint32_t kv_head_count;             /* :23 */
-  uint32_t attention_head_size;       /* :24; must be 128 */
+  uint32_t attention_head_size;       /* :24; 128 or 256 */
   uint32_t rotary_size;               /* :25 */
   uint32_t gdn_key_head_count;        /* :26 */
   uint32_t gdn_value_head_count;      /* :28 */
@@ -48,6 +48,12 @@ typedef struct gfxinfer_model_spec {
  * MLP 17408 (W3 in layers 0-55, W4 in 56-63), attention 40 Q / 8 KV heads x 128 with
  * rotary 64, GDN 16 key / 32 value heads x 128, vocabulary 151936, MTP shortlist 98304. */
 void gfxinfer_model_spec_qwen38_27b(gfxinfer_model_spec* spec);
+
+/* Fills the reference's own model shape (qwen38_spec.h:16-34): as above but attention
+ * 24 Q / 4 KV heads x 256 with rotary 64, GDN 16 key / 48 value heads x 128 (10240 conv
+ * channels), vocabulary 248320 (tokenizer 248077); MLP in W3 except the last 8 layers
+ * (converter.h:20-23 with mlp_bits 3). */
+void gfxinfer_model_spec_qwen38_reference(gfxinfer_model_spec* spec);
 
 typedef struct gfxinfer_model gfxinfer_model;
 

@@ -177,10 +177,13 @@ def _declare(L: ctypes.CDLL) -> None:
 
 
 def ptr(a: np.ndarray | None):
+    """A ctypes pointer to `a`'s data that holds a reference to `a`, so that a temporary
+    passed as ptr(np.empty(...)) or ptr(np.ascontiguousarray(x)) stays alive until the
+    call it is an argument of returns."""
     if a is None:
         return None
     assert a.flags["C_CONTIGUOUS"]
-    return a.ctypes.data
+    return a.ctypes.data_as(ctypes.c_void_p)
 
 
 # ---- fp16 / bf16 ------------------------------------------------------------

@@ -14,8 +14,11 @@ library's own tiler.
 
 A second file holds a whole synthetic model (the smallest spec the kernels take, seed
 77) in the same recipe, every matrix quantized by the reference quantizer and tiled by
-the reference tiler, for the GPU test that loads it into the library's arena.  Only
-data is committed; re-running reproduces the files.
+the reference tiler, for the GPU test that loads it into the library's arena.  A third
+holds the same kind of model at the reference model's own head shapes (256-dim
+attention heads, six query heads per KV head, GDN 16 key / 48 value heads:
+artifact_reference_tiny_spec()).  Only data is committed; re-running reproduces the
+files.
 
     python tests/golden/make_artifact_golden.py
 """
@@ -74,14 +77,16 @@ def main() -> None:
         raise SystemExit(f"reference writer failed: {rc}")
     np.savez(os.path.join(HERE, "artifact_gfx1200_small.npz"), **arrays)
     print("wrote", path, os.path.getsize(path), "bytes")
-    write_tiny_model()
+    from gfxinfer_amd.runtime import artifact_reference_tiny_spec, artifact_tiny_spec
+    write_tiny_model(artifact_tiny_spec(), "artifact_gfx1200_tiny_model.gfxi")
+    write_tiny_model(artifact_reference_tiny_spec(), "artifact_gfx1200_reference_shape_model.gfxi")
 
 
-def write_tiny_model() -> None:
-    """The synthetic model of artifact_tiny_spec() as the reference converter would write it."""
-    from gfxinfer_amd.runtime import artifact_tiny_spec, spec_tensors
+def write_tiny_model(spec, filename) -> None:
+    """The synthetic model of `spec` as the reference converter would write it."""
+    from gfxinfer_amd.runtime import spec_tensors
     tensors = []
-    for t in spec_tensors(artifact_tiny_spec()):
+    for t in spec_tensors(spec):
         name, fmt, rows, cols = t["name"], t["format"], t["rows"], t["columns"]
         values = O.synthetic_values(MODEL_SEED, name, rows * cols, t["sigma"], t["mean"])
         if fmt == 0:
@@ -94,7 +99,7 @@ def write_tiny_model() -> None:
         tiled, tscales = O.ref_tile_gfx12(codes, scales, rows, cols, fmt)
         tensors.append(dict(name=name, dtype=1, quantization=fmt, dims=(rows, cols), data=tiled.tobytes(),
                             aux=O.f32_to_f16_bits(tscales).tobytes()))
-    path = os.path.join(HERE, "artifact_gfx1200_tiny_model.gfxi")
+    path = os.path.join(HERE, filename)
     if os.path.exists(path):
         os.remove(path)
     rc = O.ref_write_artifact(path, ("gfx1200", "qwen3.8-27b", f"synthetic-{MODEL_SEED}", RECIPE), tensors)

@@ -113,6 +113,61 @@ def test_gfx1200_artifact_from_reference_writer(device):
         generated.close()
 
 
+def test_reference_shape_artifact_loads_and_runs(device):
+    """tests/golden/artifact_gfx1200_reference_shape_model.gfxi: a model of the reference's
+    own head shapes (256-dim attention heads, six query heads per KV head, rotary 64, GDN
+    16 key / 48 value heads; qwen38_spec.h:22-29) written in this repository's CPU
+    container by the reference's quantizer, gfx12 tiler and ArtifactWriter.  It loads into
+    the arena the device generator fills for the same spec, and a verifier block and an
+    MTP proposal on it match the CPU model oracle (logits within 2e-2)."""
+    import os
+    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, artifact_reference_tiny_spec, spec_tensors
+    from oracle.model import OracleModel, OracleSession
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "artifact_gfx1200_reference_shape_model.gfxi")
+    spec = artifact_reference_tiny_spec()
+    say("load the reference-shaped gfx1200 artifact")
+    loaded = SyntheticModel.from_artifact(spec, path)
+    generated = SyntheticModel(spec, SEED)
+    try:
+        names = [(t["name"], max(t["format"], 0), None) for t in spec_tensors(spec)]
+        _same_arena(generated, loaded, names)
+        V, Vt = spec.vocabulary_size, spec.tokenizer_vocabulary_size
+        oracle = OracleSession(OracleModel(spec.as_dict(), SEED), 64)
+        s = QwenDecodeSession(loaded, 64, 0, keep_logits=True)
+        try:
+            block = [5, 77, 201, 9, 130]
+            say("reference-shaped block step")
+            got = s.block_step(block)
+            want, want_logits = oracle.block_step(block)
+            logits = s.buffer("logits", np.float32, len(block) * V).reshape(len(block), V)
+            assert np.abs(logits - want_logits).max() <= 2e-2
+            assert float(want_logits.std()) > 0.01
+            top2 = np.sort(want_logits[:, :Vt], axis=1)[:, -2:]
+            sure = top2[:, 1] - top2[:, 0] > 4e-2
+            assert np.array_equal(np.asarray(got)[sure], np.asarray(want)[sure])
+        finally:
+            s.close()
+        oracle = OracleSession(OracleModel(spec.as_dict(), SEED), 64)
+        s = QwenDecodeSession(loaded, 64, 0, keep_logits=True)
+        try:
+            say("reference-shaped greedy step + MTP proposal")
+            first = s.greedy_step(42)
+            want_first, _ = oracle.block_step([42])
+            draft = s.mtp_draft(first)
+            want_draft, draft_logits, _ = oracle.mtp_proposal(first, oracle.last_hidden, 0)
+            got_logits = s.buffer("logits", np.float32, spec.mtp_draft_vocabulary)
+            assert np.abs(got_logits - draft_logits[0]).max() <= 2e-2
+            top2 = np.sort(draft_logits[0])[-2:]
+            if top2[1] - top2[0] > 4e-2:
+                assert draft == want_draft
+        finally:
+            s.close()
+    finally:
+        loaded.close()
+        generated.close()
+
+
 def test_draft_head_artifact_uses_token_ids(model, tmp_path):
     from gfxinfer_amd.runtime import SyntheticModel
     spec = _spec()

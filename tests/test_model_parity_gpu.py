@@ -1,8 +1,11 @@
 """End-to-end parity of the GPU decode session against the model-level CPU oracle
-(oracle/model.py) on a small synthetic model of the same structure: logits of
+(oracle/model.py) on small synthetic models of the same structure: logits of
 block steps (fresh state, then with K/V caches and GDN state carried over) and of an
 MTP proposal within the BASELINE logit tolerance 2e-2 absolute, greedy tokens equal
-wherever the oracle's top-1/top-2 margin exceeds twice that tolerance."""
+wherever the oracle's top-1/top-2 margin exceeds twice that tolerance.  Two head
+shapes: 128-dim attention heads with GDN ratio 4 (the BASELINE model's kind), and the
+reference model's own 256-dim heads, six query heads per KV head, rotary 64 and GDN
+16 key / 48 value heads (qwen38_spec.h:22-29)."""
 import numpy as np
 import pytest
 
@@ -14,37 +17,40 @@ SEED = 4321
 LOGIT_TOL = 2e-2
 
 
-def _spec():
-    from gfxinfer_amd.runtime import tiny_spec
+def _spec(shape="baseline"):
+    from gfxinfer_amd.runtime import reference_tiny_spec, tiny_spec
+    if shape == "reference":
+        return reference_tiny_spec()
     return tiny_spec(full_attention_interval=2, gdn_key_head_count=4)
 
 
-@pytest.fixture(scope="module")
-def pair(device):
+@pytest.fixture(scope="module", params=["baseline", "reference"])
+def pair(device, request):
     from gfxinfer_amd.runtime import SyntheticModel
     from oracle.model import OracleModel
-    spec = _spec()
-    say("tiny model for oracle parity")
+    spec = _spec(request.param)
+    say("tiny model for oracle parity", request.param)
     gpu = SyntheticModel(spec, SEED)
     cpu = OracleModel(spec.as_dict(), SEED)
-    yield gpu, cpu
+    yield gpu, cpu, spec
     gpu.close()
 
 
-def _check_tokens(got, logits):
+def _check_tokens(got, logits, some_sure=True):
+    """Tokens equal the oracle's argmax wherever its top-2 margin exceeds twice the logit
+    bar; some_sure: at least one such row (a block), not required of a single row."""
     top2 = np.sort(logits, axis=1)[:, -2:]
     margin = top2[:, 1] - top2[:, 0]
     want = np.argmax(logits, axis=1)
     sure = margin > 2 * LOGIT_TOL
-    assert sure.any()
+    assert sure.any() or not some_sure
     assert np.array_equal(np.asarray(got)[sure], want[sure])
 
 
 def test_block_steps_match_oracle(pair):
     from gfxinfer_amd.runtime import QwenDecodeSession
     from oracle.model import OracleSession
-    gpu, cpu = pair
-    spec = _spec()
+    gpu, cpu, spec = pair
     V, Vt = spec.vocabulary_size, spec.tokenizer_vocabulary_size
     s = QwenDecodeSession(gpu, 64, 0, keep_logits=True)
     o = OracleSession(cpu, 64)
@@ -63,8 +69,7 @@ def test_block_steps_match_oracle(pair):
 def test_mtp_proposal_matches_oracle(pair):
     from gfxinfer_amd.runtime import QwenDecodeSession
     from oracle.model import OracleSession
-    gpu, cpu = pair
-    spec = _spec()
+    gpu, cpu, spec = pair
     s = QwenDecodeSession(gpu, 64, 0, keep_logits=True)
     o = OracleSession(cpu, 64)
     first = s.greedy_step(77)
@@ -76,4 +81,4 @@ def test_mtp_proposal_matches_oracle(pair):
     logits = s.buffer("logits", np.float32, spec.mtp_draft_vocabulary)
     err = np.abs(logits - want_logits[0]).max()
     assert err <= LOGIT_TOL, err
-    _check_tokens([draft], want_logits)
+    _check_tokens([draft], want_logits, some_sure=False)

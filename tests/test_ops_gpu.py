@@ -266,9 +266,14 @@ def test_silu_multiply_quantize(device, gx, orc, batch):
 
 HK, HV, D = 16, 32, 128
 C = 2 * HK * D + HV * D
+# BASELINE config 4 (32 value heads) and the reference model's 48 value / 16 key heads
+# (qwen38_spec.h:26-29: 10240 conv channels, three value heads per key head).
+GDN_SHAPES = [(16, 32), (16, 48)]
 
 
-def _gdn_inputs(seed, T):
+def _gdn_inputs(seed, T, hk=HK, hv=HV):
+    HK, HV = hk, hv
+    C = 2 * HK * D + HV * D
     rng = np.random.default_rng(seed)
     qkv = _half(rng.standard_normal((T, C)))
     z = rng.standard_normal((T, HV * D)).astype(np.float32)
@@ -281,7 +286,8 @@ def _gdn_inputs(seed, T):
     return qkv, z, a, b, a_log, dt_bias, norm_w, s0
 
 
-def _gpu_window(gx, d, T, s0, logs=True):
+def _gpu_window(gx, d, T, s0, logs=True, hk=HK, hv=HV):
+    HK, HV = hk, hv
     L = gx.lib()
     fin = empty((HV, D, D), np.float32)
     out = empty((T, HV * D), np.uint16)
@@ -295,10 +301,12 @@ def _gpu_window(gx, d, T, s0, logs=True):
     return fin, out, kl, dl, yl
 
 
-def test_gdn_window_matches_oracle(device, gx, orc):
-    """Hv=32, Hk=16, d=128, T=32 tokens."""
+@pytest.mark.parametrize("HK,HV", GDN_SHAPES)
+def test_gdn_window_matches_oracle(device, gx, orc, HK, HV):
+    """Hv=32, Hk=16, d=128, T=32 tokens; and the reference model's
+    Hv=48 (ratio 3)."""
     T = 32
-    qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(41, T)
+    qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(41, T, HK, HV)
     want_s = np.empty_like(s0)
     want_o = np.empty((T, HV * D), np.uint16)
     wk, wd, wy = np.empty((T, HK * D), np.float32), np.empty((T, HV * D), np.float32), np.empty((T, HV), np.float32)
@@ -306,8 +314,8 @@ def test_gdn_window_matches_oracle(device, gx, orc):
                                 orc.ptr(nw), orc.ptr(s0), orc.ptr(want_s), orc.ptr(want_o), orc.ptr(wk), orc.ptr(wd),
                                 orc.ptr(wy), T, HK, HV, D)
     d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
-    say("gdn window T=32")
-    fin, out, kl, dl, yl = _gpu_window(gx, d, T, dev(s0))
+    say("gdn window T=32", HK, HV)
+    fin, out, kl, dl, yl = _gpu_window(gx, d, T, dev(s0), hk=HK, hv=HV)
     got_s = host(fin)
     assert np.abs(got_s - want_s).max() <= 1e-5 * max(1.0, np.abs(want_s).max())
     assert np.abs(host(kl) - wk).max() <= 1e-6
@@ -342,23 +350,25 @@ def test_gdn_closed_forms(device, gx, orc):
         assert np.abs(host(fin)[h] - want).max() <= 1e-5
 
 
-@pytest.mark.parametrize("accepted", [1, 5, 17, 32])
-def test_gdn_rollback_equals_prefix_run(device, gx, orc, accepted):
+@pytest.mark.parametrize("accepted,HK,HV", [(1, 16, 32), (5, 16, 32), (17, 16, 32), (32, 16, 32),
+                                           (3, 16, 48), (29, 16, 48)])
+def test_gdn_rollback_equals_prefix_run(device, gx, orc, accepted, HK, HV):
     """restore(A) on the pre-window state == running only the first A tokens, bit for
     bit (same fp32 operations in the same order); also against the oracle replay."""
     T, layers = 32, 2
+    C = 2 * HK * D + HV * D
     L = gx.lib()
     conv_states, conv_logs, states = [], [], []
     key_logs, delta_logs, decay_logs, prefix_states, pre = [], [], [], [], []
     for layer in range(layers):
-        qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(100 + layer, T)
+        qkv, z, a, b, a_log, dt, nw, s0 = _gdn_inputs(100 + layer, T, HK, HV)
         d = dict(qkv=dev(qkv), z=dev(z), a=dev(a), b=dev(b), a_log=dev(a_log), dt=dev(dt), nw=dev(nw))
-        say("gdn rollback window", accepted, layer)
-        _, _, kl, dl, yl = _gpu_window(gx, d, T, dev(s0))
+        say("gdn rollback window", accepted, layer, HK, HV)
+        _, _, kl, dl, yl = _gpu_window(gx, d, T, dev(s0), hk=HK, hv=HV)
         key_logs.append(host(kl)); delta_logs.append(host(dl)); decay_logs.append(host(yl))
         dp = dict(qkv=dev(qkv[:accepted]), z=dev(z[:accepted]), a=dev(a[:accepted]), b=dev(b[:accepted]),
                   a_log=d["a_log"], dt=d["dt"], nw=d["nw"])
-        fin, *_ = _gpu_window(gx, dp, accepted, dev(s0), logs=False)
+        fin, *_ = _gpu_window(gx, dp, accepted, dev(s0), logs=False, hk=HK, hv=HV)
         prefix_states.append(host(fin))
         pre.append(s0)
         rng = np.random.default_rng(200 + layer)
@@ -434,10 +444,14 @@ def test_gdn_output_quantize(device, gx, orc):
 # ---- attention ---------------------------------------------------------------------
 
 HQ, HKV, AD = 40, 8, 128
+# BASELINE config 3 (40/8 x 128) and the reference model's 24/4 x 256 (qwen38_spec.h:22-25).
+ATTN_SHAPES = [(40, 8, 128), (24, 4, 256)]
 
 
-@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 64), (32, 4065), (5, 1), (32, 1), (3, 63), (8, 60)])
-def test_attention_matches_oracle(device, gx, orc, T, base):
+@pytest.mark.parametrize("HQ,HKV,AD", ATTN_SHAPES)
+@pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 64), (32, 4065), (5, 1), (32, 1), (3, 63), (8, 60),
+                                    (1, 1), (5, 4065)])
+def test_attention_matches_oracle(device, gx, orc, T, base, HQ, HKV, AD):
     capacity = 4096 + 32
     rng = np.random.default_rng(T * 7 + base)
     q = _half(rng.standard_normal((T, HQ, AD)))
@@ -451,10 +465,10 @@ def test_attention_matches_oracle(device, gx, orc, T, base):
     orc.lib().orc_gated_attention(orc.ptr(q), orc.ptr(gate), orc.ptr(kc), orc.ptr(vc), orc.ptr(want), base, T, HQ, HKV, AD,
                                   np.float32(1 / np.sqrt(AD)))
     L = gx.lib()
-    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, capacity)
+    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, AD, capacity)
     work = empty((wb // 4,), np.float32)
     out = empty((T, HQ, AD), np.uint16)
-    say("attention", T, base)
+    say("attention", T, base, HQ, HKV, AD)
     gx.check(L.gfxinfer_launch_gated_attention_decode_block(D_(q), D_(gate), D_(kc),
                                                             D_(vc), out.data_ptr(), base, capacity, T, HQ, HKV,
                                                             AD, work.data_ptr(), wb, None))
@@ -468,8 +482,9 @@ def test_attention_matches_oracle(device, gx, orc, T, base):
     assert np.array_equal(host(out2, np.uint16), host(out, np.uint16))
 
 
+@pytest.mark.parametrize("HQ,HKV,AD", ATTN_SHAPES)
 @pytest.mark.parametrize("T,base", [(5, 200), (32, 1000), (1, 1)])
-def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base):
+def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base, HQ, HKV, AD):
     """Attention with the A4 quantizer in its combine launch == attention followed by
     gfxinfer_launch_quantize_activation_i4 on its fp16 output: same output, codes and
     scales bit for bit (direct and device position)."""
@@ -483,12 +498,12 @@ def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base)
     kc[:n] = _half(rng.standard_normal((n, HKV, AD)))
     vc[:n] = _half(rng.standard_normal((n, HKV, AD)))
     L = gx.lib()
-    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, capacity)
+    wb = L.gfxinfer_attention_workspace_bytes(T, HQ, AD, capacity)
     work = empty((wb // 4,), np.float32)
     out = empty((T, HQ, AD), np.uint16)
-    codes, scales = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ), np.uint16)
+    codes, scales = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ * AD // 128), np.uint16)
     dq, dg, dk, dv = D_(q), D_(gate), D_(kc), D_(vc)
-    say("attention then quantizer", T, base)
+    say("attention then quantizer", T, base, HQ, HKV, AD)
     gx.check(L.gfxinfer_launch_gated_attention_decode_block(dq, dg, dk, dv, out.data_ptr(), base, capacity, T, HQ,
                                                             HKV, AD, work.data_ptr(), wb, None))
     gx.check(L.gfxinfer_launch_quantize_activation_i4(out.data_ptr(), codes.data_ptr(), scales.data_ptr(),
@@ -497,7 +512,7 @@ def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base)
     pos = dev(np.array([base - 1], np.uint64))
     for indirect in (False, True):
         out2 = empty((T, HQ, AD), np.uint16)
-        codes2, scales2 = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ), np.uint16)
+        codes2, scales2 = empty((T, HQ * AD // 2), np.uint8), empty((T, HQ * AD // 128), np.uint16)
         say("attention + quantizer", T, base, indirect)
         if indirect:
             gx.check(L.gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position(
@@ -515,8 +530,10 @@ def test_attention_quantize_equals_attention_then_quantizer(device, gx, T, base)
         None) == gx.INVALID_ARGUMENT
 
 
-def test_qk_norm_rope_and_kv_append(device, gx, orc):
-    T, rot, theta, base = 5, 32, np.float32(1e7), 1234
+@pytest.mark.parametrize("HQ,HKV,AD,rot,T,base", [(40, 8, 128, 32, 5, 1234), (24, 4, 256, 64, 5, 1234),
+                                                  (24, 4, 256, 64, 32, 4064), (24, 4, 256, 64, 1, 0)])
+def test_qk_norm_rope_and_kv_append(device, gx, orc, HQ, HKV, AD, rot, T, base):
+    theta = np.float32(1e7)
     rng = np.random.default_rng(8)
     qin = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
     kin = rng.standard_normal((T, HKV, AD)).astype(np.float32)
@@ -526,7 +543,7 @@ def test_qk_norm_rope_and_kv_append(device, gx, orc):
     orc.lib().orc_head_norm_rope(orc.ptr(kin), AD, orc.ptr(kw), orc.ptr(wk), HKV, AD, rot, base, T, theta)
     L = gx.lib()
     qo, ko = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
-    say("qk norm rope")
+    say("qk norm rope", HQ, HKV, AD, rot, T, base)
     gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD,
                                                       D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD,
                                                       rot, base, T, theta, None))
@@ -539,23 +556,24 @@ def test_qk_norm_rope_and_kv_append(device, gx, orc):
         ko2.data_ptr(), HKV, AD, AD, rot, pos.data_ptr(), T, theta, None))
     assert np.array_equal(host(qo2, np.uint16), host(qo, np.uint16))
     # KV append
-    cap = 2048
+    cap = 4096 + 32
     kc, vc = empty((cap, HKV * AD), np.uint16), empty((cap, HKV * AD), np.uint16)
     val = rng.standard_normal((T, HKV * AD)).astype(np.float32)
     gx.check(L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), base, cap,
                                                T, HKV * AD, None))
     assert np.array_equal(host(kc, np.uint16)[base:base + T], host(ko, np.uint16).reshape(T, -1))
     assert np.array_equal(host(vc, np.uint16)[base:base + T], _half(val))
-    assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), cap - 2, cap,
+    assert L.gfxinfer_launch_kv_append_block(ko.data_ptr(), D_(val), kc.data_ptr(), vc.data_ptr(), cap - T + 1, cap,
                                              T, HKV * AD, None) == gx.INVALID_ARGUMENT
 
 
+@pytest.mark.parametrize("HQ,HKV,AD,rot", [(40, 8, 128, 32), (24, 4, 256, 64)])
 @pytest.mark.parametrize("T,base", [(5, 1234), (32, 7), (1, 2047)])
-def test_fused_rope_kv_append_equals_the_pair(device, gx, T, base):
+def test_fused_rope_kv_append_equals_the_pair(device, gx, T, base, HQ, HKV, AD, rot):
     """Q/K norm + RoPE with the K/V cache append in one launch == the two launches: the
     same q/k outputs and the same cache rows, bit for bit (direct and device position);
     the cache outside the block is untouched."""
-    rot, theta, cap = 32, np.float32(1e7), 2048
+    theta, cap = np.float32(1e7), 2048
     rng = np.random.default_rng(80 + T)
     qin = rng.standard_normal((T, HQ, 2 * AD)).astype(np.float32)
     kin = rng.standard_normal((T, HKV, AD)).astype(np.float32)
@@ -565,7 +583,7 @@ def test_fused_rope_kv_append_equals_the_pair(device, gx, T, base):
     L = gx.lib()
     qo, ko = empty((T, HQ, AD), np.uint16), empty((T, HKV, AD), np.uint16)
     kc, vc = dev(fill), dev(fill)
-    say("rope + kv append pair", T, base)
+    say("rope + kv append pair", T, base, HQ, HKV, AD)
     gx.check(L.gfxinfer_launch_qk_rms_norm_rope_block(D_(qin), D_(qw), qo.data_ptr(), HQ, 2 * AD,
                                                       D_(kin), D_(kw), ko.data_ptr(), HKV, AD, AD,
                                                       rot, base, T, theta, None))
@@ -618,10 +636,12 @@ def test_argmax_ties_and_mapping(device, gx, orc):
     assert int(host(one).view(np.uint32)[0]) == int(ids[np.argmax(logits[2, :98304])])
 
 
-@pytest.mark.parametrize("T", [1, 3, 5, 32])
-def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T):
+@pytest.mark.parametrize("T,HK,HV", [(1, 16, 32), (3, 16, 32), (5, 16, 32), (32, 16, 32), (5, 16, 48),
+                                     (32, 16, 48)])
+def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T, HK, HV):
     """The fused conv + recurrence launch reproduces gdn_conv_update_block followed by
     gdn_recurrent_window bit for bit (states, logs, unnormalized output)."""
+    C = 2 * HK * D + HV * D
     rng = np.random.default_rng(70 + T)
     proj = rng.standard_normal((T, C)).astype(np.float32)
     w = _bf16(rng.standard_normal((C, 4)) * 0.5)
@@ -639,7 +659,7 @@ def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T):
         sf = empty((HV, D, D), np.float32)
         mixed = empty((T, HV * D), np.float32)
         kl, dl, yl = empty((T, HK * D), np.float32), empty((T, HV * D), np.float32), empty((T, HV), np.float32)
-        say("gdn conv window", T, "fused" if fused else "two launches")
+        say("gdn conv window", T, HK, HV, "fused" if fused else "two launches")
         if fused:
             gx.check(L.gfxinfer_launch_gdn_conv_window(dp, dw, dc0, cf.data_ptr(), clog.data_ptr(), da, db, dal, ddt,
                                                        ds0, sf.data_ptr(), mixed.data_ptr(), kl.data_ptr(),
@@ -740,7 +760,7 @@ def test_single_token_launchers_equal_block_forms(device, gx, orc):
     vc = np.zeros((capacity, HKV, AD), np.uint16)
     kc[:count] = _half(rng.standard_normal((count, HKV, AD)))
     vc[:count] = _half(rng.standard_normal((count, HKV, AD)))
-    wb = L.gfxinfer_attention_workspace_bytes(1, HQ, capacity)
+    wb = L.gfxinfer_attention_workspace_bytes(1, HQ, AD, capacity)
     work = empty((wb // 4,), np.float32)
     o1, o2 = empty((1, HQ, AD), np.uint16), empty((1, HQ, AD), np.uint16)
     say("single attention vs block")

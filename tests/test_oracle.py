@@ -225,3 +225,19 @@ def test_dequant_dot_gemv_close_to_exact(orc):
     aq = a.astype(np.float64) * np.repeat(as16.view(np.float16).astype(np.float64), 128, axis=1)
     exact = aq @ wq.T
     assert np.allclose(y, exact, rtol=1e-4, atol=1e-6)
+
+
+def test_ptr_keeps_temporaries_alive(orc):
+    """orc.ptr() of a temporary (np.empty(...) inline, or a dtype conversion that copies)
+    keeps the array alive through the call: the oracle writes into it and the result is
+    readable afterwards through the pointer's own reference."""
+    import ctypes
+    import gc
+    x = np.arange(256, dtype=np.float64)  # converted (copied) to fp32 inline below
+    p_in = orc.ptr(np.ascontiguousarray(x, dtype=np.float32))
+    p_out = orc.ptr(np.empty(256, np.uint16))
+    gc.collect()
+    orc.lib().orc_f32_to_f16_array(p_in, p_out, 256)
+    back = np.ctypeslib.as_array(ctypes.cast(p_out, ctypes.POINTER(ctypes.c_uint16)), shape=(256,))
+    assert np.array_equal(back.view(np.float16).astype(np.float64), x)
+    assert orc.ptr(None) is None
