@@ -68,7 +68,6 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gfx950_i4_gemm_half": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, I32, P]),
     "gfxinfer_launch_gfx950_i4_gemm_fused": (I32, [I32, P, SZ, P, P, SZ, U32, I32, P]),
     "gfxinfer_launch_gfx950_i8_gemm": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, P]),
-    "gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4": (I32, [I32, P, P, P, P, P, P, P, P, P, P, SZ, SZ, U32, P, P]),
     "gfxinfer_gemm_argmax_workspace_bytes": (SZ, [SZ, U32]),
     "gfxinfer_launch_gfx950_i4_gemm_argmax": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, SZ, P, P]),
     "gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, P]),

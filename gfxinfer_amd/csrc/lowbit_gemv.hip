@@ -218,77 +218,7 @@ struct GemmArgs {
   // b / splits and writes fp32 plane `split` ([splits][batch][rows] per matrix); the
   // consumer sums the planes in plane order.  1 = one plane, the plain product.
   uint32_t splits;
-  // SwiGLU tail (matrix 0 = gate, matrix 1 = up, equal rows, one split): the workgroup
-  // that completes the last of the 16 tiles (8 gate + 8 up) of a 128-row group writes
-  // the A4 codes of fp16(silu(gate) * up) over that group, as silu_multiply_quantize_i4
-  // does.  group_counters[rows / 128] are zero at launch and left zero.
-  unsigned* group_counters;
-  uint8_t* swiglu_codes;   // [batch][rows / 2]
-  __half* swiglu_scales;   // [batch][rows / 128]
 };
-
-__device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
-
-// Device-coherent (agent-scope relaxed atomic) stores and loads: on gfx950 they are
-// global stores / loads with the sc1 bit, written through to and read from the device's
-// coherence point instead of a per-XCD L2, so a workgroup on another XCD sees them
-// without an L2 write-back or invalidation (which a device-scope fence would do, for
-// the whole L2, in every workgroup).
-__device__ __forceinline__ void coherent_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float coherent_load(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The SwiGLU + A4 step of one 128-row group (qwen_ops.hip:120-163, the arithmetic of
-// silu_multiply_kernel<true>): wave w of the finishing workgroup takes tokens w,
-// w + waves, ...; lane i the columns 2i, 2i + 1.  Every load of a pass of up to eight
-// tokens is issued before the first use.
-__device__ void swiglu_group(const GemmArgs& args, unsigned group, unsigned wave, unsigned waves,
-                             unsigned lane) {
-  constexpr unsigned kPass = 8;
-  const uint32_t rows = args.matrix[0].tiles * 16u;
-  const float* gate = static_cast<const float*>(args.matrix[0].output);
-  const float* up = static_cast<const float*>(args.matrix[1].output);
-  for (unsigned first = wave; first < args.batch; first += kPass * waves) {
-    float2 g[kPass], u[kPass];
-#pragma unroll
-    for (unsigned k = 0; k < kPass; ++k) {
-      const unsigned t = first + k * waves;
-      const std::size_t at = static_cast<std::size_t>(t < args.batch ? t : 0u) * rows + group * 128u + 2u * lane;
-      g[k].x = coherent_load(gate + at);
-      g[k].y = coherent_load(gate + at + 1);
-      u[k].x = coherent_load(up + at);
-      u[k].y = coherent_load(up + at + 1);
-    }
-#pragma unroll
-    for (unsigned k = 0; k < kPass; ++k) {
-      const unsigned t = first + k * waves;
-      if (t >= args.batch) break;  // wave-uniform
-      const __half p0 = to_half(silu(g[k].x) * u[k].x);
-      const __half p1 = to_half(silu(g[k].y) * u[k].y);
-      quantize_group_a4(p0, p1, args.swiglu_codes + static_cast<std::size_t>(t) * (rows / 2) + group * 64u,
-                        args.swiglu_scales + static_cast<std::size_t>(t) * (rows / 128) + group, lane);
-    }
-  }
-}
-
-// Arrival of the wave that stored `tiles_done` finished tiles of one 128-row group with
-// coherent stores: once those stores have completed, a device-scope counter counts the
-// group's tiles, and the wave that brings it to 16 reads the group with coherent loads
-// and runs its SwiGLU tail.  No wave waits for another workgroup; the workgroup's other
-// waves have already left.
-__device__ void swiglu_arrival(const GemmArgs& args, unsigned tile, unsigned tiles_done, unsigned lane) {
-  const unsigned group = tile / 8u;
-  __builtin_amdgcn_s_waitcnt(0);  // the coherent stores have completed
-  unsigned prev = 0u;
-  if (lane == 0) prev = atomicAdd(args.group_counters + group, tiles_done);
-  prev = __builtin_amdgcn_readfirstlane(prev);
-  if (prev + tiles_done != 16u) return;
-  swiglu_group(args, group, 0u, 1u, lane);
-  if (lane == 0) atomicExch(args.group_counters + group, 0u);
-}
 
 // Canonical summation over K.  Every GEMM variant adds the int32 group partials the
 // same way, so an output depends only on (row, token, K, splits): not on the batch,
@@ -466,10 +396,6 @@ __device__ __forceinline__ void gemm_store_tile(const GemmArgs& args, const Gemm
       __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[r] = to_half(total[t][r]);
-    } else if (args.group_counters != nullptr) {  // read by another workgroup's SwiGLU tail
-      float* o = reinterpret_cast<float*>(matrix.output) + out;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) coherent_store(o + r, total[t][r]);
     } else {
       float4 value = {total[t][0], total[t][1], total[t][2], total[t][3]};
       *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
@@ -785,7 +711,6 @@ __global__ __launch_bounds__((NTB == 2 || ABits == 8) ? 512 : 1024) void lowbit_
   }
   gemm_store_tile<GP, NTB, HalfOut>(args, matrix, total, ranges, lane, layout.results_offset, tile, split,
                                     rows);
-  if (args.group_counters != nullptr) swiglu_arrival(args, tile, 1u, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1259,17 +1184,12 @@ __device__ __forceinline__ void direct_finish(const GemmArgs& args, const GemmMa
         __half* o = reinterpret_cast<__half*>(matrix.output) + out;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = to_half(total[r][t][i]);
-      } else if (args.group_counters != nullptr) {  // read by another workgroup's SwiGLU tail
-        float* o = reinterpret_cast<float*>(matrix.output) + out;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) coherent_store(o + i, total[r][t][i]);
       } else {
         float4 value = {total[r][t][0], total[r][t][1], total[r][t][2], total[r][t][3]};
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(matrix.output) + out) = value;
       }
     }
   }
-  if (args.group_counters != nullptr) swiglu_arrival(args, tile0, valid, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1353,84 +1273,15 @@ bool aligned(const void* pointer, std::size_t bytes) {
   return (reinterpret_cast<std::uintptr_t>(pointer) % bytes) == 0;
 }
 
-// GFXI_GEMM_WAVES (1..16) overrides the waves per workgroup; a tuning knob.
-int waves_override() {
-  static const int value = [] {
-    const char* text = std::getenv("GFXI_GEMM_WAVES");
-    const int v = text != nullptr ? std::atoi(text) : 0;
-    return v >= 1 && v <= 16 ? v : 0;
-  }();
-  return value;
-}
-
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per CU (and per workgroup)
 constexpr uint32_t kMaxSplits = 8;            // split-K planes per GEMM
 
-unsigned choose_waves(uint32_t groups, unsigned gp) {
-  if (const int forced = waves_override(); forced != 0) return static_cast<unsigned>(forced);
-  (void)gp;
-  unsigned waves = (groups + 9) / 10;  // about ten groups (one load chunk) per wave
+// Waves per workgroup: about ten groups of K (one load chunk) per wave.
+unsigned choose_waves(uint32_t groups) {
+  unsigned waves = (groups + 9) / 10;
   if (waves < 1) waves = 1;
   if (waves > 16) waves = 16;
   return waves;
-}
-
-// GFXI_GEMM_KERNEL=lds|direct forces one kernel family (tuning knob).  The default
-// is the LDS-staged kernel up to 8 tokens and the direct-operand kernel above.
-int kernel_override() {  // 0 default, 1 lds everywhere, 2 direct everywhere
-  static const int value = [] {
-    const char* text = std::getenv("GFXI_GEMM_KERNEL");
-    if (text == nullptr) return 0;
-    const std::string v(text);
-    return v == "lds" ? 1 : v == "direct" ? 2 : 0;
-  }();
-  return value;
-}
-
-// GFXI_GEMM_ROWTILES (1..5) overrides the direct kernel's row tiles x chunk groups
-// (tuning knob; the summation order does not depend on it).
-int rowtiles_override() {
-  static const int value = [] {
-    const char* text = std::getenv("GFXI_GEMM_ROWTILES");
-    const int v = text != nullptr ? std::atoi(text) : 0;
-    return v >= 1 && v <= 5 ? v : 0;
-  }();
-  return value;
-}
-
-// GFXI_GEMM_RESIDENT=1 caps the direct kernel's waves per workgroup so that the whole
-// grid is resident at once (tuning knob, off by default: with one wave per range of
-// the canonical K order the uncapped grids measured equal or faster).
-bool resident_cap() {
-  static const bool value = [] {
-    const char* text = std::getenv("GFXI_GEMM_RESIDENT");
-    return text != nullptr && std::atoi(text) != 0;
-  }();
-  return value;
-}
-
-// Waves per workgroup: about ten groups of K per wave; with the residency cap on, no
-// more than lets every workgroup of the grid be resident at once.
-unsigned resident_waves(const void* kernel, uint32_t groups, uint32_t blocks, std::size_t lds_bytes) {
-  unsigned want = choose_waves(groups, 1);
-  if (waves_override() != 0 || !resident_cap()) return want;
-  static int cus = [] {
-    int device = 0, count = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
-      return 256;
-    }
-    return count;
-  }();
-  for (unsigned w = want; w >= 1; --w) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, static_cast<int>(64 * w),
-                                                     lds_bytes) != hipSuccess) {
-      return want;
-    }
-    if (static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus) >= blocks) return w;
-  }
-  return want;
 }
 
 template <int Format, int ABits, bool HalfOut, bool Partials>
@@ -1453,10 +1304,9 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
     }
     // range values of the canonical K partition, summed in order at the end
     const std::size_t lds = max_ranges > 1 ? static_cast<std::size_t>(max_ranges) * r * ntb * 4u * 64u * 4u : 0;
-    const unsigned waves = std::min(
-        {resident_waves(reinterpret_cast<const void*>(kernel), args.groups / args.splits, blocks * args.splits,
-                        lds),
-         min_range_count(args.groups, args.splits), kDirectMaxWaves});
+    const unsigned waves =
+        std::min({choose_waves(args.groups / args.splits), min_range_count(args.groups, args.splits),
+                  kDirectMaxWaves});
     hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), lds, stream, args);
   };
   // Row tiles per wave (R) and groups per load chunk (CH), by grid shape (measured on
@@ -1469,28 +1319,22 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
   //   1024..2047 (down as four splits): 3 tiles, 3-group chunks (16.0 -> 14.3 us);
   //   < 1024 (q/k/v, GDN in-projection): 2 tiles, 2-group chunks at 17-32 tokens
   //   (15.3 -> 12.2 us), 2 tiles of 5-group chunks at 9-16 tokens.
-  // GFXI_GEMM_ROWTILES (1, 2 or 3) forces 1 tile x 4 groups, 2 x 5 or 3 x 2.
   uint64_t tile_splits = 0;
   for (unsigned i = 0; i < 4; ++i) {
     const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
     if (used) tile_splits += static_cast<uint64_t>(base_args.matrix[i].tiles) * base_args.splits;
   }
   const bool one_range = min_range_count(base_args.groups, base_args.splits) <= 1;
-  int shape = rowtiles_override();  // 1: 1 x 4, 2: 2 x 5, 3: 3 x 2, 4: 3 x 3, 5: 2 x 2
-  if (shape == 0) {
-    if (one_range) {
-      shape = 1;
-    } else if (tile_splits >= 2048) {
-      shape = 3;
-    } else if (tile_splits >= 1024) {
-      shape = 4;
-    } else {
-      shape = batch > 16 ? 5 : 2;
-    }
+  int shape;  // 1: 1 x 4, 2: 2 x 5, 3: 3 x 2, 4: 3 x 3, 5: 2 x 2
+  if (one_range) {
+    shape = 1;
+  } else if (tile_splits >= 2048) {
+    shape = 3;
+  } else if (tile_splits >= 1024) {
+    shape = 4;
+  } else {
+    shape = batch > 16 ? 5 : 2;
   }
-  // The SwiGLU tail counts finished tiles per 128-row group (8 tiles): a workgroup's
-  // tiles must not straddle two groups, so three-tile shapes fall back to two tiles.
-  if (base_args.group_counters != nullptr && (shape == 3 || shape == 4)) shape = batch > 16 ? 5 : 2;
   (void)total_tiles;
   if (batch <= 4) {
     go(lowbit_gemm_direct_kernel<Format, ABits, 4, 1, 3, 1, HalfOut, Partials>, 1, 1);
@@ -1521,8 +1365,7 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
   // Direct operands pay off from 9 tokens on (one token window, quad-coalesced
   // activation loads, two row tiles per workgroup); up to 8 tokens the LDS-staged
   // kernel with its packed token windows is as fast or faster.
-  const int forced = kernel_override();
-  if (forced == 2 || (forced == 0 && args.batch > 8)) {
+  if (args.batch > 8) {
     launch_direct_kernel<Format, ABits, HalfOut, Partials>(args, total_tiles, stream);
     return;
   }
@@ -1530,8 +1373,7 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
   auto go = [&](auto kernel, unsigned gp, unsigned ch, unsigned ntb) {
     // One wave per range of the canonical K partition (at most the fewest ranges of
     // any split), within the register and LDS limits.
-    unsigned waves = std::min(choose_waves(args.groups / args.splits, 1),
-                              min_range_count(args.groups, args.splits));
+    unsigned waves = std::min(choose_waves(args.groups / args.splits), min_range_count(args.groups, args.splits));
     if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
     GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
     unsigned max_ranges = 1;
@@ -1584,8 +1426,7 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
                    const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
                    uint32_t batch, bool half_out, hipStream_t stream,
                    unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0,
-                   uint32_t splits = 1, unsigned* group_counters = nullptr,
-                   uint8_t* swiglu_codes = nullptr, uint16_t* swiglu_scales = nullptr) {
+                   uint32_t splits = 1) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W2G128, W3G128 and W4G128");
   }
@@ -1643,9 +1484,6 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
   args.groups = static_cast<uint32_t>(columns / kGroup);
   args.batch = batch;
   args.splits = splits;
-  args.group_counters = group_counters;
-  args.swiglu_codes = swiglu_codes;
-  args.swiglu_scales = reinterpret_cast<__half*>(swiglu_scales);
   if (tiles * splits > std::numeric_limits<uint32_t>::max() / 2) {
     return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " grid is too large");
   }
@@ -1792,13 +1630,9 @@ extern "C" uint32_t gfxinfer_gemm_split_count(size_t rows, size_t columns, uint3
   // below that leaves CUs idle or runs a partial second round), each split keeping at
   // least eight groups of K.  The count depends on the shape only, never on the batch:
   // the split is part of the summation order, so a block of tokens and one-token
-  // steps must use the same one.  GFXI_GEMM_SPLIT_TARGET overrides the target (tuning
-  // knob; it changes the summation order of split GEMMs).
-  static const uint64_t target = [] {
-    const char* text = std::getenv("GFXI_GEMM_SPLIT_TARGET");
-    const long v = text != nullptr ? std::atol(text) : 0;
-    return v > 0 ? static_cast<uint64_t>(v) : uint64_t{1024};
-  }();
+  // steps must use the same one.  1024 workgroups: four planes for the 320-tile
+  // projections, the best of 1-5 planes in 27B verify rounds.
+  constexpr uint64_t target = 1024;
   (void)batch;
   if (rows == 0 || columns < kGroup) return 1;
   const uint64_t tiles = (rows + 15) / 16;
@@ -1855,24 +1689,6 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
   return gemm_entry("gfx950 fused INT4 GEMM", format, bindings, matrix_count, 4,
                     packed_activations, activation_scales, nullptr, columns, batch, false,
                     static_cast<hipStream_t>(stream));
-}
-
-extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4(
-    int32_t format, const uint8_t* gate_weights, const uint16_t* gate_scales, const uint8_t* up_weights,
-    const uint16_t* up_scales, const uint8_t* packed_activations, const uint16_t* activation_scales,
-    float* gate_output, float* up_output, uint8_t* packed_output, uint16_t* output_scales, size_t rows,
-    size_t columns, uint32_t batch, uint32_t* group_counters, void* stream) {
-  if (gate_output == nullptr || up_output == nullptr || packed_output == nullptr ||
-      output_scales == nullptr || group_counters == nullptr || rows == 0 || rows % kGroup != 0 ||
-      !aligned(gate_output, 16) || !aligned(up_output, 16) || !aligned(group_counters, 4)) {
-    return fail(GFXI_INVALID_ARGUMENT, "fused gate/up GEMM + SwiGLU needs gate/up outputs, A4 outputs, "
-                                       "rows divisible by 128 and a counter per 128 rows");
-  }
-  const MatrixBinding bindings[2] = {{gate_weights, gate_scales, gate_output, rows},
-                                     {up_weights, up_scales, up_output, rows}};
-  return gemm_entry("fused gate/up GEMM + SwiGLU", format, bindings, 2, 4, packed_activations,
-                    activation_scales, nullptr, columns, batch, false, static_cast<hipStream_t>(stream),
-                    nullptr, 0, 1, group_counters, packed_output, output_scales);
 }
 
 extern "C" size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch) {

@@ -307,8 +307,8 @@ struct gfxinfer_session {
         input, mixer_update, mixer_planes, post_attention, L.post_norm, nullptr, act_codes,
         act_scales, H, batch, spec.rms_norm_epsilon, 1, stream));
     GFXI_TRY(trace_post(L, batch));
-    // The gate/up grid and SwiGLU -> A4 stay two launches: the one-launch form
-    // (gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4, same codes) measured slower on
+    // The gate/up grid and SwiGLU -> A4 stay two launches: a one-launch form (the
+    // workgroup completing each 128-row group writing its codes) measured slower on
     // MI355X, its cross-workgroup completion costing more than the second launch.
     GFXI_TRY(gemm_fused({{&L.gate, gate_output}, {&L.up, up_output}}, batch));
     GFXI_TRY(gfxinfer_launch_silu_multiply_quantize_i4(gate_output, up_output, mlp_codes,

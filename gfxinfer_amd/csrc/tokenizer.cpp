@@ -325,7 +325,9 @@ const ByteAlphabet& alphabet() {
 bool is_letter(uint32_t c) { return (U_GET_GC_MASK(static_cast<UChar32>(c)) & U_GC_L_MASK) != 0; }
 bool is_mark(uint32_t c) { return (U_GET_GC_MASK(static_cast<UChar32>(c)) & U_GC_M_MASK) != 0; }
 bool is_number(uint32_t c) { return (U_GET_GC_MASK(static_cast<UChar32>(c)) & U_GC_N_MASK) != 0; }
-bool is_space(uint32_t c) { return u_isUWhiteSpace(static_cast<UChar32>(c)) != 0; }
+// \s under PCRE2_UCP (the reference's regex engine, tokenizer.cpp:143-146): \p{Z}, \h and
+// \v, i.e. Unicode White_Space plus U+180E, which PCRE2 keeps in \h.
+bool is_space(uint32_t c) { return c == 0x180Eu || u_isUWhiteSpace(static_cast<UChar32>(c)) != 0; }
 bool is_newline(uint32_t c) { return c == '\r' || c == '\n'; }
 
 // Case-insensitive match of an ASCII letter (s also matches U+017F, which case-folds

@@ -149,21 +149,6 @@ int32_t gfxinfer_launch_gfx950_i4_gemm_fused(int32_t format,
                                              uint32_t batch, int32_t sequential_w3,
                                              void* stream);
 
-/* The MLP's gate/up projections and SwiGLU -> A4 in one launch: gate and up outputs fp32
- * [batch, rows] as gfxinfer_launch_gfx950_i4_gemm_fused writes them, and the A4 codes
- * [batch, rows/2] + fp16 scales [batch, rows/128] of fp16(silu(gate) * up) that
- * gfxinfer_launch_silu_multiply_quantize_i4 makes from them, bit for bit.  The workgroup
- * finishing the last tile of a 128-row group (counted in group_counters, rows/128 words
- * that must be zero before the first call and are left zero) writes that group's codes;
- * no workgroup waits for another.  Calls that overlap on one counter array race.  No
- * reference counterpart: the reference launches the pair (qwen_runtime.cpp:331-347,
- * 519-544; qwen_ops.hip:120-163). */
-int32_t gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4(
-    int32_t format, const uint8_t* gate_weights, const uint16_t* gate_scales, const uint8_t* up_weights,
-    const uint16_t* up_scales, const uint8_t* packed_activations, const uint16_t* activation_scales,
-    float* gate_output, float* up_output, uint8_t* packed_output, uint16_t* output_scales, size_t rows,
-    size_t columns, uint32_t batch, uint32_t* group_counters, void* stream);
-
 /* Bytes of workspace gfxinfer_launch_gfx950_i4_gemm_argmax needs: one 8-byte key per
  * (token, 16-row tile). */
 size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch);

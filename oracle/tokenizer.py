@@ -13,8 +13,12 @@ A restatement, in Python, of /root/reference/src/tokenizer.cpp:
                            BPE-merged; the best-ranked pair is joined at every
                            non-overlapping occurrence, left to right, until none is left)
 NFC comes from `unicodedata` (the reference uses ICU) and the pattern runs on the
-`regex` module (the reference uses PCRE2 with UTF/UCP); both are pinned against HF
-`tokenizers` on the committed fixture in tests/test_tokenizer.py.
+`regex` module (the reference uses PCRE2 with UTF/UCP).  Under PCRE2_UCP, \s is
+\p{Z} plus \h plus \v, which is Unicode White_Space plus U+180E (MONGOLIAN VOWEL
+SEPARATOR, kept in PCRE2's \h); `regex`'s \s is White_Space alone, so the pattern below
+spells \s as [\s\u180E] and \S as its complement.  The split is pinned against PCRE2
+itself (the system libpcre2-8, the library the reference links) and the whole encoder
+against HF `tokenizers` on the committed fixture in tests/test_tokenizer.py.
 """
 from __future__ import annotations
 
@@ -25,7 +29,12 @@ import regex
 
 PATTERN = regex.compile(
     r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?[\p{L}\p{M}]+|\p{N}"
-    r"| ?[^\s\p{L}\p{M}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+")
+    r"| ?[^\s\u180E\p{L}\p{M}\p{N}]+[\r\n]*|[\s\u180E]*[\r\n]+|[\s\u180E]+(?![^\s\u180E])|[\s\u180E]+")
+
+
+def pretokens(text: str) -> list[str]:
+    """The pre-token split of already-normalized text (tokenizer.cpp:135-172)."""
+    return PATTERN.findall(text)
 
 
 def byte_alphabet() -> list[str]:
@@ -93,7 +102,7 @@ class OracleTokenizer:
 
     def _segment(self, text: str) -> list[int]:
         out = []
-        for piece in PATTERN.findall(unicodedata.normalize("NFC", text)):
+        for piece in pretokens(unicodedata.normalize("NFC", text)):
             out.extend(self._bpe(piece))
         return out
 

@@ -428,35 +428,3 @@ def test_stream_read_floor_entry(gx, device):
         with pytest.raises(gx.GfxinferError):
             gx.debug_stream_read(data, nbytes, sink, width)
 
-
-@pytest.mark.parametrize("fmt,rows,cols,batch", [
-    (2, 17408, 5120, 5), (2, 17408, 5120, 1), (3, 17408, 5120, 32), (2, 17408, 5120, 16),
-    (3, 512, 256, 3), (2, 1024, 1280, 9), (3, 384, 640, 24)])
-def test_gemm_swiglu_equals_fused_gemm_then_silu(device, gx, orc, fmt, rows, cols, batch):
-    """gate/up GEMM with the SwiGLU -> A4 tail in one launch == the fused gate/up GEMM
-    followed by silu_multiply_quantize_i4, bit for bit, on two calls in a row (the
-    group counters are left zero for the next call)."""
-    L = gx.lib()
-    g = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=rows + batch)
-    u = _problem(orc, gx, fmt, 4, rows, cols, batch, seed=rows + batch + 1)
-    dgw, dgs, duw, dus = dev(g["tiled"]), dev(g["tscales"]), dev(u["tiled"]), dev(u["tscales"])
-    da, das = dev(g["acts"]), dev(g["as16"])
-    want_g, want_u = empty((batch, rows), np.float32), empty((batch, rows), np.float32)
-    want_c, want_s = empty((batch, rows // 2), np.uint8), empty((batch, rows // 128), np.uint16)
-    say("gate/up pair + SwiGLU launches", fmt, rows, cols, batch)
-    gx.launch_i4_gemm_fused(fmt, [(dgw, dgs, want_g, rows), (duw, dus, want_u, rows)], da, das, cols, batch)
-    gx.check(L.gfxinfer_launch_silu_multiply_quantize_i4(want_g.data_ptr(), want_u.data_ptr(), want_c.data_ptr(),
-                                                         want_s.data_ptr(), rows, batch, None))
-    counters = empty((rows // 128,), np.uint32)
-    for call in range(2):
-        got_g, got_u = empty((batch, rows), np.float32), empty((batch, rows), np.float32)
-        got_c, got_s = empty((batch, rows // 2), np.uint8), empty((batch, rows // 128), np.uint16)
-        say("gate/up GEMM + SwiGLU in one launch", call)
-        gx.check(L.gfxinfer_launch_gfx950_i4_gemm_swiglu_quantize_i4(
-            fmt, dgw.data_ptr(), dgs.data_ptr(), duw.data_ptr(), dus.data_ptr(), da.data_ptr(), das.data_ptr(),
-            got_g.data_ptr(), got_u.data_ptr(), got_c.data_ptr(), got_s.data_ptr(), rows, cols, batch,
-            counters.data_ptr(), None))
-        assert np.array_equal(host(got_g), host(want_g)) and np.array_equal(host(got_u), host(want_u))
-        assert np.array_equal(host(got_c), host(want_c))
-        assert np.array_equal(host(got_s, np.uint16), host(want_s, np.uint16))
-        assert not host(counters, np.uint32).any()

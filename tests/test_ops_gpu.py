@@ -393,12 +393,19 @@ def test_gdn_rollback_equals_prefix_run(device, gx, orc, accepted, HK, HV):
         assert np.array_equal(host(cs, np.uint16)[layer], wc)
 
 
-def test_gdn_restore_rejects_bad_accept(gx):
-    fake = 1 << 20
+def test_gdn_restore_rejects_bad_accept(device, gx):
+    """Accepted counts of 0 or above the logged tokens, and more than 32 logged tokens,
+    are rejected before any launch (real buffers, sized for 64 logged tokens)."""
     L = gx.lib()
-    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
-    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 32, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
-    assert L.gfxinfer_launch_gdn_restore_prefix_all(fake, fake, fake, fake, fake, fake, C, 2, 64, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    layers, logged = 2, 64
+    bufs = [empty((layers, C, 4), np.uint16), empty((layers, HV, D, D), np.float32),
+            empty((layers, logged, C), np.uint16), empty((layers, logged, HK * D), np.float32),
+            empty((layers, logged, HV * D), np.float32), empty((layers, logged, HV), np.float32)]
+    ptrs = [b.data_ptr() for b in bufs]
+    say("gdn restore rejects bad accepted counts")
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(*ptrs, C, layers, 32, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(*ptrs, C, layers, 32, 0, HK, HV, D, None) == gx.INVALID_ARGUMENT
+    assert L.gfxinfer_launch_gdn_restore_prefix_all(*ptrs, C, layers, 64, 33, HK, HV, D, None) == gx.INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("T,in_place", [(32, False), (5, True), (1, True)])

@@ -2,8 +2,9 @@
 cli/main.cpp:1037-1039): the library (C-ABI, gfxinfer_tokenizer_*) against the Python
 oracle (oracle/tokenizer.py), and the oracle pinned against HF `tokenizers` 0.22, an
 independent implementation of the tokenizer.json format, on the committed fixture
-tests/golden/tokenizer_small.json (written by tests/golden/make_tokenizer_fixture.py).
-CPU only."""
+tests/golden/tokenizer_small.json (written by tests/golden/make_tokenizer_fixture.py),
+and its pre-token split against PCRE2 itself (the system libpcre2-8 the reference links,
+with the reference's pattern and flags).  CPU only."""
 import json
 import os
 import random
@@ -50,6 +51,12 @@ def oracle(document):
     return OracleTokenizer(document)
 
 
+# U+180E is \s for PCRE2 with UCP (\h keeps it) but not for White_Space-based engines
+# such as HF's: these cases follow the reference's engine.
+MVS_CASES = ["a!\u180e", "x \u180e y", "\u180e\u180e\n", "word\u180e!!", "\u180e", "a\u180e\u180eb",
+             "!!\u180e\r\n", " \u180e  z"]
+
+
 def random_texts(count=300, seed=7):
     rng = random.Random(seed)
     pool = list("abcXYZ éèüßñ ΩЖ你好🙂 0123456789 .,!?'\"-_()[]{}<>/\\|@#$%^&*+=~` \t\n\r") + \
@@ -68,8 +75,64 @@ def test_oracle_matches_hf_tokenizers(document, oracle):
         assert oracle.decode_bytes(want).decode("utf-8") == hf.decode(want, skip_special_tokens=False)
 
 
+def _pcre2_split(lib, code, text: str) -> list[str]:
+    """split_pretokens (tokenizer.cpp:135-172): anchored matches from each offset."""
+    import ctypes
+    raw = text.encode("utf-8")
+    match = lib.pcre2_match_data_create_from_pattern_8(code, None)
+    out, offset = [], 0
+    try:
+        while offset < len(raw):
+            rc = lib.pcre2_match_8(code, raw, len(raw), offset, 0x80000000, match, None)  # PCRE2_ANCHORED
+            assert rc >= 1, (text, offset)
+            vec = ctypes.cast(lib.pcre2_get_ovector_pointer_8(match), ctypes.POINTER(ctypes.c_size_t))
+            assert vec[0] == offset and vec[1] > offset
+            out.append(raw[vec[0]:vec[1]].decode("utf-8"))
+            offset = vec[1]
+    finally:
+        lib.pcre2_match_data_free_8(match)
+    return out
+
+
+def test_oracle_pretokens_match_pcre2():
+    """The oracle's pre-token split equals PCRE2's with the reference's pattern and
+    flags (PCRE2_UTF | PCRE2_UCP, tokenizer.cpp:137-146), U+180E included."""
+    import ctypes
+    import ctypes.util
+    from oracle.tokenizer import pretokens
+    name = ctypes.util.find_library("pcre2-8") or "libpcre2-8.so.0"
+    try:
+        lib = ctypes.CDLL(name)
+    except OSError:
+        pytest.skip("libpcre2-8 is not installed")
+    P, SZ = ctypes.c_void_p, ctypes.c_size_t
+    lib.pcre2_compile_8.restype = P
+    lib.pcre2_compile_8.argtypes = [ctypes.c_char_p, SZ, ctypes.c_uint32, ctypes.POINTER(ctypes.c_int),
+                                    ctypes.POINTER(SZ), P]
+    lib.pcre2_match_data_create_from_pattern_8.restype = P
+    lib.pcre2_match_data_create_from_pattern_8.argtypes = [P, P]
+    lib.pcre2_match_8.restype = ctypes.c_int
+    lib.pcre2_match_8.argtypes = [P, ctypes.c_char_p, SZ, SZ, ctypes.c_uint32, P, P]
+    lib.pcre2_get_ovector_pointer_8.restype = P
+    lib.pcre2_get_ovector_pointer_8.argtypes = [P]
+    lib.pcre2_match_data_free_8.argtypes = [P]
+    lib.pcre2_code_free_8.argtypes = [P]
+    pattern = (r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?[\p{L}\p{M}]+|\p{N}"
+               r"| ?[^\s\p{L}\p{M}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+")
+    err, off = ctypes.c_int(0), SZ(0)
+    code = lib.pcre2_compile_8(pattern.encode(), SZ(-1).value, 0x00080000 | 0x00020000,  # UTF | UCP
+                               ctypes.byref(err), ctypes.byref(off), None)
+    assert code, err.value
+    try:
+        for text in CASES + MVS_CASES + random_texts(seed=17):
+            nfc = unicodedata.normalize("NFC", text)
+            assert pretokens(nfc) == _pcre2_split(lib, code, nfc), repr(text)
+    finally:
+        lib.pcre2_code_free_8(code)
+
+
 def test_library_matches_oracle(library, oracle):
-    for text in CASES + random_texts(seed=11):
+    for text in CASES + MVS_CASES + random_texts(seed=11):
         ids = library.encode(text)
         assert ids == oracle.encode(text), repr(text)
         assert library.decode_bytes(ids) == oracle.decode_bytes(ids)

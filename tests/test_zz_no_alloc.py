@@ -54,10 +54,18 @@ def test_no_alloc_head_equals_workspace_entry(device, gx, orc):
 
 
 def test_no_alloc_head_rejects_oversize(device, gx):
+    """Every caller buffer is real and sized for the shape (no made-up address reaches
+    the library); the key-count check rejects the shape before any launch."""
     L = gx.lib()
-    fake = 1 << 20  # never dereferenced: validation fails before any launch
-    rows, batch = 272000, 32  # 17000 tiles x 32 tokens > 524288 keys
-    rc = L.gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc(gx.W4G128, fake, fake, fake, fake, None, rows, 128,
-                                                          batch, rows, None, fake, None)
+    rows, cols, batch = 272000, 128, 32  # 17000 tiles x 32 tokens > 524288 keys
+    w = empty((rows * cols // 2,), np.uint8)          # W4 codes, 17.4 MB
+    ws = empty((rows * cols // 128,), np.uint16)      # fp16 weight scales
+    a = empty((batch, cols // 2), np.uint8)           # A4 codes
+    sa = empty((batch, cols // 128), np.uint16)       # fp16 activation scales
+    tokens = empty((batch,), np.uint32)
+    say("no-alloc head rejects an oversize shape")
+    rc = L.gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc(gx.W4G128, w.data_ptr(), ws.data_ptr(), a.data_ptr(),
+                                                          sa.data_ptr(), None, rows, cols, batch, rows, None,
+                                                          tokens.data_ptr(), None)
     assert rc == gx.INVALID_ARGUMENT
     assert "524288" in gx.last_error()
