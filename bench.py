@@ -130,7 +130,8 @@ def gemv_bench(steps, warmup, rows=17408, cols=5120, batch=5, copies=16, windows
 
 def verify_gemm_bench(batches=(5, 16, 32), budget=640e6, reps=20):
     """one dense decoder block's projection set in W3A4 (q/k/v from
-    hidden 5120 with 40 Q / 8 KV heads x 128, o, SwiGLU MLP 5120 -> 17408 -> 5120) at
+    hidden 5120 with 40 Q / 8 KV heads x 128 -- q the gated query + gate rows, 2 x 40 x 128
+    = 10240, as the verifier's q_proj --, o, SwiGLU MLP 5120 -> 17408 -> 5120) at
     k + 1 = 5, 16, 32 rows, launched the way the verifier launches them (q/k/v and
     gate/up fused into one grid each, o and down as split-K planes), and the W4 LM head
     [151936, 5120] with the fused greedy argmax.  Each launch is timed alone under graph
@@ -153,7 +154,7 @@ def verify_gemm_bench(batches=(5, 16, 32), budget=640e6, reps=20):
         return [(c0, s0)] + [(c0.clone(), s0.clone()) for _ in range(n - 1)]
 
     torch.manual_seed(0x5EED)
-    mats = {"q": (w3, H, H), "k": (w3, 1024, H), "v": (w3, 1024, H), "o": (w3, H, H),
+    mats = {"q": (w3, 2 * H, H), "k": (w3, 1024, H), "v": (w3, 1024, H), "o": (w3, H, H),
             "gate": (w3, I, H), "up": (w3, I, H), "down": (w3, H, I)}
     groups = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
     copies = {}
