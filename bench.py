@@ -307,11 +307,13 @@ def gemv_table_bench(reps=40, budget=600e6):
 
 
 def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
-    """Yardstick for the GEMV roofline: one launch of a plain streaming read
-    (gfxinfer_debug_stream_read) of the headline GEMV's algorithmic bytes, half and
-    twice that, and the LM head's size, rotating over copies (about 640 MB, beyond the
-    256 MB Infinity Cache) and over launch widths.  One JSON line per case and one per
-    size with the fastest width."""
+    """Yardstick for the GEMV roofline: one launch of a plain streaming read of the
+    headline GEMV's algorithmic bytes, half and twice that, and the LM head's size,
+    rotating over copies (about 640 MB, beyond the 256 MB Infinity Cache).  Two read
+    shapes: the grid-stride loop (gfxinfer_debug_stream_read) over launch widths, and
+    the one-shot read (gfxinfer_debug_stream_read_oneshot: every load of a lane issued
+    at once, non-temporal) over loads per lane.  One JSON line per case and one per
+    size and shape with the fastest case."""
     import math
     import torch
     import gfxinfer_amd as gx
@@ -319,10 +321,12 @@ def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
     stream = torch.cuda.Stream()
     data = torch.randint(0, 2**31 - 1, (total // 4,), dtype=torch.int32, device="cuda")
     widths = (1024, 1088, 2048, 4096, 8192)  # 1088: the headline GEMV's workgroup count
-    sink = torch.zeros(max(widths) * 256, dtype=torch.int32, device="cuda")
     headline = algorithmic_bytes(17408, 5120, 5)
+    sizes = (headline // 2, headline, 2 * headline, 423624704)
+    # grid-stride: one entry per lane; one-shot: one entry per 16-byte piece
+    sink = torch.zeros(max(max(widths) * 256, max(sizes) // 16), dtype=torch.int32, device="cuda")
     out = []
-    for nbytes in (headline // 2, headline, 2 * headline, 423624704):
+    for nbytes in sizes:
         nbytes -= nbytes % 16
         slot = (nbytes + 255) // 256 * 256
         copies = max(1, min(total // slot, math.ceil(budget / slot)))
@@ -331,7 +335,22 @@ def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
             def fn(i, width=width):
                 gx.debug_stream_read(data.data_ptr() + (i % copies) * slot, nbytes, sink, width, stream=stream)
             us = _graph_time(stream, fn, max(copies, 16) // copies * copies, reps)
-            line = {"read_floor": nbytes, "workgroups": width, "copies": copies, "us": round(us, 3),
+            line = {"read_floor": nbytes, "shape": "grid-stride", "workgroups": width, "copies": copies,
+                    "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                    "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            print(json.dumps(line), flush=True)
+            if best is None or us < best["us"]:
+                best = line
+        out.append(dict(best, best=True))
+        print(json.dumps(out[-1]), flush=True)
+        best = None
+        for loads in (1, 2, 4, 8):
+            def fn(i, loads=loads):
+                gx.debug_stream_read_oneshot(data.data_ptr() + (i % copies) * slot, nbytes, sink, loads,
+                                             stream=stream)
+            us = _graph_time(stream, fn, max(copies, 16) // copies * copies, reps)
+            line = {"read_floor": nbytes, "shape": "one-shot", "loads_per_lane": loads,
+                    "workgroups": -(-nbytes // (4096 * loads)), "copies": copies, "us": round(us, 3),
                     "gbs": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
             print(json.dumps(line), flush=True)
             if best is None or us < best["us"]:

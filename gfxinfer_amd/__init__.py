@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, P]),
     "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
     "gfxinfer_debug_stream_read": (I32, [P, SZ, P, U32, P]),
+    "gfxinfer_debug_stream_read_oneshot": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled_indirect": (I32, [I32, P, P, P, P, SZ, SZ, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled_batch": (I32, [I32, P, P, P, P, P, P, U32, SZ, SZ, P]),
@@ -284,6 +285,10 @@ def debug_gemm_partials(fmt, w, abits, a, rows, columns, batch, partials, stream
 
 def debug_stream_read(data, nbytes, sink, workgroups, stream=None):
     check(lib().gfxinfer_debug_stream_read(_p(data), nbytes, _p(sink), workgroups, _stream(stream)))
+
+
+def debug_stream_read_oneshot(data, nbytes, sink, loads_per_lane, stream=None):
+    check(lib().gfxinfer_debug_stream_read_oneshot(_p(data), nbytes, _p(sink), loads_per_lane, _stream(stream)))
 
 
 def launch_row_gather_tiled(fmt, w, ws, out, row, rows, columns, stream=None):

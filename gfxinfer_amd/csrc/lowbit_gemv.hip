@@ -1868,6 +1868,51 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   if (fold == 0x9E3779B9u) sink[lane] = fold;
 }
 
+// The same read with no loop: lane l of workgroup b issues all of its U 16-byte loads
+// at once (pieces b * 256 U + u * 256 + l, u < U, non-temporal as the GEMMs' weight
+// loads), so every byte of the launch is requested in the first instructions of its
+// waves.  Lanes past the end read the last piece again.
+template <int U>
+__global__ __launch_bounds__(256) void stream_read_oneshot_kernel(const uint4* __restrict__ data, size_t count,
+                                                                  uint32_t* sink) {
+  const size_t base = static_cast<size_t>(blockIdx.x) * 256u * U + threadIdx.x;
+  u32x4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t i = min(base + static_cast<size_t>(u) * 256u, count - 1u);
+    v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(data) + i);
+  }
+  uint32_t fold = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) fold ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  if (fold == 0x9E3779B9u) sink[min(base, count - 1u)] = fold;
+}
+
+extern "C" int32_t gfxinfer_debug_stream_read_oneshot(const void* data, size_t bytes, uint32_t* sink,
+                                                      uint32_t loads_per_lane, void* stream) {
+  if (data == nullptr || sink == nullptr) return fail(GFXI_INVALID_ARGUMENT, "null buffer");
+  if (bytes == 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(data) % 16 != 0) {
+    return fail(GFXI_INVALID_ARGUMENT, "stream read needs a 16-byte aligned, nonzero multiple of 16 bytes");
+  }
+  const size_t count = bytes / 16;
+  const size_t per_workgroup = static_cast<size_t>(256) * loads_per_lane;
+  if (loads_per_lane == 0 || (count + per_workgroup - 1) / per_workgroup > (1u << 24)) {
+    return fail(GFXI_INVALID_ARGUMENT, "loads_per_lane must be 1, 2, 4 or 8 and the grid at most 2^24 workgroups");
+  }
+  const dim3 grid(static_cast<unsigned>((count + per_workgroup - 1) / per_workgroup));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* d = static_cast<const uint4*>(data);
+  switch (loads_per_lane) {
+    case 1: hipLaunchKernelGGL(stream_read_oneshot_kernel<1>, grid, dim3(256), 0, s, d, count, sink); break;
+    case 2: hipLaunchKernelGGL(stream_read_oneshot_kernel<2>, grid, dim3(256), 0, s, d, count, sink); break;
+    case 4: hipLaunchKernelGGL(stream_read_oneshot_kernel<4>, grid, dim3(256), 0, s, d, count, sink); break;
+    case 8: hipLaunchKernelGGL(stream_read_oneshot_kernel<8>, grid, dim3(256), 0, s, d, count, sink); break;
+    default:
+      return fail(GFXI_INVALID_ARGUMENT, "loads_per_lane must be 1, 2, 4 or 8 and the grid at most 2^24 workgroups");
+  }
+  return launch_status("one-shot stream read");
+}
+
 extern "C" int32_t gfxinfer_debug_stream_read(const void* data, size_t bytes, uint32_t* sink,
                                               uint32_t workgroups, void* stream) {
   if (data == nullptr || sink == nullptr) return fail(GFXI_INVALID_ARGUMENT, "null buffer");

@@ -208,6 +208,14 @@ int32_t gfxinfer_debug_gemm_partials(int32_t format, const uint8_t* tiled_weight
 int32_t gfxinfer_debug_stream_read(const void* data, size_t bytes, uint32_t* sink,
                                    uint32_t workgroups, void* stream);
 
+/* Calibration: the same read with every load of a lane in flight at once (no loop):
+ * ceil(bytes / (4096 * loads_per_lane)) workgroups of 256 lanes, each lane issuing
+ * loads_per_lane (1, 2, 4 or 8) non-temporal 16-byte loads, as the GEMMs load their
+ * weights.  `sink` must hold bytes / 16 uint32 and is written only in the unlikely
+ * case a lane's XOR of its data equals 0x9E3779B9.  No reference counterpart. */
+int32_t gfxinfer_debug_stream_read_oneshot(const void* data, size_t bytes, uint32_t* sink,
+                                           uint32_t loads_per_lane, void* stream);
+
 /* lowbit_gemv.h:46-54 (launch_lowbit_row_gather_tiled): fp16 row
  * out[c] = fp16(w(row, c) * ws(row, c/128)).  W3G128 and W4G128. */
 int32_t gfxinfer_launch_lowbit_row_gather_tiled(int32_t format, const uint8_t* tiled_weights,

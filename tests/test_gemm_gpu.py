@@ -428,3 +428,21 @@ def test_stream_read_floor_entry(gx, device):
         with pytest.raises(gx.GfxinferError):
             gx.debug_stream_read(data, nbytes, sink, width)
 
+
+def test_stream_read_oneshot_entry(gx, device):
+    """The one-shot calibration read covers sizes that leave a partial last workgroup
+    (lanes past the end re-read the last piece), never writes a sink that is exactly
+    bytes / 16 entries long for data whose XOR is not the marker, and rejects
+    misaligned, empty and unsupported requests."""
+    import torch
+    data = torch.zeros(3 * 256 * 16 + 7 * 16, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(data.numel() // 16, dtype=torch.int32, device="cuda")
+    for loads in (1, 2, 4, 8):
+        gx.debug_stream_read_oneshot(data, data.numel(), sink, loads)
+        gx.debug_stream_read_oneshot(data, 16, sink, loads)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    for nbytes, loads in ((0, 1), (24, 1), (16, 0), (16, 3), (16, 16)):
+        with pytest.raises(gx.GfxinferError):
+            gx.debug_stream_read_oneshot(data, nbytes, sink, loads)
+
