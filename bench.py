@@ -360,19 +360,20 @@ def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
     return out
 
 
-def gdn_window_bench(tokens=32, layers=48, reps=20, seed=2026):
+def gdn_window_bench(tokens=32, layers=48, reps=20, seed=2026, value_heads=32):
     """the GDN verify window at 27B shapes (32 value heads x 128 x 128
     fp32 state, 16 key heads x 128) over `tokens` tokens with every per-token log the
     rollback needs (conv inputs, normalized keys, deltas, decays), for `layers` layers'
     own buffers, then the prefix restore of all layers to a seeded accepted length drawn
     uniformly from [0, tokens].  Inputs follow the config: projected q/k/v ~ N(0, 1),
     a, b ~ N(0, 1) (decay = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)).
+    value_heads=48 times the reference model's GDN (qwen38_spec.h:26-29).
     Correctness of both launches: tests/test_ops_gpu.py, tests/test_runtime_gpu.py."""
     import numpy as np
     import torch
     import gfxinfer_amd as gx
 
-    HK, HV, D, T = 16, 32, 128, tokens
+    HK, HV, D, T = 16, value_heads, 128, tokens
     C = 2 * HK * D + HV * D
     L = gx.lib()
     torch.manual_seed(seed)
@@ -413,9 +414,11 @@ def gdn_window_bench(tokens=32, layers=48, reps=20, seed=2026):
     window_bytes = (2 * state + T * C * 4 + T * HV * 8 + T * HV * D * 4 + C * 4 * 2 * 2
                     + T * (C * 2 + HK * D * 4 + HV * D * 4 + HV * 4))
     restore_bytes = layers * (2 * state + C * 4 * 2 * 2 + accepted * (C * 2 + HK * D * 4 + HV * D * 4 + HV * 4))
-    lines = [{"gdn": "conv_window", "tokens": T, "us_per_layer": round(window_us, 3), "bytes": window_bytes,
+    lines = [{"gdn": "conv_window", "tokens": T, "value_heads": HV, "us_per_layer": round(window_us, 3),
+              "bytes": window_bytes,
               "gbs": round(window_bytes / window_us / 1e3, 1)},
-             {"gdn": "restore_prefix_all", "layers": layers, "accepted": accepted, "us": round(restore_us, 3),
+             {"gdn": "restore_prefix_all", "value_heads": HV, "layers": layers, "accepted": accepted,
+              "us": round(restore_us, 3),
               "bytes": restore_bytes, "gbs": round(restore_bytes / restore_us / 1e3, 1),
               "frac_hbm": round(restore_bytes / restore_us / 1e3 / HBM_PEAK_GBS, 4)}]
     for line in lines:
@@ -437,15 +440,18 @@ def _matrix_bytes(model, names):
     return total
 
 
-def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates=True):
+def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates=True, shape="27b"):
     """Full synthetic 27B-shaped model: hipGraph-captured MTP chain +
     64-layer verifier of depth D, forced seeded 85 % Bernoulli acceptance, rollback or
     state swap per round.  Emitted tok/s = sum(accepted + 1) / time, verified tok/s =
-    sum(D + 1) / time (the reference's evaluated target tokens)."""
+    sum(D + 1) / time (the reference's evaluated target tokens).  shape "27b": the
+    BASELINE configs' heads (40/8 x 128 attention, 16/32 GDN, vocabulary 151936);
+    "reference": the reference's own model (qwen38_spec.h:16-34: 24/4 x 256 attention,
+    16/48 GDN, vocabulary 248320), same widths, depth and formats otherwise."""
     import numpy as np
-    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, qwen38_27b_spec
+    from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, qwen38_27b_spec, qwen38_reference_spec
 
-    spec = qwen38_27b_spec()
+    spec = qwen38_reference_spec() if shape == "reference" else qwen38_27b_spec()
     t0 = time.perf_counter()
     model = SyntheticModel(spec, seed)
     create_s = time.perf_counter() - t0
@@ -489,7 +495,10 @@ def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates
             results.update(reference_bench_rates(model, spec))
     finally:
         model.close()
-    return {"model_weight_bytes": verifier_bytes + proposal_bytes, "create_s": round(create_s, 3),
+    return {"model": {"shape": shape, "attention_heads": spec.attention_head_count, "kv_heads": spec.kv_head_count,
+                      "head_size": spec.attention_head_size, "gdn_key_heads": spec.gdn_key_head_count,
+                      "gdn_value_heads": spec.gdn_value_head_count, "vocabulary": spec.vocabulary_size},
+            "model_weight_bytes": verifier_bytes + proposal_bytes, "create_s": round(create_s, 3),
             "verifier_weight_bytes": verifier_bytes, "proposal_weight_bytes": proposal_bytes,
             **results}
 
@@ -722,6 +731,8 @@ def main():
     ap.add_argument("--no-reference-rates", action="store_true",
                     help="skip the verifier-only block_step and proposal-only rates (a round profile "
                          "then ends with the last round)")
+    ap.add_argument("--verify-model", choices=("27b", "reference"), default="27b",
+                    help="verify-round model heads: the BASELINE 27B shape or the reference's own model")
     ap.add_argument("--verify-depths", default="4,8,16,31",
                     help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -738,6 +749,9 @@ def main():
                     help="time a plain streaming read of the GEMV's bytes (what one launch can reach)")
     ap.add_argument("--gdn-window", action="store_true",
                     help="time BASELINE config 4 (32-token GDN window with logs + restore to a seeded length)")
+    ap.add_argument("--gdn-tokens", type=int, default=32, help="--gdn-window tokens per window")
+    ap.add_argument("--gdn-value-heads", type=int, default=32,
+                    help="--gdn-window value heads (32: the BASELINE config; 48: the reference model)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -755,7 +769,7 @@ def main():
         gemv_table_bench()
         return
     if args.gdn_window:
-        gdn_window_bench()
+        gdn_window_bench(tokens=args.gdn_tokens, value_heads=args.gdn_value_heads)
         return
     if args.read_floor:
         read_floor_bench()
@@ -820,7 +834,7 @@ def main():
     if not args.no_verify:
         depths = tuple(int(d) for d in args.verify_depths.split(",") if d)
         out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds,
-                                     reference_rates=not args.no_reference_rates)
+                                     reference_rates=not args.no_reference_rates, shape=args.verify_model)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

@@ -469,8 +469,9 @@ constexpr unsigned kGdnMaxTokens = 32;
 // slices, value, decay and beta) is read while token t computes, and the loop body is
 // unrolled by two so the hand-over costs no register moves.  The arithmetic per token
 // does not depend on the window length, so a window equals the same tokens one by one.
+template <unsigned VC>
 __device__ __forceinline__ void gdn_scan(float (&S)[8], const float (*kn)[kGdnD], const float (*qn)[kGdnD],
-                                         const float (*vv)[kGdnCols], const float* decay_s,
+                                         const float (*vv)[VC], const float* decay_s,
                                          const float* beta_s, unsigned T, unsigned ks, unsigned col,
                                          float* mixed, float* delta_log, std::size_t value_elements,
                                          std::size_t out_column) {
@@ -634,14 +635,14 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs args) {
 
 // Causal conv + gated delta rule over a window in one launch (the pair
 // gdn_conv_kernel -> gdn_recurrent_kernel with identical arithmetic).  Each
-// workgroup (value head h, 16 state columns) needs the conv outputs of the 2 x 128
-// query/key channels of its key head and of its own 16 value channels: it stages
-// fp16(projected) of those 272 channels for every token in LDS (independent loads),
-// computes the 4-tap conv + SiLU per (token, channel) in parallel, then normalizes
-// and runs the recurrence.  The query/key conv channels are shared by
-// value_heads/key_heads x 8 workgroups; the one with h % ratio == 0 and column block
-// 0 writes their final conv state and log, every workgroup writes those of its
-// value channels.  Conv states must not be updated in place (other workgroups may
+// workgroup (value head h, Cols = 16 or 32 state columns) needs the conv outputs of
+// the 2 x 128 query/key channels of its key head and of its own Cols value channels:
+// it stages fp16(projected) of those 2 x 128 + Cols channels for every token in LDS
+// (independent loads), computes the 4-tap conv + SiLU per (token, channel) in
+// parallel, then normalizes and runs the recurrence.  The query/key conv channels are
+// shared by value_heads/key_heads x 128/Cols workgroups; the one with h % ratio == 0
+// and column block 0 writes their final conv state and log, every workgroup writes
+// those of its value channels.  Conv states must not be updated in place (other workgroups may
 // still read the initial state).
 struct GdnWindowArgs {
   const float* projected;       // [T][C] fp32 (C = 2*Hk*D + Hv*D)
@@ -652,25 +653,35 @@ struct GdnWindowArgs {
   GdnArgs gdn;                  // .qkv unused
 };
 
-constexpr unsigned kWindowChannels = 2 * kGdnD + kGdnCols;  // 272
-// Sixteen waves share the loads, the conv and the norms; waves 0-3 (16 columns x 16
-// row slices) run the recurrence, whose arithmetic is the same at any workgroup size.
+// Sixteen waves share the loads, the conv and the norms; waves 0 .. Cols/4 - 1 (Cols
+// columns x 16 row slices) run the recurrence, whose arithmetic per column is the same
+// at any workgroup size.  Cols = 16 or 32 state columns per workgroup: the results do
+// not depend on it (every column, conv channel and norm is computed the same way), only
+// the grid does.  A 1024-thread workgroup holds a CU alone (two of them never share
+// one, whatever their LDS), so a grid past one workgroup per CU runs in two rounds;
+// launches whose 16-column grid would overfill the GPU take 32 columns per workgroup
+// instead, half the grid, and each of those shares the query/key conv of its key head
+// among half as many workgroups.
 constexpr unsigned kWindowThreads = 1024;
-constexpr unsigned kWindowRecurrenceWaves = kGdnCols / 4;
+constexpr unsigned kComputeUnits = 256;  // MI355X
 
+template <unsigned Cols>
 __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArgs w) {
   constexpr unsigned D = kGdnD;
+  constexpr unsigned kWindowChannels = 2 * D + Cols;  // q and k of the key head, Cols v columns
+  constexpr unsigned kWindowRecurrenceWaves = Cols / 4;
+  static_assert(Cols % 16 == 0 && kWindowRecurrenceWaves <= kWindowThreads / 64, "column block");
   const GdnArgs& args = w.gdn;
   __shared__ float qn[kGdnMaxTokens][D];
   __shared__ float kn[kGdnMaxTokens][D];
-  __shared__ float vv[kGdnMaxTokens][kGdnCols];
+  __shared__ float vv[kGdnMaxTokens][Cols];
   __shared__ __half xs[kGdnMaxTokens + 3][kWindowChannels];  // x[t-3..T-1] per channel
   __shared__ float cw[kWindowChannels][4];
   __shared__ float decay_s[kGdnMaxTokens];
   __shared__ float beta_s[kGdnMaxTokens];
-  __shared__ float tile[D][kGdnCols + 1];
+  __shared__ float tile[D][Cols + 1];
 
-  const unsigned blocks_per_head = D / kGdnCols;
+  const unsigned blocks_per_head = D / Cols;
   const unsigned h = blockIdx.x / blocks_per_head;
   const unsigned cb = blockIdx.x - h * blocks_per_head;
   const unsigned ratio = args.value_heads / args.key_heads;
@@ -687,24 +698,24 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   auto channel = [&](unsigned j) -> std::size_t {
     if (j < D) return static_cast<std::size_t>(kh) * D + j;
     if (j < 2 * D) return key_elements + static_cast<std::size_t>(kh) * D + (j - D);
-    return 2 * key_elements + static_cast<std::size_t>(h) * D + cb * kGdnCols + (j - 2 * D);
+    return 2 * key_elements + static_cast<std::size_t>(h) * D + cb * Cols + (j - 2 * D);
   };
 
   // Stage 1: every global load is issued before the first use (one memory latency):
-  // the state tile, fp16(projected) of the 272 channels per token as 4-channel runs,
-  // a/b of the head, the conv weights and the initial conv state.
+  // the state tile, fp16(projected) of the 2 D + Cols channels per token as 4-channel
+  // runs, a/b of the head, the conv weights and the initial conv state.
   constexpr unsigned NT = kWindowThreads;
-  constexpr unsigned kQuads = kWindowChannels / 4;                           // 68
-  constexpr unsigned kTileQuads = D * (kGdnCols / 4);                         // 512
-  constexpr unsigned kTileLoads = (kTileQuads + NT - 1) / NT;                 // 1
-  constexpr unsigned kInputLoads = (kGdnMaxTokens * kQuads + NT - 1) / NT;    // 3
-  constexpr unsigned kChannelLoads = (kWindowChannels + NT - 1) / NT;         // 1
+  constexpr unsigned kQuads = kWindowChannels / 4;                          // 68 / 72
+  constexpr unsigned kTileQuads = D * (Cols / 4);                           // 512 / 1024
+  constexpr unsigned kTileLoads = (kTileQuads + NT - 1) / NT;               // 1
+  constexpr unsigned kInputLoads = (kGdnMaxTokens * kQuads + NT - 1) / NT;  // 3
+  constexpr unsigned kChannelLoads = (kWindowChannels + NT - 1) / NT;       // 1
   const unsigned quads = T * kQuads;
-  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
+  const float* initial = args.initial + static_cast<std::size_t>(h) * D * D + cb * Cols;
   f32x4 tv[kTileLoads];
 #pragma unroll
   for (unsigned u = 0; u < kTileLoads; ++u) {
-    const unsigned i = tid + u * NT, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    const unsigned i = tid + u * NT, r = i / (Cols / 4), c4 = i - r * (Cols / 4);
     if (i < kTileQuads) {
       tv[u] = *reinterpret_cast<const f32x4*>(initial + static_cast<std::size_t>(r) * D + c4 * 4);
     }
@@ -741,7 +752,7 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
 
 #pragma unroll
   for (unsigned u = 0; u < kTileLoads; ++u) {
-    const unsigned i = tid + u * NT, r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+    const unsigned i = tid + u * NT, r = i / (Cols / 4), c4 = i - r * (Cols / 4);
     if (i < kTileQuads) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) tile[r][c4 * 4 + e] = tv[u][e];
@@ -840,7 +851,7 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   }
   __syncthreads();
 
-  // Stage 4: the recurrence (gdn_scan, as gdn_recurrent_kernel), on waves 0-3.
+  // Stage 4: the recurrence (gdn_scan, as gdn_recurrent_kernel), on waves 0 .. Cols/4 - 1.
   const unsigned ks = lane & 15u;
   const unsigned col = wave * 4u + (lane >> 4);
   const bool recurrent = wave < kWindowRecurrenceWaves;
@@ -848,7 +859,7 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   if (recurrent) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) S[i] = tile[ks * 8 + i][col];
-    const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * kGdnCols + col;
+    const std::size_t out_column = static_cast<std::size_t>(h) * D + cb * Cols + col;
     gdn_scan(S, kn, qn, vv, decay_s, beta_s, T, ks, col, args.mixed, args.delta_log, value_elements,
              out_column);
   }  // recurrent
@@ -858,9 +869,9 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
     for (int i = 0; i < 8; ++i) tile[ks * 8 + i][col] = S[i];
   }
   __syncthreads();
-  float* final_state = args.final_state + static_cast<std::size_t>(h) * D * D + cb * kGdnCols;
-  for (unsigned i = tid; i < D * (kGdnCols / 4); i += blockDim.x) {
-    const unsigned r = i / (kGdnCols / 4), c4 = i - r * (kGdnCols / 4);
+  float* final_state = args.final_state + static_cast<std::size_t>(h) * D * D + cb * Cols;
+  for (unsigned i = tid; i < D * (Cols / 4); i += blockDim.x) {
+    const unsigned r = i / (Cols / 4), c4 = i - r * (Cols / 4);
     f32x4 v = {tile[r][c4 * 4 + 0], tile[r][c4 * 4 + 1], tile[r][c4 * 4 + 2], tile[r][c4 * 4 + 3]};
     *reinterpret_cast<f32x4*>(final_state + static_cast<std::size_t>(r) * D + c4 * 4) = v;
   }
@@ -1574,8 +1585,12 @@ extern "C" int32_t gfxinfer_launch_gdn_conv_window(
                   GdnArgs{nullptr, projected_a, projected_b, bf16_a_log, bf16_dt_bias,
                           initial_recurrent_state, final_recurrent_state, mixed, key_log, delta_log,
                           decay_log, batch, key_heads, value_heads}};
-  hipLaunchKernelGGL(gdn_window_kernel, dim3(value_heads * (kGdnD / kGdnCols)), dim3(kWindowThreads), 0,
-                     static_cast<hipStream_t>(stream), w);
+  const auto st = static_cast<hipStream_t>(stream);
+  if (value_heads * (kGdnD / 16) > kComputeUnits) {
+    hipLaunchKernelGGL(gdn_window_kernel<32>, dim3(value_heads * (kGdnD / 32)), dim3(kWindowThreads), 0, st, w);
+  } else {
+    hipLaunchKernelGGL(gdn_window_kernel<16>, dim3(value_heads * (kGdnD / 16)), dim3(kWindowThreads), 0, st, w);
+  }
   return launch_status("fused GDN conv/window launch failed");
 }
 

@@ -643,11 +643,12 @@ def test_argmax_ties_and_mapping(device, gx, orc):
     assert int(host(one).view(np.uint32)[0]) == int(ids[np.argmax(logits[2, :98304])])
 
 
-@pytest.mark.parametrize("T,HK,HV", [(1, 16, 32), (3, 16, 32), (5, 16, 32), (32, 16, 32), (5, 16, 48),
-                                     (32, 16, 48)])
+@pytest.mark.parametrize("T,HK,HV", [(1, 16, 32), (3, 16, 32), (5, 16, 32), (32, 16, 32), (1, 16, 48),
+                                     (5, 16, 48), (32, 16, 48), (32, 16, 64)])
 def test_gdn_conv_window_equals_conv_then_window(device, gx, orc, T, HK, HV):
     """The fused conv + recurrence launch reproduces gdn_conv_update_block followed by
-    gdn_recurrent_window bit for bit (states, logs, unnormalized output)."""
+    gdn_recurrent_window bit for bit (states, logs, unnormalized output).  32 value
+    heads run 16 state columns per workgroup, 48 and 64 run 32."""
     C = 2 * HK * D + HV * D
     rng = np.random.default_rng(70 + T)
     proj = rng.standard_normal((T, C)).astype(np.float32)
