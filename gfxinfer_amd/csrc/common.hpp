@@ -16,6 +16,9 @@
 namespace gfx950 {
 
 constexpr std::size_t kGroup = 128;  // quantization group along K
+// MI355X: 256 CUs.  A workgroup of more than eight waves holds a CU alone (two of
+// them never share one), so a grid of such workgroups larger than this runs in rounds.
+constexpr unsigned kComputeUnits = 256;
 constexpr unsigned kWave = 64;       // CDNA wavefront
 
 // Records the message for gfxinfer_last_error() and returns the code.

@@ -1375,6 +1375,13 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
     // any split), within the register and LDS limits.
     unsigned waves = std::min(choose_waves(args.groups / args.splits), min_range_count(args.groups, args.splits));
     if ((ntb == 2 || ABits == 8) && waves > 8) waves = 8;
+    // More workgroups than CUs: keep them at eight waves or fewer, each wave taking
+    // consecutive ranges, so that two share a CU and the grid runs in one round (the
+    // range values and their sum are the same whichever wave computes a range).
+    if (waves > 8 && static_cast<uint64_t>(total_tiles) * args.splits > kComputeUnits) {
+      const unsigned per_wave = (waves + 7) / 8;
+      waves = (waves + per_wave - 1) / per_wave;
+    }
     GemmLds layout = gemm_lds_layout(gp * ch, batch, ABits, ntb);
     unsigned max_ranges = 1;
     for (unsigned sp = 0; sp < args.splits; ++sp) {

@@ -663,7 +663,6 @@ struct GdnWindowArgs {
 // instead, half the grid, and each of those shares the query/key conv of its key head
 // among half as many workgroups.
 constexpr unsigned kWindowThreads = 1024;
-constexpr unsigned kComputeUnits = 256;  // MI355X
 
 template <unsigned Cols>
 __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArgs w) {
