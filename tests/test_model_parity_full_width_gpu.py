@@ -1,11 +1,13 @@
 """Verify-step parity at the 27B widths against the model-level CPU oracle.
 
 A reduced-depth model keeps every width of the 27B shape (hidden 5120, MLP 17408 in W3
-then W4, 40 query / 8 KV heads x 128, GDN 16 key / 32 value heads x 128) with four
-layers (GDN, attention, GDN, attention) and an 8192-row W4 LM head, so the composed pass
-meets the oracle on the paths the small model never reaches: K = 5120 and 17408 cut
-into several canonical ranges, split-K planes summed by the residual norm, the 9-32-row
-direct GEMM, 40/8 x 128 attention over a context.
+then W4) with four layers (GDN, attention, GDN, attention) and an 8192-row W4 LM head,
+at two head shapes: the BASELINE configs' (40 query / 8 KV heads x 128, GDN 16 key / 32
+value heads x 128) and the reference's own model's (qwen38_spec.h:22-29: 24 / 4 x 256,
+GDN 16 / 48, where the GDN window runs 32 state columns per workgroup).  So the composed
+pass meets the oracle on the paths the small model never reaches: K = 5120 and 17408
+cut into several canonical ranges, split-K planes summed by the residual norm, the
+9-32-row direct GEMM, attention of either head size over a context.
 
 The comparison is teacher-forced stage by stage: the session records every layer's
 stage boundaries (gfxinfer_session_set_layer_trace) -- the rows entering the layer, the
@@ -44,31 +46,36 @@ LOGIT_TOL = 2e-2
 MARGIN = 2 * LOGIT_TOL
 
 
-def _spec():
+HEADS = {
+    "baseline": dict(attention_head_count=40, kv_head_count=8, attention_head_size=128, gdn_value_head_count=32),
+    "reference": dict(attention_head_count=24, kv_head_count=4, attention_head_size=256, gdn_value_head_count=48),
+}
+
+
+def _spec(heads):
     from gfxinfer_amd.runtime import tiny_spec
     return tiny_spec(hidden_size=5120, intermediate_size=17408, layer_count=4, full_attention_interval=2,
-                     attention_head_count=40, kv_head_count=8, rotary_size=64, gdn_key_head_count=16,
-                     gdn_value_head_count=32, vocabulary_size=8192, tokenizer_vocabulary_size=8000,
-                     mtp_draft_vocabulary=4096, w3_mlp_layers=2)
+                     rotary_size=64, gdn_key_head_count=16, vocabulary_size=8192,
+                     tokenizer_vocabulary_size=8000, mtp_draft_vocabulary=4096, w3_mlp_layers=2, **HEADS[heads])
 
 
-@pytest.fixture(scope="module")
-def models(device, gx):
+@pytest.fixture(scope="module", params=sorted(HEADS))
+def models(request, device, gx):
     from gfxinfer_amd.runtime import SyntheticModel
     from oracle.model import OracleModel
-    spec = _spec()
-    say("full-width 4-layer model on the GPU")
+    spec = _spec(request.param)
+    say("full-width 4-layer model on the GPU,", request.param, "heads")
     gpu = SyntheticModel(spec, SEED)
     say("full-width oracle models (reference and library K order)")
     reference = OracleModel(spec.as_dict(), SEED)
     library = OracleModel(spec.as_dict(), SEED,
                           k_order=lambda rows, cols: int(gx.lib().gfxinfer_gemm_split_count(rows, cols, 1)))
-    yield gpu, reference, library
+    yield spec, gpu, reference, library
     gpu.close()
 
 
-def _prompt(seed, n):
-    return [int(t) for t in np.random.default_rng(seed).integers(0, _spec().tokenizer_vocabulary_size, n)]
+def _prompt(spec, seed, n):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, spec.tokenizer_vocabulary_size, n)]
 
 
 def _margins(logits, vocab):
@@ -79,9 +86,9 @@ def _margins(logits, vocab):
 class Traced:
     """A session with its layer trace buffer, parsed into the trace's sections."""
 
-    def __init__(self, gpu, keep_logits=True):
+    def __init__(self, gpu, spec, keep_logits=True):
         from gfxinfer_amd.runtime import QwenDecodeSession
-        self.spec = _spec()
+        self.spec = spec
         self.session = QwenDecodeSession(gpu, CTX, 0, keep_logits=keep_logits)
         self.trace = empty((self.session.layer_trace_bytes(),), np.uint8)
         self.session.set_layer_trace(self.trace.data_ptr(), self.trace.numel())
@@ -121,9 +128,8 @@ class Traced:
         self.session.close()
 
 
-def _load_states(oracle, session):
+def _load_states(oracle, session, spec):
     """The oracle session takes the GPU session's recurrent states and K/V caches."""
-    spec = _spec()
     hv, d = spec.gdn_value_head_count, spec.gdn_head_size
     gdn = session.buffer("gdn_states", np.float32).reshape(len(oracle.state), hv, d, d)
     conv = session.buffer("conv_states", np.uint16).reshape(len(oracle.conv), -1, 4)
@@ -172,10 +178,10 @@ def _teacher_forced(oracle, traced, count, position, exact, label):
 
 
 def _check_block(traced, oracles, block, position):
-    spec = _spec()
+    spec = traced.spec
     V, Vt = spec.vocabulary_size, spec.tokenizer_vocabulary_size
     for oracle in oracles:
-        _load_states(oracle, traced.session)
+        _load_states(oracle, traced.session, spec)
     say("full-width block", len(block), "at", position)
     got = traced.session.block_step(block)
     logits = traced.session.buffer("logits", np.float32, len(block) * V).reshape(len(block), V)
@@ -202,12 +208,12 @@ def test_full_width_verify_blocks_match_oracle(models):
     1e-5 of the teacher-forced library-order oracle's (the recurrences sum in different
     orders, so the states, unlike the fp16 rows, differ in the last bits)."""
     from oracle.model import OracleSession
-    gpu, reference, library = models
-    traced = Traced(gpu)
+    spec, gpu, reference, library = models
+    traced = Traced(gpu, spec)
     oracles = [OracleSession(library, CTX), OracleSession(reference, CTX)]
     try:
-        _check_block(traced, oracles, _prompt(SEED, 5), 0)
-        _check_block(traced, oracles, _prompt(SEED + 1, 32), 5)
+        _check_block(traced, oracles, _prompt(spec, SEED, 5), 0)
+        _check_block(traced, oracles, _prompt(spec, SEED + 1, 32), 5)
         got = traced.session.buffer("gdn_states", np.float32).reshape(len(oracles[0].state),
                                                                       *oracles[0].state[0].shape)
         want = np.stack(oracles[0].state)
@@ -226,10 +232,9 @@ def test_full_width_planted_round_and_rollback(models):
     from gfxinfer_amd.runtime import QwenDecodeSession
     from oracle import oracle as O
     from oracle.model import OracleSession
-    gpu, _, library = models
-    spec = _spec()
+    spec, gpu, _, library = models
     Vt = spec.tokenizer_vocabulary_size
-    prompt = _prompt(2, 5)
+    prompt = _prompt(spec, 2, 5)
     serial = QwenDecodeSession(gpu, CTX, 0)
     try:
         say("full-width serial stream")
@@ -241,7 +246,7 @@ def test_full_width_planted_round_and_rollback(models):
         serial.close()
     drafts = list(stream)
     drafts[3] = (drafts[3] + 1) % Vt
-    traced = Traced(gpu, keep_logits=False)
+    traced = Traced(gpu, spec, keep_logits=False)
     session = traced.session
     oracle = OracleSession(library, CTX)
     try:
@@ -249,7 +254,7 @@ def test_full_width_planted_round_and_rollback(models):
         assert session.prefill(prompt) == seed
         pre_states = session.buffer("gdn_states", np.float32)
         pre_conv = session.buffer("conv_states", np.uint16)
-        _load_states(oracle, session)
+        _load_states(oracle, session, spec)
         r = session.speculative_step_planted(seed, drafts)
         assert r.accepted_drafts == 3 and r.tokens == stream[:4], (r.accepted_drafts, r.tokens, stream)
         assert session.position() == len(prompt) + 4
