@@ -42,6 +42,7 @@ pytestmark = pytest.mark.gpu
 
 SEED = 5120
 CTX = 128
+DEEP_CTX = 4096  # the BASELINE model's context
 LOGIT_TOL = 2e-2
 MARGIN = 2 * LOGIT_TOL
 
@@ -86,10 +87,10 @@ def _margins(logits, vocab):
 class Traced:
     """A session with its layer trace buffer, parsed into the trace's sections."""
 
-    def __init__(self, gpu, spec, keep_logits=True):
+    def __init__(self, gpu, spec, keep_logits=True, ctx=CTX):
         from gfxinfer_amd.runtime import QwenDecodeSession
         self.spec = spec
-        self.session = QwenDecodeSession(gpu, CTX, 0, keep_logits=keep_logits)
+        self.session = QwenDecodeSession(gpu, ctx, 0, keep_logits=keep_logits)
         self.trace = empty((self.session.layer_trace_bytes(),), np.uint8)
         self.session.set_layer_trace(self.trace.data_ptr(), self.trace.numel())
 
@@ -133,8 +134,8 @@ def _load_states(oracle, session, spec):
     hv, d = spec.gdn_value_head_count, spec.gdn_head_size
     gdn = session.buffer("gdn_states", np.float32).reshape(len(oracle.state), hv, d, d)
     conv = session.buffer("conv_states", np.uint16).reshape(len(oracle.conv), -1, 4)
-    keys = session.buffer("key_caches", np.uint16).reshape(len(oracle.kcache), CTX, -1)
-    values = session.buffer("value_caches", np.uint16).reshape(len(oracle.vcache), CTX, -1)
+    keys = session.buffer("key_caches", np.uint16).reshape(len(oracle.kcache), oracle.capacity, -1)
+    values = session.buffer("value_caches", np.uint16).reshape(len(oracle.vcache), oracle.capacity, -1)
     oracle.state = [gdn[i].copy() for i in range(len(oracle.state))]
     oracle.conv = [conv[i].copy() for i in range(len(oracle.conv))]
     oracle.kcache = [keys[i].copy() for i in range(len(oracle.kcache))]
@@ -218,6 +219,24 @@ def test_full_width_verify_blocks_match_oracle(models):
                                                                       *oracles[0].state[0].shape)
         want = np.stack(oracles[0].state)
         assert np.abs(got - want).max() <= 1e-5 * max(1.0, float(np.abs(want).max()))
+    finally:
+        traced.close()
+
+
+def test_full_width_block_deep_in_context(models):
+    """A 32-token block at position 4000 of a 4096-position context, after a chunked
+    prefill of 4000 tokens, layer by layer against the oracle run from the session's own
+    caches and states: attention over 4032 positions inside the composed pass (the split
+    kernels with their positions spread over many splits, the combine over all of them)."""
+    from oracle.model import OracleSession
+    spec, gpu, reference, library = models
+    traced = Traced(gpu, spec, ctx=DEEP_CTX)
+    oracles = [OracleSession(library, DEEP_CTX), OracleSession(reference, DEEP_CTX)]
+    try:
+        say("full-width prefill of 4000 tokens")
+        traced.session.prefill(_prompt(spec, SEED + 2, 4000))
+        assert traced.session.position() == 4000
+        _check_block(traced, oracles, _prompt(spec, SEED + 3, 32), 4000)
     finally:
         traced.close()
 
