@@ -11,6 +11,10 @@ vocabulary (:635-639), and the MTP proposal (:715-867).  Activations are A4G128
 the exact per-group integer partials and the per-group fp32 epilogue.
 Weights are the synthetic checkpoint of gfxinfer_model_create_synthetic, regenerated
 with oracle.synthetic_values and quantized with the restated quantize_group128.
+The layer wiring (norms, residual adds, attention gate, partial rotary, GQA grouping,
+the GDN conv / decay / beta / delta rule / gated norm, final norm and head) is pinned
+against HF transformers' Qwen3.5 text model with the same weights and float
+projections (tests/test_oracle_model_hf.py), with planted wiring mistakes shown to fail.
 """
 from __future__ import annotations
 
