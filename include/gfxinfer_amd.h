@@ -571,7 +571,9 @@ size_t gfxinfer_qwen38_scratch_bytes(uint32_t max_batch, size_t capacity);
  * null stream).  The buffer stays the caller's; it must outlive the launches. */
 int32_t gfxinfer_qwen38_bind_scratch(void* stream, void* scratch, size_t bytes, uint32_t max_batch,
                                      size_t capacity);
-/* Forgets the stream's binding (GFXI_INVALID_ARGUMENT if it has none). */
+/* Forgets the stream's binding (GFXI_INVALID_ARGUMENT if it has none).  Bindings are
+ * keyed by the stream handle: unbind before destroying the stream, since a stream
+ * created later may reuse the handle and would otherwise find the old buffer. */
 int32_t gfxinfer_qwen38_unbind_scratch(void* stream);
 
 /* qwen_ops.h:246-254: one token attending to the first token_count cached positions. */
