@@ -85,6 +85,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes": (I32, [P, P, U32, P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_dual_rms_norm_concat": (I32, [P, P, P, P, P, SZ, F32, I32, P]),
     "gfxinfer_launch_mtp_input_quantize_i4": (I32, [I32, P, P, SZ, U32, P, P, P, P, P, P, P, SZ, F32, I32, P]),
+    "gfxinfer_launch_mtp_input_quantize_i4_from_keys": (I32, [I32, P, P, SZ, P, SZ, P, P, P, P, P, P, P, P, SZ, F32, I32, P]),
     "gfxinfer_launch_dual_rms_norm_concat_batch": (I32, [P, P, P, P, P, SZ, U32, F32, I32, P]),
     "gfxinfer_launch_silu_multiply": (I32, [P, P, P, SZ, P]),
     "gfxinfer_launch_silu_multiply_quantize_i4": (I32, [P, P, P, P, SZ, U32, P]),

@@ -98,6 +98,42 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// The row an argmax key names: the key's low word is 0xffffffff - row (so that equal
+// values keep the lowest row); key 0 ("no candidate") names row 0.
+__device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
+  return key == 0ull ? 0u : 0xffffffffu - static_cast<uint32_t>(key);
+}
+
+// The largest of `count` argmax keys, reduced by the whole workgroup (blockDim.x a
+// multiple of 64, at most 1024 threads), in every thread; `partial` holds one key per
+// wave.  Keys are compared as integers, so the order of the reduction does not matter.
+__device__ __forceinline__ unsigned long long block_max_key(const unsigned long long* keys, uint32_t count,
+                                                            unsigned long long* partial) {
+  constexpr unsigned kLoads = 8;
+  unsigned long long best = 0ull;
+  for (uint32_t base = 0; base < count; base += blockDim.x * kLoads) {
+    unsigned long long k[kLoads];
+#pragma unroll
+    for (unsigned u = 0; u < kLoads; ++u) {
+      const uint32_t i = base + u * blockDim.x + threadIdx.x;
+      const unsigned long long key = keys[i < count ? i : 0u];  // unconditional: no load waits on a branch
+      k[u] = i < count ? key : 0ull;
+    }
+#pragma unroll
+    for (unsigned u = 0; u < kLoads; ++u) best = k[u] > best ? k[u] : best;
+  }
+#pragma unroll
+  for (int offset = 32; offset != 0; offset >>= 1) {
+    const unsigned long long other = __shfl_xor(best, offset);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = best;
+  __syncthreads();
+  best = partial[0];
+  for (unsigned w = 1; w < blockDim.x / 64; ++w) best = partial[w] > best ? partial[w] : best;
+  return best;
+}
+
 // One wave quantizes 128 fp16 values (two per lane) to A4G128 exactly as
 // quantize_activation_i4 (lowbit_gemv.hip:373-407) does.
 __device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_t* codes,

@@ -294,10 +294,6 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t row, 
   return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - row);
 }
 
-__device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
-  return key == 0ull ? 0u : 0xffffffffu - static_cast<uint32_t>(key);
-}
-
 // Dynamic LDS: one private region per wave holding the activations of the
 // wave's current chunk of groups for every live token ([batch][pitch]), a 16-byte
 // zero line read by lanes outside a group's token window, and the chunk's
@@ -1707,12 +1703,11 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(
     const uint8_t* packed_activations, const uint16_t* activation_scales, float* logits,
     size_t rows, size_t columns, uint32_t batch, size_t argmax_rows, const uint32_t* token_ids,
     void* workspace, size_t workspace_bytes, uint32_t* tokens, void* stream) {
-  if (tokens == nullptr || workspace == nullptr || argmax_rows == 0 || argmax_rows > rows ||
-      rows > 0xffffffffu || workspace_bytes < gfxinfer_gemm_argmax_workspace_bytes(rows, batch) ||
-      !aligned(workspace, 8)) {
-    return fail(GFXI_INVALID_ARGUMENT, "fused GEMM argmax needs tokens, 1 <= argmax rows <= rows "
-                                       "and an 8-byte aligned workspace of "
-                                       "gfxinfer_gemm_argmax_workspace_bytes() bytes");
+  if (workspace == nullptr || argmax_rows == 0 || argmax_rows > rows || rows > 0xffffffffu ||
+      workspace_bytes < gfxinfer_gemm_argmax_workspace_bytes(rows, batch) || !aligned(workspace, 8)) {
+    return fail(GFXI_INVALID_ARGUMENT, "fused GEMM argmax needs 1 <= argmax rows <= rows and an "
+                                       "8-byte aligned workspace of gfxinfer_gemm_argmax_workspace_bytes() "
+                                       "bytes");
   }
   const MatrixBinding binding{tiled_weights, tiled_weight_scales, logits, rows};
   auto* keys = static_cast<unsigned long long*>(workspace);
@@ -1720,7 +1715,7 @@ extern "C" int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(
   const int32_t status = gemm_entry("fused GEMM argmax", format, &binding, 1, 4, packed_activations,
                                     activation_scales, nullptr, columns, batch, false, s, keys,
                                     static_cast<uint32_t>(argmax_rows));
-  if (status != GFXI_OK) return status;
+  if (status != GFXI_OK || tokens == nullptr) return status;  // no tokens: the keys are the output
   hipLaunchKernelGGL(argmax_keys_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, keys,
                      static_cast<uint32_t>(rows / 16), token_ids, tokens);
   return launch_status("fused GEMM argmax reduction launch failed");

@@ -261,6 +261,12 @@ struct DualNormArgs {
   const __half* embed_scales;
   uint32_t embed_rows, token;
   const uint32_t* indirect_token;  // if set, the token id is read here
+  // If set, the token is the argmax of these per-tile keys of one token's fused head GEMM
+  // (mapped through key_token_ids if set) and is also written to *key_token_out.
+  const unsigned long long* keys;
+  uint32_t key_count;
+  const uint32_t* key_token_ids;
+  uint32_t* key_token_out;
   uint32_t elements;
   float epsilon;
   bool unit_offset;
@@ -278,8 +284,17 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
   const uint32_t half_offset = second ? elements : 0u;
   uint32_t hin[Slots], wpair[Slots];
   if (EmbedFormat != 0 && !second) {
-    // the token's embedding row, dequantized per column pair
-    const uint32_t token = a.indirect_token != nullptr ? *a.indirect_token : a.token;
+    // the token's embedding row, dequantized per column pair; the token is the previous
+    // proposal's greedy pick when its argmax keys are given (a workgroup-uniform branch)
+    uint32_t token;
+    if (a.keys != nullptr) {
+      __shared__ unsigned long long key_partial[16];
+      const uint32_t index = argmax_key_row(block_max_key(a.keys, a.key_count, key_partial));
+      token = a.key_token_ids != nullptr ? a.key_token_ids[index] : index;
+      if (threadIdx.x == 0) *a.key_token_out = token;
+    } else {
+      token = a.indirect_token != nullptr ? *a.indirect_token : a.token;
+    }
     const std::size_t groups = elements / kGroup;
     if constexpr (EmbedFormat == GFXI_W4G128) {
       // W4: one byte holds the lane pair's two codes (even column in the low nibble).
@@ -1353,12 +1368,13 @@ extern "C" int32_t gfxinfer_launch_dual_rms_norm_concat_batch(
   return launch_status("batched dual RMSNorm/concat launch failed");
 }
 
-extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
-    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
-    size_t embedding_rows, uint32_t token, const uint32_t* indirect_token,
-    const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
-    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
-    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream) {
+namespace gfx950 {
+namespace {
+int32_t mtp_input_entry(int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+                        size_t embedding_rows, DualNormArgs a, const uint16_t* embedding_bf16_norm,
+                        const uint16_t* conditioning, const uint16_t* conditioning_bf16_norm,
+                        uint16_t* concatenated_output, uint8_t* packed_output, uint16_t* scales,
+                        size_t elements, float epsilon, int32_t add_unit_offset, void* stream) {
   if (!valid_weight_format(embedding_format)) {
     return fail(GFXI_UNSUPPORTED, "MTP input: embedding format must be W2G128, W3G128 or W4G128");
   }
@@ -1371,7 +1387,6 @@ extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
     return fail(GFXI_INVALID_ARGUMENT, "invalid MTP input arguments (K divisible by 128 up to 6144, "
                                        "4-byte aligned rows)");
   }
-  DualNormArgs a{};
   a.left_weight = embedding_bf16_norm;
   a.right = reinterpret_cast<const __half*>(conditioning);
   a.right_weight = conditioning_bf16_norm;
@@ -1381,8 +1396,6 @@ extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
   a.embed_codes = embedding_codes;
   a.embed_scales = reinterpret_cast<const __half*>(embedding_scales);
   a.embed_rows = static_cast<uint32_t>(embedding_rows);
-  a.token = token;
-  a.indirect_token = indirect_token;
   a.elements = static_cast<uint32_t>(elements);
   a.epsilon = epsilon;
   a.unit_offset = add_unit_offset != 0;
@@ -1395,6 +1408,42 @@ extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
     hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W4G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
   }
   return launch_status("MTP input (embedding + dual RMSNorm + A4) launch failed");
+}
+}  // namespace
+}  // namespace gfx950
+
+extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4(
+    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+    size_t embedding_rows, uint32_t token, const uint32_t* indirect_token,
+    const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
+    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream) {
+  DualNormArgs a{};
+  a.token = token;
+  a.indirect_token = indirect_token;
+  return mtp_input_entry(embedding_format, embedding_codes, embedding_scales, embedding_rows, a,
+                         embedding_bf16_norm, conditioning, conditioning_bf16_norm, concatenated_output,
+                         packed_output, scales, elements, epsilon, add_unit_offset, stream);
+}
+
+extern "C" int32_t gfxinfer_launch_mtp_input_quantize_i4_from_keys(
+    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+    size_t embedding_rows, const uint64_t* argmax_keys, size_t key_count, const uint32_t* token_ids,
+    uint32_t* token_out, const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
+    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream) {
+  if (argmax_keys == nullptr || token_out == nullptr || key_count == 0 || key_count > (1u << 26)) {
+    return fail(GFXI_INVALID_ARGUMENT, "MTP input from keys: keys and token output must be set, "
+                                       "1..2^26 keys");
+  }
+  DualNormArgs a{};
+  a.keys = reinterpret_cast<const unsigned long long*>(argmax_keys);
+  a.key_count = static_cast<uint32_t>(key_count);
+  a.key_token_ids = token_ids;
+  a.key_token_out = token_out;
+  return mtp_input_entry(embedding_format, embedding_codes, embedding_scales, embedding_rows, a,
+                         embedding_bf16_norm, conditioning, conditioning_bf16_norm, concatenated_output,
+                         packed_output, scales, elements, epsilon, add_unit_offset, stream);
 }
 
 // ---- SwiGLU -----------------------------------------------------------------

@@ -443,15 +443,28 @@ struct gfxinfer_session {
   }
 
   // qwen_runtime.cpp:715-867 launch_mtp_proposal.  output_token == nullptr only
-  // advances the MTP K/V cache (826-829).
+  // advances the MTP K/V cache (826-829).  In a chain, keys_token (not null) takes the
+  // token from the previous proposal's draft-head keys left in argmax_keys and writes it
+  // there, and reduce == false leaves this proposal's own keys for the next one (its
+  // token then reaches *output_token from that proposal's input launch).
   int32_t mtp_proposal(uint32_t token, const uint32_t* device_token, const uint16_t* conditioning,
                        std::size_t position, uint32_t* output_token,
-                       const uint64_t* device_position) {
-    // embedding gather + dual norm/concat + A4 quantizer in one launch
-    GFXI_TRY(gfxinfer_launch_mtp_input_quantize_i4(
-        embedding.format, embedding.weights, embedding.scales, embedding.rows, token, device_token,
-        mtp_pre_embedding_norm, conditioning, mtp_pre_hidden_norm, nullptr, act_codes, act_scales, H,
-        spec.rms_norm_epsilon, 1, stream));
+                       const uint64_t* device_position, uint32_t* keys_token = nullptr,
+                       bool reduce = true) {
+    // embedding gather + dual norm/concat + A4 quantizer in one launch (+ the previous
+    // proposal's argmax reduction)
+    if (keys_token != nullptr) {
+      GFXI_TRY(gfxinfer_launch_mtp_input_quantize_i4_from_keys(
+          embedding.format, embedding.weights, embedding.scales, embedding.rows,
+          static_cast<const uint64_t*>(argmax_keys), draft_head.rows / 16, draft_token_ids, keys_token,
+          mtp_pre_embedding_norm, conditioning, mtp_pre_hidden_norm, nullptr, act_codes, act_scales, H,
+          spec.rms_norm_epsilon, 1, stream));
+    } else {
+      GFXI_TRY(gfxinfer_launch_mtp_input_quantize_i4(
+          embedding.format, embedding.weights, embedding.scales, embedding.rows, token, device_token,
+          mtp_pre_embedding_norm, conditioning, mtp_pre_hidden_norm, nullptr, act_codes, act_scales, H,
+          spec.rms_norm_epsilon, 1, stream));
+    }
     GFXI_TRY(gfxinfer_launch_gfx950_i4_gemm_half(mtp_fc.format, mtp_fc.weights, mtp_fc.scales,
                                                  act_codes, act_scales, mtp_input, mtp_fc.rows,
                                                  mtp_fc.columns, 1, 0, stream));
@@ -462,7 +475,8 @@ struct gfxinfer_session {
                              output_token == nullptr));
     if (output_token == nullptr) return ok();
     GFXI_TRY(mlp_tail(mtp, mtp_input, mtp_hidden, mtp_final_norm, 1));
-    return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, output_token, draft_token_ids);
+    return gemm_argmax(draft_head, 1, spec.mtp_draft_vocabulary, reduce ? output_token : nullptr,
+                       draft_token_ids);
   }
 
   // The MTP K/V update of mtp_proposal(token, ..., nullptr) for `count` consecutive
@@ -599,12 +613,14 @@ struct gfxinfer_session {
   // 660-673).  verify_drafts is the buffer the verifier reads.
   int32_t chain_and_verify(uint32_t seed, bool indirect, unsigned draft_count,
                            std::size_t base_mtp, const PlantedDrafts* planted) {
+    // Proposal i > 0 takes its token from proposal i - 1's draft-head keys and writes it
+    // to draft_tokens[i - 1]; the last proposal reduces its own keys.
     for (unsigned i = 0; i < draft_count; ++i) {
-      const uint32_t* device_token =
-          i == 0 ? (indirect ? graph_seed : nullptr) : draft_tokens + i - 1;
+      const uint32_t* device_token = i == 0 && indirect ? graph_seed : nullptr;
       const uint16_t* conditioning = i == 0 ? target_hidden_snapshot : mtp_hidden;
       GFXI_TRY(mtp_proposal(seed, device_token, conditioning, base_mtp + i, draft_tokens + i,
-                            indirect ? graph_mtp_positions + i : nullptr));
+                            indirect ? graph_mtp_positions + i : nullptr,
+                            i == 0 ? nullptr : draft_tokens + i - 1, i + 1 == draft_count));
     }
     const uint32_t* drafts = draft_tokens;
     if (planted != nullptr) {

@@ -159,7 +159,9 @@ size_t gfxinfer_gemm_argmax_workspace_bytes(size_t rows, uint32_t batch);
  * the LM-head projection + launch_argmax_batch pair of the verifier tail
  * (qwen_runtime.cpp:635-639) and the draft head + launch_argmax_mapped pair of the MTP
  * step (qwen_runtime.cpp:859-866) with two launches and no logits round trip; logits
- * [batch, rows] are written too when `logits` is not NULL. */
+ * [batch, rows] are written too when `logits` is not NULL.  With tokens NULL only the GEMM
+ * runs and the workspace holds the per-(token, tile) keys for a later reduction
+ * (gfxinfer_launch_mtp_input_quantize_i4_from_keys). */
 int32_t gfxinfer_launch_gfx950_i4_gemm_argmax(int32_t format, const uint8_t* tiled_weights,
                                               const uint16_t* tiled_weight_scales,
                                               const uint8_t* packed_activations,
@@ -322,6 +324,21 @@ int32_t gfxinfer_launch_mtp_input_quantize_i4(
     int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
     size_t embedding_rows, uint32_t token, const uint32_t* indirect_token,
     const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
+    const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
+    uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream);
+
+/* gfxinfer_launch_mtp_input_quantize_i4 whose token is the previous proposal's greedy
+ * pick: the argmax of the `key_count` per-tile keys a gfxinfer_launch_gfx950_i4_gemm_argmax
+ * call with tokens NULL left for one token (key_count = rows / 16 of that head), remapped
+ * through token_ids when it is not NULL.  The token is written to *token_out (what that
+ * call's own reduction would have written) and its embedding row feeds the dual
+ * RMSNorm/concat and the A4 quantizer as above.  One launch where the MTP chain had the
+ * draft head's argmax reduction and the next proposal's input (qwen_runtime.cpp:862-866,
+ * then :728-758).  No reference counterpart. */
+int32_t gfxinfer_launch_mtp_input_quantize_i4_from_keys(
+    int32_t embedding_format, const uint8_t* embedding_codes, const uint16_t* embedding_scales,
+    size_t embedding_rows, const uint64_t* argmax_keys, size_t key_count, const uint32_t* token_ids,
+    uint32_t* token_out, const uint16_t* embedding_bf16_norm, const uint16_t* conditioning,
     const uint16_t* conditioning_bf16_norm, uint16_t* concatenated_output, uint8_t* packed_output,
     uint16_t* scales, size_t elements, float epsilon, int32_t add_unit_offset, void* stream);
 

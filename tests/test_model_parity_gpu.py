@@ -82,3 +82,35 @@ def test_mtp_proposal_matches_oracle(pair):
     err = np.abs(logits - want_logits[0]).max()
     assert err <= LOGIT_TOL, err
     _check_tokens([draft], want_logits, some_sure=False)
+
+
+def test_mtp_chain_drafts_match_oracle(pair):
+    """The D drafts of a speculative round (each proposal after the first taking its token
+    from the previous proposal's draft-head keys) equal the oracle's chain of MTP proposals
+    (qwen_runtime.cpp:1448-1462: proposal i + 1 conditioned on proposal i's hidden row)
+    wherever the oracle's top-2 margin is clear.  The oracle is teacher-forced on the
+    session's own drafts (its hidden row does not depend on the pick), so a near tie at
+    one step does not end the comparison."""
+    from gfxinfer_amd.runtime import QwenDecodeSession
+    from oracle.model import OracleSession
+    gpu, cpu, spec = pair
+    depth = 4
+    s = QwenDecodeSession(gpu, 64, depth + 1)
+    o = OracleSession(cpu, 64)
+    first = s.greedy_step(77)
+    want_first, _ = o.block_step([77])
+    assert first == want_first[0]
+    say("speculative round, depth", depth)
+    s.speculative_step_forced(first, depth, 0)
+    drafts = [int(t) for t in s.buffer("drafts", np.uint32, depth)]
+    token, hidden = first, o.last_hidden
+    checked = 0
+    for i in range(depth):
+        want, logits, hidden = o.mtp_proposal(token, hidden, i)
+        top2 = np.sort(logits[0])[-2:]
+        if top2[1] - top2[0] > 2 * LOGIT_TOL:
+            assert drafts[i] == want, (i, drafts, want)
+            checked += 1
+        token = drafts[i]
+    say("drafts", drafts, "checked", checked)
+    assert checked >= 1

@@ -212,6 +212,64 @@ def test_mtp_input_equals_gather_dual_norm_quantizer(device, gx, orc, fmt):
                                                    None) == gx.INVALID_ARGUMENT
 
 
+@pytest.mark.parametrize("mapped", [False, True])
+def test_mtp_input_from_keys_equals_reduction_then_input(device, gx, orc, mapped):
+    """A draft head run keys-only (fused GEMM argmax with tokens NULL), then the MTP input
+    launch that reduces those keys itself, gives the token the fused head's own reduction
+    gives (through token_ids or not), writes it, and produces the same codes, scales and
+    concat as the MTP input launch given that token."""
+    fmt, n, rows, head_rows, limit = 3, 5120, 64, 4096, 4000
+    rng = np.random.default_rng(71 + mapped)
+    w = (rng.standard_normal((rows, n)) * 0.05).astype(np.float32)
+    _, codes, sc = orc.quantize_group128(w, fmt)
+    tcodes, tscales = gx.tile_group128(fmt, codes, sc, rows, n)
+    hw = (rng.standard_normal((head_rows, n)) * 0.02).astype(np.float32)
+    _, hcodes, hsc = orc.quantize_group128(hw, fmt)
+    htc, hts = gx.tile_group128(fmt, hcodes, hsc, head_rows, n)
+    x16 = _half(rng.standard_normal((1, n)))
+    a4, as16 = orc.quantize_activation_i4(x16)
+    cond = _half(rng.standard_normal(n) * 3)
+    ew, cw = _bf16(rng.standard_normal(n) * 0.05), _bf16(rng.standard_normal(n) * 0.05)
+    ids = (np.arange(head_rows, dtype=np.uint32) * 7 + 3) % rows
+    dtc, dts, dhtc, dhts, da, das, dcond, dew, dcw, dids = (
+        D_(v) for v in (tcodes, tscales, htc, hts, a4, as16, cond, ew, cw, ids))
+    ids_ptr = dids if mapped else None
+    L = gx.lib()
+    work_bytes = L.gfxinfer_gemm_argmax_workspace_bytes(head_rows, 1)
+    work = empty((work_bytes // 8,), np.uint64)
+    token = empty((1,), np.uint32)
+    say("fused head with its reduction, mapped" if mapped else "fused head with its reduction")
+    gx.check(L.gfxinfer_launch_gfx950_i4_gemm_argmax(fmt, dhtc, dhts, da, das, None, head_rows, n, 1, limit,
+                                                     ids_ptr, work.data_ptr(), work_bytes, token.data_ptr(), None))
+    want_token = int(host(token, np.uint32)[0])
+    concat, c4, s4 = empty((2 * n,), np.uint16), empty((n,), np.uint8), empty((2 * n // 128,), np.uint16)
+    gx.check(L.gfxinfer_launch_mtp_input_quantize_i4(fmt, dtc, dts, rows, want_token, None, dew, dcond, dcw,
+                                                     concat.data_ptr(), c4.data_ptr(), s4.data_ptr(), n, EPS, 1,
+                                                     None))
+    work.zero_()
+    say("keys-only head, then MTP input from the keys")
+    gx.check(L.gfxinfer_launch_gfx950_i4_gemm_argmax(fmt, dhtc, dhts, da, das, None, head_rows, n, 1, limit,
+                                                     ids_ptr, work.data_ptr(), work_bytes, None, None))
+    got_token = empty((1,), np.uint32)
+    concat2, c42, s42 = empty((2 * n,), np.uint16), empty((n,), np.uint8), empty((2 * n // 128,), np.uint16)
+    gx.check(L.gfxinfer_launch_mtp_input_quantize_i4_from_keys(
+        fmt, dtc, dts, rows, work.data_ptr(), head_rows // 16, ids_ptr, got_token.data_ptr(), dew, dcond, dcw,
+        concat2.data_ptr(), c42.data_ptr(), s42.data_ptr(), n, EPS, 1, None))
+    assert int(host(got_token, np.uint32)[0]) == want_token
+    assert np.array_equal(host(concat2, np.uint16), host(concat, np.uint16))
+    assert np.array_equal(host(c42), host(c4))
+    assert np.array_equal(host(s42, np.uint16), host(s4, np.uint16))
+    # the oracle's argmax of the same logits picks the same row
+    logits = empty((1, head_rows), np.float32)
+    gx.check(L.gfxinfer_launch_gfx950_i4_gemm_argmax(fmt, dhtc, dhts, da, das, logits.data_ptr(), head_rows, n, 1,
+                                                     limit, None, work.data_ptr(), work_bytes, None, None))
+    row = int(np.argmax(host(logits)[0, :limit]))
+    assert want_token == (int(ids[row]) if mapped else row)
+    assert L.gfxinfer_launch_mtp_input_quantize_i4_from_keys(
+        fmt, dtc, dts, rows, work.data_ptr(), head_rows // 16, ids_ptr, None, dew, dcond, dcw, None,
+        c42.data_ptr(), s42.data_ptr(), n, EPS, 1, None) == gx.INVALID_ARGUMENT
+
+
 @pytest.mark.parametrize("batch", [1, 7, 32])
 def test_dual_rms_norm_concat_batch_rows_equal_single(device, gx, orc, batch):
     """Each row of the batched launcher is bit-identical to the single-row launcher on
