@@ -1,4 +1,4 @@
-"""CPU oracle of the byte-level BPE tokenizer (test infrastructure only: imported by
+r"""CPU oracle of the byte-level BPE tokenizer (test infrastructure only: imported by
 tests/, never by the product).
 
 A restatement, in Python, of /root/reference/src/tokenizer.cpp:
