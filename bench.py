@@ -306,6 +306,53 @@ def gemv_table_bench(reps=40, budget=600e6):
     return out
 
 
+def gemm_family_bench(reps=40, budget=600e6, batches=(1, 2, 3, 4, 5, 8), headline=False):
+    """The two A4 GEMM kernel families side by side (v_mfma_i32_16x16x64_i8 against
+    v_dot8_i32_i4) at 1-8 tokens on the config-2 shapes, the down shape as split-K planes
+    and the MTP draft head (W4 [98304, 5120]), over rotating weight copies beyond the
+    Infinity Cache.  One JSON line per (shape, batch, family); the families' outputs are
+    bit-identical (tests/test_gemm_dot_gpu.py)."""
+    import torch
+    import gfxinfer_amd as gx
+
+    torch.manual_seed(0x6E8)
+    stream = torch.cuda.Stream()
+    out = []
+    shapes = ((gx.W3G128, 3, 17408, 5120), (gx.W4G128, 4, 17408, 5120), (gx.W3G128, 3, 5120, 17408),
+              (gx.W4G128, 4, 5120, 17408), (gx.W4G128, 4, 98304, 5120))
+    if headline:  # the profiled subset: the headline shape at 1 and 5 tokens
+        shapes, batches = shapes[:1], (1, 5)
+    for fmt, wbits, rows, cols in shapes:
+        w = torch.randn(rows, cols, device="cuda") * 0.02
+        c0 = torch.empty(gx.tile_bytes(fmt, rows, cols), dtype=torch.uint8, device="cuda")
+        s0 = torch.empty(rows * cols // 128, dtype=torch.int16, device="cuda")
+        gx.launch_quantize_group128(fmt, w, rows, cols, c0, s0)
+        del w
+        n = max(2, int(budget // c0.numel()))
+        weights = [(c0, s0)] + [(c0.clone(), s0.clone()) for _ in range(n - 1)]
+        for batch in batches:
+            x = torch.randn(batch, cols, device="cuda").half()
+            a = torch.empty(batch, cols // 2, dtype=torch.uint8, device="cuda")
+            sa = torch.empty(batch, cols // 128, dtype=torch.int16, device="cuda")
+            gx.launch_quantize_activation_i4(x, a, sa, cols, batch)
+            splits = gx.gemm_split_count(rows, cols, batch)
+            y = torch.empty(splits, batch, rows, device="cuda")
+            for sp in sorted({1, splits}):
+                for family, name in ((gx.GEMM_MFMA, "mfma"), (gx.GEMM_DOT, "dot")):
+                    def fn(i, family=family, sp=sp):
+                        gx.check(gx.debug_gemm_family(family, fmt, weights[i][0], weights[i][1], a, sa, rows,
+                                                      cols, batch, out=y, splits=sp, stream=stream))
+                    us = _graph_time(stream, fn, n, reps)
+                    nbytes = algorithmic_bytes(rows, cols, batch, wbits=wbits) + (sp - 1) * batch * rows * 4
+                    line = {"gemm_family": name, "format": f"W{wbits}A4", "rows": rows, "columns": cols,
+                            "batch": batch, "splits": sp, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                    out.append(line)
+                    print(json.dumps(line), flush=True)
+        del weights
+    return out
+
+
 def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
     """Yardstick for the GEMV roofline: one launch of a plain streaming read of the
     headline GEMV's algorithmic bytes, half and twice that, and the LM head's size,
@@ -743,6 +790,9 @@ def main():
                     help="time BASELINE config 3 (one block's projections + LM head argmax at 5/16/32 rows)")
     ap.add_argument("--gemv-table", action="store_true",
                     help="time BASELINE config 2 (W3A4/W4A4 GEMV, up and down shapes, batch 1 and 5)")
+    ap.add_argument("--gemm-families", nargs="?", const="all", choices=("all", "headline"),
+                    help="time the MFMA and v_dot8 A4 GEMM kernel families at 1-8 tokens side by side "
+                         "(headline: W3A4 [17408,5120] at 1 and 5 tokens only)")
     ap.add_argument("--prefill", action="store_true",
                     help="time chunked prefill against the reference's serial prefill loop (27B shapes)")
     ap.add_argument("--read-floor", action="store_true",
@@ -767,6 +817,9 @@ def main():
         return
     if args.gemv_table:
         gemv_table_bench()
+        return
+    if args.gemm_families:
+        gemm_family_bench(headline=args.gemm_families == "headline")
         return
     if args.gdn_window:
         gdn_window_bench(tokens=args.gdn_tokens, value_heads=args.gdn_value_heads)

@@ -72,6 +72,7 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gfx950_i4_gemm_argmax": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, SZ, P, P]),
     "gfxinfer_launch_gfx950_i4_gemm_argmax_no_alloc": (I32, [I32, P, P, P, P, P, SZ, SZ, U32, SZ, P, P, P]),
     "gfxinfer_debug_gemm_partials": (I32, [I32, P, I32, P, SZ, SZ, U32, P, P]),
+    "gfxinfer_debug_gemm_family": (I32, [I32, I32, P, P, P, P, P, I32, P, P, U32, SZ, SZ, U32, U32, P]),
     "gfxinfer_debug_stream_read": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_debug_stream_read_oneshot": (I32, [P, SZ, P, U32, P]),
     "gfxinfer_launch_lowbit_row_gather_tiled": (I32, [I32, P, P, P, SZ, SZ, SZ, P]),
@@ -282,6 +283,17 @@ def launch_i8_gemm(fmt, w, ws, a, as_, out, rows, columns, batch, stream=None):
 
 def debug_gemm_partials(fmt, w, abits, a, rows, columns, batch, partials, stream=None):
     check(lib().gfxinfer_debug_gemm_partials(fmt, _p(w), abits, _p(a), rows, columns, batch, _p(partials), _stream(stream)))
+
+
+GEMM_MFMA, GEMM_DOT = 1, 2
+
+
+def debug_gemm_family(family, fmt, w, ws, a, as_, rows, columns, batch, out=None, half_output=False,
+                      partials=None, argmax_keys=None, argmax_rows=0, splits=1, stream=None):
+    """One A4 GEMM launch through a named kernel family (GEMM_MFMA or GEMM_DOT); returns the status."""
+    return int(lib().gfxinfer_debug_gemm_family(family, fmt, _p(w), _p(ws), _p(a), _p(as_), _p(out),
+                                                1 if half_output else 0, _p(partials), _p(argmax_keys),
+                                                argmax_rows, rows, columns, batch, splits, _stream(stream)))
 
 
 def debug_stream_read(data, nbytes, sink, workgroups, stream=None):

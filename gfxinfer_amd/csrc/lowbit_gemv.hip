@@ -13,6 +13,7 @@
 #include <limits>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -1189,6 +1190,279 @@ __device__ __forceinline__ void direct_finish(const GemmArgs& args, const GemmMa
 }
 
 // ---------------------------------------------------------------------------
+// Dot-product GEMV: W3/W4 weights x A4 activations, 1-8 tokens, on v_dot8_i32_i4
+// (eight signed nibble products per lane per instruction) instead of MFMA.
+//
+// A wave serves a quad of four consecutive 16-row tiles and one range of the
+// canonical K partition.  It loads each (tile, group) chunk exactly as the MFMA
+// kernels do -- lane l gets piece (kb = l / 16, row m = l % 16), one coalesced
+// 768/1024-byte load per chunk -- and then exchanges pieces between the four lane
+// rows (v_permlane32_swap, v_permlane16_swap) so that lane (q, m) holds the whole
+// 128-column group of row m of tile q.  Every lane then works on the same group, so
+// a token's 64 bytes of A4 codes are wave-uniform: they come from scalar loads and
+// feed v_dot8 from SGPRs, with no activation staging, no LDS and no operand
+// expansion on the activation side.  W4 nibbles are used as stored; a W3 lane piece
+// becomes four nibble dwords holding 2w per column with about four instructions each.
+// Each lane owns one (row, token) value per token, so the fp32 epilogue is one
+// fmaf per (row, token, group) and no cross-lane sum is needed.
+// ---------------------------------------------------------------------------
+
+constexpr unsigned kDotMaxWaves = 8;
+constexpr unsigned kDotMaxGroups = 10;  // largest canonical range (range_count: at most ten groups)
+
+// Per-wave LDS staging of a range: A4 codes [NT][kDotMaxGroups][64 B] filled by whole
+// 1 KiB DMA instructions, then the activation scales (six dwords per token).
+template <int NT>
+constexpr unsigned kDotCodeDma = (NT * kDotMaxGroups * 4u + 63u) / 64u;
+template <int NT>
+constexpr unsigned kDotCodeRegion = kDotCodeDma<NT> * 1024u;
+template <int NT>
+constexpr unsigned kDotRegion = kDotCodeRegion<NT> + 256u;
+
+// Three W3 dwords of one lane piece (32 columns) -> four nibble dwords in column
+// order: nibble i of dword j holds 2w of column 8j + i (the 3-bit two's complement
+// code in bits 1..3 of a nibble reads as 2w).  Per byte of s0/s1/s2 the codes of
+// operand registers 0/2/4 sit in bits 0..2 and those of 1/3/5 in bits 3..5, so
+// ((s & 0x3F) + (s & 0x38)) << 1 puts them in bits 1..3 and 5..7 (no carry: the
+// sum is below 128); registers 6 and 7 are split over bits 6..7 of s0/s2 and s1.
+__device__ __forceinline__ void w3_nibbles(unsigned s0, unsigned s1, unsigned s2, unsigned* n) {
+  n[0] = ((s0 & 0x3F3F3F3Fu) + (s0 & 0x38383838u)) << 1;
+  n[1] = ((s1 & 0x3F3F3F3Fu) + (s1 & 0x38383838u)) << 1;
+  n[2] = ((s2 & 0x3F3F3F3Fu) + (s2 & 0x38383838u)) << 1;
+  n[3] = ((s0 >> 4) & 0x0C0C0C0Cu) | ((s1 >> 5) & 0x02020202u) | (s2 & 0xC0C0C0C0u) |
+         ((s1 >> 2) & 0x20202020u);
+}
+
+// 4 x 4 exchange between the lane rows (16 lanes each): on entry r[q] holds, in lane
+// row k, a dword of piece k of tile q; on exit r[k] holds, in lane row q, the same
+// dword of piece k of tile q.  v_permlane32_swap exchanges the upper half of its
+// first operand with the lower half of its second, v_permlane16_swap the odd rows of
+// its first operand with the even rows of its second.
+__device__ __forceinline__ void exchange_rows(unsigned& r0, unsigned& r1, unsigned& r2, unsigned& r3) {
+  const u32x2 a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+  const u32x2 b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+  const u32x2 c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const u32x2 d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  r0 = c[0];
+  r1 = c[1];
+  r2 = d[0];
+  r3 = d[1];
+}
+
+// NT = the launch's token count.
+template <int Format, int NT, bool HalfOut, bool Partials>
+__global__ __launch_bounds__(kDotMaxWaves * 64) void lowbit_gemm_dot_kernel(GemmArgs args) {
+  static_assert(Format == GFXI_W3G128 || Format == GFXI_W4G128, "nibble dot needs W3 or W4");
+  constexpr unsigned LB = lane_bytes(Format);
+  constexpr unsigned WD = LB / 4;
+  // The dot of 2w (W3) or w (W4) with a: 1/F folded into the activation scale keeps
+  // fmaf(float(P), ws * as, v) exact, as in the MFMA kernels.
+  constexpr float kInvF = Format == GFXI_W3G128 ? 0.5F : 1.0F;
+  constexpr int kShift = Format == GFXI_W3G128 ? 1 : 0;
+  // Dynamic LDS: one staging region per wave (kDotRegion), then the range values
+  // [ranges][NT][64] fp32 summed in range order at the end.
+  extern __shared__ __align__(16) uint8_t dot_lds[];
+
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned waves = blockDim.x >> 6;
+  const unsigned q = lane >> 4, m = lane & 15u;
+
+  const unsigned split = blockIdx.x % args.splits;
+  unsigned quad = blockIdx.x / args.splits;
+  unsigned index = 0;
+#pragma unroll
+  for (unsigned i = 1; i < 4; ++i) {
+    if (quad >= args.tile_begin[i]) index = i;
+  }
+  const GemmMatrix matrix = args.matrix[index];
+  quad -= args.tile_begin[index];
+  const unsigned tile0 = quad * 4u;
+  const unsigned valid = min(4u, matrix.tiles - tile0);  // tiles of this quad inside the matrix
+  const uint32_t groups = args.groups;
+  const uint32_t batch = args.batch;
+  const uint32_t rows = matrix.tiles * 16u;
+  const auto weights = buffer(matrix.weights + static_cast<std::size_t>(tile0) * groups * 64u * LB,
+                              valid * groups * 64u * LB);
+  const auto weight_scales =
+      buffer(matrix.scales + static_cast<std::size_t>(tile0) * groups * 16u, valid * groups * 32u);
+  const uint32_t row_bytes = args.columns / 2u;
+  const auto activations = buffer(args.activations, batch * row_bytes);
+  const auto activation_scales = buffer(args.activation_scales, Partials ? 0u : batch * groups * 2u);
+  uint8_t* stage = dot_lds + wave * kDotRegion<NT>;
+  float* dot_results = reinterpret_cast<float*>(dot_lds + waves * kDotRegion<NT>);
+  const unsigned row = (tile0 + q) * 16u + m;
+  const bool live = q < valid;
+
+  const GroupRange own = split_groups(groups, split, args.splits);
+  const unsigned ranges = range_count(own.end - own.begin);
+  const unsigned range_begin = ranges * wave / waves;
+  const unsigned range_end = ranges * (wave + 1u) / waves;
+  const unsigned ws_voffset = live ? (q * groups * 16u + m) * 2u : 0x80000000u;
+
+  float total[NT];
+  for (unsigned range = range_begin; range < range_end; ++range) {
+    const GroupRange span = canonical_range(groups, split, args.splits, range, ranges);
+    const unsigned count = span.end - span.begin;  // 1..kDotMaxGroups
+    // 1) The range's A4 codes ([token][group][64 B]) and activation scales go memory ->
+    //    LDS first: anything requested after the weight stream arrives about one stream
+    //    time later.  Scales: six dwords per token from the pair holding its first group.
+#pragma unroll
+    for (unsigned d = 0; d < kDotCodeDma<NT>; ++d) {
+      const unsigned piece = d * 64u + lane;
+      const unsigned t = piece / (kDotMaxGroups * 4u), rem = piece % (kDotMaxGroups * 4u);
+      const unsigned i = rem / 4u, j = rem % 4u;
+      const unsigned off = (t < NT && i < count) ? t * row_bytes + (span.begin + i) * 64u + j * 16u : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(activations, (lds_void*)(stage + d * 1024u), 16, off, 0, 0, 0);
+    }
+    if constexpr (!Partials) {
+      const unsigned t = lane / 6u, d = lane % 6u;
+      const unsigned off = t < NT ? (((t * groups + span.begin) >> 1) + d) * 4u : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(activation_scales, (lds_void*)(stage + kDotCodeRegion<NT>), 4, off, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2) The range's weight scales, then all of its weights, in flight together.  Every
+    //    load is issued (past the range or the matrix through an out-of-range offset:
+    //    zeros, no traffic) so that the count of loads after the DMA is a constant.
+    unsigned short wsr[kDotMaxGroups];
+#pragma unroll
+    for (unsigned i = 0; i < kDotMaxGroups; ++i) {
+      if constexpr (!Partials) {
+        wsr[i] = __builtin_amdgcn_raw_buffer_load_b16(weight_scales, i < count ? ws_voffset + i * 32u : 0x80000000u,
+                                                      span.begin * 32u, 0);
+      }
+    }
+    constexpr unsigned kChunk = 64u * LB;  // bytes of one (tile, group) chunk
+    constexpr unsigned kHalf = kDotMaxGroups / 2;
+    // The range's first group in one SGPR, the group within the range as the immediate
+    // offset (the second half of the range has an SGPR of its own: 9 x 1024 B would
+    // overflow the 12-bit immediate), the tile in the lane offset.
+    const unsigned first = __builtin_amdgcn_readfirstlane(span.begin * kChunk);
+    const unsigned second = __builtin_amdgcn_readfirstlane((span.begin + kHalf) * kChunk);
+    unsigned w[kDotMaxGroups][4][WD];
+#pragma unroll
+    for (unsigned i = 0; i < kDotMaxGroups; ++i) {
+      const unsigned soffset = i < kHalf ? first : second;
+      const unsigned imm = (i % kHalf) * kChunk;
+#pragma unroll
+      for (unsigned t = 0; t < 4; ++t) {
+        const unsigned voffset = (t < valid && i < count) ? t * groups * kChunk + lane * LB + imm : 0x80000000u;
+        if constexpr (Format == GFXI_W3G128) {
+          const u32x3 x = __builtin_amdgcn_raw_buffer_load_b96(weights, voffset, soffset, kStreaming);
+          w[i][t][0] = x[0];
+          w[i][t][1] = x[1];
+          w[i][t][2] = x[2];
+        } else {
+          const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(weights, voffset, soffset, kStreaming);
+          w[i][t][0] = x[0];
+          w[i][t][1] = x[1];
+          w[i][t][2] = x[2];
+          w[i][t][3] = x[3];
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The compiler does not order LDS reads after buffer -> LDS loads: wait until only the
+    // loads issued after the DMA may still be in flight (loads complete in issue order).
+    constexpr unsigned kAfter = (Partials ? 0u : kDotMaxGroups) + kDotMaxGroups * 4u;
+    static_assert(kAfter <= 63, "vmcnt holds at most 63");
+    __builtin_amdgcn_s_waitcnt(static_cast<int>((kAfter & 15u) | ((kAfter >> 4) << 14) | (7u << 4) | (15u << 8)));
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* stage_scales = reinterpret_cast<const uint16_t*>(stage + kDotCodeRegion<NT>);
+    float v[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) v[t] = 0.0F;
+#pragma unroll
+    for (unsigned i = 0; i < kDotMaxGroups; ++i) {
+      if (i >= count) continue;  // wave-uniform
+      const unsigned g = span.begin + i;
+#pragma unroll
+      for (unsigned d = 0; d < WD; ++d) exchange_rows(w[i][0][d], w[i][1][d], w[i][2][d], w[i][3][d]);
+      // nib[4k + j]: columns 32k + 8j .. 32k + 8j + 7 of the group, in A4 nibble order
+      unsigned nib[16];
+#pragma unroll
+      for (unsigned k = 0; k < 4; ++k) {
+        if constexpr (Format == GFXI_W3G128) {
+          w3_nibbles(w[i][k][0], w[i][k][1], w[i][k][2], nib + 4 * k);
+        } else {
+#pragma unroll
+          for (unsigned j = 0; j < 4; ++j) nib[4 * k + j] = w[i][k][j];
+        }
+      }
+      float ws = 0.0F;
+      if constexpr (!Partials) ws = __half2float(__ushort_as_half(wsr[i]));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        // the token's 128 codes of group g: the same LDS address in every lane (broadcast)
+        const u32x4* a = reinterpret_cast<const u32x4*>(stage + (t * kDotMaxGroups + i) * 64u);
+        int p0 = 0, p1 = 0;
+#pragma unroll
+        for (unsigned j = 0; j < 4; ++j) {
+          const u32x4 x = a[j];
+          p0 = __builtin_amdgcn_sdot8(static_cast<int>(x[0]), static_cast<int>(nib[4 * j]), p0, false);
+          p1 = __builtin_amdgcn_sdot8(static_cast<int>(x[1]), static_cast<int>(nib[4 * j + 1]), p1, false);
+          p0 = __builtin_amdgcn_sdot8(static_cast<int>(x[2]), static_cast<int>(nib[4 * j + 2]), p0, false);
+          p1 = __builtin_amdgcn_sdot8(static_cast<int>(x[3]), static_cast<int>(nib[4 * j + 3]), p1, false);
+        }
+        const int p = p0 + p1;  // exact
+        if constexpr (Partials) {
+          if (live) args.partials[(static_cast<std::size_t>(t) * rows + row) * groups + g] = p >> kShift;
+        } else {
+          const unsigned short h = stage_scales[t * 12u + (span.begin & 1u) + i];
+          const float as = __half2float(__ushort_as_half(h)) * kInvF;
+          v[t] = fmaf(static_cast<float>(p), ws * as, v[t]);
+        }
+      }
+    }
+    if constexpr (!Partials) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) total[t] = v[t];
+      if (ranges > 1) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) dot_results[(range * NT + t) * 64u + lane] = v[t];
+      }
+    }
+  }
+  if constexpr (Partials) return;
+
+  if (ranges > 1) {
+    // The split's value: range values added in range order, by wave 0.
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) total[t] = dot_results[t * 64u + lane];
+    for (unsigned rg = 1; rg < ranges; ++rg) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) total[t] += dot_results[(rg * NT + t) * 64u + lane];
+    }
+  }
+  if (args.argmax_keys != nullptr) {
+    // Fused greedy argmax: the best of each tile's 16 rows (one lane row) per token.
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      unsigned long long best = live ? argmax_key(total[t], row, args.argmax_rows) : 0ull;
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
+        const unsigned long long other = __shfl_xor(best, 1 << step);
+        best = other > best ? other : best;
+      }
+      if (live && m == 0) args.argmax_keys[static_cast<std::size_t>(t) * matrix.tiles + tile0 + q] = best;
+    }
+  }
+  if (!live || matrix.output == nullptr) return;
+  const std::size_t plane = static_cast<std::size_t>(split) * batch * rows;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const std::size_t out = plane + static_cast<std::size_t>(t) * rows + row;
+    if constexpr (HalfOut) {
+      reinterpret_cast<__half*>(matrix.output)[out] = to_half(total[t]);
+    } else {
+      reinterpret_cast<float*>(matrix.output)[out] = total[t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tiled row gather (lowbit_gemv.hip:191-231): out[c] = fp16(w(row,c) * ws(row,g)).
 // ---------------------------------------------------------------------------
 
@@ -1356,8 +1630,62 @@ void launch_direct_kernel(const GemmArgs& base_args, uint32_t total_tiles, hipSt
   }
 }
 
+// Kernel family of a GEMM launch: chosen by shape, or forced by the test/bench entry.
+enum GemmFamily : int32_t { kFamilyAuto = 0, kFamilyMfma = 1, kFamilyDot = 2 };
+
+// Whether the dot kernel can run a launch: W3/W4 x A4 at 1-8 tokens, activation scales
+// read as aligned dword pairs (4-byte aligned, even group count).
+bool dot_supported(int32_t format, int abits, const GemmArgs& args, bool partials) {
+  return abits == 4 && (format == GFXI_W3G128 || format == GFXI_W4G128) && args.batch <= 8 &&
+         (partials || (args.groups % 2 == 0 && aligned(args.activation_scales, 4)));
+}
+
+template <int Format, bool HalfOut, bool Partials>
+void launch_dot_kernel(const GemmArgs& base_args, hipStream_t stream) {
+  if constexpr (Format == GFXI_W3G128 || Format == GFXI_W4G128) {
+    GemmArgs args = base_args;
+    uint32_t blocks = 0;
+    for (unsigned i = 0; i < 4; ++i) {
+      args.tile_begin[i] = blocks;
+      // unused trailing slots repeat the last matrix with zero tiles
+      const bool used = i == 0 || base_args.tile_begin[i] != base_args.tile_begin[4];
+      if (used) blocks += (args.matrix[i].tiles + 3) / 4;
+    }
+    args.tile_begin[4] = blocks;
+    unsigned max_ranges = 1;
+    for (unsigned sp = 0; sp < args.splits; ++sp) {
+      const GroupRange g = split_groups(args.groups, sp, args.splits);
+      max_ranges = std::max(max_ranges, range_count(g.end - g.begin));
+    }
+    const unsigned waves = std::min(min_range_count(args.groups, args.splits), kDotMaxWaves);
+    auto go = [&](auto kernel, auto nt) {
+      constexpr int NT = decltype(nt)::value;
+      const std::size_t lds = static_cast<std::size_t>(waves) * kDotRegion<NT> +
+                              (max_ranges > 1 ? static_cast<std::size_t>(max_ranges) * NT * 64u * 4u : 0);
+      hipLaunchKernelGGL(kernel, dim3(blocks * args.splits), dim3(64 * waves), lds, stream, args);
+    };
+    switch (args.batch) {
+      case 1: go(lowbit_gemm_dot_kernel<Format, 1, HalfOut, Partials>, std::integral_constant<int, 1>{}); break;
+      case 2: go(lowbit_gemm_dot_kernel<Format, 2, HalfOut, Partials>, std::integral_constant<int, 2>{}); break;
+      case 3: go(lowbit_gemm_dot_kernel<Format, 3, HalfOut, Partials>, std::integral_constant<int, 3>{}); break;
+      case 4: go(lowbit_gemm_dot_kernel<Format, 4, HalfOut, Partials>, std::integral_constant<int, 4>{}); break;
+      case 5: go(lowbit_gemm_dot_kernel<Format, 5, HalfOut, Partials>, std::integral_constant<int, 5>{}); break;
+      case 6: go(lowbit_gemm_dot_kernel<Format, 6, HalfOut, Partials>, std::integral_constant<int, 6>{}); break;
+      case 7: go(lowbit_gemm_dot_kernel<Format, 7, HalfOut, Partials>, std::integral_constant<int, 7>{}); break;
+      default: go(lowbit_gemm_dot_kernel<Format, 8, HalfOut, Partials>, std::integral_constant<int, 8>{}); break;
+    }
+  } else {
+    (void)base_args;
+    (void)stream;
+  }
+}
+
 template <int Format, int ABits, bool HalfOut, bool Partials>
-void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
+void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t stream, int32_t family) {
+  if (family == kFamilyDot) {
+    launch_dot_kernel<Format, HalfOut, Partials>(args, stream);
+    return;
+  }
   // Direct operands pay off from 9 tokens on (one token window, quad-coalesced
   // activation loads, two row tiles per workgroup); up to 8 tokens the LDS-staged
   // kernel with its packed token windows is as fast or faster.
@@ -1405,13 +1733,14 @@ void launch_gemm_kernel(const GemmArgs& args, uint32_t total_tiles, hipStream_t 
 }
 
 template <int ABits, bool HalfOut, bool Partials>
-void dispatch_gemm(int32_t format, const GemmArgs& args, uint32_t total_tiles, hipStream_t stream) {
+void dispatch_gemm(int32_t format, const GemmArgs& args, uint32_t total_tiles, hipStream_t stream,
+                   int32_t family) {
   if (format == GFXI_W2G128) {
-    launch_gemm_kernel<GFXI_W2G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+    launch_gemm_kernel<GFXI_W2G128, ABits, HalfOut, Partials>(args, total_tiles, stream, family);
   } else if (format == GFXI_W3G128) {
-    launch_gemm_kernel<GFXI_W3G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+    launch_gemm_kernel<GFXI_W3G128, ABits, HalfOut, Partials>(args, total_tiles, stream, family);
   } else {
-    launch_gemm_kernel<GFXI_W4G128, ABits, HalfOut, Partials>(args, total_tiles, stream);
+    launch_gemm_kernel<GFXI_W4G128, ABits, HalfOut, Partials>(args, total_tiles, stream, family);
   }
 }
 
@@ -1429,7 +1758,7 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
                    const uint16_t* activation_scales, int32_t* partials, std::size_t columns,
                    uint32_t batch, bool half_out, hipStream_t stream,
                    unsigned long long* argmax_keys = nullptr, uint32_t argmax_rows = 0,
-                   uint32_t splits = 1) {
+                   uint32_t splits = 1, int32_t family = kFamilyAuto) {
   if (!valid_weight_format(format)) {
     return fail(GFXI_UNSUPPORTED, std::string(name) + " supports W2G128, W3G128 and W4G128");
   }
@@ -1491,14 +1820,21 @@ int32_t gemm_entry(const char* name, int32_t format, const MatrixBinding* bindin
     return fail(GFXI_INVALID_ARGUMENT, std::string(name) + " grid is too large");
   }
   const auto total = static_cast<uint32_t>(tiles);
+  const bool dot_ok = dot_supported(format, activation_bits, args, partials != nullptr);
+  if (family == kFamilyDot && !dot_ok) {
+    return fail(GFXI_UNSUPPORTED, std::string(name) +
+                                      ": the dot kernel runs W3/W4 x A4 at 1-8 tokens with 4-byte "
+                                      "aligned activation scales and an even group count");
+  }
+  if (family == kFamilyAuto) family = kFamilyMfma;
   if (partials != nullptr) {
-    if (activation_bits == 4) dispatch_gemm<4, false, true>(format, args, total, stream);
-    else dispatch_gemm<8, false, true>(format, args, total, stream);
+    if (activation_bits == 4) dispatch_gemm<4, false, true>(format, args, total, stream, family);
+    else dispatch_gemm<8, false, true>(format, args, total, stream, family);
   } else if (activation_bits == 4) {
-    if (half_out) dispatch_gemm<4, true, false>(format, args, total, stream);
-    else dispatch_gemm<4, false, false>(format, args, total, stream);
+    if (half_out) dispatch_gemm<4, true, false>(format, args, total, stream, family);
+    else dispatch_gemm<4, false, false>(format, args, total, stream, family);
   } else {
-    dispatch_gemm<8, false, false>(format, args, total, stream);
+    dispatch_gemm<8, false, false>(format, args, total, stream, family);
   }
   return launch_status((std::string(name) + " launch failed").c_str());
 }
@@ -1802,6 +2138,26 @@ extern "C" int32_t gfxinfer_debug_gemm_partials(int32_t format, const uint8_t* t
                               nullptr, rows};
   return gemm_entry("gfx950 GEMM partials", format, &binding, 1, activation_bits, activations,
                     nullptr, partials, columns, batch, false, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_debug_gemm_family(int32_t family, int32_t format, const uint8_t* tiled_weights,
+                                              const uint16_t* tiled_weight_scales,
+                                              const uint8_t* packed_activations,
+                                              const uint16_t* activation_scales, void* output,
+                                              int32_t half_output, int32_t* partials,
+                                              unsigned long long* argmax_keys, uint32_t argmax_rows,
+                                              size_t rows, size_t columns, uint32_t batch,
+                                              uint32_t splits, void* stream) {
+  if (family != kFamilyMfma && family != kFamilyDot) {
+    return fail(GFXI_INVALID_ARGUMENT, "kernel family must be 1 (MFMA) or 2 (dot)");
+  }
+  const uint16_t* scales =
+      partials != nullptr ? reinterpret_cast<const uint16_t*>(tiled_weights) : tiled_weight_scales;
+  const MatrixBinding binding{tiled_weights, scales, output, rows};
+  return gemm_entry("gfx950 GEMM (kernel family)", format, &binding, 1, 4, packed_activations,
+                    partials != nullptr ? nullptr : activation_scales, partials, columns, batch,
+                    half_output != 0, static_cast<hipStream_t>(stream), argmax_keys, argmax_rows, splits,
+                    family);
 }
 
 extern "C" int32_t gfxinfer_launch_lowbit_row_gather_tiled(int32_t format,

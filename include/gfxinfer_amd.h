@@ -202,6 +202,24 @@ int32_t gfxinfer_debug_gemm_partials(int32_t format, const uint8_t* tiled_weight
                                      size_t rows, size_t columns, uint32_t batch,
                                      int32_t* partials, void* stream);
 
+/* Test and bench hook, no reference counterpart: one A4 GEMM launch through a named
+ * kernel family, 1 = the MFMA kernels (16x16x64 int8, used for every shape by the
+ * launchers above) or 2 = the v_dot8_i32_i4 kernel (W3/W4, 1-8 tokens, activation
+ * scales 4-byte aligned, K/128 even; otherwise GFXI_UNSUPPORTED).  Both families
+ * give bit-identical results.  The outputs are those of the launchers above:
+ * `output` fp32 (or fp16 when half_output != 0) [splits][batch][rows]; with
+ * `partials` non-null the int32 partials of gfxinfer_debug_gemm_partials instead
+ * (scales unused); with `argmax_keys` non-null the fused head's per-tile keys
+ * ([batch][rows/16], rows >= argmax_rows never win; `output` may then be NULL). */
+int32_t gfxinfer_debug_gemm_family(int32_t family, int32_t format, const uint8_t* tiled_weights,
+                                   const uint16_t* tiled_weight_scales,
+                                   const uint8_t* packed_activations,
+                                   const uint16_t* activation_scales, void* output,
+                                   int32_t half_output, int32_t* partials,
+                                   unsigned long long* argmax_keys, uint32_t argmax_rows,
+                                   size_t rows, size_t columns, uint32_t batch, uint32_t splits,
+                                   void* stream);
+
 /* Calibration: a plain streaming read of `bytes` from `data` (16-byte aligned,
  * a nonzero multiple of 16) by `workgroups` x 256 lanes, so that a weight-streaming
  * kernel's time can be set beside what one launch reading the same bytes takes on the
