@@ -98,6 +98,37 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Largest 64-bit key over the wave, in every lane: DPP moves of both words within each
+// 16-lane row (the pairings of row16_max), then the four row maxima read out to
+// scalars.  Keys compare as integers, so the pairing does not change the result.
+template <int Ctrl>
+__device__ __forceinline__ unsigned long long dpp_move_key(unsigned long long v) {
+  const unsigned lo = static_cast<unsigned>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<unsigned>(v)), Ctrl, 0xF, 0xF, false));
+  const unsigned hi = static_cast<unsigned>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<unsigned>(v >> 32)), Ctrl, 0xF, 0xF, false));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long v) {
+  unsigned long long o = dpp_move_key<kDppXor1>(v);
+  v = o > v ? o : v;
+  o = dpp_move_key<kDppXor2>(v);
+  v = o > v ? o : v;
+  o = dpp_move_key<kDppHalfMirror>(v);
+  v = o > v ? o : v;
+  o = dpp_move_key<kDppMirror>(v);
+  v = o > v ? o : v;
+  unsigned long long best = 0ull;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<unsigned>(v)), 16 * r));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<unsigned>(v >> 32)), 16 * r));
+    const unsigned long long k = (static_cast<unsigned long long>(hi) << 32) | lo;
+    best = k > best ? k : best;
+  }
+  return best;
+}
+
 // The row an argmax key names: the key's low word is 0xffffffff - row (so that equal
 // values keep the lowest row); key 0 ("no candidate") names row 0.
 __device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
@@ -122,11 +153,7 @@ __device__ __forceinline__ unsigned long long block_max_key(const unsigned long 
 #pragma unroll
     for (unsigned u = 0; u < kLoads; ++u) best = k[u] > best ? k[u] : best;
   }
-#pragma unroll
-  for (int offset = 32; offset != 0; offset >>= 1) {
-    const unsigned long long other = __shfl_xor(best, offset);
-    best = other > best ? other : best;
-  }
+  best = wave_max_key(best);
   if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = best;
   __syncthreads();
   best = partial[0];

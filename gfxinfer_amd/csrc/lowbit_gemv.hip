@@ -1521,11 +1521,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_keys_kernel(
 #pragma unroll
     for (unsigned u = 0; u < kArgmaxLoads; ++u) best = k[u] > best ? k[u] : best;
   }
-#pragma unroll
-  for (int offset = 32; offset != 0; offset >>= 1) {
-    const unsigned long long other = __shfl_xor(best, offset);
-    best = other > best ? other : best;
-  }
+  best = wave_max_key(best);
   if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -34,13 +34,22 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
 // A4 codes of the next projection, independent of this build's launch shape: a code that
 // flips between two summation orders changes a projection by a whole quantization step.
 // Needs blockDim.x >= 256; all threads return the total.  The caller synchronizes the
-// workgroup between writing `row` and this call.
+// workgroup between writing `row` and this call.  The tree runs on VALU lane moves, not
+// LDS round trips: step 16 takes the upper row of each 32-lane half with
+// v_permlane16_swap, steps 8..1 are DPP row_shl moves (lane l reads lane l + d of its
+// row); the lanes that feed lane 0 of each half add exactly the values the shfl_down
+// tree adds, in the same order.
+// MaxElements bounds `elements` (one batch of LDS reads per chain when it is at most
+// 256 x 24, no loop).
+template <uint32_t MaxElements = 32768>
 __device__ float reference_square_sum(const __half* row, uint32_t elements, float* scratch) {
   const unsigned t = threadIdx.x;
   float s = 0.0F;
+  __builtin_assume(elements <= MaxElements);
   if (t < 256u) {
-    // Eight LDS reads in flight per batch; the fmaf chain keeps index order.
-    constexpr unsigned kBatch = 8;
+    // Every chain of rows up to 6144 elements in one batch of LDS reads; the fmaf
+    // chain keeps index order.
+    constexpr unsigned kBatch = 24;
     for (uint32_t i0 = t; i0 < elements; i0 += 256u * kBatch) {
       float f[kBatch];
 #pragma unroll
@@ -54,11 +63,15 @@ __device__ float reference_square_sum(const __half* row, uint32_t elements, floa
       }
     }
   }
-  s += __shfl_down(s, 16, 32);
-  s += __shfl_down(s, 8, 32);
-  s += __shfl_down(s, 4, 32);
-  s += __shfl_down(s, 2, 32);
-  s += __shfl_down(s, 1, 32);
+  {
+    const unsigned u = __float_as_uint(s);
+    const auto swapped = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    s += __uint_as_float(swapped[1]);  // rows 0 and 2 now read rows 1 and 3
+  }
+  s += dpp_move<0x108>(s);  // row_shl:8
+  s += dpp_move<0x104>(s);  // row_shl:4
+  s += dpp_move<0x102>(s);  // row_shl:2
+  s += dpp_move<0x101>(s);  // row_shl:1
   if (t < 256u && (t & 31u) == 0u) scratch[t >> 5] = s;
   __syncthreads();
   const float a0 = scratch[0] + scratch[4], a1 = scratch[1] + scratch[5];
@@ -167,8 +180,11 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
       }
     }
   }
-  // 2) Residual add (fp16 rounding of the sum), staged for the sum of squares.
+  // 2) Residual add (fp16 rounding of the sum), staged for the sum of squares.  The
+  //    residual rows go to memory only at the end, so that no wave waits for those
+  //    stores on the way through the reduction.
   float x[Slots][2];
+  __half2 sum_pair[Slots];
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     x[j][0] = 0.0F;
@@ -188,15 +204,16 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
         }
         a = to_half(__half2float(a) + u.x);
         b = to_half(__half2float(b) + u.y);
-        *reinterpret_cast<__half2*>(residual_out + base + i) = __halves2half2(a, b);
       }
+      sum_pair[j] = __halves2half2(a, b);
       x[j][0] = __half2float(a);
       x[j][1] = __half2float(b);
       *reinterpret_cast<__half2*>(staged + i) = __halves2half2(a, b);
     }
   }
   __syncthreads();
-  const float inverse = inverse_rms(reference_square_sum(staged, elements, scratch), elements, epsilon);
+  const float inverse =
+      inverse_rms(reference_square_sum<Slots * 16u * 128u>(staged, elements, scratch), elements, epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t g = wave + j * waves;
@@ -214,6 +231,13 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
       const uint32_t groups = elements / 128u;
       quantize_group_a4(n0, n1, codes + static_cast<std::size_t>(blockIdx.x) * (elements / 2) + g * 64u,
                         scales + static_cast<std::size_t>(blockIdx.x) * groups + g, lane);
+    }
+  }
+  if constexpr (Residual) {
+#pragma unroll
+    for (unsigned j = 0; j < Slots; ++j) {
+      const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
+      if (i < elements) *reinterpret_cast<__half2*>(residual_out + base + i) = sum_pair[j];
     }
   }
 }
@@ -359,7 +383,8 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
     if (i < elements) *reinterpret_cast<uint32_t*>(staged + i) = hin[j];
   }
   __syncthreads();
-  const float inverse = inverse_rms(reference_square_sum(staged, elements, scratch), elements, a.epsilon);
+  const float inverse =
+      inverse_rms(reference_square_sum<Slots * 16u * 128u>(staged, elements, scratch), elements, a.epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t g = wave + j * waves;
@@ -1069,8 +1094,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   for (unsigned j = 0; j < J; ++j) n[j] = x[j] * (inverse * (1.0F + bf16_to_float(wb[j])));
   float v0 = n[0];
   const unsigned half = a.rotary / 2;
-  // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.
-  const float partner = __shfl(n[0], lane < half ? lane + half : lane - half);
+  // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.  At
+  // rotary 64 (both model shapes) that is the other half of the wave: one
+  // v_permlane32_swap instead of an LDS permute.
+  float partner;
+  if (half == 32u) {
+    const unsigned u = __float_as_uint(n[0]);
+    const auto swapped = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    partner = __uint_as_float(lane < 32u ? swapped[1] : swapped[0]);
+  } else {
+    partner = __shfl(n[0], lane < half ? lane + half : lane - half);
+  }
   if (lane < a.rotary) {
     const unsigned fi = lane % half;
     const float exponent = (2.0F * static_cast<float>(fi)) / static_cast<float>(a.rotary);
