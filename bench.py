@@ -749,11 +749,28 @@ def pmc_probe(launches=8, rows=17408, cols=5120, batch=5):
                       "gemm_algorithmic_bytes": algorithmic_bytes(rows, cols, batch)}))
 
 
+def headline_kernel_digest():
+    """SHA-256 (first 16 hex digits) of the headline kernel's source: lowbit_gemv.hip from
+    its operand expansion through lowbit_gemm_kernel, plus common.hpp.  A committed
+    profile records the digest of the source it measured, so a changed kernel shows up
+    as a stale profile instead of passing its old counters on."""
+    import hashlib
+    csrc = os.path.join(ROOT, "gfxinfer_amd", "csrc")
+    text = open(os.path.join(csrc, "lowbit_gemv.hip")).read()
+    begin, end = text.index("// Operand expansion."), text.index("// Direct-operand GEMM.")
+    digest = hashlib.sha256(text[begin:end].encode())
+    digest.update(open(os.path.join(csrc, "common.hpp"), "rb").read())
+    return digest.hexdigest()[:16]
+
+
 def committed_profile():
     """The headline kernel's committed rocprofv3 summary: its file, average dispatch
     duration (kernel trace) and HBM bytes per launch (FETCH_SIZE + WRITE_SIZE passes,
-    calibrated), or None where the summary lacks them."""
+    calibrated), or None where the summary lacks them.  When the kernel source no longer
+    has the digest the summary records, the traffic figure is withheld (None) and the
+    summary is marked stale."""
     out = {"file": os.path.relpath(PROFILE, ROOT), "kernel_us": None, "traffic": None}
+    recorded = None
     try:
         for line in open(PROFILE):
             if line.startswith("traffic_bytes_per_launch"):
@@ -762,8 +779,15 @@ def committed_profile():
                 out["kernel_us"] = float(line.split("=")[1].split()[0])
             elif line.startswith("tree"):
                 out["tree"] = line.split("=", 1)[1].strip()
+            elif line.startswith("kernel_source_sha256"):
+                recorded = line.split("=", 1)[1].strip()
     except (OSError, ValueError, IndexError):
         pass
+    out["kernel_source_sha256"] = headline_kernel_digest()
+    out["source_matches"] = recorded == out["kernel_source_sha256"]
+    if not out["source_matches"]:
+        out["stale"] = "the kernel source differs from the one the summary measured: traffic withheld"
+        out["traffic"] = None
     return out
 
 

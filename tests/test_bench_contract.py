@@ -29,3 +29,18 @@ def test_headline_algorithmic_bytes():
     # W4, the down shape and one token change only the terms they name
     assert bench.algorithmic_bytes(5120, 17408, 1, wbits=4) == (
         5120 * 17408 // 2 + 5120 * 136 * 2 + 17408 // 2 + 136 * 2 + 5120 * 4)
+
+
+def test_committed_traffic_is_withheld_when_the_kernel_source_changed(tmp_path, monkeypatch):
+    """The roofline's traffic comes from a committed PMC summary; it is reported only
+    while the headline kernel's source still has the digest that summary measured."""
+    import bench
+    digest = bench.headline_kernel_digest()
+    summary = tmp_path / "summary.txt"
+    for recorded, expect in ((digest, 35403459), ("0" * 16, None)):
+        summary.write_text(f"kernel_avg_us = 9.6\ntraffic_bytes_per_launch = 35403459\n"
+                           f"kernel_source_sha256 = {recorded}\n")
+        monkeypatch.setattr(bench, "PROFILE", str(summary))
+        profile = bench.committed_profile()
+        assert profile["traffic"] == expect
+        assert profile["source_matches"] == (expect is not None)
