@@ -487,14 +487,18 @@ def _matrix_bytes(model, names):
     return total
 
 
-def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates=True, shape="27b"):
+def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates=True, shape="27b",
+                 long_context=3584):
     """Full synthetic 27B-shaped model: hipGraph-captured MTP chain +
     64-layer verifier of depth D, forced seeded 85 % Bernoulli acceptance, rollback or
     state swap per round.  Emitted tok/s = sum(accepted + 1) / time, verified tok/s =
     sum(D + 1) / time (the reference's evaluated target tokens).  shape "27b": the
     BASELINE configs' heads (40/8 x 128 attention, 16/32 GDN, vocabulary 151936);
     "reference": the reference's own model (qwen38_spec.h:16-34: 24/4 x 256 attention,
-    16/48 GDN, vocabulary 248320), same widths, depth and formats otherwise."""
+    16/48 GDN, vocabulary 248320), same widths, depth and formats otherwise.  The rounds
+    run in a 4096-token context from its start (positions below ~450), and again
+    (`depth_D_from_P` entries) after a chunked prefill of `long_context` seeded tokens, so
+    that attention reads the keys and values of ~3.6-4.1 K positions."""
     import numpy as np
     from gfxinfer_amd.runtime import QwenDecodeSession, SyntheticModel, qwen38_27b_spec, qwen38_reference_spec
 
@@ -538,6 +542,30 @@ def verify_bench(depths=(4, 31), rounds=60, warmup=8, seed=2026, reference_rates
                 "weight_gbs": round(round_bytes * n / elapsed / 1e9, 1),
                 "weight_frac_of_hbm_peak": round(round_bytes * n / elapsed / 1e9 / HBM_PEAK_GBS, 4),
             }
+            if long_context:
+                session = QwenDecodeSession(model, 4096, depth + 1)
+                prompt = rng.integers(0, spec.tokenizer_vocabulary_size, long_context)
+                token = session.prefill([int(t) for t in prompt])
+                for _ in range(2):
+                    token = session.speculative_step_forced(token, depth, _forced_acceptance(rng, depth)).tokens[-1]
+                start = session.position()
+                emitted = verified = 0
+                n = min(rounds, (4096 - start) // (depth + 1) - 1)
+                t0 = time.perf_counter()
+                for _ in range(n):
+                    r = session.speculative_step_forced(token, depth, _forced_acceptance(rng, depth))
+                    emitted += len(r.tokens)
+                    verified += depth + 1
+                    token = r.tokens[-1]
+                elapsed = time.perf_counter() - t0
+                end = session.position()
+                session.close()
+                results[f"depth_{depth}_from_{long_context}"] = {
+                    "rounds": n, "positions": [start, end],
+                    "ms_per_round": round(elapsed / n * 1e3, 4),
+                    "emitted_tok_s": round(emitted / elapsed, 2),
+                    "verified_tok_s": round(verified / elapsed, 2),
+                }
         if reference_rates:
             results.update(reference_bench_rates(model, spec))
     finally:

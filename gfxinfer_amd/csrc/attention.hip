@@ -268,42 +268,88 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
   const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
   const float* po = a.partial_o + static_cast<std::size_t>(linear) * a.splits * kD + 2 * lane;
-  // Splits in batches of kBatch with every load of a batch issued before its first use
-  // (a long context has hundreds of splits); the sums still run in split order.
-  constexpr unsigned kBatch = 8;
-  float best = -INFINITY;
-  for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
-    float m[kBatch];
-#pragma unroll
-    for (unsigned k = 0; k < kBatch; ++k) m[k] = s0 + k < used ? ml[2 * (s0 + k)] : -INFINITY;
-#pragma unroll
-    for (unsigned k = 0; k < kBatch; ++k) best = fmaxf(best, m[k]);
-  }
   float o0[kG], o1[kG], total = 0.0F;
 #pragma unroll
   for (unsigned j = 0; j < kG; ++j) o0[j] = o1[j] = 0.0F;
-  for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
-    float2 mls[kBatch], v[kBatch][kG];
+  if (used <= 128u) {
+    // Up to 128 splits (a 4096-position context at either head size): lane s holds the
+    // (max, sum) of splits s and 64 + s, loaded at once; the maximum is a DPP wave
+    // reduction and each split's weight exp(m - best) is computed once, in its lane,
+    // and read out to a scalar where the output rows are accumulated.  The output rows
+    // stream in batches of kBatch splits, each batch's loads issued while the previous
+    // batch is accumulated; the accumulation keeps split order.
+    const unsigned sa = lane, sb = 64u + lane;
+    const float2 pa = *reinterpret_cast<const float2*>(ml + 2 * (sa < used ? sa : 0u));
+    const float2 pb = *reinterpret_cast<const float2*>(ml + 2 * (sb < used ? sb : 0u));
+    const float best = wave_max(fmaxf(sa < used ? pa.x : -INFINITY, sb < used ? pb.x : -INFINITY));
+    const float wa = sa < used ? expf(pa.x - best) : 0.0F;
+    const float wb = sb < used ? expf(pb.x - best) : 0.0F;
+    total = wave_sum(fmaf(pb.y, wb, pa.y * wa));
+    constexpr unsigned kBatch = 16;
+    float2 cur[kBatch][kG], next[kBatch][kG];
+    auto fetch = [&](float2 (&v)[kBatch][kG], unsigned s0) __attribute__((always_inline)) {
 #pragma unroll
-    for (unsigned k = 0; k < kBatch; ++k) {
-      const unsigned s = s0 + k < used ? s0 + k : s0;
-      mls[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
-#pragma unroll
-      for (unsigned j = 0; j < kG; ++j) {
-        v[k][j] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD + 128 * j);
-      }
-    }
-    // No early exit: the loads above stay ahead of every use (splits past `used` are
-    // loaded again from split s0 and skipped here, in split order as before).
-#pragma unroll
-    for (unsigned k = 0; k < kBatch; ++k) {
-      if (s0 + k < used) {
-        const float w = expf(mls[k].x - best);
-        total = fmaf(mls[k].y, w, total);
+      for (unsigned k = 0; k < kBatch; ++k) {
+        const unsigned s = s0 + k < used ? s0 + k : used - 1u;  // past the last split: loaded, not used
 #pragma unroll
         for (unsigned j = 0; j < kG; ++j) {
-          o0[j] = fmaf(v[k][j].x, w, o0[j]);
-          o1[j] = fmaf(v[k][j].y, w, o1[j]);
+          v[k][j] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD + 128 * j);
+        }
+      }
+    };
+    fetch(cur, 0);
+    for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
+      if (s0 + kBatch < used) fetch(next, s0 + kBatch);
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) {
+        const unsigned s = s0 + k;
+        if (s < used) {
+          const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s < 64u ? wa : wb), s & 63u));
+#pragma unroll
+          for (unsigned j = 0; j < kG; ++j) {
+            o0[j] = fmaf(cur[k][j].x, w, o0[j]);
+            o1[j] = fmaf(cur[k][j].y, w, o1[j]);
+          }
+        }
+      }
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k)
+#pragma unroll
+        for (unsigned j = 0; j < kG; ++j) cur[k][j] = next[k][j];
+    }
+  } else {
+    // Longer contexts: splits in batches of kBatch with every load of a batch issued
+    // before its first use; the sums run in split order.
+    constexpr unsigned kBatch = 8;
+    float best = -INFINITY;
+    for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
+      float m[kBatch];
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) m[k] = s0 + k < used ? ml[2 * (s0 + k)] : -INFINITY;
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) best = fmaxf(best, m[k]);
+    }
+    for (unsigned s0 = 0; s0 < used; s0 += kBatch) {
+      float2 mls[kBatch], v[kBatch][kG];
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) {
+        const unsigned s = s0 + k < used ? s0 + k : s0;
+        mls[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
+#pragma unroll
+        for (unsigned j = 0; j < kG; ++j) {
+          v[k][j] = *reinterpret_cast<const float2*>(po + static_cast<std::size_t>(s) * kD + 128 * j);
+        }
+      }
+#pragma unroll
+      for (unsigned k = 0; k < kBatch; ++k) {
+        if (s0 + k < used) {
+          const float w = expf(mls[k].x - best);
+          total = fmaf(mls[k].y, w, total);
+#pragma unroll
+          for (unsigned j = 0; j < kG; ++j) {
+            o0[j] = fmaf(v[k][j].x, w, o0[j]);
+            o1[j] = fmaf(v[k][j].y, w, o1[j]);
+          }
         }
       }
     }
