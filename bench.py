@@ -353,6 +353,44 @@ def gemm_family_bench(reps=40, budget=600e6, batches=(1, 2, 3, 4, 5, 8), headlin
     return out
 
 
+def attention_bench(reps=50):
+    """Gated GQA decode attention with the A4 quantizer of the o projection
+    (split + combine launches) at the verifier's block sizes, for both head shapes, at a
+    short and a 4 K context: microseconds per call from HIP events around graph replays,
+    and the K/V bytes it reads (every visible position of every KV head, fp16)."""
+    import torch
+    import gfxinfer_amd as gx
+
+    L = gx.lib()
+    stream = torch.cuda.Stream()
+    capacity = 4096 + 32
+    out = []
+    for hq, hkv, d in ((40, 8, 128), (24, 4, 256)):
+        kc = (torch.randn(capacity, hkv, d, device="cuda") * 0.5).half()
+        vc = (torch.randn(capacity, hkv, d, device="cuda") * 0.5).half()
+        for t in (1, 5, 32):
+            q = torch.randn(t, hq, d, device="cuda").half()
+            gate = torch.randn(t, hq, 2 * d, device="cuda")
+            o = torch.empty(t, hq, d, device="cuda").half()
+            codes = torch.empty(t, hq * d // 2, dtype=torch.uint8, device="cuda")
+            scales = torch.empty(t, hq * d // 128, dtype=torch.int16, device="cuda")
+            wb = L.gfxinfer_attention_workspace_bytes(t, hq, d, capacity)
+            work = torch.empty(wb // 4, device="cuda")
+            for base in (400, 4064):
+                def fn(_i, base=base):
+                    gx.check(L.gfxinfer_launch_gated_attention_decode_block_quantize_i4(
+                        q.data_ptr(), gate.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
+                        codes.data_ptr(), scales.data_ptr(), base, capacity, t, hq, hkv, d, work.data_ptr(), wb,
+                        stream.cuda_stream))
+                us = _graph_time(stream, fn, 8, reps)
+                kv = (base + t - 1) * hkv * d * 2 * 2
+                line = {"attention": f"{hq}/{hkv}x{d}", "tokens": t, "positions": base + t - 1, "us": round(us, 3),
+                        "kv_bytes": kv, "gbs": round(kv / us / 1e3, 1)}
+                out.append(line)
+                print(json.dumps(line), flush=True)
+    return out
+
+
 def read_floor_bench(reps=20, budget=640e6, total=1280 << 20):
     """Yardstick for the GEMV roofline: one launch of a plain streaming read of the
     headline GEMV's algorithmic bytes, half and twice that, and the LM head's size,
@@ -845,6 +883,8 @@ def main():
     ap.add_argument("--gemm-families", nargs="?", const="all", choices=("all", "headline"),
                     help="time the MFMA and v_dot8 A4 GEMM kernel families at 1-8 tokens side by side "
                          "(headline: W3A4 [17408,5120] at 1 and 5 tokens only)")
+    ap.add_argument("--attention", action="store_true",
+                    help="time gated decode attention (+A4) at 1/5/32 tokens, short and 4 K contexts")
     ap.add_argument("--prefill", action="store_true",
                     help="time chunked prefill against the reference's serial prefill loop (27B shapes)")
     ap.add_argument("--read-floor", action="store_true",
@@ -869,6 +909,9 @@ def main():
         return
     if args.gemv_table:
         gemv_table_bench()
+        return
+    if args.attention:
+        attention_bench()
         return
     if args.gemm_families:
         gemm_family_bench(headline=args.gemm_families == "headline")

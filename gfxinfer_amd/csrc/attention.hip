@@ -243,31 +243,34 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   }
 }
 
-// Merge the splits of each (token, q head) and apply the sigmoid gate.  One
-// wave per (token, head); lane owns head dims 128 j + 2l, 128 j + 2l + 1 of each 128-dim
-// group j of the head.  With codes set, the wave also quantizes each group of its head
-// to A4G128 as quantize_activation_i4 does on the fp16 output row
-// ([T][Hq * D] -> codes [T][Hq * D / 2], scales [T][Hq * D / 128]).
+// Merge the splits of each (token, q head) and apply the sigmoid gate.  One wave per
+// (token, head, 128-dim group j of the head); lane owns head dims 128 j + 2l and
+// 128 j + 2l + 1.  The waves of a head's groups compute the same weights and sum.  With
+// codes set, the wave also quantizes its group to A4G128 as quantize_activation_i4 does
+// on the fp16 output row ([T][Hq * D] -> codes [T][Hq * D / 2], scales [T][Hq * D / 128]).
 template <unsigned kD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, const float* __restrict__ gate,
                                                                 __half* __restrict__ output,
                                                                 uint8_t* __restrict__ codes,
                                                                 __half* __restrict__ scales) {
   constexpr unsigned kSplit = split_positions<kD>();
-  constexpr unsigned kG = kD / 128;  // 128-dim groups per head
+  constexpr unsigned kGroups = kD / 128;  // 128-dim groups per head: one wave each
+  constexpr unsigned kG = 1;              // groups per wave
   const uint32_t linear = blockIdx.x * 4u + (threadIdx.x >> 6);
-  if (linear >= a.tokens * a.q_heads) return;
+  if (linear >= a.tokens * a.q_heads * kGroups) return;
   const unsigned lane = threadIdx.x & 63u;
-  const uint32_t t = linear / a.q_heads, qh = linear - t * a.q_heads;
+  const uint32_t th = linear / kGroups, group = linear - th * kGroups;  // (token, head), group
+  const uint32_t t = th / a.q_heads, qh = th - t * a.q_heads;
   // The gate row first: it does not depend on the position.
-  const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD;
+  const float* g = gate + static_cast<std::size_t>(t) * a.q_heads * kD * 2 + static_cast<std::size_t>(qh) * kD * 2 + kD +
+                   128 * group;
   float2 gv[kG];
 #pragma unroll
   for (unsigned j = 0; j < kG; ++j) gv[j] = *reinterpret_cast<const float2*>(g + 128 * j + 2 * lane);
   const uint64_t count = base_count_of(a) + t;
   const unsigned used = static_cast<unsigned>((count + kSplit - 1) / kSplit);
-  const float* ml = a.partial_ml + static_cast<std::size_t>(linear) * a.splits * 2;
-  const float* po = a.partial_o + static_cast<std::size_t>(linear) * a.splits * kD + 2 * lane;
+  const float* ml = a.partial_ml + static_cast<std::size_t>(th) * a.splits * 2;
+  const float* po = a.partial_o + static_cast<std::size_t>(th) * a.splits * kD + 128 * group + 2 * lane;
   float o0[kG], o1[kG], total = 0.0F;
 #pragma unroll
   for (unsigned j = 0; j < kG; ++j) o0[j] = o1[j] = 0.0F;
@@ -358,13 +361,14 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a, cons
   for (unsigned j = 0; j < kG; ++j) {
     const float g0 = 1.0F / (1.0F + expf(-gv[j].x));
     const float g1 = 1.0F / (1.0F + expf(-gv[j].y));
-    __half* out = output + static_cast<std::size_t>(linear) * kD + 128 * j + 2 * lane;
+    const unsigned jg = group + j;
+    __half* out = output + static_cast<std::size_t>(th) * kD + 128 * jg + 2 * lane;
     const __half h0 = to_half(o0[j] / total * g0), h1 = to_half(o1[j] / total * g1);
     out[0] = h0;
     out[1] = h1;
     if (codes != nullptr) {
-      quantize_group_a4(h0, h1, codes + static_cast<std::size_t>(linear) * (kD / 2) + 64 * j,
-                        scales + static_cast<std::size_t>(linear) * kG + j, lane);
+      quantize_group_a4(h0, h1, codes + static_cast<std::size_t>(th) * (kD / 2) + 64 * jg,
+                        scales + static_cast<std::size_t>(th) * kGroups + jg, lane);
     }
   }
 }
@@ -430,7 +434,7 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
     hipLaunchKernelGGL((attention_split_kernel<256, 4>), grid, block, 0, stream, args);
   }
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
-  const dim3 combine_grid((batch * q_heads + 3) / 4);
+  const dim3 combine_grid((batch * q_heads * (head_size / 128) + 3) / 4);  // one wave per 128-dim group
   __half* out16 = reinterpret_cast<__half*>(output);
   __half* scales16 = reinterpret_cast<__half*>(scales);
   if (head_size == 128) {
