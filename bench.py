@@ -353,7 +353,7 @@ def gemm_family_bench(reps=40, budget=600e6, batches=(1, 2, 3, 4, 5, 8), headlin
     return out
 
 
-def attention_bench(reps=50):
+def attention_bench(reps=50, contexts=(400, 4064)):
     """Gated GQA decode attention with the A4 quantizer of the o projection
     (split + combine launches) at the verifier's block sizes, for both head shapes, at a
     short and a 4 K context: microseconds per call from HIP events around graph replays,
@@ -376,7 +376,7 @@ def attention_bench(reps=50):
             scales = torch.empty(t, hq * d // 128, dtype=torch.int16, device="cuda")
             wb = L.gfxinfer_attention_workspace_bytes(t, hq, d, capacity)
             work = torch.empty(wb // 4, device="cuda")
-            for base in (400, 4064):
+            for base in contexts:
                 def fn(_i, base=base):
                     gx.check(L.gfxinfer_launch_gated_attention_decode_block_quantize_i4(
                         q.data_ptr(), gate.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
@@ -870,6 +870,8 @@ def main():
                          "then ends with the last round)")
     ap.add_argument("--verify-model", choices=("27b", "reference"), default="27b",
                     help="verify-round model heads: the BASELINE 27B shape or the reference's own model")
+    ap.add_argument("--long-context", type=int, default=3584,
+                    help="prefill length before the long-context verify rounds (0: skip them)")
     ap.add_argument("--verify-depths", default="4,8,16,31",
                     help="comma-separated MTP depths of the verify-round measurement")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -885,6 +887,8 @@ def main():
                          "(headline: W3A4 [17408,5120] at 1 and 5 tokens only)")
     ap.add_argument("--attention", action="store_true",
                     help="time gated decode attention (+A4) at 1/5/32 tokens, short and 4 K contexts")
+    ap.add_argument("--attention-context", type=int, default=0,
+                    help="--attention at this one context (visible positions of the first token) only")
     ap.add_argument("--prefill", action="store_true",
                     help="time chunked prefill against the reference's serial prefill loop (27B shapes)")
     ap.add_argument("--read-floor", action="store_true",
@@ -911,7 +915,7 @@ def main():
         gemv_table_bench()
         return
     if args.attention:
-        attention_bench()
+        attention_bench(contexts=(args.attention_context,) if args.attention_context else (400, 4064))
         return
     if args.gemm_families:
         gemm_family_bench(headline=args.gemm_families == "headline")
@@ -982,7 +986,8 @@ def main():
     if not args.no_verify:
         depths = tuple(int(d) for d in args.verify_depths.split(",") if d)
         out["verify"] = verify_bench(depths=depths, rounds=args.verify_rounds,
-                                     reference_rates=not args.no_reference_rates, shape=args.verify_model)
+                                     reference_rates=not args.no_reference_rates, shape=args.verify_model,
+                                     long_context=args.long_context)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
