@@ -9,6 +9,7 @@
 #include <cmath>
 #include <limits>
 #include <string>
+#include <utility>
 
 #include "common.hpp"
 
@@ -137,13 +138,21 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
 }
 
 // Register-resident variant for rows of up to Slots * 16 * 128 elements (even
-// count): one workgroup of up to 16 waves per row, wave w owns 128-element slots
-// w, w + waves, ...; each lane keeps its two values per slot in registers, so the
-// row is read once, reduced once and (Quantize) each 128 group is one wave's A4
-// quantizer.  Every global load (row, weights, all update planes) is issued before
-// the first use.  The update is the sum of `planes` fp32 planes `plane_stride`
-// apart, added in plane order (the split-K GEMM's output).  Same arithmetic per
-// element as rms_norm_kernel.
+// count): up to 16 waves per workgroup, wave w owns 128-element slots w, w + waves, ...;
+// each lane keeps its two values per slot in registers, so the row is read once and
+// reduced once.  Every global load (row, all update planes) is issued before the first
+// use.  The update is the sum of `planes` fp32 planes `plane_stride` apart, added in
+// plane order (the split-K GEMM's output).  Same arithmetic per element as
+// rms_norm_kernel.
+//
+// A row may be shared by `parts` workgroups: each one loads and reduces the whole row
+// (the sum of squares needs every element), then normalizes, quantizes and stores only
+// its own share of the row's 128-element slots.  The per-element work after the sum
+// (normalization, the A4 quantizer's maximum and exact divisions) is most of a row's
+// VALU time; split over `parts` compute units it no longer serializes on one.  Workgroup
+// b runs row (b / 8 / parts) * 8 + b % 8, part (b / 8) % parts, so that with the
+// round-robin dispatch over the eight XCDs the parts of a row share one L2.  Outputs
+// must not overlap the inputs when parts > 1 (the host falls back to one part).
 constexpr unsigned kNormSlots = 10;
 constexpr unsigned kNormPlaneSlots = 3;  // split-update variant: rows up to 6144
 constexpr unsigned kNormMaxPlanes = 8;
@@ -156,12 +165,20 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     const __half* __restrict__ input, const float* __restrict__ update,
     __half* __restrict__ residual_out, const uint16_t* __restrict__ weight,
     __half* __restrict__ output, uint8_t* __restrict__ codes, __half* __restrict__ scales,
-    uint32_t elements, float epsilon, bool unit_offset, uint32_t planes, uint64_t plane_stride) {
+    uint32_t elements, float epsilon, bool unit_offset, uint32_t planes, uint64_t plane_stride,
+    uint32_t rows, uint32_t parts) {
   __shared__ float scratch[16];
   __shared__ __half staged[Slots * 16u * 128u];  // the row, for the reference-ordered sum
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-  const std::size_t base = static_cast<std::size_t>(blockIdx.x) * elements;
-  // 1) Loads.  Dead slots read element 0 (always valid) and are ignored.
+  const uint32_t k = blockIdx.x / 8u;
+  const uint32_t row = (k / parts) * 8u + blockIdx.x % 8u;
+  if (row >= rows) return;  // whole workgroup: padding of the XCD-major grid
+  const uint32_t part = k % parts;
+  const uint32_t slot_count = (elements + 127u) / 128u;
+  const uint32_t own_begin = slot_count * part / parts, own_end = slot_count * (part + 1u) / parts;
+  const std::size_t base = static_cast<std::size_t>(row) * elements;
+  // 1) Loads.  Dead slots read element 0 (always valid) and are ignored.  The weights
+  //    are loaded for the slots this workgroup normalizes: own_begin + wave + j * waves.
   uint32_t hin[Slots];
   uint32_t wpair[Slots];  // the two bf16 weights of each lane's pair
   float2 upd[Slots][MaxPlanes];
@@ -170,7 +187,8 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
     const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
     const uint32_t at = i < elements ? i : 0u;
     hin[j] = *reinterpret_cast<const uint32_t*>(input + base + at);
-    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
+    const uint32_t wi = (own_begin + wave + j * waves) * 128u + 2u * lane;
+    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + (wi < elements ? wi : 0u));
     if constexpr (Residual) {
 #pragma unroll
       for (unsigned p = 0; p < MaxPlanes; ++p) {
@@ -183,12 +201,9 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
   // 2) Residual add (fp16 rounding of the sum), staged for the sum of squares.  The
   //    residual rows go to memory only at the end, so that no wave waits for those
   //    stores on the way through the reduction.
-  float x[Slots][2];
   __half2 sum_pair[Slots];
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
-    x[j][0] = 0.0F;
-    x[j][1] = 0.0F;
     const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
     if (i < elements) {
       __half a = __ushort_as_half(static_cast<unsigned short>(hin[j] & 0xffffu));
@@ -206,38 +221,41 @@ __global__ __launch_bounds__(1024) void rms_norm_rows_kernel(
         b = to_half(__half2float(b) + u.y);
       }
       sum_pair[j] = __halves2half2(a, b);
-      x[j][0] = __half2float(a);
-      x[j][1] = __half2float(b);
-      *reinterpret_cast<__half2*>(staged + i) = __halves2half2(a, b);
+      *reinterpret_cast<__half2*>(staged + i) = sum_pair[j];
     }
   }
   __syncthreads();
   const float inverse =
       inverse_rms(reference_square_sum<Slots * 16u * 128u>(staged, elements, scratch), elements, epsilon);
+  // 3) This workgroup's slots: normalized values from the staged row, A4 codes.
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
-    const uint32_t g = wave + j * waves;
+    const uint32_t g = own_begin + wave + j * waves;
+    if (g >= own_end) break;  // wave-uniform
     const uint32_t i = g * 128u + 2u * lane;
-    if (g * 128u >= elements) break;  // wave-uniform
     __half n0 = __float2half(0.0F), n1 = n0;
     if (i < elements) {
+      const __half2 v = *reinterpret_cast<const __half2*>(staged + i);
       const float w0 = bf16_to_float(static_cast<uint16_t>(wpair[j] & 0xffffu));
       const float w1 = bf16_to_float(static_cast<uint16_t>(wpair[j] >> 16));
-      n0 = to_half(x[j][0] * inverse * (unit_offset ? w0 + 1.0F : w0));
-      n1 = to_half(x[j][1] * inverse * (unit_offset ? w1 + 1.0F : w1));
+      n0 = to_half(__low2float(v) * inverse * (unit_offset ? w0 + 1.0F : w0));
+      n1 = to_half(__high2float(v) * inverse * (unit_offset ? w1 + 1.0F : w1));
       if (output != nullptr) *reinterpret_cast<__half2*>(output + base + i) = __halves2half2(n0, n1);
     }
     if constexpr (Quantize) {
       const uint32_t groups = elements / 128u;
-      quantize_group_a4(n0, n1, codes + static_cast<std::size_t>(blockIdx.x) * (elements / 2) + g * 64u,
-                        scales + static_cast<std::size_t>(blockIdx.x) * groups + g, lane);
+      quantize_group_a4(n0, n1, codes + static_cast<std::size_t>(row) * (elements / 2) + g * 64u,
+                        scales + static_cast<std::size_t>(row) * groups + g, lane);
     }
   }
   if constexpr (Residual) {
 #pragma unroll
     for (unsigned j = 0; j < Slots; ++j) {
-      const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
-      if (i < elements) *reinterpret_cast<__half2*>(residual_out + base + i) = sum_pair[j];
+      const uint32_t g = wave + j * waves;
+      const uint32_t i = g * 128u + 2u * lane;
+      if (g >= own_begin && g < own_end && i < elements) {
+        *reinterpret_cast<__half2*>(residual_out + base + i) = sum_pair[j];
+      }
     }
   }
 }
@@ -1199,30 +1217,41 @@ __global__ __launch_bounds__(256) void argmax_kernel(
 
 bool valid_epsilon(float epsilon) { return std::isfinite(epsilon) && epsilon > 0.0F; }
 
+// Workgroups per row of rms_norm_rows_kernel: enough that the rows' workgroups cover
+// the GPU (at most 256, one per CU for a 1024-thread workgroup), at most kNormMaxParts
+// and never more than the row's 128-element slots.
+constexpr uint32_t kNormMaxParts = 10;
+uint32_t norm_parts(uint32_t rows, uint32_t elements) {
+  const uint32_t row_octets = (rows + 7u) / 8u;
+  const uint32_t slots = (elements + 127u) / 128u;
+  return std::max(1u, std::min({kNormMaxParts, slots, 32u / row_octets}));
+}
+
 template <bool Residual, bool Quantize>
 void launch_norm(bool fast, unsigned per_wave_slots, uint32_t planes, dim3 block, std::size_t smem,
-                 uint32_t batch, hipStream_t stream, const __half* in, const float* update,
+                 uint32_t batch, uint32_t parts, hipStream_t stream, const __half* in, const float* update,
                  __half* ro, const uint16_t* weight, __half* out, uint8_t* codes, __half* sc,
                  uint32_t e, float epsilon, bool unit, uint64_t plane_stride) {
+  const dim3 grid(parts == 1 ? batch : 8u * parts * ((batch + 7u) / 8u));
   if (fast && per_wave_slots <= kNormPlaneSlots && (planes == 1 || Residual)) {
     if (planes == 1) {
-      hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, 1>), dim3(batch),
+      hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, 1>), grid,
                          block, 0, stream, in, update, ro, weight, out, codes, sc, e, epsilon, unit,
-                         planes, plane_stride);
+                         planes, plane_stride, batch, parts);
     } else if (planes == 4) {  // the session's split-K plane count: loads without conditions
       hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots, Residual ? 4 : 1, true>),
-                         dim3(batch), block, 0, stream, in, update, ro, weight, out, codes, sc, e,
-                         epsilon, unit, planes, plane_stride);
+                         grid, block, 0, stream, in, update, ro, weight, out, codes, sc, e,
+                         epsilon, unit, planes, plane_stride, batch, parts);
     } else {
       hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormPlaneSlots,
                                                Residual ? kNormMaxPlanes : 1>),
-                         dim3(batch), block, 0, stream, in, update, ro, weight, out, codes, sc, e,
-                         epsilon, unit, planes, plane_stride);
+                         grid, block, 0, stream, in, update, ro, weight, out, codes, sc, e,
+                         epsilon, unit, planes, plane_stride, batch, parts);
     }
   } else if (fast && planes == 1) {
-    hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormSlots, 1>), dim3(batch), block,
+    hipLaunchKernelGGL((rms_norm_rows_kernel<Residual, Quantize, kNormSlots, 1>), grid, block,
                        0, stream, in, update, ro, weight, out, codes, sc, e, epsilon, unit, planes,
-                       plane_stride);
+                       plane_stride, batch, parts);
   } else {
     hipLaunchKernelGGL((rms_norm_kernel<Residual, Quantize>), dim3(batch), dim3(256), smem, stream,
                        in, update, ro, weight, out, codes, sc, e, epsilon, unit, planes,
@@ -1264,17 +1293,36 @@ int32_t norm_entry(const char* name, bool residual, bool quantize, const uint16_
   const unsigned per_wave = (slots + waves - 1) / waves;
   const dim3 block(64u * waves);
   const uint64_t stride = static_cast<uint64_t>(batch) * e;
+  // Several workgroups per row only when no output overlaps an input: a part's stores
+  // must not reach what another part of the same row still reads (in-place calls run
+  // one workgroup per row, whose loads all precede its stores).
+  auto range = [](const void* p, std::size_t bytes) {
+    const auto b = reinterpret_cast<std::uintptr_t>(p);
+    return std::pair<std::uintptr_t, std::uintptr_t>{b, p == nullptr ? b : b + bytes};
+  };
+  const std::size_t row_bytes = static_cast<std::size_t>(batch) * e * 2;
+  const std::pair<std::uintptr_t, std::uintptr_t> reads[] = {
+      range(input, row_bytes), range(residual ? update : nullptr, planes * stride * 4), range(weight, e * 2)};
+  const std::pair<std::uintptr_t, std::uintptr_t> writes[] = {
+      range(residual ? residual_out : nullptr, row_bytes), range(output, row_bytes),
+      range(quantize ? codes : nullptr, row_bytes / 4), range(quantize ? scales : nullptr, row_bytes / 128)};
+  bool disjoint = true;
+  for (const auto& w : writes) {
+    for (const auto& r : reads) disjoint = disjoint && (w.first == w.second || r.first == r.second ||
+                                                        w.second <= r.first || r.second <= w.first);
+  }
+  const uint32_t parts = disjoint ? norm_parts(batch, e) : 1u;
   if (residual && quantize) {
-    launch_norm<true, true>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+    launch_norm<true, true>(fast, per_wave, planes, block, smem, batch, parts, stream, in, update, ro,
                             weight, out, codes, sc, e, epsilon, unit, stride);
   } else if (residual) {
-    launch_norm<true, false>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+    launch_norm<true, false>(fast, per_wave, planes, block, smem, batch, parts, stream, in, update, ro,
                              weight, out, codes, sc, e, epsilon, unit, stride);
   } else if (quantize) {
-    launch_norm<false, true>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+    launch_norm<false, true>(fast, per_wave, planes, block, smem, batch, parts, stream, in, update, ro,
                              weight, out, codes, sc, e, epsilon, unit, stride);
   } else {
-    launch_norm<false, false>(fast, per_wave, planes, block, smem, batch, stream, in, update, ro,
+    launch_norm<false, false>(fast, per_wave, planes, block, smem, batch, parts, stream, in, update, ro,
                               weight, out, codes, sc, e, epsilon, unit, stride);
   }
   return launch_status((std::string(name) + " launch failed").c_str());

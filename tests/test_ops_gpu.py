@@ -111,7 +111,8 @@ def test_residual_add_rms_norm_and_fused_quantize(device, gx, orc, batch):
 
 
 @pytest.mark.parametrize("n,batch,planes", [(5120, 5, 4), (5120, 32, 8), (5120, 1, 2), (6144, 3, 3),
-                                            (10240, 2, 4), (640, 7, 5), (5120, 4, 1)])
+                                            (10240, 2, 4), (640, 7, 5), (5120, 4, 1), (5120, 13, 4),
+                                            (5120, 40, 4), (256, 6, 4)])
 def test_residual_norm_sums_update_planes(device, gx, orc, n, batch, planes):
     """Planes entry == the plain fused entry on the fp32 sum of the planes taken in
     plane order (bit-exact: same additions, same kernel arithmetic); the residual is
@@ -153,6 +154,33 @@ def test_residual_norm_sums_update_planes(device, gx, orc, n, batch, planes):
         dr.data_ptr(), dr.data_ptr(), 9, dr.data_ptr(), dw.data_ptr(), dr.data_ptr(), dr.data_ptr(),
         dr.data_ptr(), n, batch, EPS, 1, None)
     assert bad == gx.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("batch", [1, 5, 32])
+def test_residual_norm_in_place_equals_out_of_place(device, gx, orc, batch):
+    """The residual written over its own input (one workgroup per row, every load before
+    any store) equals the out-of-place call, which shares each row among several
+    workgroups."""
+    n, planes = 5120, 4
+    rng = np.random.default_rng(500 + batch)
+    res = _half(rng.standard_normal((batch, n)))
+    upd = (rng.standard_normal((planes, batch, n)) * 0.5).astype(np.float32)
+    w = _bf16(np.round(rng.standard_normal(n) * 64) / 1024)
+    L = gx.lib()
+    du, dw = dev(upd), dev(w)
+    outs = []
+    for in_place in (False, True):
+        dr = dev(res)
+        ro = dr if in_place else empty((batch, n), np.uint16)
+        no = empty((batch, n), np.uint16)
+        codes, scales = empty((batch, n // 2), np.uint8), empty((batch, n // 128), np.uint16)
+        say("residual norm in place", in_place, batch)
+        gx.check(L.gfxinfer_launch_residual_add_rms_norm_quantize_i4_planes(
+            dr.data_ptr(), du.data_ptr(), planes, ro.data_ptr(), dw.data_ptr(), no.data_ptr(),
+            codes.data_ptr(), scales.data_ptr(), n, batch, EPS, 1, None))
+        outs.append([host(ro, np.uint16), host(no, np.uint16), host(codes), host(scales, np.uint16)])
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("n", [5120, 130, 129, 7168])  # register-resident rows; odd / long: strided
