@@ -321,10 +321,21 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
   const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const uint32_t elements = a.elements;
   const std::size_t row = blockIdx.y;
-  const bool second = blockIdx.x != 0;
+  // gridDim.x = 2 * parts: each half row is shared by `parts` workgroups, which all load
+  // and reduce the whole half and normalize / quantize their own share of its slots.
+  const uint32_t parts = gridDim.x / 2u;
+  const bool second = blockIdx.x >= parts;
+  const uint32_t part = blockIdx.x % parts;
+  const uint32_t slot_count = (elements + 127u) / 128u;
+  const uint32_t own_begin = slot_count * part / parts, own_end = slot_count * (part + 1u) / parts;
   const uint16_t* weight = second ? a.right_weight : a.left_weight;
   const uint32_t half_offset = second ? elements : 0u;
   uint32_t hin[Slots], wpair[Slots];
+#pragma unroll
+  for (unsigned j = 0; j < Slots; ++j) {
+    const uint32_t wi = (own_begin + wave + j * waves) * 128u + 2u * lane;
+    wpair[j] = *reinterpret_cast<const uint32_t*>(weight + (wi < elements ? wi : 0u));
+  }
   if (EmbedFormat != 0 && !second) {
     // the token's embedding row, dequantized per column pair; the token is the previous
     // proposal's greedy pick when its argmax keys are given (a workgroup-uniform branch)
@@ -333,7 +344,7 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
       __shared__ unsigned long long key_partial[16];
       const uint32_t index = argmax_key_row(block_max_key(a.keys, a.key_count, key_partial));
       token = a.key_token_ids != nullptr ? a.key_token_ids[index] : index;
-      if (threadIdx.x == 0) *a.key_token_out = token;
+      if (threadIdx.x == 0 && part == 0) *a.key_token_out = token;
     } else {
       token = a.indirect_token != nullptr ? *a.indirect_token : a.token;
     }
@@ -350,7 +361,6 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
       for (unsigned j = 0; j < Slots; ++j) {
         const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
         const uint32_t at = i < elements ? i : 0u;
-        wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
         code[j] = a.embed_codes[chunk_offset(EmbedFormat, table_row, at, groups) + (at % 32u) / 2u];
         scale_bits[j] = __half_as_ushort(a.embed_scales[scale_offset(table_row, at / kGroup, groups)]);
       }
@@ -369,8 +379,6 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
 #pragma unroll
     for (unsigned j = 0; j < Slots; ++j) {
       const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
-      const uint32_t at = i < elements ? i : 0u;
-      wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
       hin[j] = 0u;
       if (i < elements && token < a.embed_rows) {
         const uint8_t* chunk = a.embed_codes + chunk_offset(EmbedFormat, token, i, groups);
@@ -389,15 +397,11 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
       const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
       const uint32_t at = i < elements ? i : 0u;
       hin[j] = *reinterpret_cast<const uint32_t*>(input + at);
-      wpair[j] = *reinterpret_cast<const uint32_t*>(weight + at);
     }
   }
-  float x[Slots][2];
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
     const uint32_t i = (wave + j * waves) * 128u + 2u * lane;
-    x[j][0] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] & 0xffffu)));
-    x[j][1] = __half2float(__ushort_as_half(static_cast<unsigned short>(hin[j] >> 16)));
     if (i < elements) *reinterpret_cast<uint32_t*>(staged + i) = hin[j];
   }
   __syncthreads();
@@ -405,15 +409,16 @@ __global__ __launch_bounds__(1024) void dual_rms_norm_rows_kernel(DualNormArgs a
       inverse_rms(reference_square_sum<Slots * 16u * 128u>(staged, elements, scratch), elements, a.epsilon);
 #pragma unroll
   for (unsigned j = 0; j < Slots; ++j) {
-    const uint32_t g = wave + j * waves;
+    const uint32_t g = own_begin + wave + j * waves;
     const uint32_t i = g * 128u + 2u * lane;
-    if (g * 128u >= elements) break;  // wave-uniform
+    if (g >= own_end) break;  // wave-uniform
     __half n0 = __float2half(0.0F), n1 = n0;
     if (i < elements) {
+      const __half2 v = *reinterpret_cast<const __half2*>(staged + i);
       const float w0 = bf16_to_float(static_cast<uint16_t>(wpair[j] & 0xffffu));
       const float w1 = bf16_to_float(static_cast<uint16_t>(wpair[j] >> 16));
-      n0 = to_half(x[j][0] * inverse * (a.unit_offset ? w0 + 1.0F : w0));
-      n1 = to_half(x[j][1] * inverse * (a.unit_offset ? w1 + 1.0F : w1));
+      n0 = to_half(__low2float(v) * inverse * (a.unit_offset ? w0 + 1.0F : w0));
+      n1 = to_half(__high2float(v) * inverse * (a.unit_offset ? w1 + 1.0F : w1));
       if (a.output != nullptr) {
         *reinterpret_cast<__half2*>(a.output + row * 2u * elements + half_offset + i) = __halves2half2(n0, n1);
       }
@@ -1482,12 +1487,26 @@ int32_t mtp_input_entry(int32_t embedding_format, const uint8_t* embedding_codes
   a.epsilon = epsilon;
   a.unit_offset = add_unit_offset != 0;
   const auto s = static_cast<hipStream_t>(stream);
+  // Each half row is shared by up to kNormMaxParts workgroups (the A4 quantizer of a
+  // whole half is VALU-bound on one compute unit) unless an output overlaps the
+  // conditioning row or the argmax keys, which every part reads.
+  auto disjoint = [](const void* w, std::size_t wn, const void* r, std::size_t rn) {
+    const auto wb = reinterpret_cast<std::uintptr_t>(w), rb = reinterpret_cast<std::uintptr_t>(r);
+    return w == nullptr || r == nullptr || wb + wn <= rb || rb + rn <= wb;
+  };
+  bool separate = true;
+  for (const auto& [w, wn] : {std::pair<const void*, std::size_t>{concatenated_output, 4 * elements},
+                              {packed_output, elements}, {scales, 4 * elements / kGroup}}) {
+    separate = separate && disjoint(w, wn, conditioning, 2 * elements) &&
+               disjoint(w, wn, a.keys, std::size_t{a.key_count} * 8u);
+  }
+  const dim3 grid(2u * (separate ? std::min<uint32_t>(kNormMaxParts, static_cast<uint32_t>(elements / kGroup)) : 1u));
   if (embedding_format == GFXI_W2G128) {
-    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W2G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W2G128, true>), grid, dim3(1024), 0, s, a);
   } else if (embedding_format == GFXI_W3G128) {
-    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W3G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W3G128, true>), grid, dim3(1024), 0, s, a);
   } else {
-    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W4G128, true>), dim3(2, 1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL((dual_rms_norm_rows_kernel<3, GFXI_W4G128, true>), grid, dim3(1024), 0, s, a);
   }
   return launch_status("MTP input (embedding + dual RMSNorm + A4) launch failed");
 }
