@@ -49,7 +49,35 @@ struct AttnArgs {
   const uint64_t* indirect_position;  // if set: base_count = *p + 1
   uint32_t tokens, q_heads, kv_heads, splits, capacity;
   float scale;
+  // Fused Q/K RMSNorm + RoPE + K/V append (attention_split_kernel<D, W, true>): fp32
+  // inputs as qk_norm_rope_kernel takes them (q_in [T][Hq][q_stride], k_in
+  // [T][Hkv][k_stride], v_in [T][Hkv][D]); token t sits at position base_count - 1 + t.
+  const float* q_in;
+  const uint16_t* q_weight;
+  const float* k_in;
+  const uint16_t* k_weight;
+  const float* v_in;
+  __half* key_cache_out;    // == key_cache
+  __half* value_cache_out;  // == value_cache
+  uint32_t q_stride, k_stride, rotary;
+  float theta;
 };
+
+// Query rows (q_heads / kv_heads x tokens) a fused-RoPE attention workgroup normalizes,
+// rotates and keeps in LDS (the LDS of the four-wave kernel stays within 64 KB).
+constexpr unsigned fused_rope_rows(unsigned head_size) { return head_size == 128 ? 32u : 30u; }
+// ... and at most one token per wave and eight query heads per KV head (the input rows
+// are held in registers).  A wave's token costs one cos / sin evaluation and its query
+// rows on the path to the first MFMA: measured against the RoPE launch + attention pair,
+// one token per wave saves 1.35 us per call (one token), two per wave lose 0.56 us (five).
+constexpr unsigned kRopeTokensPerWave = 1;
+constexpr unsigned kRopeMaxGroup = 8;
+bool fused_rope_supported(uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size) {
+  if ((head_size != 128 && head_size != 256) || kv_heads == 0 || q_heads % kv_heads != 0) return false;
+  const uint32_t group = q_heads / kv_heads;
+  return batch >= 1 && batch <= 4 * kRopeTokensPerWave && group <= kRopeMaxGroup &&
+         group * batch <= fused_rope_rows(head_size);
+}
 
 __device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
   return a.indirect_position != nullptr ? *a.indirect_position + 1u : a.base_count;
@@ -57,8 +85,16 @@ __device__ __forceinline__ uint64_t base_count_of(const AttnArgs& a) {
 
 // Waves = 4 or 8 per workgroup: each wave takes every Waves-th 16-row tile of the
 // (token, q head) rows of its KV head; eight waves for blocks of more than four tiles.
-template <unsigned kD, unsigned Waves>
+//
+// Rope = true (four waves, at most fused_rope_rows(kD) query rows): the workgroup also does
+// what qk_norm_rope_kernel with the K/V append does for its KV head, with the same
+// arithmetic: it normalizes and rotates its query rows into LDS (cos / sin once per
+// token), and the workgroup whose split holds a new position writes that position's
+// normalized, rotated K row and fp16 V row to the caches and to its own K / V^T tiles
+// (the staging skips new positions, whose cache rows are not written yet).
+template <unsigned kD, unsigned Waves, bool Rope = false>
 __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a) {
+  static_assert(!Rope || Waves == 4, "fused RoPE runs on the four-wave kernel");
   constexpr unsigned kSplit = split_positions<kD>();
   constexpr unsigned kTiles = kSplit / 16;  // score tiles of 16 positions
   constexpr unsigned kSteps = kSplit / 32;  // P.V K-steps of 32 positions
@@ -70,6 +106,7 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   // f16 MFMAs then carry ~22 significant bits of p, close to the reference's fp32 P.V.
   __shared__ __align__(16) _Float16 ps[Waves][16][kRow];
   __shared__ __align__(16) _Float16 ps_lo[Waves][16][kRow];
+  __shared__ __align__(16) _Float16 qs[Rope ? fused_rope_rows(kD) : 1][kD + kPad];  // rotated Q rows
 
   // Workgroups in split-major order (KV head fastest): the splits that hold visible
   // positions come first in dispatch order, ahead of the ones that exit at once.
@@ -89,6 +126,13 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   // zeros past the last row.
   auto load_q = [&](unsigned rt, h8 (&q)[kQ]) __attribute__((always_inline)) {
     const unsigned qrow = rt * 16 + m;
+    if constexpr (Rope) {
+#pragma unroll
+      for (unsigned s = 0; s < kQ; ++s) {
+        q[s] = rt < row_tiles && qrow < rows ? *reinterpret_cast<const h8*>(&qs[qrow][32 * s + 8 * kb]) : h8{};
+      }
+      return;
+    }
     if (rt < row_tiles && qrow < rows) {
       const unsigned t = qrow / group, g = qrow - t * group;
       const __half* src = a.query + (static_cast<std::size_t>(t) * a.q_heads + hk * group + g) * kD + 8 * kb;
@@ -133,28 +177,110 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
     vb[u] = *reinterpret_cast<const u32x4*>(a.value_cache + (pb * a.kv_heads + hk) * kD + d8);
   }
   h8 q_next[kQ];
-  load_q(wave, q_next);
+  if constexpr (!Rope) load_q(wave, q_next);
+  // Positions from `fresh` on are the block's own tokens: with Rope their cache rows are
+  // written by this launch, so the staging below leaves them to the RoPE step.
+  const uint64_t fresh = Rope ? base - 1 : ~uint64_t{0};
+  if constexpr (Rope) {
+    // Wave w takes token w (at most four tokens, at most eight query heads per KV
+    // head): every input row is loaded up front (one memory latency, behind the K/V
+    // tile loads), then cos / sin once per token, its query rows and, when the token's
+    // position falls in this split, its K / V rows.
+    constexpr unsigned J = kD / 64;
+    float qx[kRopeTokensPerWave][kRopeMaxGroup][J], kx[kRopeTokensPerWave][J], vx[kRopeTokensPerWave][J];
+    uint16_t qw[J], kw[J];
+#pragma unroll
+    for (unsigned j = 0; j < J; ++j) {
+      qw[j] = a.q_weight[lane + 64 * j];
+      kw[j] = a.k_weight[lane + 64 * j];
+    }
+#pragma unroll
+    for (unsigned i = 0; i < kRopeTokensPerWave; ++i) {
+      const unsigned t = wave + Waves * i;
+      if (t >= a.tokens) break;  // wave-uniform
+#pragma unroll
+      for (unsigned g = 0; g < kRopeMaxGroup; ++g) {
+        if (g >= group) break;  // workgroup-uniform
+        const float* in = a.q_in + (static_cast<std::size_t>(t) * a.q_heads + hk * group + g) * a.q_stride;
+#pragma unroll
+        for (unsigned j = 0; j < J; ++j) qx[i][g][j] = in[lane + 64 * j];
+      }
+      const uint64_t position = fresh + t;
+      if (position >= p0 && position < p0 + kSplit) {  // wave-uniform
+        const std::size_t src = static_cast<std::size_t>(t) * a.kv_heads + hk;
+#pragma unroll
+        for (unsigned j = 0; j < J; ++j) {
+          kx[i][j] = a.k_in[src * a.k_stride + lane + 64 * j];
+          vx[i][j] = a.v_in[src * kD + lane + 64 * j];
+        }
+      }
+    }
+#pragma unroll
+    for (unsigned i = 0; i < kRopeTokensPerWave; ++i) {
+      const unsigned t = wave + Waves * i;
+      if (t >= a.tokens) break;
+      const uint64_t position = fresh + t;
+      float c = 1.0F, sn = 0.0F;
+      if (lane < a.rotary) rope_cos_sin(static_cast<float>(position), a.rotary, a.theta, lane, c, sn);
+#pragma unroll
+      for (unsigned g = 0; g < kRopeMaxGroup; ++g) {
+        if (g >= group) break;
+        __half h[J];
+        norm_rope_row<kD>(qx[i][g], qw, a.rotary, c, sn, lane, h);
+#pragma unroll
+        for (unsigned j = 0; j < J; ++j) {
+          *reinterpret_cast<unsigned short*>(&qs[t * group + g][lane + 64 * j]) = __half_as_ushort(h[j]);
+        }
+      }
+      if (position >= p0 && position < p0 + kSplit) {
+        __half h[J];
+        norm_rope_row<kD>(kx[i], kw, a.rotary, c, sn, lane, h);
+        const std::size_t row = (position * a.kv_heads + hk) * kD;
+        const unsigned local = static_cast<unsigned>(position - p0);
+#pragma unroll
+        for (unsigned j = 0; j < J; ++j) {
+          const __half vh = to_half(vx[i][j]);
+          a.key_cache_out[row + lane + 64 * j] = h[j];
+          a.value_cache_out[row + lane + 64 * j] = vh;
+          *reinterpret_cast<unsigned short*>(&ks[local][lane + 64 * j]) = __half_as_ushort(h[j]);
+          *reinterpret_cast<unsigned short*>(&vt[lane + 64 * j][local]) = __half_as_ushort(vh);
+        }
+      }
+    }
+  }
 #pragma unroll
   for (unsigned u = 0; u < kStage; ++u) {
     const unsigned i = tid + u * kThreads;
     const unsigned p = i / (kD / 8), d8 = (i % (kD / 8)) * 8;
     if (p0 + p >= limit) kr[u] = u32x4{0, 0, 0, 0};
-    *reinterpret_cast<u32x4*>(&ks[p][d8]) = kr[u];
+    if (!Rope || p0 + p < fresh || p0 + p >= limit) *reinterpret_cast<u32x4*>(&ks[p][d8]) = kr[u];
   }
 #pragma unroll
   for (unsigned u = 0; u < kVItems; ++u) {
     const unsigned i = tid + u * kThreads;
     const unsigned pair = i % (kSplit / 2), d8 = (i / (kSplit / 2)) * 8;
-    if (p0 + 2 * pair >= limit) va[u] = u32x4{0, 0, 0, 0};
-    if (p0 + 2 * pair + 1 >= limit) vb[u] = u32x4{0, 0, 0, 0};
+    const uint64_t pa = p0 + 2 * pair, pb = pa + 1;
+    if (pa >= limit) va[u] = u32x4{0, 0, 0, 0};
+    if (pb >= limit) vb[u] = u32x4{0, 0, 0, 0};
+    // With Rope a pair may hold a new position (written by the RoPE step): then only the
+    // older half (if any) is staged, as a 16-bit store.
+    const bool a_staged = !Rope || pa < fresh || pa >= limit;
+    const bool b_staged = !Rope || pb < fresh || pb >= limit;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const unsigned lo = (va[u][e / 2] >> (16 * (e % 2))) & 0xffffu;
       const unsigned hi = (vb[u][e / 2] >> (16 * (e % 2))) & 0xffffu;
-      *reinterpret_cast<unsigned*>(&vt[d8 + e][2 * pair]) = lo | (hi << 16);
+      if (a_staged && b_staged) {
+        *reinterpret_cast<unsigned*>(&vt[d8 + e][2 * pair]) = lo | (hi << 16);
+      } else if (a_staged) {
+        *reinterpret_cast<unsigned short*>(&vt[d8 + e][2 * pair]) = static_cast<unsigned short>(lo);
+      } else if (b_staged) {
+        *reinterpret_cast<unsigned short*>(&vt[d8 + e][2 * pair + 1]) = static_cast<unsigned short>(hi);
+      }
     }
   }
   __syncthreads();
+  if constexpr (Rope) load_q(wave, q_next);
 
   for (unsigned rt = wave; rt < row_tiles; rt += Waves) {
     // This tile's Q operand was loaded one tile ahead; the next tile's goes out now.
@@ -394,6 +520,22 @@ extern "C" size_t gfxinfer_attention_workspace_bytes(uint32_t batch, uint32_t q_
 
 namespace gfx950 {
 namespace {
+// The combine launch of a split launch: one wave per (token, head, 128-dim group).
+int32_t launch_combine(const AttnArgs& args, const float* gate, uint16_t* output, uint8_t* codes,
+                       uint16_t* scales, uint32_t head_size, hipStream_t stream) {
+  const dim3 combine_grid((args.tokens * args.q_heads * (head_size / 128) + 3) / 4);
+  __half* out16 = reinterpret_cast<__half*>(output);
+  __half* scales16 = reinterpret_cast<__half*>(scales);
+  if (head_size == 128) {
+    hipLaunchKernelGGL(attention_combine_kernel<128>, combine_grid, dim3(256), 0, stream, args, gate, out16,
+                       codes, scales16);
+  } else {
+    hipLaunchKernelGGL(attention_combine_kernel<256>, combine_grid, dim3(256), 0, stream, args, gate, out16,
+                       codes, scales16);
+  }
+  return launch_status("gated attention combine launch failed");
+}
+
 int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t* key_cache,
                         const uint16_t* value_cache, uint16_t* output, uint64_t base_count,
                         const uint64_t* indirect, size_t capacity, uint32_t batch, uint32_t q_heads,
@@ -434,17 +576,67 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
     hipLaunchKernelGGL((attention_split_kernel<256, 4>), grid, block, 0, stream, args);
   }
   if (const int32_t s = launch_status("gated attention split launch failed"); s != GFXI_OK) return s;
-  const dim3 combine_grid((batch * q_heads * (head_size / 128) + 3) / 4);  // one wave per 128-dim group
-  __half* out16 = reinterpret_cast<__half*>(output);
-  __half* scales16 = reinterpret_cast<__half*>(scales);
-  if (head_size == 128) {
-    hipLaunchKernelGGL(attention_combine_kernel<128>, combine_grid, dim3(256), 0, stream, args, gate, out16,
-                       codes, scales16);
-  } else {
-    hipLaunchKernelGGL(attention_combine_kernel<256>, combine_grid, dim3(256), 0, stream, args, gate, out16,
-                       codes, scales16);
+  return launch_combine(args, gate, output, codes, scales, head_size, stream);
+}
+
+int32_t rope_attention_entry(const float* query_input, const uint16_t* query_weight, size_t query_stride,
+                             const float* key_input, const uint16_t* key_weight, size_t key_stride,
+                             const float* value_input, size_t rotary, float theta, const float* gate,
+                             uint16_t* key_cache, uint16_t* value_cache, uint16_t* output, uint8_t* codes,
+                             uint16_t* scales, uint64_t position, const uint64_t* indirect, size_t capacity,
+                             uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size,
+                             float* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (query_input == nullptr || query_weight == nullptr || key_input == nullptr || key_weight == nullptr ||
+      value_input == nullptr || gate == nullptr || key_cache == nullptr || value_cache == nullptr ||
+      output == nullptr || codes == nullptr || scales == nullptr || workspace == nullptr || batch == 0 ||
+      q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0 || (head_size != 128 && head_size != 256) ||
+      rotary == 0 || rotary > 64 || rotary % 2 != 0 || query_stride < head_size || key_stride < head_size ||
+      !std::isfinite(theta) || theta <= 0.0F || capacity == 0 || capacity > (1u << 24) ||
+      (indirect == nullptr && (position >= capacity || batch > capacity - position))) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid fused Q/K RMSNorm/RoPE/K-V append/attention arguments");
   }
-  return launch_status("gated attention combine launch failed");
+  if (!fused_rope_supported(batch, q_heads, kv_heads, head_size)) {
+    return fail(GFXI_UNSUPPORTED, "fused RoPE attention takes at most 4 tokens, 8 query heads per KV head and " +
+                                      std::to_string(fused_rope_rows(head_size)) +
+                                      " query rows per KV head; use the RoPE launch then the attention launch");
+  }
+  if (workspace_bytes < gfxinfer_attention_workspace_bytes(batch, q_heads, head_size, capacity)) {
+    return fail(GFXI_INVALID_ARGUMENT, "attention workspace is too small");
+  }
+  const auto splits = static_cast<uint32_t>(split_count(head_size, capacity));
+  AttnArgs args{};
+  args.query = nullptr;
+  args.key_cache = reinterpret_cast<const __half*>(key_cache);
+  args.value_cache = reinterpret_cast<const __half*>(value_cache);
+  args.partial_o = workspace;
+  args.partial_ml = workspace + static_cast<std::size_t>(batch) * q_heads * splits * head_size;
+  args.base_count = position + 1;
+  args.indirect_position = indirect;
+  args.tokens = batch;
+  args.q_heads = q_heads;
+  args.kv_heads = kv_heads;
+  args.splits = splits;
+  args.capacity = static_cast<uint32_t>(capacity);
+  args.scale = 1.0F / std::sqrt(static_cast<float>(head_size));
+  args.q_in = query_input;
+  args.q_weight = query_weight;
+  args.k_in = key_input;
+  args.k_weight = key_weight;
+  args.v_in = value_input;
+  args.key_cache_out = reinterpret_cast<__half*>(key_cache);
+  args.value_cache_out = reinterpret_cast<__half*>(value_cache);
+  args.q_stride = static_cast<uint32_t>(query_stride);
+  args.k_stride = static_cast<uint32_t>(key_stride);
+  args.rotary = static_cast<uint32_t>(rotary);
+  args.theta = theta;
+  const dim3 grid(splits * kv_heads), block(256);
+  if (head_size == 128) {
+    hipLaunchKernelGGL((attention_split_kernel<128, 4, true>), grid, block, 0, stream, args);
+  } else {
+    hipLaunchKernelGGL((attention_split_kernel<256, 4, true>), grid, block, 0, stream, args);
+  }
+  if (const int32_t s = launch_status("fused RoPE attention split launch failed"); s != GFXI_OK) return s;
+  return launch_combine(args, gate, output, codes, scales, head_size, stream);
 }
 }  // namespace
 }  // namespace gfx950
@@ -491,4 +683,36 @@ extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indi
   return attention_entry(query, gate, key_cache, value_cache, output, 0, base_position, capacity, batch,
                          q_heads, kv_heads, head_size, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream), codes, scales);
+}
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
+    const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
+    const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride, const float* value_input,
+    size_t rotary_size, float rope_theta, const float* gate, uint16_t* key_cache, uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, size_t position, size_t capacity, uint32_t batch,
+    uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace, size_t workspace_bytes,
+    void* stream) {
+  return rope_attention_entry(query_input, query_bf16_weight, query_input_stride, key_input, key_bf16_weight,
+                              key_input_stride, value_input, rotary_size, rope_theta, gate, key_cache,
+                              value_cache, output, codes, scales, position, nullptr, capacity, batch, q_heads,
+                              kv_heads, head_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
+    const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
+    const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride, const float* value_input,
+    size_t rotary_size, float rope_theta, const float* gate, uint16_t* key_cache, uint16_t* value_cache,
+    uint16_t* output, uint8_t* codes, uint16_t* scales, const uint64_t* base_position, size_t capacity,
+    uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (base_position == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect position is null");
+  return rope_attention_entry(query_input, query_bf16_weight, query_input_stride, key_input, key_bf16_weight,
+                              key_input_stride, value_input, rotary_size, rope_theta, gate, key_cache,
+                              value_cache, output, codes, scales, 0, base_position, capacity, batch, q_heads,
+                              kv_heads, head_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t gfxinfer_fused_rope_attention_supported(uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                                                           uint32_t head_size) {
+  return fused_rope_supported(batch, q_heads, kv_heads, head_size) ? 1 : 0;
 }

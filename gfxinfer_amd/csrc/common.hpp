@@ -161,6 +161,59 @@ __device__ __forceinline__ unsigned long long block_max_key(const unsigned long 
   return best;
 }
 
+__device__ __forceinline__ float bf16_to_float(uint16_t value) {
+  return __uint_as_float(static_cast<uint32_t>(value) << 16U);  // qwen_ops.hip:27-29
+}
+
+// RoPE rotation of lane `lane` < rotary at `position` (qwen_ops.hip:599-676): the angle
+// position * theta^(-2 (lane % (rotary / 2)) / rotary); cos and sin of it.
+__device__ __forceinline__ void rope_cos_sin(float position, unsigned rotary, float theta, unsigned lane,
+                                             float& c, float& s) {
+  const unsigned half = rotary / 2;
+  const unsigned fi = lane % half;
+  const float exponent = (2.0F * static_cast<float>(fi)) / static_cast<float>(rotary);
+  const float inverse_frequency = powf(theta, -exponent);
+  const float angle = position * inverse_frequency;
+  c = cosf(angle);
+  s = sinf(angle);
+}
+
+// Q/K RMSNorm (eps 1e-6, weights 1 + w) then RoPE of one head row of D values held by
+// one wave (all 64 lanes active): lane l holds elements l + 64 j of the row and of its
+// bf16 weights.  Dims < rotary rotate with their partner i +- rotary/2 (at rotary 64,
+// the other half of the wave: one v_permlane32_swap); c / s are rope_cos_sin's values
+// for the lane (unused past rotary).
+template <unsigned D>
+__device__ __forceinline__ void norm_rope_row(const float (&x)[D / 64], const uint16_t (&wb)[D / 64],
+                                              unsigned rotary, float c, float s, unsigned lane,
+                                              __half (&h)[D / 64]) {
+  constexpr unsigned J = D / 64;
+  float square = 0.0F;
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) square += x[j] * x[j];
+  const float inverse = rsqrtf(wave_sum(square) / static_cast<float>(D) + 1.0e-6F);
+  float n[J];
+#pragma unroll
+  for (unsigned j = 0; j < J; ++j) n[j] = x[j] * (inverse * (1.0F + bf16_to_float(wb[j])));
+  float v0 = n[0];
+  const unsigned half = rotary / 2;
+  float partner;
+  if (half == 32u) {
+    const unsigned u = __float_as_uint(n[0]);
+    const auto swapped = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    partner = __uint_as_float(lane < 32u ? swapped[1] : swapped[0]);
+  } else {
+    partner = __shfl(n[0], lane < half ? lane + half : lane - half);
+  }
+  if (lane < rotary) {
+    const float rotated = lane < half ? -partner : partner;
+    v0 = fmaf(n[0], c, rotated * s);
+  }
+  h[0] = to_half(v0);
+#pragma unroll
+  for (unsigned j = 1; j < J; ++j) h[j] = to_half(n[j]);
+}
+
 // One wave quantizes 128 fp16 values (two per lane) to A4G128 exactly as
 // quantize_activation_i4 (lowbit_gemv.hip:373-407) does.
 __device__ __forceinline__ void quantize_group_a4(__half x0h, __half x1h, uint8_t* codes,

@@ -19,10 +19,6 @@ namespace {
 using u32x4 = unsigned __attribute__((ext_vector_type(4)));
 using f32x4 = float __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float bf16_to_float(uint16_t value) {
-  return __uint_as_float(static_cast<uint32_t>(value) << 16U);  // qwen_ops.hip:27-29
-}
-
 __device__ __forceinline__ float silu(float x) { return x / (1.0F + expf(-x)); }
 
 
@@ -1108,38 +1104,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
 #pragma unroll
     for (unsigned j = 0; j < J; ++j) value[j] = v[lane + 64 * j];
   }
-  float square = 0.0F;
-#pragma unroll
-  for (unsigned j = 0; j < J; ++j) square += x[j] * x[j];
-  const float inverse = rsqrtf(wave_sum(square) / static_cast<float>(D) + 1.0e-6F);
-  float n[J];
-#pragma unroll
-  for (unsigned j = 0; j < J; ++j) n[j] = x[j] * (inverse * (1.0F + bf16_to_float(wb[j])));
-  float v0 = n[0];
-  const unsigned half = a.rotary / 2;
-  // rotary <= 64: only dims < 64 rotate; the partner of dim i is i +- rotary/2.  At
-  // rotary 64 (both model shapes) that is the other half of the wave: one
-  // v_permlane32_swap instead of an LDS permute.
-  float partner;
-  if (half == 32u) {
-    const unsigned u = __float_as_uint(n[0]);
-    const auto swapped = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    partner = __uint_as_float(lane < 32u ? swapped[1] : swapped[0]);
-  } else {
-    partner = __shfl(n[0], lane < half ? lane + half : lane - half);
-  }
-  if (lane < a.rotary) {
-    const unsigned fi = lane % half;
-    const float exponent = (2.0F * static_cast<float>(fi)) / static_cast<float>(a.rotary);
-    const float inverse_frequency = powf(a.theta, -exponent);
-    const float angle = position * inverse_frequency;
-    const float rotated = lane < half ? -partner : partner;
-    v0 = fmaf(n[0], cosf(angle), rotated * sinf(angle));
-  }
+  float c = 1.0F, sn = 0.0F;
+  if (lane < a.rotary) rope_cos_sin(position, a.rotary, a.theta, lane, c, sn);
   __half h[J];
-  h[0] = to_half(v0);
-#pragma unroll
-  for (unsigned j = 1; j < J; ++j) h[j] = to_half(n[j]);
+  norm_rope_row<D>(x, wb, a.rotary, c, sn, lane, h);
 #pragma unroll
   for (unsigned j = 0; j < J; ++j) out[lane + 64 * j] = h[j];
   if (append) {

@@ -266,6 +266,30 @@ struct gfxinfer_session {
                           bool stop_after_append) {
     GFXI_TRY(gemm_fused({{&L.q, projected_main}, {&L.k, projected_k}, {&L.v, projected_v}}, batch));
     const std::size_t hd = spec.attention_head_size;
+    if (!stop_after_append && gfxinfer_fused_rope_attention_supported(batch, spec.attention_head_count,
+                                                                      spec.kv_head_count,
+                                                                      static_cast<uint32_t>(hd)) != 0) {
+      // Small blocks (the MTP proposal, short verifier blocks): Q/K norm + RoPE, the K/V
+      // append and the attention in two launches, the split workgroups doing the RoPE
+      // step; the same values as the three launches below.
+      if (device_position == nullptr) {
+        GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
+            projected_main, L.q_norm, 2 * hd, projected_k, L.k_norm, hd, projected_v, spec.rotary_size,
+            spec.rope_theta, projected_main, key_cache, value_cache, attention_output, act_codes,
+            act_scales, position, config.maximum_context_tokens, batch, spec.attention_head_count,
+            spec.kv_head_count, spec.attention_head_size, attention_workspace, attention_workspace_bytes,
+            stream));
+      } else {
+        GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
+            projected_main, L.q_norm, 2 * hd, projected_k, L.k_norm, hd, projected_v, spec.rotary_size,
+            spec.rope_theta, projected_main, key_cache, value_cache, attention_output, act_codes,
+            act_scales, device_position, config.maximum_context_tokens, batch, spec.attention_head_count,
+            spec.kv_head_count, spec.attention_head_size, attention_workspace, attention_workspace_bytes,
+            stream));
+      }
+      GFXI_TRY(trace_codes(L, true, attn_width, batch));
+      return gemm_planes(L.o, mixer_update, batch, mixer_planes);
+    }
     // Q/K norm + RoPE and the K/V cache append of the block in one launch (the
     // reference's launch pair, bit for bit).
     if (device_position == nullptr) {
