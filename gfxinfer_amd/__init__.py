@@ -110,8 +110,10 @@ SIGNATURES: dict[str, tuple] = {
     "gfxinfer_launch_gated_attention_decode_block_indirect_position": (I32, [P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_quantize_i4": (I32, [P, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
     "gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_position": (I32, [P, P, P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
-    "gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4": (I32, [P, P, SZ, P, P, SZ, P, SZ, F32, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
-    "gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position": (I32, [P, P, SZ, P, P, SZ, P, SZ, F32, P, P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4": (I32, [P, P, SZ, P, P, SZ, P, SZ, F32, P, P, P, P, P, P, P, SZ, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position": (I32, [P, P, SZ, P, P, SZ, P, SZ, F32, P, P, P, P, P, P, P, P, SZ, U32, U32, U32, U32, P, SZ, P]),
+    "gfxinfer_rope_table_bytes": (SZ, [SZ, SZ]),
+    "gfxinfer_launch_rope_table": (I32, [P, SZ, SZ, F32, P]),
     "gfxinfer_fused_rope_attention_supported": (I32, [U32, U32, U32, U32]),
     "gfxinfer_launch_gdn_conv_update": (I32, [P, P, P, P, SZ, P]),
     "gfxinfer_launch_gdn_recurrent_decode": (I32, [P, P, P, P, P, P, P, P, P, U32, U32, U32, P, P]),

@@ -61,16 +61,18 @@ struct AttnArgs {
   __half* value_cache_out;  // == value_cache
   uint32_t q_stride, k_stride, rotary;
   float theta;
+  // Optional (cos, sin) of every position and rotary frequency ([capacity][rotary / 2]
+  // float2, gfxinfer_launch_rope_table's values): read instead of evaluated.
+  const float2* rope_table;
 };
 
 // Query rows (q_heads / kv_heads x tokens) a fused-RoPE attention workgroup normalizes,
 // rotates and keeps in LDS (the LDS of the four-wave kernel stays within 64 KB).
 constexpr unsigned fused_rope_rows(unsigned head_size) { return head_size == 128 ? 32u : 30u; }
-// ... and at most one token per wave and eight query heads per KV head (the input rows
-// are held in registers).  A wave's token costs one cos / sin evaluation and its query
-// rows on the path to the first MFMA: measured against the RoPE launch + attention pair,
-// one token per wave saves 1.35 us per call (one token), two per wave lose 0.56 us (five).
-constexpr unsigned kRopeTokensPerWave = 1;
+// ... and at most two tokens per wave and eight query heads per KV head (the input rows
+// are held in registers).  A wave's tokens cost their cos / sin (evaluated, or read from
+// a table) and their query rows on the path to the first MFMA.
+constexpr unsigned kRopeTokensPerWave = 2;
 constexpr unsigned kRopeMaxGroup = 8;
 bool fused_rope_supported(uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size) {
   if ((head_size != 128 && head_size != 256) || kv_heads == 0 || q_heads % kv_heads != 0) return false;
@@ -182,12 +184,13 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
   // written by this launch, so the staging below leaves them to the RoPE step.
   const uint64_t fresh = Rope ? base - 1 : ~uint64_t{0};
   if constexpr (Rope) {
-    // Wave w takes token w (at most four tokens, at most eight query heads per KV
-    // head): every input row is loaded up front (one memory latency, behind the K/V
+    // Wave w takes tokens w and w + 4 (at most eight tokens, at most eight query heads per
+    // KV head): every input row is loaded up front (one memory latency, behind the K/V
     // tile loads), then cos / sin once per token, its query rows and, when the token's
     // position falls in this split, its K / V rows.
     constexpr unsigned J = kD / 64;
     float qx[kRopeTokensPerWave][kRopeMaxGroup][J], kx[kRopeTokensPerWave][J], vx[kRopeTokensPerWave][J];
+    float2 cs[kRopeTokensPerWave];
     uint16_t qw[J], kw[J];
 #pragma unroll
     for (unsigned j = 0; j < J; ++j) {
@@ -206,6 +209,10 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
         for (unsigned j = 0; j < J; ++j) qx[i][g][j] = in[lane + 64 * j];
       }
       const uint64_t position = fresh + t;
+      cs[i] = float2{1.0F, 0.0F};
+      if (a.rope_table != nullptr && lane < a.rotary) {
+        cs[i] = a.rope_table[position * (a.rotary / 2) + lane % (a.rotary / 2)];
+      }
       if (position >= p0 && position < p0 + kSplit) {  // wave-uniform
         const std::size_t src = static_cast<std::size_t>(t) * a.kv_heads + hk;
 #pragma unroll
@@ -220,8 +227,10 @@ __global__ __launch_bounds__(Waves * 64) void attention_split_kernel(AttnArgs a)
       const unsigned t = wave + Waves * i;
       if (t >= a.tokens) break;
       const uint64_t position = fresh + t;
-      float c = 1.0F, sn = 0.0F;
-      if (lane < a.rotary) rope_cos_sin(static_cast<float>(position), a.rotary, a.theta, lane, c, sn);
+      float c = cs[i].x, sn = cs[i].y;
+      if (a.rope_table == nullptr && lane < a.rotary) {
+        rope_cos_sin(static_cast<float>(position), a.rotary, a.theta, lane, c, sn);
+      }
 #pragma unroll
       for (unsigned g = 0; g < kRopeMaxGroup; ++g) {
         if (g >= group) break;
@@ -559,10 +568,20 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
   const auto splits = static_cast<uint32_t>(split_count(head_size, capacity));
   float* partial_o = workspace;
   float* partial_ml = workspace + static_cast<std::size_t>(batch) * q_heads * splits * head_size;
-  AttnArgs args{reinterpret_cast<const __half*>(query), reinterpret_cast<const __half*>(key_cache),
-                reinterpret_cast<const __half*>(value_cache), partial_o, partial_ml, base_count, indirect,
-                batch, q_heads, kv_heads, splits, static_cast<uint32_t>(capacity),
-                1.0F / std::sqrt(static_cast<float>(head_size))};
+  AttnArgs args{};
+  args.query = reinterpret_cast<const __half*>(query);
+  args.key_cache = reinterpret_cast<const __half*>(key_cache);
+  args.value_cache = reinterpret_cast<const __half*>(value_cache);
+  args.partial_o = partial_o;
+  args.partial_ml = partial_ml;
+  args.base_count = base_count;
+  args.indirect_position = indirect;
+  args.tokens = batch;
+  args.q_heads = q_heads;
+  args.kv_heads = kv_heads;
+  args.splits = splits;
+  args.capacity = static_cast<uint32_t>(capacity);
+  args.scale = 1.0F / std::sqrt(static_cast<float>(head_size));
   const unsigned rows = (q_heads / kv_heads) * batch;
   const bool wide = rows > 4 * 16;
   const dim3 grid(splits * kv_heads), block(wide ? 512 : 256);
@@ -581,7 +600,8 @@ int32_t attention_entry(const uint16_t* query, const float* gate, const uint16_t
 
 int32_t rope_attention_entry(const float* query_input, const uint16_t* query_weight, size_t query_stride,
                              const float* key_input, const uint16_t* key_weight, size_t key_stride,
-                             const float* value_input, size_t rotary, float theta, const float* gate,
+                             const float* value_input, size_t rotary, float theta, const float* rope_table,
+                             const float* gate,
                              uint16_t* key_cache, uint16_t* value_cache, uint16_t* output, uint8_t* codes,
                              uint16_t* scales, uint64_t position, const uint64_t* indirect, size_t capacity,
                              uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size,
@@ -596,7 +616,7 @@ int32_t rope_attention_entry(const float* query_input, const uint16_t* query_wei
     return fail(GFXI_INVALID_ARGUMENT, "invalid fused Q/K RMSNorm/RoPE/K-V append/attention arguments");
   }
   if (!fused_rope_supported(batch, q_heads, kv_heads, head_size)) {
-    return fail(GFXI_UNSUPPORTED, "fused RoPE attention takes at most 4 tokens, 8 query heads per KV head and " +
+    return fail(GFXI_UNSUPPORTED, "fused RoPE attention takes at most 8 tokens, 8 query heads per KV head and " +
                                       std::to_string(fused_rope_rows(head_size)) +
                                       " query rows per KV head; use the RoPE launch then the attention launch");
   }
@@ -629,6 +649,7 @@ int32_t rope_attention_entry(const float* query_input, const uint16_t* query_wei
   args.k_stride = static_cast<uint32_t>(key_stride);
   args.rotary = static_cast<uint32_t>(rotary);
   args.theta = theta;
+  args.rope_table = reinterpret_cast<const float2*>(rope_table);
   const dim3 grid(splits * kv_heads), block(256);
   if (head_size == 128) {
     hipLaunchKernelGGL((attention_split_kernel<128, 4, true>), grid, block, 0, stream, args);
@@ -688,12 +709,14 @@ extern "C" int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indi
 extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
     const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
     const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride, const float* value_input,
-    size_t rotary_size, float rope_theta, const float* gate, uint16_t* key_cache, uint16_t* value_cache,
+    size_t rotary_size, float rope_theta, const float* rope_table, const float* gate, uint16_t* key_cache,
+    uint16_t* value_cache,
     uint16_t* output, uint8_t* codes, uint16_t* scales, size_t position, size_t capacity, uint32_t batch,
     uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace, size_t workspace_bytes,
     void* stream) {
   return rope_attention_entry(query_input, query_bf16_weight, query_input_stride, key_input, key_bf16_weight,
-                              key_input_stride, value_input, rotary_size, rope_theta, gate, key_cache,
+                              key_input_stride, value_input, rotary_size, rope_theta, rope_table, gate,
+                              key_cache,
                               value_cache, output, codes, scales, position, nullptr, capacity, batch, q_heads,
                               kv_heads, head_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
@@ -701,13 +724,15 @@ extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize
 extern "C" int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
     const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
     const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride, const float* value_input,
-    size_t rotary_size, float rope_theta, const float* gate, uint16_t* key_cache, uint16_t* value_cache,
+    size_t rotary_size, float rope_theta, const float* rope_table, const float* gate, uint16_t* key_cache,
+    uint16_t* value_cache,
     uint16_t* output, uint8_t* codes, uint16_t* scales, const uint64_t* base_position, size_t capacity,
     uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t head_size, float* workspace,
     size_t workspace_bytes, void* stream) {
   if (base_position == nullptr) return fail(GFXI_INVALID_ARGUMENT, "indirect position is null");
   return rope_attention_entry(query_input, query_bf16_weight, query_input_stride, key_input, key_bf16_weight,
-                              key_input_stride, value_input, rotary_size, rope_theta, gate, key_cache,
+                              key_input_stride, value_input, rotary_size, rope_theta, rope_table, gate,
+                              key_cache,
                               value_cache, output, codes, scales, 0, base_position, capacity, batch, q_heads,
                               kv_heads, head_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

@@ -1120,6 +1120,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   }
 }
 
+// (cos, sin) per (position, rotary frequency): rope_cos_sin's values, for the fused RoPE
+// attention's table.
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* table, uint32_t positions, uint32_t rotary,
+                                                         float theta) {
+  const uint32_t half = rotary / 2;
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<std::size_t>(positions) * half) return;
+  const uint32_t p = static_cast<uint32_t>(i / half), f = static_cast<uint32_t>(i % half);
+  float c, sn;
+  rope_cos_sin(static_cast<float>(p), rotary, theta, f, c, sn);
+  table[i] = float2{c, sn};
+}
+
 // K (fp16) and V (fp32 -> fp16) rows into the contiguous cache at the (device)
 // position (qwen_ops.hip:678-696).
 __global__ __launch_bounds__(256) void kv_append_kernel(
@@ -1891,4 +1904,24 @@ extern "C" int32_t gfxinfer_launch_argmax_mapped(const float* logits, const uint
   hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), logits,
                      token_ids, token, static_cast<uint32_t>(vocabulary_size), vocabulary_size);
   return launch_status("mapped argmax launch failed");
+}
+
+extern "C" size_t gfxinfer_rope_table_bytes(size_t positions, size_t rotary_size) {
+  if (positions == 0 || positions > (1u << 24) || rotary_size < 2 || rotary_size > 64 || rotary_size % 2 != 0) {
+    return 0;
+  }
+  return positions * (rotary_size / 2) * 2 * sizeof(float);
+}
+
+extern "C" int32_t gfxinfer_launch_rope_table(float* table, size_t positions, size_t rotary_size, float rope_theta,
+                                              void* stream) {
+  if (table == nullptr || gfxinfer_rope_table_bytes(positions, rotary_size) == 0 || !std::isfinite(rope_theta) ||
+      rope_theta <= 0.0F) {
+    return fail(GFXI_INVALID_ARGUMENT, "invalid RoPE table arguments (1..2^24 positions, even rotary size 2..64)");
+  }
+  const std::size_t n = positions * (rotary_size / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<float2*>(table),
+                     static_cast<uint32_t>(positions), static_cast<uint32_t>(rotary_size), rope_theta);
+  return launch_status("RoPE table launch failed");
 }

@@ -169,6 +169,7 @@ struct gfxinfer_session {
   float *projected_main{}, *projected_z{}, *projected_a{}, *projected_b{}, *projected_k{};
   float *projected_v{}, *gdn_mixed{}, *mixer_update{}, *gate_output{}, *up_output{};
   float *mlp_update{}, *logits{}, *attention_workspace{};
+  float* rope_table{};  // (cos, sin) per (position, rotary frequency), filled at creation
   // Split-K plane counts of the last projections into mixer_update / mlp_update.
   uint32_t mixer_planes = 1, mlp_planes = 1;
   void* argmax_keys{};
@@ -269,20 +270,21 @@ struct gfxinfer_session {
     if (!stop_after_append && gfxinfer_fused_rope_attention_supported(batch, spec.attention_head_count,
                                                                       spec.kv_head_count,
                                                                       static_cast<uint32_t>(hd)) != 0) {
-      // Small blocks (the MTP proposal, short verifier blocks): Q/K norm + RoPE, the K/V
-      // append and the attention in two launches, the split workgroups doing the RoPE
-      // step; the same values as the three launches below.
+      // Blocks of up to eight tokens (the MTP proposal, short verifier blocks): Q/K norm +
+      // RoPE, the K/V append and the attention in two launches, the split workgroups doing
+      // the RoPE step with the session's cos / sin table; the same values as the three
+      // launches below.
       if (device_position == nullptr) {
         GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
             projected_main, L.q_norm, 2 * hd, projected_k, L.k_norm, hd, projected_v, spec.rotary_size,
-            spec.rope_theta, projected_main, key_cache, value_cache, attention_output, act_codes,
+            spec.rope_theta, rope_table, projected_main, key_cache, value_cache, attention_output, act_codes,
             act_scales, position, config.maximum_context_tokens, batch, spec.attention_head_count,
             spec.kv_head_count, spec.attention_head_size, attention_workspace, attention_workspace_bytes,
             stream));
       } else {
         GFXI_TRY(gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
             projected_main, L.q_norm, 2 * hd, projected_k, L.k_norm, hd, projected_v, spec.rotary_size,
-            spec.rope_theta, projected_main, key_cache, value_cache, attention_output, act_codes,
+            spec.rope_theta, rope_table, projected_main, key_cache, value_cache, attention_output, act_codes,
             act_scales, device_position, config.maximum_context_tokens, batch, spec.attention_head_count,
             spec.kv_head_count, spec.attention_head_size, attention_workspace, attention_workspace_bytes,
             stream));
@@ -1002,6 +1004,7 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
         {"argmax_keys", &s->argmax_keys, s->argmax_keys_bytes},
         {"attention_workspace", reinterpret_cast<void**>(&s->attention_workspace),
          s->attention_workspace_bytes},
+        {"rope_table", reinterpret_cast<void**>(&s->rope_table), gfxinfer_rope_table_bytes(ctx, sp.rotary_size)},
         {"selected", reinterpret_cast<void**>(&s->selected), B * 4},
         {"drafts", reinterpret_cast<void**>(&s->draft_tokens), B * 4},
         {"verify_drafts", reinterpret_cast<void**>(&s->verify_drafts), B * 4},
@@ -1058,6 +1061,9 @@ extern "C" int32_t gfxinfer_session_create(gfxinfer_model* model,
         if (auto e = hipMemsetAsync(p, 0, bytes, s->stream); e != hipSuccess) {
           status = hip_fail(e, "recurrent state initialization failed");
         }
+      }
+      if (status == GFXI_OK) {
+        status = gfxinfer_launch_rope_table(s->rope_table, ctx, sp.rotary_size, sp.rope_theta, s->stream);
       }
       if (status == GFXI_OK) status = s->write_round_scalars(0, -1, 0, 0, 1);
       if (status == GFXI_OK) status = s->sync("decode session initialization failed");

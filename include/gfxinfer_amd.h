@@ -545,12 +545,14 @@ int32_t gfxinfer_launch_gated_attention_decode_block_quantize_i4_indirect_positi
  * attention's split workgroups normalize and rotate their KV head's query rows themselves,
  * and the workgroup whose split holds a new position writes that position's K / V rows
  * (token t at position + t) to the caches.  The query/key outputs of the RoPE launcher are
- * not written.  Shapes gfxinfer_fused_rope_attention_supported() refuses return
- * GFXI_UNSUPPORTED. */
+ * not written.  rope_table, if not NULL, holds gfxinfer_launch_rope_table's (cos, sin)
+ * values for every position of the cache (read instead of evaluated: same results).
+ * Shapes gfxinfer_fused_rope_attention_supported() refuses return GFXI_UNSUPPORTED. */
 int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
     const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
     const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride,
-    const float* value_input, size_t rotary_size, float rope_theta, const float* gate,
+    const float* value_input, size_t rotary_size, float rope_theta, const float* rope_table,
+    const float* gate,
     uint16_t* key_cache, uint16_t* value_cache, uint16_t* output, uint8_t* codes, uint16_t* scales,
     size_t position, size_t capacity, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
     uint32_t head_size, float* workspace, size_t workspace_bytes, void* stream);
@@ -558,15 +560,24 @@ int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
 int32_t gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
     const float* query_input, const uint16_t* query_bf16_weight, size_t query_input_stride,
     const float* key_input, const uint16_t* key_bf16_weight, size_t key_input_stride,
-    const float* value_input, size_t rotary_size, float rope_theta, const float* gate,
+    const float* value_input, size_t rotary_size, float rope_theta, const float* rope_table,
+    const float* gate,
     uint16_t* key_cache, uint16_t* value_cache, uint16_t* output, uint8_t* codes, uint16_t* scales,
     const uint64_t* base_position, size_t capacity, uint32_t batch, uint32_t q_heads,
     uint32_t kv_heads, uint32_t head_size, float* workspace, size_t workspace_bytes, void* stream);
-/* 1 if the fused entries take the shape: head size 128 or 256, at most 4 tokens, at most 8
+/* 1 if the fused entries take the shape: head size 128 or 256, at most 8 tokens, at most 8
  * query heads per KV head and at most 32 (head size 128) or 30 (256) query rows per KV
  * head (q_heads / kv_heads x batch); 0 otherwise. */
 int32_t gfxinfer_fused_rope_attention_supported(uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                                                 uint32_t head_size);
+
+/* No reference counterpart: (cos, sin) of the RoPE angle position * theta^(-2 f / rotary)
+ * for positions 0..positions-1 and frequencies f < rotary / 2, as float2
+ * [positions][rotary / 2] (evaluated as the RoPE launchers evaluate it, bit for bit), for
+ * the rope_table argument above.  rotary even, 2..64. */
+size_t gfxinfer_rope_table_bytes(size_t positions, size_t rotary_size);
+int32_t gfxinfer_launch_rope_table(float* table, size_t positions, size_t rotary_size, float rope_theta,
+                                   void* stream);
 
 /* ---- single-token launchers: the one-token calls of greedy_step and the MTP proposal ---
  * Each is its block launcher at batch 1 (same kernels, bit-identical results). */

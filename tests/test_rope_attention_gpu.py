@@ -2,8 +2,9 @@
 (gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4[_indirect_position]).
 
 The fused entry must give what its three-launch form gives (the RoPE launch with the K/V
-append, then the attention launch with the A4 quantizer), bit for bit: the attention
-output, its A4 codes and scales, and every cache row.  The cases put the block's new
+append, then the attention launch with the A4 quantizer), bit for bit, with its cos / sin
+evaluated and read from gfxinfer_launch_rope_table's table alike: the attention output,
+its A4 codes and scales, and every cache row.  The cases put the block's new
 positions inside one split, across a split boundary, at the start of the context and at
 the end of the cache, at both model head shapes; the cache rows outside the block must
 keep their contents.
@@ -30,15 +31,16 @@ def _fp16(x):
 CASES = [
     # (HQ, HKV, D, rotary, T, position): 64-position splits at D = 128, 32 at D = 256
     (40, 8, 128, 32, 1, 400),
-    (40, 8, 128, 32, 4, 1234),
-    (40, 8, 128, 32, 4, 62),    # positions 62..65 across the split boundary at 64
+    (40, 8, 128, 32, 5, 1234),  # five tokens: two on the first wave
+    (40, 8, 128, 32, 5, 61),    # positions 61..65 across the split boundary at 64
     (40, 8, 128, 32, 3, 0),     # the context's first tokens
-    (40, 8, 128, 32, 4, 2044),  # the last rows of a 2048-row cache
+    (40, 8, 128, 32, 6, 2042),  # the last rows of a 2048-row cache
     (24, 4, 256, 64, 1, 0),
-    (24, 4, 256, 64, 4, 30),    # across the 32-position split boundary
+    (24, 4, 256, 64, 5, 30),    # across the 32-position split boundary
     (24, 4, 256, 64, 2, 1500),
     (8, 1, 128, 64, 4, 100),    # eight query heads per KV head
-    (16, 8, 256, 64, 4, 31),
+    (8, 4, 128, 64, 8, 100),    # eight tokens: two per wave
+    (16, 8, 256, 64, 8, 29),    # eight tokens across a split boundary at head size 256
 ]
 
 
@@ -74,14 +76,16 @@ def test_fused_rope_attention_equals_three_launches(device, gx, HQ, HKV, D, rot,
     # the block's cache rows were written, the others kept
     assert not np.array_equal(want[2][position:position + T], fill_k[position:position + T])
     pos = dev(np.array([position], np.uint64))
-    for indirect in (False, True):
+    table = empty((L.gfxinfer_rope_table_bytes(cap, rot) // 4,), np.float32)
+    gx.check(L.gfxinfer_launch_rope_table(table.data_ptr(), cap, rot, theta, None))
+    for indirect, rope_table in ((False, None), (False, table.data_ptr()), (True, table.data_ptr())):
         kc2, vc2 = dev(fill_k), dev(fill_v)
         out2 = empty((T, HQ * D), np.uint16)
         codes2, scales2 = empty((T, HQ * D // 2), np.uint8), empty((T, HQ * D // 128), np.uint16)
         work.zero_()
-        say("fused rope attention", HQ, HKV, D, T, position, indirect)
+        say("fused rope attention", HQ, HKV, D, T, position, indirect, rope_table is not None)
         args = (dq.data_ptr(), dqw.data_ptr(), 2 * D, dk.data_ptr(), dkw.data_ptr(), D, dv.data_ptr(), rot, theta,
-                dq.data_ptr(), kc2.data_ptr(), vc2.data_ptr(), out2.data_ptr(), codes2.data_ptr(),
+                rope_table, dq.data_ptr(), kc2.data_ptr(), vc2.data_ptr(), out2.data_ptr(), codes2.data_ptr(),
                 scales2.data_ptr())
         tail = (cap, T, HQ, HKV, D, work.data_ptr(), wb, None)
         if indirect:
@@ -98,8 +102,10 @@ def test_fused_rope_attention_limits(device, gx):
     """Blocks of more tokens or query rows per KV head than the fused kernel keeps are refused
     (GFXI_UNSUPPORTED, the caller runs the three launches); bad arguments fail closed."""
     L = gx.lib()
-    assert L.gfxinfer_fused_rope_attention_supported(4, 40, 8, 128) == 1   # 20 rows
-    assert L.gfxinfer_fused_rope_attention_supported(5, 40, 8, 128) == 0   # 5 tokens
+    assert L.gfxinfer_fused_rope_attention_supported(6, 40, 8, 128) == 1   # 30 rows
+    assert L.gfxinfer_fused_rope_attention_supported(7, 40, 8, 128) == 0   # 35 rows
+    assert L.gfxinfer_fused_rope_attention_supported(8, 8, 4, 128) == 1    # 16 rows, 8 tokens
+    assert L.gfxinfer_fused_rope_attention_supported(9, 8, 8, 128) == 0    # 9 tokens
     assert L.gfxinfer_fused_rope_attention_supported(4, 8, 1, 128) == 1    # 32 rows
     assert L.gfxinfer_fused_rope_attention_supported(4, 8, 1, 256) == 0    # 32 rows > 30
     assert L.gfxinfer_fused_rope_attention_supported(1, 16, 1, 128) == 0   # 16 query heads per KV head
@@ -108,18 +114,22 @@ def test_fused_rope_attention_limits(device, gx):
     buf = empty((1 << 20,), np.float32)
     p = buf.data_ptr()
     wb = L.gfxinfer_attention_workspace_bytes(8, HQ, D, cap)
-    # five tokens
+    # 5 x 7 = 35 rows > 32
     assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
-        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), p, p, p, p, p, p, 0, cap, 5, HQ, HKV, D, p, wb, None
+        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), None, p, p, p, p, p, p, 0, cap, 7, HQ, HKV, D, p, wb, None
     ) == gx.UNSUPPORTED
     # position + batch beyond the cache
     assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
-        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), p, p, p, p, p, p, cap - 2, cap, 3, HQ, HKV, D, p, wb, None
+        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), None, p, p, p, p, p, p, cap - 2, cap, 3, HQ, HKV, D, p, wb, None
     ) == gx.INVALID_ARGUMENT
     # odd rotary size, null device position
     assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4(
-        p, p, 2 * D, p, p, D, p, 31, np.float32(1e7), p, p, p, p, p, p, 0, cap, 3, HQ, HKV, D, p, wb, None
+        p, p, 2 * D, p, p, D, p, 31, np.float32(1e7), None, p, p, p, p, p, p, 0, cap, 3, HQ, HKV, D, p, wb, None
     ) == gx.INVALID_ARGUMENT
+    # the table entry's own limits
+    assert L.gfxinfer_rope_table_bytes(4096, 64) == 4096 * 32 * 8
+    assert L.gfxinfer_rope_table_bytes(4096, 63) == 0
+    assert L.gfxinfer_launch_rope_table(None, 4096, 64, np.float32(1e7), None) == gx.INVALID_ARGUMENT
     assert L.gfxinfer_launch_qk_rms_norm_rope_kv_append_attention_quantize_i4_indirect_position(
-        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), p, p, p, p, p, p, None, cap, 3, HQ, HKV, D, p, wb, None
+        p, p, 2 * D, p, p, D, p, 32, np.float32(1e7), None, p, p, p, p, p, p, None, cap, 3, HQ, HKV, D, p, wb, None
     ) == gx.INVALID_ARGUMENT
