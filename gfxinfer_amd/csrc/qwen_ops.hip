@@ -788,9 +788,10 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
                                               channel(q * 4));
     }
   }
-  // Token tid's a/b (token 0's for threads past the window: loaded, never used) and the
-  // head's dt_bias / A_log, unconditionally so that no load waits on a branch.
-  const std::size_t ab = static_cast<std::size_t>(tid < T ? tid : 0u) * args.value_heads + h;
+  // Token `lane`'s a/b for the last wave, which computes decay and beta (token 0's for
+  // lanes past the window: loaded, never used), and the head's dt_bias / A_log, all
+  // unconditionally so that no load waits on a branch.
+  const std::size_t ab = static_cast<std::size_t>(lane < T ? lane : 0u) * args.value_heads + h;
   const float a_in = args.a[ab], b_in = args.b[ab];
   const uint16_t dt_bias = args.dt_bias[h], a_log = args.a_log[h];
   uint16_t wv[kChannelLoads][4];
@@ -846,18 +847,6 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
       xs[2][j] = iv[u][3];
     }
   }
-  // decay and beta per token (qwen_ops.hip:342-349).
-  if (tid < T) {
-    const float a_value = a_in + bf16_to_float(dt_bias);
-    const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
-    const float g = -expf(bf16_to_float(a_log)) * softplus;
-    const float decay = expf(g);
-    decay_s[tid] = decay;
-    beta_s[tid] = 1.0F / (1.0F + expf(-b_in));
-    if (args.decay_log != nullptr && cb == 0) {
-      args.decay_log[static_cast<std::size_t>(tid) * args.value_heads + h] = decay;
-    }
-  }
   __syncthreads();
 
   // Final conv state = the last four inputs x[T-4..T-1] = xs[T-1..T+2] (xs[0..2]
@@ -874,27 +863,22 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
   }
 
   // Stage 2: conv + SiLU per (token, channel) -> fp16 -> float (gdn_conv_kernel order).
-  for (unsigned i = tid; i < T * kWindowChannels; i += blockDim.x) {
-    const unsigned t = i / kWindowChannels, j = i - t * kWindowChannels;
+  // Wave w convolves the query and key channels of tokens w, w + 16, ... (lane l: channels
+  // 2l, 2l + 1 of each) and normalizes them in registers: the norms' sums then run over
+  // the same lane layout as a separate pass over the staged values would.  The value
+  // channels go to the threads from the last one down, so that waves without a token of
+  // their own take them first; the last wave also computes decay and beta.
+  constexpr unsigned NTHREADS = kWindowThreads;
+  auto conv_silu = [&](unsigned t, unsigned j) {
     float conv = 0.0F;
 #pragma unroll
     for (int tap = 0; tap < 4; ++tap) conv = fmaf(__half2float(xs[t + tap][j]), cw[j][tap], conv);
-    const float y = __half2float(to_half(silu(conv)));
-    if (j < D) {
-      qn[t][j] = y;
-    } else if (j < 2 * D) {
-      kn[t][j - D] = y;
-    } else {
-      vv[t][j - 2 * D] = y;
-    }
-  }
-  __syncthreads();
-
-  // Stage 3: normalized q (with the 1/sqrt(D) query scale) and k per token.
+    return __half2float(to_half(silu(conv)));
+  };
   const float query_scale = 0.08838834764831845F;  // 1/sqrt(128), qwen_ops.hip:325
-  for (unsigned t = wave; t < T; t += NT / 64) {
-    const float q0 = qn[t][2 * lane], q1 = qn[t][2 * lane + 1];
-    const float k0 = kn[t][2 * lane], k1 = kn[t][2 * lane + 1];
+  for (unsigned t = wave; t < T; t += NTHREADS / 64) {
+    const float q0 = conv_silu(t, 2 * lane), q1 = conv_silu(t, 2 * lane + 1);
+    const float k0 = conv_silu(t, D + 2 * lane), k1 = conv_silu(t, D + 2 * lane + 1);
     const float iq = rsqrtf(wave_sum(q0 * q0 + q1 * q1) + 1.0e-6F) * query_scale;
     const float ik = rsqrtf(wave_sum(k0 * k0 + k1 * k1) + 1.0e-6F);
     qn[t][2 * lane] = q0 * iq;
@@ -905,6 +889,22 @@ __global__ __launch_bounds__(kWindowThreads) void gdn_window_kernel(GdnWindowArg
       float* kl = args.key_log + static_cast<std::size_t>(t) * key_elements + kh * D;
       kl[2 * lane] = k0 * ik;
       kl[2 * lane + 1] = k1 * ik;
+    }
+  }
+  for (unsigned i = NTHREADS - 1u - tid; i < T * Cols; i += NTHREADS) {
+    const unsigned t = i / Cols, c = i - t * Cols;
+    vv[t][c] = conv_silu(t, 2 * D + c);
+  }
+  // decay and beta per token (qwen_ops.hip:342-349), lane t of the last wave.
+  if (wave == NTHREADS / 64 - 1u && lane < T) {
+    const float a_value = a_in + bf16_to_float(dt_bias);
+    const float softplus = a_value > 20.0F ? a_value : log1pf(expf(a_value));
+    const float g = -expf(bf16_to_float(a_log)) * softplus;
+    const float decay = expf(g);
+    decay_s[lane] = decay;
+    beta_s[lane] = 1.0F / (1.0F + expf(-b_in));
+    if (args.decay_log != nullptr && cb == 0) {
+      args.decay_log[static_cast<std::size_t>(lane) * args.value_heads + h] = decay;
     }
   }
   __syncthreads();
